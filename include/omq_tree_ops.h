@@ -1,0 +1,211 @@
+/*
+ * omq_tree_ops.h -- C ABI of the MI355X (gfx950) wave-MCTS tree-operation library
+ * (libomq_tree_ops.so).
+ *
+ * The library implements the tree operations of a batched, wave-parallel MCTS over
+ * CSR trees: PUCT selection with virtual loss, leaf expansion that appends children
+ * to the CSR arrays, and backup along the selected paths.  Every pointer in the
+ * structures below is a DEVICE pointer (memory owned by the caller, e.g. torch
+ * tensors); every entry point launches work on the HIP stream it is given and
+ * returns without synchronising.  Entry points return 0 on success and a negative
+ * OMQ_E_* code on a rejected argument or a failed launch; omq_last_error() then
+ * holds a message for the calling thread.
+ *
+ * Tree layout (per tree t, node ids local to the tree, node i of tree t stored at
+ * index t*capacity + i in every node array):
+ *   visit_counts[i]  int32   N   (includes in-flight virtual loss between select and backup)
+ *   value_sums[i]    float   W
+ *   priors[i]        float   P
+ *   parents[i]       int32   parent node, -1 for the root
+ *   first_child[i]   int32   CSR row offset: edge index of the first child, -1 if none
+ *   num_children[i]  int32   CSR row length
+ *   actions[i]       int32   action that leads from the parent to node i, -1 for the root
+ *   num_nodes[t]     int32   allocated nodes (the number of edges is num_nodes-1)
+ * Children are allocated by a bump pointer in blocks, and nodes and edges are bumped by
+ * the same amount, so edge e always points at node e+1.  The CSR column array is therefore
+ * implicit: the children of i are the nodes first_child[i]+1 ... first_child[i]+num_children[i].
+ *
+ * Reference interface replaced (cosmosapjw-quantum/omoknuni_quantum):
+ *   the pybind11 module `mcts_cuda_kernels` (python/mcts/gpu/mcts_kernels.cu:2342-2410)
+ *   reached through MCTSGPUAccelerator (python/mcts/gpu/mcts_gpu_accelerator.py:81-207)
+ *   and the torch.library ops of python/mcts/gpu/torch_custom_ops.py:26-193, together
+ *   with the CPU tree python/mcts/cpu/cython_tree_optimized.pyx that the CPU backend
+ *   drives.  Each entry point below names the functions it replaces.
+ */
+#ifndef OMQ_TREE_OPS_H
+#define OMQ_TREE_OPS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OMQ_ABI_VERSION 1
+
+/* error codes */
+#define OMQ_OK 0
+#define OMQ_E_ARG (-1)     /* invalid argument (size, mode, null pointer)  */
+#define OMQ_E_LAUNCH (-2)  /* HIP launch or runtime error                  */
+#define OMQ_E_LIMIT (-3)   /* size beyond a compiled limit (wave, row, depth) */
+
+/* game models (how legal actions of a node are derived) */
+#define OMQ_GAME_BOARD 0   /* legal = empty cells of the root board minus the actions on the path */
+#define OMQ_GAME_GO 1      /* as BOARD over num_actions-1 cells, plus a pass action (num_actions-1) that is always legal */
+#define OMQ_GAME_SPARSE 2  /* legal = hash-keyed sample of min_legal..max_legal distinct actions of [0,num_actions) */
+
+/* expansion policies */
+#define OMQ_EXPAND_FULL 0          /* every legal action becomes a child */
+#define OMQ_EXPAND_REFERENCE_PW 1  /* progressive widening of the reference CPU driver */
+
+/* backup sign conventions */
+#define OMQ_SIGN_LEAF_POSITIVE 0   /* W[x] += v * (-1)^(distance of x from the leaf) */
+#define OMQ_SIGN_ROOT_POSITIVE 1   /* W[x] += v * (-1)^(depth of x) */
+
+/* W accumulation */
+#define OMQ_WACC_ORDERED 0  /* per node, contributions added in simulation order (deterministic) */
+#define OMQ_WACC_ATOMIC 1   /* hardware float atomics per path entry (order not fixed) */
+
+/* limits of this build */
+#define OMQ_MAX_WAVE 4096   /* simulations per tree per wave */
+#define OMQ_MAX_ROW 512     /* children per node (a selection row is held in registers) */
+#define OMQ_MAX_DEPTH 128   /* nodes on a path */
+#define OMQ_MAX_ACTIONS 8192
+
+typedef struct omq_forest {
+  int32_t num_trees;        /* T */
+  int32_t capacity;         /* node capacity per tree */
+  int32_t num_actions;      /* A */
+  int32_t game;             /* OMQ_GAME_* */
+  int32_t legal_words;      /* 32-bit words of a board legal mask: (num_actions+31)/32 */
+  int32_t min_legal;        /* OMQ_GAME_SPARSE: fewest legal actions of a node */
+  int32_t max_legal;        /* OMQ_GAME_SPARSE: most legal actions of a node */
+  int32_t reserved;
+  int32_t* visit_counts;    /* [T*capacity] */
+  float* value_sums;        /* [T*capacity] */
+  float* priors;            /* [T*capacity] */
+  int32_t* parents;         /* [T*capacity] */
+  int32_t* first_child;     /* [T*capacity] */
+  int32_t* num_children;    /* [T*capacity] */
+  int32_t* actions;         /* [T*capacity] */
+  int32_t* num_nodes;       /* [T] */
+  uint64_t* root_keys;      /* [T] hash key of each root position */
+  uint32_t* root_legal;     /* [T*legal_words] legal actions at the root (BOARD, GO) */
+} omq_forest;
+
+/* Per-wave scratch and outputs, allocated by the caller for max_wave simulations per tree. */
+typedef struct omq_wave {
+  int32_t max_wave;         /* capacity of the per-simulation arrays, <= OMQ_MAX_WAVE */
+  int32_t max_depth;        /* path capacity, <= OMQ_MAX_DEPTH */
+  int32_t* paths;           /* [T*max_wave*max_depth] node ids root..leaf of every simulation */
+  int32_t* path_len;        /* [T*max_wave] */
+  int32_t* leaves;          /* [T*max_wave] leaf node of every simulation */
+  int32_t* sim_uid;         /* [T*max_wave] index of the simulation's leaf among the unique leaves */
+  int32_t* uleaf;           /* [T*max_wave] unique leaves, in order of first occurrence */
+  int32_t* ufirst;          /* [T*max_wave] first simulation that reached each unique leaf */
+  int32_t* ucount;          /* [T] number of unique leaves */
+  int32_t* glog;            /* [T*max_wave*max_depth*4] visited-node groups: node, depth, seg, len */
+  int32_t* gcount;          /* [T] number of groups */
+  uint16_t* gmembers;       /* [T*max_depth*max_wave] simulations of each group, in simulation order */
+  uint64_t* ukey;           /* [T*max_wave] hash key of each unique leaf */
+  int32_t* ulegal;          /* [T*max_wave] number of legal actions of each unique leaf */
+  int32_t* uedge;           /* [T*max_wave] edge offset of the children created, -1 if not expanded */
+  int32_t* unew;            /* [T*max_wave] number of children created */
+  float* policy;            /* [T*max_wave*num_actions] evaluator policy rows of the unique leaves */
+  float* values;            /* [T*max_wave] evaluator values of the unique leaves */
+  float* sim_value;         /* [T*max_wave] backup scratch: signed leaf value of every simulation */
+  int64_t* stats;           /* [T*OMQ_NSTATS] accumulated operation counters */
+  int32_t* status;          /* [4] device-side error flags (bit set, never cleared by the library) */
+} omq_wave;
+
+/* stats counters (per tree, accumulated over waves) */
+#define OMQ_ST_INTERNAL 0     /* groups that selected a child (distinct internal nodes per wave) */
+#define OMQ_ST_ROWSUM 1       /* sum of row lengths read by those groups */
+#define OMQ_ST_PATHNODES 2    /* distinct path nodes (groups) */
+#define OMQ_ST_PATHENTRIES 3  /* sum over simulations of path length */
+#define OMQ_ST_ULEAVES 4      /* unique leaves */
+#define OMQ_ST_EXPANDED 5     /* leaves expanded */
+#define OMQ_ST_NEWCHILD 6     /* children created */
+#define OMQ_ST_SIMS 7         /* simulations selected */
+#define OMQ_ST_STEPS 8        /* argmax steps (simulation x level decisions) */
+#define OMQ_ST_CAPFAIL 9      /* expansions refused for lack of capacity */
+#define OMQ_NSTATS 16
+
+/* device status bits */
+#define OMQ_STATUS_NOCHILD 1    /* best-child returned -1 at an expanded node */
+#define OMQ_STATUS_ROWLIMIT 2   /* a row longer than OMQ_MAX_ROW was met or refused */
+
+/* ---- library ---------------------------------------------------------------------- */
+int omq_abi_version(void);
+const char* omq_last_error(void);
+
+/* Reset every tree to a lone root: N=1, P=1, W=0, no children, num_nodes=1.
+ * Replaces CythonLockFreeTree.__cinit__/reset (python/mcts/cpu/cython_tree_optimized.pyx:64-103,537-558)
+ * and CSRTree.reset (python/mcts/gpu/csr_tree.py). */
+int omq_forest_reset(const omq_forest* f, void* stream);
+
+/* Select one wave of `wave_size` simulations in every tree, with virtual loss.
+ * Result equals running CythonLockFreeTree.select_path (cython_tree_optimized.pyx:177-202,
+ * best child :421-464) for simulations 0..wave_size-1 one after another: every node on a
+ * path receives +(int)virtual_loss visits as the simulation arrives, and later simulations
+ * see it.  Writes paths, path_len, leaves, the unique-leaf list and the group log, and adds
+ * the virtual loss to visit_counts.  vl_atomic=1 applies the virtual loss with one atomic
+ * per path entry instead of one add per visited node.
+ * Replaces fused_select_expand(_optimized) / parallel_select_with_virtual_loss /
+ * batch_apply_virtual_loss (python/mcts/gpu/mcts_kernels.cu:451-643,845-860,962-1053). */
+int omq_select(const omq_forest* f, const omq_wave* w, int32_t wave_size, float c_puct,
+               float virtual_loss, int32_t max_depth, int32_t vl_atomic, void* stream);
+
+/* Compute the hash key and the number of legal actions of every unique leaf of the wave.
+ * (Game-model step between selection and evaluation; no reference counterpart in the
+ * kernel module: the reference reads GPUGameStates, python/mcts/gpu/gpu_game_states.py.) */
+int omq_leaf_info(const omq_forest* f, const omq_wave* w, void* stream);
+
+/* Synthetic evaluator: for every unique leaf, priors = softmax of seeded approximately
+ * normal logits (scale logit_scale) over its legal actions, written into policy rows at
+ * the legal action slots only; value = 2u-1 with u a 24-bit hash fraction of the leaf key.
+ * Stands in for Evaluator.evaluate_batch (python/mcts/core/evaluator.py:85-104). */
+int omq_synthetic_evaluate(const omq_forest* f, const omq_wave* w, float logit_scale,
+                           void* stream);
+
+/* Expand the unique leaves of the wave in first-occurrence order: priors = policy at the legal
+ * actions renormalised over them; progressive widening (OMQ_EXPAND_REFERENCE_PW) sizes the root
+ * row from the root's visit count without the wave's in-flight virtual loss
+ * (wave_size*(int)virtual_loss); at the root, optional Dirichlet mixing with the noise
+ * vector root_noise[t*num_actions + i] (i = position among the root's legal actions, double);
+ * children allocated by bump pointer, skipping a leaf whose children do not fit.
+ * Replaces OptimizedCPUWaveSearch._batch_expand_and_backup expansion part
+ * (python/mcts/cpu/optimized_wave_search.py:367-438) + CythonLockFreeTree.expand_node
+ * (cython_tree_optimized.pyx:232-277) and batched_add_children (mcts_kernels.cu:1122-1189). */
+int omq_expand(const omq_forest* f, const omq_wave* w, int32_t wave_size, float virtual_loss,
+               int32_t expand_policy, const double* root_noise, double dirichlet_epsilon,
+               void* stream);
+
+/* Back up the wave: for every node x on the path of every simulation,
+ * N[x] += 1 - (int)virtual_loss (reverting the virtual loss of omq_select) and
+ * W[x] += sign * value(leaf).  w_mode OMQ_WACC_ORDERED adds the contributions to each node
+ * in simulation order (bit-identical to the sequential reference loop).
+ * Replaces CythonLockFreeTree.backup_value (cython_tree_optimized.pyx:204-230),
+ * OptimizedCPUWaveSearch._batch_backup_paths (optimized_wave_search.py:457-483),
+ * vectorized_backup / batch_remove_virtual_loss (mcts_kernels.cu:121-158,934-953). */
+int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float virtual_loss,
+               int32_t sign_mode, int32_t w_mode, void* stream);
+
+/* Reference-style path backup over an explicit path matrix (no group log needed):
+ * paths[b*max_depth + d], d < path_len[b], root first; values[b] is the leaf value;
+ * N[x] += 1, W[x] += sign * values[b] with float atomics; tree index tree_of[b].
+ * Replaces vectorized_backup (mcts_kernels.cu:121-158 / torch_custom_ops.py mcts::vectorized_backup). */
+int omq_paths_backup(const omq_forest* f, const int32_t* paths, const int32_t* path_len,
+                     const int32_t* tree_of, const float* values, int32_t batch, int32_t max_depth,
+                     int32_t sign_mode, void* stream);
+
+/* Reference-style virtual loss on a node list: visit_counts[tree_of[i]*capacity + nodes[i]]
+ * += delta (atomic).  delta > 0 applies, delta < 0 reverts.
+ * Replaces batch_apply_virtual_loss / batch_remove_virtual_loss (mcts_kernels.cu:845-860,934-953). */
+int omq_virtual_loss(const omq_forest* f, const int32_t* nodes, const int32_t* tree_of,
+                     int32_t count, int32_t delta, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OMQ_TREE_OPS_H */

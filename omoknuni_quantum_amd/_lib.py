@@ -1,0 +1,111 @@
+"""ctypes binding of libomq_tree_ops.so (the C ABI declared in include/omq_tree_ops.h).
+
+The library is loaded from the package directory; there is no fallback.  A missing or
+stale library raises ``LibraryNotBuilt`` so that no caller silently runs anything else.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_NAME = "libomq_tree_ops.so"
+LIB_PATH = os.path.join(_HERE, LIB_NAME)
+
+ABI_VERSION = 1
+
+# constants of include/omq_tree_ops.h
+OMQ_OK = 0
+OMQ_GAME_BOARD, OMQ_GAME_GO, OMQ_GAME_SPARSE = 0, 1, 2
+OMQ_EXPAND_FULL, OMQ_EXPAND_REFERENCE_PW = 0, 1
+OMQ_SIGN_LEAF_POSITIVE, OMQ_SIGN_ROOT_POSITIVE = 0, 1
+OMQ_WACC_ORDERED, OMQ_WACC_ATOMIC = 0, 1
+OMQ_MAX_WAVE, OMQ_MAX_ROW, OMQ_MAX_DEPTH, OMQ_MAX_ACTIONS = 4096, 512, 128, 8192
+OMQ_NSTATS = 16
+STAT_NAMES = [
+    "internal", "rowsum", "pathnodes", "pathentries", "uleaves", "expanded", "newchild",
+    "sims", "steps", "capfail",
+]
+OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT = 1, 2
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+
+
+class OmqForest(ctypes.Structure):
+    _fields_ = [
+        ("num_trees", _i32), ("capacity", _i32), ("num_actions", _i32), ("game", _i32),
+        ("legal_words", _i32), ("min_legal", _i32), ("max_legal", _i32), ("reserved", _i32),
+        ("visit_counts", _p), ("value_sums", _p), ("priors", _p), ("parents", _p),
+        ("first_child", _p), ("num_children", _p), ("actions", _p), ("num_nodes", _p),
+        ("root_keys", _p), ("root_legal", _p),
+    ]
+
+
+class OmqWave(ctypes.Structure):
+    _fields_ = [
+        ("max_wave", _i32), ("max_depth", _i32),
+        ("paths", _p), ("path_len", _p), ("leaves", _p), ("sim_uid", _p), ("uleaf", _p),
+        ("ufirst", _p), ("ucount", _p), ("glog", _p), ("gcount", _p), ("gmembers", _p),
+        ("ukey", _p), ("ulegal", _p), ("uedge", _p), ("unew", _p), ("policy", _p),
+        ("values", _p), ("sim_value", _p), ("stats", _p), ("status", _p),
+    ]
+
+
+# exported symbols and their signatures (name -> (restype, argtypes))
+_FP = ctypes.POINTER(OmqForest)
+_WP = ctypes.POINTER(OmqWave)
+SIGNATURES = {
+    "omq_abi_version": (ctypes.c_int, []),
+    "omq_last_error": (ctypes.c_char_p, []),
+    "omq_forest_reset": (ctypes.c_int, [_FP, _p]),
+    "omq_select": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, ctypes.c_float, _i32, _i32, _p]),
+    "omq_leaf_info": (ctypes.c_int, [_FP, _WP, _p]),
+    "omq_synthetic_evaluate": (ctypes.c_int, [_FP, _WP, ctypes.c_float, _p]),
+    "omq_expand": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _p, ctypes.c_double, _p]),
+    "omq_backup": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _i32, _p]),
+    "omq_paths_backup": (ctypes.c_int, [_FP, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
+    "omq_virtual_loss": (ctypes.c_int, [_FP, _p, _p, _i32, _i32, _p]),
+}
+
+
+class LibraryNotBuilt(RuntimeError):
+    pass
+
+
+class OmqError(RuntimeError):
+    pass
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load the HIP library once; raise LibraryNotBuilt when it is absent."""
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = path or LIB_PATH
+        if not os.path.exists(p):
+            raise LibraryNotBuilt(
+                f"{p} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+                " (hipcc --offload-arch=gfx950); there is no fallback implementation")
+        lib = ctypes.CDLL(p)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.omq_abi_version() != ABI_VERSION:
+            raise LibraryNotBuilt(f"{p} has ABI {lib.omq_abi_version()}, expected {ABI_VERSION}")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != OMQ_OK:
+        msg = load().omq_last_error()
+        raise OmqError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")

@@ -1,0 +1,235 @@
+"""Device-resident forest of CSR trees and the per-wave driver over the HIP library.
+
+All tree arrays and wave buffers are torch tensors on one HIP device, allocated once at
+capacity (no growth inside a search).  Every operation is launched through the C ABI of
+libomq_tree_ops.so on torch's current stream of that device; nothing synchronises inside a
+wave.  The wave loop follows the reference driver (python/mcts/core/mcts.py:1020-1063,
+python/mcts/cpu/optimized_wave_search.py:153-177): select -> evaluate unique leaves ->
+expand -> backup.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from .. import _lib
+from ..synthetic.games import GameModel
+
+
+@dataclass
+class SearchParams:
+    c_puct: float = 1.414
+    virtual_loss: float = 3.0
+    max_depth: int = 100
+    expand_policy: int = _lib.OMQ_EXPAND_FULL
+    sign_mode: int = _lib.OMQ_SIGN_LEAF_POSITIVE
+    w_mode: int = _lib.OMQ_WACC_ORDERED
+    vl_atomic: bool = False
+    dirichlet_epsilon: float = 0.0
+
+
+def _u64_to_i64(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint64).view(np.int64)
+
+
+class WaveEngine:
+    """T independent trees of one game model, sharing wave buffers of max_wave simulations."""
+
+    def __init__(self, model: GameModel, num_trees: int, capacity: int, max_wave: int,
+                 max_depth: int = 100, device: str | torch.device = "cuda",
+                 params: SearchParams | None = None):
+        self.lib = _lib.load()
+        if not torch.cuda.is_available():
+            raise RuntimeError("WaveEngine needs a HIP device (torch.cuda.is_available() is False)")
+        if max_wave > _lib.OMQ_MAX_WAVE or max_depth > _lib.OMQ_MAX_DEPTH:
+            raise ValueError(f"max_wave {max_wave} / max_depth {max_depth} beyond the library "
+                             f"limits {_lib.OMQ_MAX_WAVE} / {_lib.OMQ_MAX_DEPTH}")
+        self.model = model
+        self.T = int(num_trees)
+        self.cap = int(capacity)
+        self.MW = int(max_wave)
+        self.MD = int(max_depth)
+        self.A = model.num_actions
+        self.device = torch.device(device)
+        self.params = params or SearchParams()
+        dev = self.device
+        T, cap, MW, MD, A = self.T, self.cap, self.MW, self.MD, self.A
+        i32, f32, i64 = torch.int32, torch.float32, torch.int64
+
+        def z(n, dt):
+            return torch.zeros(n, dtype=dt, device=dev)
+
+        # tree arrays
+        self.N = z(T * cap, i32)
+        self.W = z(T * cap, f32)
+        self.P = z(T * cap, f32)
+        self.parent = z(T * cap, i32)
+        self.first = z(T * cap, i32)
+        self.nchild = z(T * cap, i32)
+        self.action = z(T * cap, i32)
+        self.num_nodes = z(T, i32)
+        self.root_keys = z(T, i64)
+        self.root_legal = z(T * model.legal_words, i32)
+        # wave buffers
+        self.paths = z(T * MW * MD, i32)
+        self.path_len = z(T * MW, i32)
+        self.leaves = z(T * MW, i32)
+        self.sim_uid = z(T * MW, i32)
+        self.uleaf = z(T * MW, i32)
+        self.ufirst = z(T * MW, i32)
+        self.ucount = z(T, i32)
+        self.glog = z(T * MW * MD * 4, i32)
+        self.gcount = z(T, i32)
+        self.gmembers = z(T * MD * MW, torch.int16)
+        self.ukey = z(T * MW, i64)
+        self.ulegal = z(T * MW, i32)
+        self.uedge = z(T * MW, i32)
+        self.unew = z(T * MW, i32)
+        self.policy = z(T * MW * A, f32)
+        self.values = z(T * MW, f32)
+        self.sim_value = z(T * MW, f32)
+        self.stats = z(T * _lib.OMQ_NSTATS, i64)
+        self.status = z(4, i32)
+        self.noise = z(T * A, torch.float64)
+        self.has_noise = False
+
+        f = _lib.OmqForest()
+        f.num_trees, f.capacity, f.num_actions, f.game = T, cap, A, model.code
+        f.legal_words = model.legal_words
+        f.min_legal, f.max_legal = model.min_legal, model.max_legal
+        for name, t in (("visit_counts", self.N), ("value_sums", self.W), ("priors", self.P),
+                        ("parents", self.parent), ("first_child", self.first),
+                        ("num_children", self.nchild), ("actions", self.action),
+                        ("num_nodes", self.num_nodes), ("root_keys", self.root_keys),
+                        ("root_legal", self.root_legal)):
+            setattr(f, name, t.data_ptr())
+        w = _lib.OmqWave()
+        w.max_wave, w.max_depth = MW, MD
+        for name in ("paths", "path_len", "leaves", "sim_uid", "uleaf", "ufirst", "ucount",
+                     "glog", "gcount", "gmembers", "ukey", "ulegal", "uedge", "unew", "policy",
+                     "values", "sim_value", "stats", "status"):
+            setattr(w, name, getattr(self, name).data_ptr())
+        self.forest = f
+        self.wave = w
+        self.forest_ref = ctypes.byref(self.forest)
+        self.wave_ref = ctypes.byref(self.wave)
+
+    # ---- plumbing ---------------------------------------------------------------------
+    def stream_handle(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def set_roots(self, keys: np.ndarray, legal: np.ndarray | None = None,
+                  noise: np.ndarray | None = None) -> None:
+        """Root keys uint64[T], root legal masks uint32[T, legal_words], noise float64[T, A]."""
+        self.root_keys.copy_(torch.from_numpy(_u64_to_i64(keys)))
+        if legal is not None:
+            lw = np.ascontiguousarray(legal, dtype=np.uint32).reshape(-1).view(np.int32)
+            self.root_legal.copy_(torch.from_numpy(lw.copy()))
+        self.has_noise = noise is not None
+        if noise is not None:
+            self.noise.copy_(torch.from_numpy(np.ascontiguousarray(noise, dtype=np.float64).reshape(-1)))
+
+    def _check(self, rc: int, what: str) -> None:
+        _lib.check(rc, what)
+
+    # ---- operations -------------------------------------------------------------------
+    def reset(self) -> None:
+        self._check(self.lib.omq_forest_reset(self.forest_ref, self.stream_handle()),
+                    "omq_forest_reset")
+
+    def select(self, wave_size: int) -> None:
+        p = self.params
+        self._check(self.lib.omq_select(self.forest_ref, self.wave_ref, wave_size, p.c_puct,
+                                        p.virtual_loss, p.max_depth, int(p.vl_atomic),
+                                        self.stream_handle()), "omq_select")
+
+    def leaf_info(self) -> None:
+        self._check(self.lib.omq_leaf_info(self.forest_ref, self.wave_ref, self.stream_handle()),
+                    "omq_leaf_info")
+
+    def expand(self, wave_size: int) -> None:
+        p = self.params
+        noise = self.noise.data_ptr() if (self.has_noise and p.dirichlet_epsilon > 0) else None
+        self._check(self.lib.omq_expand(self.forest_ref, self.wave_ref, wave_size,
+                                        p.virtual_loss, p.expand_policy, noise,
+                                        p.dirichlet_epsilon, self.stream_handle()), "omq_expand")
+
+    def backup(self, wave_size: int) -> None:
+        p = self.params
+        self._check(self.lib.omq_backup(self.forest_ref, self.wave_ref, wave_size, p.virtual_loss,
+                                        p.sign_mode, p.w_mode, self.stream_handle()),
+                    "omq_backup")
+
+    def run_wave(self, wave_size: int, evaluator, timer=None) -> None:
+        """One wave in every tree: select, leaf info, evaluate, expand, backup."""
+        if timer is not None:
+            timer.mark("tree")
+        self.select(wave_size)
+        self.leaf_info()
+        if timer is not None:
+            timer.mark("eval")
+        evaluator.evaluate_wave(self)
+        if timer is not None:
+            timer.mark("tree")
+        self.expand(wave_size)
+        self.backup(wave_size)
+        if timer is not None:
+            timer.mark(None)
+
+    def search(self, num_simulations: int, wave_size: int, evaluator, timer=None) -> None:
+        """MCTS.search on every tree: reset, root expansion (one-simulation wave on the lone
+        root; mcts.py:1659-1691), then waves of min(wave_size, remaining) simulations."""
+        if wave_size > self.MW:
+            raise ValueError(f"wave_size {wave_size} > max_wave {self.MW}")
+        self.reset()
+        self.run_wave(1, evaluator, timer)
+        done = 0
+        while done < num_simulations:
+            w = min(wave_size, num_simulations - done)
+            self.run_wave(w, evaluator, timer)
+            done += w
+
+    # ---- results ----------------------------------------------------------------------
+    def check_status(self) -> None:
+        st = int(self.status[0].item())
+        if st & _lib.OMQ_STATUS_ROWLIMIT:
+            raise _lib.OmqError(f"a node has more than {_lib.OMQ_MAX_ROW} legal actions; "
+                                "its expansion was refused by the library")
+
+    def root_policies(self) -> np.ndarray:
+        """pi[t, a] = N(child_a) / sum N over root children (mcts.py:1069-1137); uniform over
+        the action space for a tree whose root has no children."""
+        T, cap, A = self.T, self.cap, self.A
+        roots = torch.arange(T, device=self.device, dtype=torch.int64) * cap
+        first = self.first[roots].to(torch.int64)
+        k = self.nchild[roots].to(torch.int64)
+        kmax = int(k.max().item()) if T > 0 else 0
+        pol = torch.zeros((T, A), dtype=torch.float64, device=self.device)
+        if kmax > 0:
+            j = torch.arange(kmax, device=self.device, dtype=torch.int64)
+            valid = j[None, :] < k[:, None]
+            idx = roots[:, None] + first[:, None] + 1 + j[None, :]
+            idx = torch.where(valid, idx, roots[:, None])
+            visits = torch.where(valid, self.N[idx], 0).to(torch.float64)
+            acts = torch.where(valid, self.action[idx], 0).to(torch.int64)
+            pol.scatter_add_(1, acts, visits)
+        tot = pol.sum(dim=1, keepdim=True)
+        out = torch.where(tot > 0, pol / torch.where(tot > 0, tot, 1.0), 1.0 / A)
+        return out.cpu().numpy()
+
+    def host_tree(self, t: int) -> dict:
+        """Copy of tree t's used prefix (tests and debugging)."""
+        n = int(self.num_nodes[t].item())
+        b = t * self.cap
+        out = {}
+        for name in ("N", "W", "P", "parent", "first", "nchild", "action"):
+            out[name] = getattr(self, name)[b:b + n].cpu().numpy()
+        out["num_nodes"] = n
+        return out
+
+    def host_stats(self) -> dict:
+        st = self.stats.view(self.T, _lib.OMQ_NSTATS).sum(dim=0).cpu().numpy()
+        return {name: int(st[i]) for i, name in enumerate(_lib.STAT_NAMES)}

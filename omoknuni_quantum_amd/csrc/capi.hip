@@ -1,0 +1,219 @@
+// C ABI of libomq_tree_ops.so: argument checks, error reporting, launches.
+// Declarations and the reference functions each entry point replaces: include/omq_tree_ops.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "omq_tree_ops.h"
+
+namespace omq {
+size_t select_lds_bytes(int W);
+hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_puct,
+                         float virtual_loss, int max_depth, int vl_atomic, hipStream_t stream);
+hipError_t launch_leaf_info(const omq_forest& f, const omq_wave& w, int W, hipStream_t st);
+hipError_t launch_synth_eval(const omq_forest& f, const omq_wave& w, int W, float scale,
+                             hipStream_t st);
+hipError_t launch_expand(const omq_forest& f, const omq_wave& w, int W, float virtual_loss,
+                         int policy, const double* noise, double eps, hipStream_t st);
+hipError_t launch_backup(const omq_forest& f, const omq_wave& w, int W, float virtual_loss,
+                         int sign_mode, int w_mode, hipStream_t st);
+hipError_t launch_paths_backup(const omq_forest& f, const int32_t* paths, const int32_t* plen,
+                               const int32_t* tree_of, const float* values, int batch,
+                               int max_depth, int sign_mode, hipStream_t st);
+hipError_t launch_virtual_loss(const omq_forest& f, const int32_t* nodes, const int32_t* tree_of,
+                               int count, int delta, hipStream_t st);
+hipError_t launch_reset(const omq_forest& f, hipStream_t st);
+size_t leaf_lds_per_wave_host(const omq_forest& f);
+}  // namespace omq
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return OMQ_OK;
+  return fail(OMQ_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+}
+
+int check_forest(const omq_forest* f) {
+  if (!f) return fail(OMQ_E_ARG, "forest is null");
+  if (f->num_trees <= 0 || f->capacity <= 0)
+    return fail(OMQ_E_ARG, "num_trees (%d) and capacity (%d) must be positive", f->num_trees,
+                f->capacity);
+  if (f->num_actions <= 0 || f->num_actions > OMQ_MAX_ACTIONS)
+    return fail(OMQ_E_LIMIT, "num_actions %d outside [1, %d]", f->num_actions, OMQ_MAX_ACTIONS);
+  if (f->game != OMQ_GAME_BOARD && f->game != OMQ_GAME_GO && f->game != OMQ_GAME_SPARSE)
+    return fail(OMQ_E_ARG, "unknown game model %d", f->game);
+  if (f->game != OMQ_GAME_SPARSE) {
+    if (f->legal_words != (f->num_actions + 31) / 32)
+      return fail(OMQ_E_ARG, "legal_words %d != ceil(num_actions/32) = %d", f->legal_words,
+                  (f->num_actions + 31) / 32);
+    if (f->num_actions > OMQ_MAX_ROW + (f->game == OMQ_GAME_GO ? 1 : 0))
+      return fail(OMQ_E_LIMIT, "board with %d actions exceeds the row limit %d", f->num_actions,
+                  OMQ_MAX_ROW);
+  } else {
+    if (f->min_legal < 1 || f->max_legal < f->min_legal || f->max_legal > 64 ||
+        f->max_legal > f->num_actions)
+      return fail(OMQ_E_ARG, "sparse legal range [%d, %d] must lie in [1, min(64, A)]",
+                  f->min_legal, f->max_legal);
+  }
+  if (!f->visit_counts || !f->value_sums || !f->priors || !f->parents || !f->first_child ||
+      !f->num_children || !f->actions || !f->num_nodes || !f->root_keys)
+    return fail(OMQ_E_ARG, "forest has a null array");
+  if (f->game != OMQ_GAME_SPARSE && !f->root_legal)
+    return fail(OMQ_E_ARG, "board forest without root_legal");
+  return OMQ_OK;
+}
+
+int check_wave(const omq_forest* f, const omq_wave* w, int wave_size) {
+  if (!w) return fail(OMQ_E_ARG, "wave buffers are null");
+  if (w->max_wave <= 0 || w->max_wave > OMQ_MAX_WAVE)
+    return fail(OMQ_E_LIMIT, "max_wave %d outside [1, %d]", w->max_wave, OMQ_MAX_WAVE);
+  if (w->max_depth <= 0 || w->max_depth > OMQ_MAX_DEPTH)
+    return fail(OMQ_E_LIMIT, "max_depth %d outside [1, %d]", w->max_depth, OMQ_MAX_DEPTH);
+  if (wave_size <= 0 || wave_size > w->max_wave)
+    return fail(OMQ_E_ARG, "wave_size %d outside [1, max_wave=%d]", wave_size, w->max_wave);
+  if (!w->paths || !w->path_len || !w->leaves || !w->sim_uid || !w->uleaf || !w->ufirst ||
+      !w->ucount || !w->glog || !w->gcount || !w->gmembers || !w->ukey || !w->ulegal ||
+      !w->uedge || !w->unew || !w->policy || !w->values || !w->sim_value || !w->stats ||
+      !w->status)
+    return fail(OMQ_E_ARG, "wave buffers have a null array");
+  (void)f;
+  return OMQ_OK;
+}
+
+int check_leaf_lds(const omq_forest* f) {
+  if (omq::leaf_lds_per_wave_host(*f) > 64 * 1024)
+    return fail(OMQ_E_LIMIT, "per-leaf LDS need %zu bytes exceeds 64 KiB",
+                omq::leaf_lds_per_wave_host(*f));
+  return OMQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int omq_abi_version(void) { return OMQ_ABI_VERSION; }
+
+const char* omq_last_error(void) { return g_err.c_str(); }
+
+int omq_forest_reset(const omq_forest* f, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  return hip_status(omq::launch_reset(*f, (hipStream_t)stream), "omq_forest_reset");
+}
+
+int omq_select(const omq_forest* f, const omq_wave* w, int32_t wave_size, float c_puct,
+               float virtual_loss, int32_t max_depth, int32_t vl_atomic, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  rc = check_wave(f, w, wave_size);
+  if (rc) return rc;
+  if (max_depth <= 0 || max_depth > w->max_depth)
+    return fail(OMQ_E_ARG, "max_depth %d outside [1, wave max_depth=%d]", max_depth,
+                w->max_depth);
+  if (!(virtual_loss >= 0.0f) || virtual_loss > 1048576.0f)
+    return fail(OMQ_E_ARG, "virtual_loss %g must be in [0, 2^20]", (double)virtual_loss);
+  return hip_status(omq::launch_select(*f, *w, wave_size, c_puct, virtual_loss, max_depth,
+                                       vl_atomic ? 1 : 0, (hipStream_t)stream),
+                    "omq_select");
+}
+
+int omq_leaf_info(const omq_forest* f, const omq_wave* w, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  rc = check_wave(f, w, w ? w->max_wave : 1);
+  if (rc) return rc;
+  rc = check_leaf_lds(f);
+  if (rc) return rc;
+  return hip_status(omq::launch_leaf_info(*f, *w, w->max_wave, (hipStream_t)stream),
+                    "omq_leaf_info");
+}
+
+int omq_synthetic_evaluate(const omq_forest* f, const omq_wave* w, float logit_scale,
+                           void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  rc = check_wave(f, w, w ? w->max_wave : 1);
+  if (rc) return rc;
+  rc = check_leaf_lds(f);
+  if (rc) return rc;
+  return hip_status(
+      omq::launch_synth_eval(*f, *w, w->max_wave, logit_scale, (hipStream_t)stream),
+      "omq_synthetic_evaluate");
+}
+
+int omq_expand(const omq_forest* f, const omq_wave* w, int32_t wave_size, float virtual_loss,
+               int32_t expand_policy, const double* root_noise, double dirichlet_epsilon,
+               void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  rc = check_wave(f, w, wave_size);
+  if (rc) return rc;
+  rc = check_leaf_lds(f);
+  if (rc) return rc;
+  if (expand_policy != OMQ_EXPAND_FULL && expand_policy != OMQ_EXPAND_REFERENCE_PW)
+    return fail(OMQ_E_ARG, "unknown expansion policy %d", expand_policy);
+  if (!(dirichlet_epsilon >= 0.0 && dirichlet_epsilon <= 1.0))
+    return fail(OMQ_E_ARG, "dirichlet_epsilon %g outside [0, 1]", dirichlet_epsilon);
+  return hip_status(omq::launch_expand(*f, *w, wave_size, virtual_loss, expand_policy,
+                                       root_noise, dirichlet_epsilon, (hipStream_t)stream),
+                    "omq_expand");
+}
+
+int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float virtual_loss,
+               int32_t sign_mode, int32_t w_mode, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  rc = check_wave(f, w, wave_size);
+  if (rc) return rc;
+  if (sign_mode != OMQ_SIGN_LEAF_POSITIVE && sign_mode != OMQ_SIGN_ROOT_POSITIVE)
+    return fail(OMQ_E_ARG, "unknown sign mode %d", sign_mode);
+  if (w_mode != OMQ_WACC_ORDERED && w_mode != OMQ_WACC_ATOMIC)
+    return fail(OMQ_E_ARG, "unknown W accumulation mode %d", w_mode);
+  return hip_status(omq::launch_backup(*f, *w, wave_size, virtual_loss, sign_mode, w_mode,
+                                       (hipStream_t)stream),
+                    "omq_backup");
+}
+
+int omq_paths_backup(const omq_forest* f, const int32_t* paths, const int32_t* path_len,
+                     const int32_t* tree_of, const float* values, int32_t batch,
+                     int32_t max_depth, int32_t sign_mode, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  if (batch < 0 || max_depth <= 0) return fail(OMQ_E_ARG, "batch/max_depth out of range");
+  if (batch == 0) return OMQ_OK;
+  if (!paths || !path_len || !values) return fail(OMQ_E_ARG, "null path arrays");
+  if (sign_mode != OMQ_SIGN_LEAF_POSITIVE && sign_mode != OMQ_SIGN_ROOT_POSITIVE)
+    return fail(OMQ_E_ARG, "unknown sign mode %d", sign_mode);
+  return hip_status(omq::launch_paths_backup(*f, paths, path_len, tree_of, values, batch,
+                                             max_depth, sign_mode, (hipStream_t)stream),
+                    "omq_paths_backup");
+}
+
+int omq_virtual_loss(const omq_forest* f, const int32_t* nodes, const int32_t* tree_of,
+                     int32_t count, int32_t delta, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  if (count < 0) return fail(OMQ_E_ARG, "count %d < 0", count);
+  if (count == 0) return OMQ_OK;
+  if (!nodes) return fail(OMQ_E_ARG, "null node list");
+  return hip_status(omq::launch_virtual_loss(*f, nodes, tree_of, count, delta,
+                                             (hipStream_t)stream),
+                    "omq_virtual_loss");
+}
+
+}  // extern "C"

@@ -1,0 +1,260 @@
+// Device-side helpers shared by the tree-operation kernels (gfx950, wave64).
+//
+// Arithmetic rules: every floating-point expression here is evaluated in IEEE binary32 with
+// round-to-nearest-even, no contraction into FMA (-ffp-contract=off), correctly rounded
+// division and square root (-fhip-fp32-correctly-rounded-divide-sqrt).  Under those rules the
+// expressions give the same bits on any IEEE machine, which is what makes the selection
+// decisions and the synthetic workload reproducible on the host.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "omq_tree_ops.h"
+
+namespace omq {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------------------
+// Hashing: SplitMix64 finaliser (Steele, Lea, Flood, "Fast splittable pseudorandom number
+// generators", OOPSLA 2014; constants of Vigna's splitmix64.c).
+// ---------------------------------------------------------------------------------------
+constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ull;
+constexpr uint64_t kSaltValue = 0xD1B54A32D192ED03ull;
+constexpr uint64_t kSaltLogit = 0xC2B2AE3D27D4EB4Full;
+constexpr uint64_t kSaltCount = 0x165667B19E3779F9ull;
+constexpr uint64_t kSaltFloyd = 0xFF51AFD7ED558CCDull;
+
+__host__ __device__ inline uint64_t splitmix64(uint64_t x) {
+  uint64_t z = x + kGolden;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// key of the child reached from a node with key `k` by action `a`
+__host__ __device__ inline uint64_t child_key(uint64_t k, int a) {
+  return splitmix64(k ^ ((uint64_t)(a + 1) * kGolden));
+}
+
+// leaf value in [-1, 1): v = 2u - 1, u = 24-bit hash fraction (exact in binary32)
+__device__ inline float key_value(uint64_t k) {
+  uint32_t u24 = (uint32_t)(splitmix64(k ^ kSaltValue) >> 40);
+  float u = (float)u24 * (1.0f / 16777216.0f);
+  return 2.0f * u - 1.0f;
+}
+
+// Approximately standard-normal draw for (key, action): Irwin-Hall sum of twelve discrete
+// uniforms (u16 + 1/2)/65536 minus 6.  Mean 0, variance 1 - 2^-32.  Computed in integers and
+// converted exactly: z = (S + 6 - 393216) / 65536 with |S + 6 - 393216| < 2^19.
+__device__ inline float key_normal(uint64_t k, int a) {
+  uint64_t h0 = splitmix64(k ^ ((uint64_t)(a + 1) * kSaltLogit));
+  uint64_t h1 = splitmix64(h0);
+  uint64_t h2 = splitmix64(h1);
+  int32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s += (int32_t)((h0 >> (16 * i)) & 0xFFFF);
+    s += (int32_t)((h1 >> (16 * i)) & 0xFFFF);
+    s += (int32_t)((h2 >> (16 * i)) & 0xFFFF);
+  }
+  return (float)(s + 6 - 393216) * (1.0f / 65536.0f);
+}
+
+// e^x from basic operations: Cody-Waite reduction x = k ln2 + r (ln2 split into a 15-bit
+// head and a tail, so k*head is exact for |k| < 2^9), degree-6 Taylor polynomial of e^r in
+// Horner form, scaling by 2^k.  Results below e^-87 are returned as 0 (no subnormals).
+__device__ inline float exp_cw(float x) {
+  if (!(x > -87.0f)) return 0.0f;
+  if (x > 88.0f) x = 88.0f;
+  const float k = __builtin_rintf(x * 1.44269502f);
+  const float r = (x - k * 0.693145751953125f) - k * 1.42860677e-06f;
+  float p = 1.0f / 720.0f;
+  p = p * r + 1.0f / 120.0f;
+  p = p * r + 1.0f / 24.0f;
+  p = p * r + 1.0f / 6.0f;
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  return __builtin_ldexpf(p, (int)k);
+}
+
+// ---------------------------------------------------------------------------------------
+// Wave64 helpers
+// ---------------------------------------------------------------------------------------
+__device__ inline int lane_id() { return __lane_id(); }
+
+__device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// index of the lowest set bit of a non-zero mask
+__device__ inline int lowest_lane(uint64_t m) { return __ffsll((unsigned long long)m) - 1; }
+
+__device__ inline float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ inline int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+
+// Max over the 64 lanes (any value, no NaN), broadcast to every lane.  Max is exact and
+// order-free, so the DPP reduction tree below (row shifts, then row broadcasts into lane 63)
+// gives the same result as any other order.
+__device__ inline float wave_max_f32(float x) {
+  const int ninf = (int)0xFF800000u;
+  int xi = __float_as_int(x);
+  int y;
+  y = __builtin_amdgcn_update_dpp(ninf, xi, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x = fmaxf(x, __int_as_float(y)); xi = __float_as_int(x);
+  y = __builtin_amdgcn_update_dpp(ninf, xi, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x = fmaxf(x, __int_as_float(y)); xi = __float_as_int(x);
+  y = __builtin_amdgcn_update_dpp(ninf, xi, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x = fmaxf(x, __int_as_float(y)); xi = __float_as_int(x);
+  y = __builtin_amdgcn_update_dpp(ninf, xi, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x = fmaxf(x, __int_as_float(y)); xi = __float_as_int(x);
+  y = __builtin_amdgcn_update_dpp(ninf, xi, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x = fmaxf(x, __int_as_float(y)); xi = __float_as_int(x);
+  y = __builtin_amdgcn_update_dpp(ninf, xi, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  x = fmaxf(x, __int_as_float(y)); xi = __float_as_int(x);
+  return __int_as_float(__builtin_amdgcn_readlane(xi, 63));
+}
+
+// Canonical wave sum: lane l has already accumulated, in ascending element order starting
+// from +0, the elements whose index is congruent to l mod 64; the 64 partial sums are then
+// combined by the xor butterfly with distances 32,16,8,4,2,1.  Every lane ends with the same
+// value.  (The host restatement of this order must match it exactly.)
+__device__ inline float wave_sum_canonical(float partial) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) partial = partial + __shfl_xor(partial, off, 64);
+  return partial;
+}
+__device__ inline double wave_sum_canonical_d(double partial) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) partial = partial + __shfl_xor(partial, off, 64);
+  return partial;
+}
+
+__device__ inline int wave_sum_i(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// exclusive prefix sum over lanes (lane 0 gets 0); total returned through *total
+__device__ inline int wave_excl_scan(int v, int* total) {
+  const int lane = lane_id();
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  *total = __shfl(x, 63, 64);
+  return x - v;
+}
+
+// ---------------------------------------------------------------------------------------
+// Game models: legal actions of a leaf
+// ---------------------------------------------------------------------------------------
+
+// number of legal actions of a SPARSE-model node with key k
+__device__ inline int sparse_legal_count(const omq_forest& f, uint64_t k) {
+  const uint32_t span = (uint32_t)(f.max_legal - f.min_legal + 1);
+  return f.min_legal + (int)((uint32_t)(splitmix64(k ^ kSaltCount) >> 33) % span);
+}
+
+// Sorted legal list of a SPARSE-model node: Floyd's sampling of n distinct values of
+// [0, A) (Bentley & Floyd, "A sample of brilliance", CACM 30(9), 1987), then sorted by rank.
+// Requires n <= 64.  `list` is wave-private LDS of at least n entries.  Returns n.
+__device__ inline int sparse_legal_list(const omq_forest& f, uint64_t k, int* list) {
+  const int lane = lane_id();
+  const int A = f.num_actions;
+  const int n = sparse_legal_count(f, k);
+  int mine = -1;  // lane i holds the i-th sampled value
+  for (int i = 0; i < n; ++i) {
+    const int j = A - n + i;
+    const uint32_t r =
+        (uint32_t)(splitmix64(k ^ ((uint64_t)(j + 1) * kSaltFloyd)) >> 32) % (uint32_t)(j + 1);
+    const bool hit = __ballot(lane < i && mine == (int)r) != 0;
+    if (lane == i) mine = hit ? j : (int)r;
+  }
+  // rank sort (values are distinct)
+  int rank = 0;
+  for (int i = 0; i < n; ++i) {
+    const int v = readlane_i(mine, i);
+    rank += (lane < n && v < mine) ? 1 : 0;
+  }
+  if (lane < n) list[rank] = mine;
+  wave_sync();
+  return n;
+}
+
+// Load the actions on the path of simulation s (depths 1..L-1) into lanes: lane j holds
+// the action at depth j+1 (and depth j+65 in *a_hi).  Returns L.
+__device__ inline int load_path_actions(const omq_forest& f, const omq_wave& w, int t, int s,
+                                        int* a_lo, int* a_hi) {
+  const int lane = lane_id();
+  const int64_t tb = (int64_t)t * f.capacity;
+  const int L = w.path_len[(int64_t)t * w.max_wave + s];
+  const int32_t* path = w.paths + ((int64_t)t * w.max_wave + s) * w.max_depth;
+  int lo = -1, hi = -1;
+  if (lane + 1 < L) lo = f.actions[tb + path[lane + 1]];
+  if (lane + 65 < L) hi = f.actions[tb + path[lane + 65]];
+  *a_lo = lo;
+  *a_hi = hi;
+  return L;
+}
+
+// Board legal mask of a leaf into wave-private LDS words: root mask minus path cells.
+// For OMQ_GAME_GO the pass action (A-1) is never cleared.
+__device__ inline void board_legal_mask(const omq_forest& f, int t, int L, int a_lo, int a_hi,
+                                        uint32_t* mask) {
+  const int lane = lane_id();
+  const int nw = f.legal_words;
+  const uint32_t* root = f.root_legal + (int64_t)t * nw;
+  for (int i = lane; i < nw; i += kWave) mask[i] = root[i];
+  wave_sync();
+  const int pass = (f.game == OMQ_GAME_GO) ? f.num_actions - 1 : -1;
+  if (lane + 1 < L && a_lo >= 0 && a_lo != pass)
+    atomicAnd(&mask[a_lo >> 5], ~(1u << (a_lo & 31)));
+  if (lane + 65 < L && a_hi >= 0 && a_hi != pass)
+    atomicAnd(&mask[a_hi >> 5], ~(1u << (a_hi & 31)));
+  wave_sync();
+}
+
+// Sorted legal list from a board mask (ascending actions).  Returns the count.
+__device__ inline int board_legal_list(const omq_forest& f, const uint32_t* mask, int* list) {
+  const int lane = lane_id();
+  const int A = f.num_actions;
+  int base = 0;
+  for (int c = 0; c < A; c += kWave) {
+    const int a = c + lane;
+    const bool legal = a < A && ((mask[a >> 5] >> (a & 31)) & 1u);
+    const uint64_t b = __ballot(legal);
+    if (legal) {
+      const int pos = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0));
+      list[pos] = a;
+    }
+    base += __popcll(b);
+  }
+  wave_sync();
+  return base;
+}
+
+// Legal list of unique leaf u of tree t (sorted ascending) into wave-private LDS.
+// `mask` must hold legal_words words (board games), `list` the maximum legal count.
+__device__ inline int leaf_legal_list(const omq_forest& f, const omq_wave& w, int t, int u,
+                                      uint32_t* mask, int* list) {
+  if (f.game == OMQ_GAME_SPARSE) {
+    return sparse_legal_list(f, w.ukey[(int64_t)t * w.max_wave + u], list);
+  }
+  const int s0 = w.ufirst[(int64_t)t * w.max_wave + u];
+  int a_lo, a_hi;
+  const int L = load_path_actions(f, w, t, s0, &a_lo, &a_hi);
+  board_legal_mask(f, t, L, a_lo, a_hi, mask);
+  return board_legal_list(f, mask, list);
+}
+
+}  // namespace omq

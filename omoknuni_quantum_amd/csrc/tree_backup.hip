@@ -1,0 +1,204 @@
+// Backup with virtual-loss revert (gfx950).
+//
+// Sequential definition: for every simulation s in order and every node x on its path,
+//   N[x] = N[x] - VL + 1                      (cython_tree_optimized.pyx:222)
+//   W[x] = W[x] + sign(x) * v(leaf of s)      (optimized_wave_search.py:472-483: leaf +v,
+//                                              parent -v, ...; or root-positive, pyx:216-224)
+// Ordered mode uses the group log of the selection: a node appears in exactly one group per
+// wave, and the group's members are in simulation order, so folding the members' signed
+// values into W[x] in that order gives the sequential result bit for bit, with no atomics.
+// Small groups are folded by one lane each; groups with more than kBigGroup members by the
+// whole wave (lanes load, one running sum through v_readlane).
+#include "omq_common.h"
+
+namespace omq {
+
+constexpr int kBackupThreads = 256;
+constexpr int kBigGroup = 32;
+
+// signed value per simulation: v(leaf), negated when the leaf depth is odd in leaf-positive
+// mode, so that the contribution at depth d is (d odd ? -sv : sv)
+__global__ void sim_value_kernel(omq_forest f, omq_wave w, int W, int sign_mode) {
+  const int t = blockIdx.y;
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= W) return;
+  const int64_t wb = (int64_t)t * w.max_wave;
+  const float v = w.values[wb + w.sim_uid[wb + s]];
+  const int L = w.path_len[wb + s];
+  const bool neg = sign_mode == OMQ_SIGN_LEAF_POSITIVE && ((L - 1) & 1);
+  w.sim_value[wb + s] = neg ? -v : v;
+}
+
+__global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_forest f, omq_wave w,
+                                                                       int vli) {
+  const int t = blockIdx.y;
+  const int lane = lane_id();
+  const int64_t tb = (int64_t)t * f.capacity;
+  const int64_t wb = (int64_t)t * w.max_wave;
+  const int MW = w.max_wave, MD = w.max_depth;
+  const int64_t gmax = (int64_t)MW * MD;
+  const int G = w.gcount[t];
+  const int waves_total = gridDim.x * (kBackupThreads / kWave);
+  const int wave_global = blockIdx.x * (kBackupThreads / kWave) + threadIdx.x / kWave;
+  const float* sv = w.sim_value + wb;
+  for (int g0 = wave_global * kWave; g0 < G; g0 += waves_total * kWave) {
+    const int g = g0 + lane;
+    int p = 0, d = 0, seg = 0, m = 0;
+    if (g < G) {
+      const int4 rec = *reinterpret_cast<const int4*>(w.glog + ((int64_t)t * gmax + g) * 4);
+      p = rec.x;
+      d = rec.y;
+      seg = rec.z;
+      m = rec.w;
+    }
+    const uint16_t* mem = w.gmembers + ((int64_t)t * MD + d) * MW + seg;
+    if (g < G && m <= kBigGroup) {
+      float acc = f.value_sums[tb + p];
+      const bool odd = d & 1;
+      int i = 0;
+      for (; i + 4 <= m; i += 4) {
+        const float c0 = sv[mem[i]], c1 = sv[mem[i + 1]], c2 = sv[mem[i + 2]],
+                    c3 = sv[mem[i + 3]];
+        acc = acc + (odd ? -c0 : c0);
+        acc = acc + (odd ? -c1 : c1);
+        acc = acc + (odd ? -c2 : c2);
+        acc = acc + (odd ? -c3 : c3);
+      }
+      for (; i < m; ++i) {
+        const float c0 = sv[mem[i]];
+        acc = acc + (odd ? -c0 : c0);
+      }
+      f.value_sums[tb + p] = acc;
+      f.visit_counts[tb + p] += m - vli * m;
+    }
+    // big groups: the whole wave, one group at a time
+    uint64_t big = __ballot(g < G && m > kBigGroup);
+    while (big) {
+      const int l = lowest_lane(big);
+      big &= big - 1;
+      const int bp = readlane_i(p, l), bd = readlane_i(d, l), bseg = readlane_i(seg, l),
+                bm = readlane_i(m, l);
+      const uint16_t* bmem = w.gmembers + ((int64_t)t * MD + bd) * MW + bseg;
+      const bool odd = bd & 1;
+      float acc = f.value_sums[tb + bp];
+      for (int c = 0; c < bm; c += kWave) {
+        float x = 0.0f;
+        if (c + lane < bm) {
+          const float v = sv[bmem[c + lane]];
+          x = odd ? -v : v;
+        }
+        const int lim = min(kWave, bm - c);
+        for (int j = 0; j < lim; ++j) acc = acc + readlane_f(x, j);
+      }
+      if (lane == 0) {
+        f.value_sums[tb + bp] = acc;
+        f.visit_counts[tb + bp] += bm - vli * bm;
+      }
+    }
+  }
+}
+
+// atomic mode: one lane per simulation walks its path with float atomics (order not fixed)
+__global__ void backup_atomic_kernel(omq_forest f, omq_wave w, int W, int vli) {
+  const int t = blockIdx.y;
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= W) return;
+  const int64_t tb = (int64_t)t * f.capacity;
+  const int64_t wb = (int64_t)t * w.max_wave;
+  const int L = w.path_len[wb + s];
+  const float v = w.sim_value[wb + s];
+  const int32_t* path = w.paths + (wb + s) * w.max_depth;
+  for (int d = 0; d < L; ++d) {
+    const int x = path[d];
+    atomicAdd(&f.visit_counts[tb + x], 1 - vli);
+    unsafeAtomicAdd(&f.value_sums[tb + x], (d & 1) ? -v : v);
+  }
+}
+
+// reference-style backup over an explicit path matrix (vectorized_backup_kernel)
+__global__ void paths_backup_kernel(omq_forest f, const int32_t* paths, const int32_t* plen,
+                                    const int32_t* tree_of, const float* values, int batch,
+                                    int max_depth, int sign_mode) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  const int t = tree_of ? tree_of[b] : 0;
+  const int64_t tb = (int64_t)t * f.capacity;
+  const int L = plen[b];
+  const float v = values[b];
+  for (int d = 0; d < L; ++d) {
+    const int x = paths[(int64_t)b * max_depth + d];
+    if (x < 0) break;
+    const int e = sign_mode == OMQ_SIGN_LEAF_POSITIVE ? (L - 1 - d) : d;
+    atomicAdd(&f.visit_counts[tb + x], 1);
+    unsafeAtomicAdd(&f.value_sums[tb + x], (e & 1) ? -v : v);
+  }
+}
+
+__global__ void virtual_loss_kernel(omq_forest f, const int32_t* nodes, const int32_t* tree_of,
+                                    int count, int delta) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const int t = tree_of ? tree_of[i] : 0;
+  const int x = nodes[i];
+  if (x < 0) return;
+  atomicAdd(&f.visit_counts[(int64_t)t * f.capacity + x], delta);
+}
+
+__global__ void reset_kernel(omq_forest f) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= f.num_trees) return;
+  const int64_t r = (int64_t)t * f.capacity;
+  f.visit_counts[r] = 1;
+  f.value_sums[r] = 0.0f;
+  f.priors[r] = 1.0f;
+  f.parents[r] = -1;
+  f.first_child[r] = -1;
+  f.num_children[r] = 0;
+  f.actions[r] = -1;
+  f.num_nodes[t] = 1;
+}
+
+// ---------------------------------------------------------------------------------------
+hipError_t launch_backup(const omq_forest& f, const omq_wave& w, int W, float virtual_loss,
+                         int sign_mode, int w_mode, hipStream_t st) {
+  const int vli = (int)virtual_loss;
+  dim3 g1((W + 255) / 256, f.num_trees);
+  hipLaunchKernelGGL(sim_value_kernel, g1, dim3(256), 0, st, f, w, W, sign_mode);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (w_mode == OMQ_WACC_ATOMIC) {
+    hipLaunchKernelGGL(backup_atomic_kernel, g1, dim3(256), 0, st, f, w, W, vli);
+    return hipGetLastError();
+  }
+  // group count is on the device; size the grid for a typical wave (groups ~ W * depth),
+  // the kernel strides over the rest
+  const int est_groups = W * 8;
+  int blocks = (est_groups + kBackupThreads - 1) / kBackupThreads;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(backup_groups_kernel, dim3(blocks, f.num_trees), dim3(kBackupThreads), 0, st,
+                     f, w, vli);
+  return hipGetLastError();
+}
+
+hipError_t launch_paths_backup(const omq_forest& f, const int32_t* paths, const int32_t* plen,
+                               const int32_t* tree_of, const float* values, int batch,
+                               int max_depth, int sign_mode, hipStream_t st) {
+  hipLaunchKernelGGL(paths_backup_kernel, dim3((batch + 255) / 256), dim3(256), 0, st, f, paths,
+                     plen, tree_of, values, batch, max_depth, sign_mode);
+  return hipGetLastError();
+}
+
+hipError_t launch_virtual_loss(const omq_forest& f, const int32_t* nodes, const int32_t* tree_of,
+                               int count, int delta, hipStream_t st) {
+  hipLaunchKernelGGL(virtual_loss_kernel, dim3((count + 255) / 256), dim3(256), 0, st, f, nodes,
+                     tree_of, count, delta);
+  return hipGetLastError();
+}
+
+hipError_t launch_reset(const omq_forest& f, hipStream_t st) {
+  hipLaunchKernelGGL(reset_kernel, dim3((f.num_trees + 255) / 256), dim3(256), 0, st, f);
+  return hipGetLastError();
+}
+
+}  // namespace omq

@@ -1,0 +1,392 @@
+// Leaf bookkeeping, synthetic evaluator and expansion (gfx950).
+//
+// Expansion follows the reference CPU driver (python/mcts/cpu/optimized_wave_search.py:367-438)
+// and CythonLockFreeTree.expand_node (python/mcts/cpu/cython_tree_optimized.pyx:232-277):
+// unique leaves in first-occurrence order; legal priors renormalised by their sum; Dirichlet
+// mixing at the root; children bumped contiguously for nodes and edges; a leaf whose children
+// do not fit is skipped (and later leaves may still fit).  The prior sum uses the canonical
+// wave order (wave_sum_canonical) in place of numpy's pairwise order.
+//
+// Kernels per wave:
+//   leaf_info_kernel    wave per unique leaf: hash key (fold over path actions), legal count
+//   synth_eval_kernel   wave per unique leaf: synthetic priors/value (evaluator stand-in)
+//   expand_plan_kernel  workgroup per tree: children counts, scan, capacity rule, row headers
+//   expand_write_kernel wave per expanded leaf: priors, children N/W/P/parent/action/row
+#include "omq_common.h"
+
+namespace omq {
+
+// wave-private LDS carve-up used by the per-leaf kernels
+struct LeafLds {
+  uint32_t* mask;  // legal_words: board legal mask
+  uint32_t* bits;  // ceil(list_cap/32): chosen flags of progressive widening
+  int* list;       // list_cap: legal actions, ascending
+  double* val;     // list_cap: priors of the legal actions
+};
+
+__host__ __device__ inline int list_cap(const omq_forest& f) {
+  return f.game == OMQ_GAME_SPARSE ? f.max_legal : f.num_actions;
+}
+
+__host__ __device__ inline size_t leaf_lds_per_wave(const omq_forest& f) {
+  const size_t lc = (size_t)list_cap(f);
+  size_t b = (size_t)f.legal_words * 4 + ((lc + 31) / 32) * 4 + lc * 4;
+  b = (b + 7) & ~(size_t)7;
+  return b + lc * 8;
+}
+
+__device__ inline LeafLds carve(const omq_forest& f, unsigned char* base, int wave) {
+  const size_t lc = (size_t)list_cap(f);
+  unsigned char* p = base + leaf_lds_per_wave(f) * wave;
+  LeafLds l;
+  l.mask = reinterpret_cast<uint32_t*>(p);
+  l.bits = l.mask + f.legal_words;
+  l.list = reinterpret_cast<int*>(l.bits + (lc + 31) / 32);
+  size_t off = (size_t)f.legal_words * 4 + ((lc + 31) / 32) * 4 + lc * 4;
+  off = (off + 7) & ~(size_t)7;
+  l.val = reinterpret_cast<double*>(p + off);
+  return l;
+}
+
+// ---------------------------------------------------------------------------------------
+__global__ void leaf_info_kernel(omq_forest f, omq_wave w) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int t = blockIdx.y;
+  const int wave = threadIdx.x / kWave;
+  const int u = blockIdx.x * (blockDim.x / kWave) + wave;
+  const int lane = lane_id();
+  const int64_t wb = (int64_t)t * w.max_wave;
+  if (u >= w.ucount[t]) return;
+  LeafLds l = carve(f, smem, wave);
+  const int s0 = w.ufirst[wb + u];
+  int a_lo, a_hi;
+  const int L = load_path_actions(f, w, t, s0, &a_lo, &a_hi);
+  uint64_t key = f.root_keys[t];
+  for (int d = 1; d < L; ++d) {
+    const int a = (d <= 64) ? readlane_i(a_lo, d - 1) : readlane_i(a_hi, d - 65);
+    key = child_key(key, a);
+  }
+  int count;
+  if (f.game == OMQ_GAME_SPARSE) {
+    count = sparse_legal_count(f, key);
+  } else {
+    board_legal_mask(f, t, L, a_lo, a_hi, l.mask);
+    int c = 0;
+    for (int i = lane; i < f.legal_words; i += kWave) c += __popc(l.mask[i]);
+    count = wave_sum_i(c);
+  }
+  if (lane == 0) {
+    w.ukey[wb + u] = key;
+    w.ulegal[wb + u] = count;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+__global__ void synth_eval_kernel(omq_forest f, omq_wave w, float scale) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int t = blockIdx.y;
+  const int wave = threadIdx.x / kWave;
+  const int u = blockIdx.x * (blockDim.x / kWave) + wave;
+  const int lane = lane_id();
+  const int64_t wb = (int64_t)t * w.max_wave;
+  if (u >= w.ucount[t]) return;
+  LeafLds l = carve(f, smem, wave);
+  const uint64_t key = w.ukey[wb + u];
+  const int n = leaf_legal_list(f, w, t, u, l.mask, l.list);
+  float* row = w.policy + (wb + u) * (int64_t)f.num_actions;
+  float mx = -__builtin_inff();
+  for (int i = lane; i < n; i += kWave) mx = fmaxf(mx, scale * key_normal(key, l.list[i]));
+  mx = wave_max_f32(mx);
+  float part = 0.0f;
+  for (int i = lane; i < n; i += kWave) {
+    const float e = exp_cw(scale * key_normal(key, l.list[i]) - mx);
+    l.val[i] = (double)e;
+    part = part + e;
+  }
+  const float S = wave_sum_canonical(part);
+  for (int i = lane; i < n; i += kWave) row[l.list[i]] = (float)l.val[i] / S;
+  if (lane == 0) w.values[wb + u] = key_value(key);
+}
+
+// ---------------------------------------------------------------------------------------
+// progressive widening of the reference CPU driver (optimized_wave_search.py:394-415 and
+// MAX_CHILDREN of cython_tree_optimized.pyx:31,239):
+//   root:     mc = max(5, min(min(L, int(10*sqrt(N0)) + 1), 15)); the chosen set is the top-mc
+//             (if L > mc, renormalised) or all L; the first min(8, |chosen|) become children
+//   non-root: the top-3 (if L > 3, renormalised) or all L
+__device__ inline int pw_root_mc(int L, int N0) {
+  const int m1 = min(L, (int)(10.0 * sqrt((double)N0)) + 1);
+  return max(5, min(m1, 15));
+}
+
+struct ExpCfg {
+  int W;
+  int vli;
+  int policy;   // OMQ_EXPAND_*
+  const double* noise;
+  double eps;
+};
+
+constexpr int kPlanThreads = 1024;
+
+__global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f, omq_wave w,
+                                                                   ExpCfg c) {
+  extern __shared__ __align__(16) int want[];  // [ucount]
+  __shared__ int s_wtot[kPlanThreads / kWave];
+  __shared__ int s_total;
+  __shared__ unsigned long long s_exp, s_new, s_fail;
+  const int t = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t tb = (int64_t)t * f.capacity;
+  const int64_t wb = (int64_t)t * w.max_wave;
+  const int U = w.ucount[t];
+  if (tid == 0) {
+    s_exp = 0;
+    s_new = 0;
+    s_fail = 0;
+  }
+  for (int u = tid; u < U; u += kPlanThreads) {
+    const int leaf = w.uleaf[wb + u];
+    const int L = w.ulegal[wb + u];
+    int k = 0;
+    if (f.num_children[tb + leaf] == 0 && L > 0) {
+      if (c.policy == OMQ_EXPAND_FULL) {
+        k = L;
+      } else if (leaf == 0) {
+        const int N0 = f.visit_counts[tb] - c.vli * c.W;
+        const int mc = pw_root_mc(L, N0);
+        k = min(L > mc ? mc : L, 8);
+      } else {
+        k = min(L, 3);
+      }
+    }
+    if (k > OMQ_MAX_ROW) {  // a selection row must fit the register tile
+      atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
+      k = 0;
+    }
+    want[u] = k;
+  }
+  __syncthreads();
+  // exclusive scan over contiguous chunks
+  const int per = (U + kPlanThreads - 1) / kPlanThreads;
+  const int lo = tid * per, hi = min(lo + per, U);
+  int sum = 0;
+  for (int i = lo; i < hi; ++i) sum += want[i];
+  int wt;
+  const int wex = wave_excl_scan(sum, &wt);
+  if (lane_id() == 0) s_wtot[tid / kWave] = wt;
+  __syncthreads();
+  int wbase = 0, total = 0;
+  for (int i = 0; i < kPlanThreads / kWave; ++i) {
+    if (i < tid / kWave) wbase += s_wtot[i];
+    total += s_wtot[i];
+  }
+  const int base = f.num_nodes[t];
+  const bool all_fit = (int64_t)base + total <= (int64_t)f.capacity;
+  // excl offsets into a second pass; want[] keeps k, offsets go to uedge directly
+  int run = wbase + wex;
+  if (all_fit) {
+    for (int i = lo; i < hi; ++i) {
+      const int k = want[i];
+      w.uedge[wb + i] = k > 0 ? base + run - 1 : -1;
+      w.unew[wb + i] = k;
+      if (k > 0) {
+        const int leaf = w.uleaf[wb + i];
+        f.first_child[tb + leaf] = base + run - 1;
+        f.num_children[tb + leaf] = k;
+        atomicAdd(&s_exp, 1ull);
+        atomicAdd(&s_new, (unsigned long long)k);
+      }
+      run += k;
+    }
+    if (tid == 0) s_total = total;
+  } else if (tid == 0) {
+    // capacity boundary: sequential first-fit in leaf order (expand_node refuses a leaf whose
+    // children do not fit; later, smaller leaves may still fit)
+    int cur = base;
+    for (int i = 0; i < U; ++i) {
+      const int k = want[i];
+      if (k > 0 && (int64_t)cur + k <= (int64_t)f.capacity) {
+        w.uedge[wb + i] = cur - 1;
+        w.unew[wb + i] = k;
+        const int leaf = w.uleaf[wb + i];
+        f.first_child[tb + leaf] = cur - 1;
+        f.num_children[tb + leaf] = k;
+        s_exp += 1;
+        s_new += (unsigned long long)k;
+        cur += k;
+      } else {
+        w.uedge[wb + i] = -1;
+        w.unew[wb + i] = 0;
+        if (k > 0) s_fail += 1;
+      }
+    }
+    s_total = cur - base;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    f.num_nodes[t] = base + s_total;
+    int64_t* st = w.stats + (int64_t)t * OMQ_NSTATS;
+    atomicAdd(reinterpret_cast<unsigned long long*>(&st[OMQ_ST_EXPANDED]), s_exp);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&st[OMQ_ST_NEWCHILD]), s_new);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&st[OMQ_ST_CAPFAIL]), s_fail);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+__global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int t = blockIdx.y;
+  const int wave = threadIdx.x / kWave;
+  const int u = blockIdx.x * (blockDim.x / kWave) + wave;
+  const int lane = lane_id();
+  const int64_t tb = (int64_t)t * f.capacity;
+  const int64_t wb = (int64_t)t * w.max_wave;
+  if (u >= w.ucount[t]) return;
+  const int k = w.unew[wb + u];
+  if (k <= 0) return;
+  LeafLds l = carve(f, smem, wave);
+  const int leaf = w.uleaf[wb + u];
+  const int cbase = w.uedge[wb + u] + 1;  // node id of the first child
+  const int n = leaf_legal_list(f, w, t, u, l.mask, l.list);
+  const float* pol = w.policy + (wb + u) * (int64_t)f.num_actions;
+
+  // legal priors renormalised by their sum (optimized_wave_search.py:384-385)
+  float part = 0.0f;
+  for (int i = lane; i < n; i += kWave) part = part + pol[l.list[i]];
+  const float S = wave_sum_canonical(part);
+  // root Dirichlet mixing (optimized_wave_search.py:388-392): numpy keeps
+  // (1-eps)*float32 in float32 and promotes the sum with the float64 noise to float64
+  const bool noisy = (leaf == 0) && c.noise != nullptr && c.eps > 0.0;
+  const float w32 = (float)(1.0 - c.eps);
+  for (int i = lane; i < n; i += kWave) {
+    const float p = pol[l.list[i]] / S;
+    if (noisy)
+      l.val[i] = (double)(w32 * p) + c.eps * c.noise[(int64_t)t * f.num_actions + i];
+    else
+      l.val[i] = (double)p;
+  }
+  wave_sync();
+
+  int nch = n;
+  if (c.policy == OMQ_EXPAND_REFERENCE_PW) {
+    const int sel = (leaf == 0) ? pw_root_mc(n, f.visit_counts[tb] - c.vli * c.W) : 3;
+    if (n > sel) {
+      // top-sel by (prior desc, action asc), kept in ascending action order, renormalised
+      const int nwords = (n + 31) / 32;
+      for (int i = lane; i < nwords; i += kWave) l.bits[i] = 0u;
+      wave_sync();
+      for (int it = 0; it < sel; ++it) {
+        double bv = -__builtin_inf();
+        int bi = 0x7FFFFFFF;
+        for (int i = lane; i < n; i += kWave) {
+          const bool taken = (l.bits[i >> 5] >> (i & 31)) & 1u;
+          if (!taken && (l.val[i] > bv || (l.val[i] == bv && i < bi))) {
+            bv = l.val[i];
+            bi = i;
+          }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+          const double ov = __shfl_xor(bv, off, 64);
+          const int oi = __shfl_xor(bi, off, 64);
+          if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+          }
+        }
+        if (lane == 0 && bi < n) l.bits[bi >> 5] |= 1u << (bi & 31);
+        wave_sync();
+      }
+      if (lane == 0) {
+        int j = 0;
+        for (int i = 0; i < n; ++i) {
+          if ((l.bits[i >> 5] >> (i & 31)) & 1u) {
+            l.val[j] = l.val[i];
+            l.list[j] = l.list[i];
+            ++j;
+          }
+        }
+      }
+      wave_sync();
+      nch = sel;
+      if (noisy) {
+        double dpart = 0.0;
+        for (int j = lane; j < nch; j += kWave) dpart = dpart + l.val[j];
+        const double Sd = wave_sum_canonical_d(dpart);
+        wave_sync();
+        for (int j = lane; j < nch; j += kWave) l.val[j] = l.val[j] / Sd;
+      } else {
+        float fpart = 0.0f;
+        for (int j = lane; j < nch; j += kWave) fpart = fpart + (float)l.val[j];
+        const float Sf = wave_sum_canonical(fpart);
+        wave_sync();
+        for (int j = lane; j < nch; j += kWave) l.val[j] = (double)((float)l.val[j] / Sf);
+      }
+      wave_sync();
+    }
+  }
+  if (k > nch) {
+    if (lane == 0) atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
+    return;
+  }
+  // children: the first k chosen actions, ascending
+  for (int j = lane; j < k; j += kWave) {
+    const int64_t node = tb + cbase + j;
+    f.visit_counts[node] = 0;
+    f.value_sums[node] = 0.0f;
+    f.priors[node] = (float)l.val[j];
+    f.parents[node] = leaf;
+    f.actions[node] = l.list[j];
+    f.first_child[node] = -1;
+    f.num_children[node] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+size_t leaf_lds_per_wave_host(const omq_forest& f) { return leaf_lds_per_wave(f); }
+
+static int leaf_waves_per_block(const omq_forest& f) {
+  const size_t per = leaf_lds_per_wave_host(f);
+  int wpb = 4;
+  while (wpb > 1 && per * wpb > 64 * 1024) wpb >>= 1;
+  return wpb;
+}
+
+hipError_t launch_leaf_info(const omq_forest& f, const omq_wave& w, int W, hipStream_t st) {
+  const int wpb = leaf_waves_per_block(f);
+  const size_t lds = leaf_lds_per_wave_host(f) * wpb;
+  dim3 grid((W + wpb - 1) / wpb, f.num_trees);
+  hipLaunchKernelGGL(leaf_info_kernel, grid, dim3(wpb * kWave), lds, st, f, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_synth_eval(const omq_forest& f, const omq_wave& w, int W, float scale,
+                             hipStream_t st) {
+  const int wpb = leaf_waves_per_block(f);
+  const size_t lds = leaf_lds_per_wave_host(f) * wpb;
+  dim3 grid((W + wpb - 1) / wpb, f.num_trees);
+  hipLaunchKernelGGL(synth_eval_kernel, grid, dim3(wpb * kWave), lds, st, f, w, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_expand(const omq_forest& f, const omq_wave& w, int W, float virtual_loss,
+                         int policy, const double* noise, double eps, hipStream_t st) {
+  ExpCfg c;
+  c.W = W;
+  c.vli = (int)virtual_loss;
+  c.policy = policy;
+  c.noise = noise;
+  c.eps = eps;
+  hipLaunchKernelGGL(expand_plan_kernel, dim3(f.num_trees), dim3(kPlanThreads),
+                     (size_t)W * sizeof(int), st, f, w, c);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int wpb = leaf_waves_per_block(f);
+  const size_t lds = leaf_lds_per_wave_host(f) * wpb;
+  dim3 grid((W + wpb - 1) / wpb, f.num_trees);
+  hipLaunchKernelGGL(expand_write_kernel, grid, dim3(wpb * kWave), lds, st, f, w, c);
+  return hipGetLastError();
+}
+
+}  // namespace omq

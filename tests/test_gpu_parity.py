@@ -1,0 +1,32 @@
+"""Parity of the HIP tree operations with the CPU oracle, wave by wave (bit-exact paths,
+visit counts, CSR rows, priors and ordered-mode W)."""
+import pytest
+
+from omoknuni_quantum_amd.synthetic.workloads import get
+from oracle.parity import run_parity
+
+CASES = {
+    # C1 at its full size, both expansion policies
+    "C1-full": ("C1", {}),
+    "C1-reference_pw": ("C1", {"expand_policy": "reference_pw"}),
+    # reduced tree counts / simulations of C2-C4 (the full sizes run in the bench tests)
+    "C2-small": ("C2", {"num_trees": 4, "num_simulations": 768, "wave_size": 256,
+                        "capacity": 200_000}),
+    "C3-small": ("C3", {"num_trees": 2, "num_simulations": 2048, "wave_size": 1024,
+                        "capacity": 500_000}),
+    "C3-capacity": ("C3", {"num_trees": 2, "num_simulations": 3072, "wave_size": 1024,
+                           "capacity": 60_000}),
+    "C4-small": ("C4", {"num_trees": 2, "num_simulations": 4096, "wave_size": 2048,
+                        "capacity": 200_000}),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", list(CASES))
+def test_wave_parity(case, device):
+    name, kw = CASES[case]
+    wl = get(name).scaled(name=case, **kw)
+    print(f"[parity] {case}: T={wl.num_trees} sims={wl.num_simulations} W={wl.wave_size}",
+          flush=True)
+    n = run_parity(wl, check_every=1, device=device)
+    assert n >= 2
