@@ -1,0 +1,207 @@
+"""Benchmark of the wave-MCTS tree operations on one MI355X.
+
+A step is one full search of the workload: every tree is reset, its root expanded, and
+num_simulations simulations are run in waves (select -> synthetic evaluator -> expand ->
+backup).  Inputs are resident in HBM before the timed region.  The metric is tree-operation
+simulations per second: simulations / time of the tree-operation kernels (select, leaf info,
+expand, backup), measured with HIP events on the launch stream; the synthetic evaluator is
+timed apart.  Prints one JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--config C2] [--cpu-baseline auto|skip]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+_ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, _ROOT)
+
+METRIC = "tree-op simulations/sec (synthetic evaluator) + achieved HBM GB/s, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+TREE_PHASES = ("select", "leaf_info", "expand", "backup")
+
+
+def algorithmic_bytes(st: dict, sims: int) -> dict:
+    """Compulsory HBM bytes of each tree-operation kernel family over the timed region,
+    from the device counters (definitions in DESIGN.md):
+      select    16 B per visited node (row header N, first, nchild + N write of the virtual
+                loss) + 12 B per child of each row scanned (N, W, P) + 4 B per path entry
+                (path output) + 8 B per simulation (leaf and path length)
+      leaf_info 4 B per path entry of the first simulation of a unique leaf (upper bound: all
+                path entries) is not counted; 12 B per unique leaf (key, legal count)
+      expand    8 B per expanded leaf (row header) + 28 B per child written (N, W, P, parent,
+                action, row offset, row length) + 4 B per prior gathered (= per child in the
+                full policy)
+      backup    16 B per visited node (N and W read and written) + 4 B per path entry
+                (signed leaf value read) + 12 B per simulation (value, uid, length)
+    """
+    G, K, PE = st["pathnodes"], st["rowsum"], st["pathentries"]
+    return {
+        "select": 16 * G + 12 * K + 4 * PE + 8 * sims,
+        "leaf_info": 12 * st["uleaves"],
+        "expand": 8 * st["expanded"] + 32 * st["newchild"],
+        "backup": 16 * G + 4 * PE + 12 * sims,
+    }
+
+
+def run(args) -> dict:
+    import torch
+
+    from omoknuni_quantum_amd import _lib
+    from omoknuni_quantum_amd.core.engine import SearchParams, WaveEngine
+    from omoknuni_quantum_amd.core.timing import PhaseTimer
+    from omoknuni_quantum_amd.synthetic.evaluator import SyntheticEvaluator
+    from omoknuni_quantum_amd.synthetic.workloads import get
+
+    wl = get(args.config)
+    if args.trees:
+        wl = wl.scaled(num_trees=args.trees)
+    dev = torch.device("cuda:0")
+    params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth,
+                          expand_policy=_lib.OMQ_EXPAND_FULL,
+                          w_mode=_lib.OMQ_WACC_ATOMIC if args.w_mode == "atomic" else _lib.OMQ_WACC_ORDERED,
+                          vl_atomic=args.vl_atomic, dirichlet_epsilon=wl.dirichlet_epsilon)
+    eng = WaveEngine(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth, dev, params)
+    keys, legal, noise = wl.root_inputs()
+    eng.set_roots(keys, legal, noise)
+    ev = SyntheticEvaluator(wl.logit_scale)
+
+    for _ in range(args.warmup):
+        eng.search(wl.num_simulations, wl.wave_size, ev)
+    torch.cuda.synchronize(dev)
+    eng.stats.zero_()
+    timer = PhaseTimer(dev)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.search(wl.num_simulations, wl.wave_size, ev, timer)
+    torch.cuda.synchronize(dev)
+    t1 = time.perf_counter()
+    eng.check_status()
+    tot = timer.totals_ms()
+    st = eng.host_stats()
+    sims = wl.num_trees * wl.num_simulations * args.steps
+    tree_ms = sum(tot.get(p, 0.0) for p in TREE_PHASES)
+    eval_ms = tot.get("eval", 0.0)
+    value = sims / (tree_ms / 1e3)
+    ab = algorithmic_bytes(st, st["sims"])
+    phases = {}
+    for p in TREE_PHASES:
+        n = timer.counts.get(p, 0)
+        ms = tot.get(p, 0.0)
+        phases[p] = {"ms_total": round(ms, 4), "launches": n,
+                     "us_per_launch": round(1e3 * ms / max(n, 1), 3),
+                     "algorithmic_GBps": round(ab[p] / (ms / 1e3) / 1e9, 2) if ms > 0 else None}
+    dominant = max(TREE_PHASES, key=lambda p: tot.get(p, 0.0))
+    dn = timer.counts[dominant]
+    d_bytes = ab[dominant] / dn
+    d_s = tot[dominant] / 1e3 / dn
+    achieved = d_bytes / d_s / 1e9
+    roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 2),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                "traffic": None, "algorithmic_bytes_per_launch": int(d_bytes),
+                "us_per_launch": round(d_s * 1e6, 3)}
+    whole_bytes = sum(ab.values())
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "simulations/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * (t1 - t0) / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": wl.name, "trees": wl.num_trees,
+                   "simulations_per_tree": wl.num_simulations, "wave": wl.wave_size,
+                   "capacity": wl.capacity, "game": wl.model.kind,
+                   "actions": wl.model.num_actions, "w_mode": args.w_mode,
+                   "vl_atomic": bool(args.vl_atomic), "parallelism": "none (1 GPU)"},
+        "roofline": roofline,
+        "tree_op_ms_per_step": round(tree_ms / args.steps, 4),
+        "eval_ms_per_step": round(eval_ms / args.steps, 4),
+        "end_to_end_sims_per_s": round(sims / (t1 - t0), 1),
+        "tree_op_algorithmic_GBps": round(whole_bytes / (tree_ms / 1e3) / 1e9, 2),
+        "phases": phases,
+        "counters": st,
+    }
+    if args.cpu_baseline != "skip":
+        out["cpu_baseline"], out["parity_full_size"] = cpu_baseline(wl, eng, args)
+    return out
+
+
+def cpu_baseline(wl, eng, args):
+    """The C oracle timed on the host on the same workload (single thread), then its final
+    trees compared bit for bit with the GPU's (state after the last timed search)."""
+    from oracle.oracle import Oracle
+    from oracle.parity import EXPAND_CODES
+
+    T = wl.num_trees if args.cpu_trees <= 0 else min(args.cpu_trees, wl.num_trees)
+    orc = Oracle(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth)
+    orc.set_params(wl.c_puct, wl.virtual_loss, EXPAND_CODES[wl.expand_policy], 0, wl.logit_scale,
+                   wl.dirichlet_epsilon)
+    keys, legal, noise = wl.root_inputs()
+    orc.set_roots(keys, legal, noise)
+    t0 = time.perf_counter()
+    for t in range(T):
+        orc.lib.orc_search_tree(orc.f, t, wl.num_simulations, wl.wave_size, wl.max_depth)
+    dt = time.perf_counter() - t0
+    cpu = {"value": round(T * wl.num_simulations / dt, 1), "unit": "simulations/s", "cores": 1,
+           "kind": "port",
+           "sample": f"{T} of {wl.num_trees} trees x {wl.num_simulations} simulations of "
+                     f"{wl.name} ({dt:.2f} s, C oracle, gcc -O3, one thread)"}
+    ok = True
+    mismatch = None
+    w_exact = args.w_mode == "ordered"
+    for t in range(T):
+        g = eng.host_tree(t)
+        o = orc.tree(t)
+        same = g["num_nodes"] == o["num_nodes"]
+        for k in ("N", "parent", "first", "nchild", "action", "P"):
+            same = same and np.array_equal(g[k], o[k])
+        if same and w_exact:
+            same = np.array_equal(g["W"].view(np.int32), o["W"].view(np.int32))
+        elif same:
+            same = np.allclose(g["W"], o["W"], rtol=1e-5, atol=1e-5)
+        if not same:
+            ok = False
+            mismatch = t
+            break
+    parity = {"trees_compared": T, "bit_exact": ok, "first_mismatch_tree": mismatch,
+              "compared": "N, W, P, parent, row offset, row length, action of every node"}
+    return cpu, parity
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="C2")
+    ap.add_argument("--trees", type=int, default=0, help="override the workload's tree count")
+    ap.add_argument("--w-mode", choices=("ordered", "atomic"), default="ordered")
+    ap.add_argument("--vl-atomic", action="store_true")
+    ap.add_argument("--cpu-baseline", choices=("auto", "skip"), default="auto")
+    ap.add_argument("--cpu-trees", type=int, default=0,
+                    help="trees of the CPU baseline sample (0 = all)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the trees of a workload are "
+                                   "independent and would be sharded one group per GPU; only "
+                                   "--gpus 1 is measured"}))
+        sys.exit(2)
+    out = run(args)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -164,20 +164,20 @@ class WaveEngine:
                     "omq_backup")
 
     def run_wave(self, wave_size: int, evaluator, timer=None) -> None:
-        """One wave in every tree: select, leaf info, evaluate, expand, backup."""
-        if timer is not None:
-            timer.mark("tree")
+        """One wave in every tree: select, leaf info, evaluate, expand, backup.  With a
+        PhaseTimer, every phase is bracketed by events on the launch stream."""
+        mark = timer.mark if timer is not None else (lambda _p: None)
+        mark("select")
         self.select(wave_size)
+        mark("leaf_info")
         self.leaf_info()
-        if timer is not None:
-            timer.mark("eval")
+        mark("eval")
         evaluator.evaluate_wave(self)
-        if timer is not None:
-            timer.mark("tree")
+        mark("expand")
         self.expand(wave_size)
+        mark("backup")
         self.backup(wave_size)
-        if timer is not None:
-            timer.mark(None)
+        mark(None)
 
     def search(self, num_simulations: int, wave_size: int, evaluator, timer=None) -> None:
         """MCTS.search on every tree: reset, root expansion (one-simulation wave on the lone

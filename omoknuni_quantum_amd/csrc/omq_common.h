@@ -120,6 +120,30 @@ __device__ inline float wave_max_f32(float x) {
   return __int_as_float(__builtin_amdgcn_readlane(xi, 63));
 }
 
+// Order-preserving map of binary32 onto uint32 (a < b  <=>  fkey(a) < fkey(b) for non-NaN
+// values; NaNs map above +inf), and its inverse.
+__device__ inline uint32_t fkey(float x) {
+  const uint32_t b = __float_as_uint(x);
+  return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+}
+__device__ inline float funkey(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+
+// Max over the 64 lanes of a uint32, broadcast to every lane.  DPP row shifts 1,2,4,8 and
+// row broadcasts 15,31 accumulate into lane 63; a lane whose DPP source is outside its row,
+// or whose row is masked off, reads its own value (max-neutral).
+__device__ inline uint32_t wave_max_u32(uint32_t x) {
+  int v = (int)x;
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x111, 0xF, 0xF, false));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x112, 0xF, 0xF, false));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x114, 0xF, 0xF, false));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x118, 0xF, 0xF, false));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false));
+  return (uint32_t)__builtin_amdgcn_readlane(v, 63);
+}
+
 // Canonical wave sum: lane l has already accumulated, in ascending element order starting
 // from +0, the elements whose index is congruent to l mod 64; the 64 partial sums are then
 // combined by the xor butterfly with distances 32,16,8,4,2,1.  Every lane ends with the same

@@ -25,7 +25,10 @@
 
 namespace omq {
 
-constexpr int kSelThreads = 1024;
+#ifndef OMQ_SEL_THREADS
+#define OMQ_SEL_THREADS 1024
+#endif
+constexpr int kSelThreads = OMQ_SEL_THREADS;
 constexpr int kSelWaves = kSelThreads / kWave;
 constexpr uint32_t kNoChild = 0xFFFFFFFFu;
 
@@ -38,82 +41,270 @@ struct SelCfg {
   int vl_atomic;
 };
 
+// The arrays the selection touches (a compact kernel argument block: passing both full
+// structures costs more scalar registers than the kernel has).
+struct SelArgs {
+  int32_t* N;
+  const float* W;
+  const float* P;
+  const int32_t* first;
+  const int32_t* nchild;
+  int32_t* paths;
+  int32_t* path_len;
+  int32_t* leaves;
+  int32_t* sim_uid;
+  int32_t* uleaf;
+  int32_t* ufirst;
+  int32_t* ucount;
+  int32_t* glog;
+  int32_t* gcount;
+  uint16_t* gmembers;
+  int64_t* stats;
+  int32_t* status;
+  int capacity;
+  int max_wave;
+  int max_depth_buf;
+};
+
+// Max of a uint32 over the 64 lanes, made uniform: DPP row shifts 1,2,4,8 (each a single
+// v_max_u32_dpp; a lane whose DPP source lies outside its row reads 0, the identity) leave
+// each row's maximum in its last lane; the four row maxima are read into scalar registers
+// and combined there.
+__device__ inline uint32_t wave_max_rows(uint32_t x) {
+  int v = (int)x;
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true));
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane(v, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane(v, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane(v, 47);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane(v, 63);
+  return max(max(r0, r1), max(r2, r3));
+}
+
 // Serial chain of row-argmaxes for one group (whole wave).  ch[r] receives, for the r-th
 // member, (child index << 16) | rank among the members that chose the same child, or
 // kNoChild.  Child counts are left in cnt_s[0..k).  Returns the first rank without a child
 // (or -1).
+//
+// Exact score (the reference's fp32 expression):
+//     sc = Q + ((c*P)*s)/d,   Q = W/((float)N + VL),  d = (float)(1+N),  s = sqrt((float)Np)
+// Each lane keeps, per child, qa = W*r' and a = (c*P)*r, with r and r' Newton-refined
+// reciprocals of d and of (float)N + VL (|r*d - 1| <= 2^-24(1+eps)), and each step ranks the
+// children by ap = fma(s, a, qa).  With U = s*(c*P)/d: |qa - Q| <= |Q|*2^-22.4,
+// |ap - (Q + U)| <= U*2^-23 + |Q|*2^-22.4 + |ap|*2^-24 and |sc - (Q + U)| <= U*2^-23 + |sc|*2^-24;
+// since U <= |ap| + |Q| + tiny, |ap - sc| <= (|ap| + QB) * 2^-21 with QB >= max |Q| a running
+// bound.  Let A = max ap and E = (|A| + QB) * 2^-20.5.  The child with ap = A has exact score
+// >= A - E; a child w whose exact score reaches the maximum then has ap_w >= A - 2E
+// (|ap_w| <= |A| + 2E keeps e_w <= E).  So the exact argmax is among the candidates
+// ap >= T = A - (|A| + QB) * 2^-19 (a further factor 2^0.5 of margin).  A single candidate is
+// the exact argmax (A is checked above -1e8, so its exact score is above the -1e9 start
+// value); otherwise the candidates are scored exactly (two correctly rounded divisions each)
+// and compared in scalar registers.  No candidate (NaN or infinite scores) or a negative c*P
+// scores every child exactly.
+//
+// An unvisited child i (N == 0) carries qa = (1024 - i) * 2^90 and a = 0: it dominates every
+// visited child, and a lower index dominates a higher one by a factor >= 1 + 2^-10, so the
+// lowest-index unvisited child is the single candidate, as the reference's first-unvisited
+// rule requires.  A padding child (index >= k) carries qa = -inf, a = 0.  Every child's state
+// after its next pick is kept too, so a pick is a register select; the state after the
+// following pick is computed at the start of the next step.  Ranks are counted per child in
+// registers.  The parent's sqrt for ranks r0..r0+63 is computed once per 64 steps (lane l
+// holds rank r0+l); the 64 records of a block are kept one per lane and stored together.
+__device__ inline float refined_rcp(float d) {
+  const float r = __builtin_amdgcn_rcpf(d);
+  return __builtin_fmaf(r, __builtin_fmaf(-d, r, 1.0f), r);
+}
+
+// approximate selection state of a child with denominator d = (float)(1+N): (qa, a), computed
+// without branches; returns whether the child is visited
+__device__ inline bool child_state(float d, float w, float cp, int i, float vlf, float* qa,
+                                   float* a) {
+  const bool vis = d != 1.0f;
+  const float qv = w * refined_rcp((d - 1.0f) + vlf);
+  const float av = cp * refined_rcp(d);
+  *qa = vis ? qv : __builtin_ldexpf((float)(1024 - i), 90);
+  *a = vis ? av : 0.0f;
+  return vis;
+}
+
 template <int R>
-__device__ int run_chain(const omq_forest& f, int64_t tb, int first, int k, int Np0, int m,
+__device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
                          const SelCfg& c, uint32_t* ch, uint16_t* cnt_s) {
   const int lane = lane_id();
-  int n[R], cnt[R];
-  float wv[R], q[R], cp[R];
+  const float vlf = c.vlf;
+  const float fvl = (float)c.vli;
+  float wv[R], cp[R], den[R], q[R], ar[R], qn[R], arn[R];
+  int cnt[R];
+  float qbl = 0.0f;
+  bool negcp = false;
 #pragma unroll
   for (int j = 0; j < R; ++j) {
     const int i = lane * R + j;
     cnt[j] = 0;
-    n[j] = 0;
-    wv[j] = 0.0f;
-    cp[j] = 0.0f;
     if (i < k) {
       const int64_t node = tb + first + 1 + i;  // child of edge first+i is node first+i+1
-      n[j] = f.visit_counts[node];
-      wv[j] = f.value_sums[node];
-      cp[j] = c.c_puct * f.priors[node];
+      const int n = f.N[node];
+      wv[j] = f.W[node];
+      cp[j] = c.c_puct * f.P[node];
+      den[j] = (float)(1 + n);
+      negcp = negcp || !(cp[j] >= 0.0f);
+      if (child_state(den[j], wv[j], cp[j], i, vlf, &q[j], &ar[j]))
+        qbl = fmaxf(qbl, __builtin_fabsf(q[j]));
+      if (child_state(den[j] + fvl, wv[j], cp[j], i, vlf, &qn[j], &arn[j]))
+        qbl = fmaxf(qbl, __builtin_fabsf(qn[j]));
+    } else {
+      wv[j] = 0.0f;
+      cp[j] = 0.0f;
+      den[j] = 2.0f;
+      q[j] = qn[j] = -__builtin_inff();
+      ar[j] = arn[j] = 0.0f;
     }
-    q[j] = wv[j] / ((float)n[j] + c.vlf);
+  }
+  // |qa| bound on |Q|: qa = Q*(1 +- 2^-22.4); the margin of T absorbs the difference
+  uint32_t QBb = wave_max_rows(__float_as_uint(qbl));  // bits of QB (non-negative)
+  const bool exact_only = __ballot(negcp) != 0;
+  if (Np0 == 0 && c.vli == 0) {
+    // N is never negative: Np = 0 at every step, the reference returns no child
+    for (int r = lane; r < m; r += kWave) ch[r] = kNoChild;
+    for (int i = lane; i < k; i += kWave) cnt_s[i] = 0;
+    wave_sync();
+    return m > 0 ? 0 : -1;
   }
   int first_end = -1;
-  for (int r = 0; r < m; ++r) {
-    const int Np = Np0 + c.vli * (r + 1);
-    int win = -1;
-    if (Np != 0) {
-      const float s = sqrtf((float)Np);
-      int uv = -1, bi = -1;
-      float bs = 0.0f;
+  int powner = -1, pjj = 0;  // the previous step's pick, whose next state is pending
+  for (int r0 = 0; r0 < m; r0 += kWave) {
+    const int Npl = Np0 + c.vli * (r0 + lane + 1);
+    const float svec = sqrtf((float)Npl);
+    const int rend = min(kWave, m - r0);
+    uint32_t rec = kNoChild;
+    for (int rr = 0; rr < rend; ++rr) {
+      // state after the next pick of the child picked in the previous step
+      {
+        float dw = den[0], ww = wv[0], cw = cp[0];
 #pragma unroll
-      for (int j = 0; j < R; ++j) {
-        const int i = lane * R + j;
-        if (i < k) {
-          if (n[j] == 0) {
-            if (uv < 0) uv = i;
-          } else {
-            float sc = q[j] + (cp[j] * s) / (float)(1 + n[j]);
-            sc = sc + 0.0f;  // -0 -> +0, so that equal scores compare equal below
-            if (sc > -1e9f && (bi < 0 || sc > bs)) {
-              bs = sc;
-              bi = i;
+        for (int j = 1; j < R; ++j) {
+          dw = (j == pjj) ? den[j] : dw;
+          ww = (j == pjj) ? wv[j] : ww;
+          cw = (j == pjj) ? cp[j] : cw;
+        }
+        float qx, ax;
+        const bool vis = child_state(dw + fvl, ww, cw, lane * R + pjj, vlf, &qx, &ax);
+        const bool mine = lane == powner;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+          const bool hit = mine && j == pjj;
+          qn[j] = hit ? qx : qn[j];
+          arn[j] = hit ? ax : arn[j];
+        }
+        // |qx| enters QB before the state becomes current (one step later at the earliest)
+        const uint32_t qo =
+            (uint32_t)readlane_i(vis ? (int)__float_as_uint(__builtin_fabsf(qx)) : 0, max(powner, 0));
+        QBb = max(QBb, powner < 0 ? 0u : qo);
+      }
+      const float s = readlane_f(svec, rr);
+      float ap[R];
+#pragma unroll
+      for (int j = 0; j < R; ++j) ap[j] = __builtin_fmaf(s, ar[j], q[j]);
+      float lm;
+      if (R == 1) {
+        lm = ap[0];
+      } else {
+        float t[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) t[j] = ap[j];
+#pragma unroll
+        for (int w = 1; w < R; w <<= 1)
+#pragma unroll
+          for (int j = 0; j + w < R; j += 2 * w) t[j] = fmaxf(t[j], t[j + w]);
+        lm = t[0];
+      }
+      const uint32_t Ak = wave_max_rows(fkey(lm));
+      const float A = funkey(Ak);
+      // T = A - (|A| + QB) * 2^-19 = A * (1 -+ 2^-19) - QB * 2^-19 (key MSB set: A >= 0)
+      const float T = __builtin_fmaf(A, (Ak & 0x80000000u) ? 0.99999809265136719f
+                                                           : 1.0000019073486328f,
+                                     __uint_as_float(QBb) * (-1.0f / 524288.0f));
+      uint32_t bits = 0;
+#pragma unroll
+      for (int j = 0; j < R; ++j) bits |= (ap[j] >= T) ? (1u << j) : 0u;
+      const uint64_t cm = __ballot(bits != 0);
+      const uint64_t mm = (R > 1) ? __ballot((bits & (bits - 1)) != 0) : 0ull;
+      int win = -1;
+      // A > -1e8 (key 0x334143DF) keeps the exact score of a single candidate above -1e9
+      if (!exact_only && cm != 0 && (cm & (cm - 1)) == 0 && mm == 0 && Ak > 0x334143DFu) {
+        const int l = lowest_lane(cm);
+        win = (R == 1) ? l : l * R + (__ffs((unsigned)readlane_i((int)bits, l)) - 1);
+      } else {
+        // exact scores of the candidates (every child if there is none or c*P < 0), compared
+        // as order-preserving keys in scalar registers, lowest index on ties; an unvisited
+        // child ranks above every visited one, lower index first
+        const bool all = exact_only || cm == 0;
+        uint32_t kx[R];
+        uint64_t cj[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+          const int i = lane * R + j;
+          const bool cand = all ? (i < k) : (((bits >> j) & 1u) != 0);
+          cj[j] = __ballot(cand);
+          kx[j] = 0u;
+          if (cand) {
+            if (den[j] == 1.0f) {
+              kx[j] = 0xFFFF0000u | (uint32_t)(0xFFFF - i);
+            } else {
+              const float qe = wv[j] / ((den[j] - 1.0f) + vlf);
+              float sc = qe + (cp[j] * s) / den[j];
+              sc = sc + 0.0f;  // -0 -> +0, so that equal scores compare equal
+              kx[j] = (sc > -1e9f) ? fkey(sc) : 0u;
             }
           }
         }
-      }
-      const uint64_t um = __ballot(uv >= 0);
-      if (um) {
-        win = readlane_i(uv, lowest_lane(um));
-      } else {
-        const float mx = wave_max_f32(bi >= 0 ? bs : -__builtin_inff());
-        const uint64_t bm = __ballot(bi >= 0 && bs == mx);
-        if (bm) win = readlane_i(bi, lowest_lane(bm));
-      }
-    }
-    if (win >= 0) {
-      const int owner = win / R;
-      const int jj = win - owner * R;
-      if (lane == owner) {
+        uint32_t bk = 0u;
+        int bidx = 0x7FFFFFFF;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
-          if (j == jj) {
-            ch[r] = ((uint32_t)win << 16) | (uint32_t)cnt[j];
-            cnt[j] += 1;
-            n[j] += c.vli;
-            q[j] = wv[j] / ((float)n[j] + c.vlf);
+          uint64_t rest = cj[j];
+          while (rest) {
+            const int l = lowest_lane(rest);
+            rest &= rest - 1;
+            const uint32_t kv = (uint32_t)readlane_i((int)kx[j], l);
+            const int idx = l * R + j;
+            if (kv > bk || (kv == bk && kv != 0u && idx < bidx)) {
+              bk = kv;
+              bidx = idx;
+            }
           }
         }
+        if (bk != 0u) win = bidx;
       }
-    } else {
-      if (lane == 0) ch[r] = kNoChild;
-      if (first_end < 0) first_end = r;
+      win = __builtin_amdgcn_readfirstlane(win);
+      uint32_t rv = kNoChild;
+      if (win >= 0) {
+        const int owner = win / R;
+        const int jj = win - owner * R;
+        const bool mine = lane == owner;
+        int cw = cnt[0];
+#pragma unroll
+        for (int j = 1; j < R; ++j) cw = (j == jj) ? cnt[j] : cw;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+          const bool hit = mine && j == jj;
+          q[j] = hit ? qn[j] : q[j];
+          ar[j] = hit ? arn[j] : ar[j];
+          den[j] = hit ? den[j] + fvl : den[j];
+          cnt[j] += hit ? 1 : 0;
+        }
+        rv = ((uint32_t)win << 16) | (uint32_t)readlane_i(cw, owner);
+        powner = __builtin_amdgcn_readfirstlane(owner);
+        pjj = __builtin_amdgcn_readfirstlane(jj);
+      } else {
+        powner = -1;
+        if (first_end < 0) first_end = r0 + rr;
+      }
+      rec = (lane == rr) ? rv : rec;
     }
+    if (lane < rend) ch[r0 + lane] = rec;
   }
 #pragma unroll
   for (int j = 0; j < R; ++j) {
@@ -124,12 +315,18 @@ __device__ int run_chain(const omq_forest& f, int64_t tb, int first, int k, int 
   return first_end;
 }
 
-__device__ inline int dispatch_chain(const omq_forest& f, int64_t tb, int first, int k, int Np0,
+__device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0,
                                      int m, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s) {
-  if (k <= 64) return run_chain<1>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-  if (k <= 128) return run_chain<2>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-  if (k <= 256) return run_chain<4>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-  return run_chain<8>(f, tb, first, k, Np0, m, c, ch, cnt_s);  // k <= OMQ_MAX_ROW = 512
+  switch ((k + kWave - 1) / kWave) {  // k <= OMQ_MAX_ROW = 512
+    case 1: return run_chain<1>(f, tb, first, k, Np0, m, c, ch, cnt_s);
+    case 2: return run_chain<2>(f, tb, first, k, Np0, m, c, ch, cnt_s);
+    case 3: return run_chain<3>(f, tb, first, k, Np0, m, c, ch, cnt_s);
+    case 4: return run_chain<4>(f, tb, first, k, Np0, m, c, ch, cnt_s);
+    case 5: return run_chain<5>(f, tb, first, k, Np0, m, c, ch, cnt_s);
+    case 6: return run_chain<6>(f, tb, first, k, Np0, m, c, ch, cnt_s);
+    case 7: return run_chain<7>(f, tb, first, k, Np0, m, c, ch, cnt_s);
+    default: return run_chain<8>(f, tb, first, k, Np0, m, c, ch, cnt_s);
+  }
 }
 
 // Block-wide exclusive scan of a[0..n) in place (n <= 4 * kSelThreads); returns the total.
@@ -161,8 +358,8 @@ __device__ int block_excl_scan(int32_t* a, int n, int* s_wtot) {
   return total;
 }
 
-__global__ __launch_bounds__(kSelThreads) void select_kernel(omq_forest f, omq_wave w,
-                                                             SelCfg c) {
+__global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c) {
+  SelArgs& w = f;
   extern __shared__ __align__(16) unsigned char smem[];
   const int W = c.W;
   uint32_t* choice = reinterpret_cast<uint32_t*>(smem);       // [W]
@@ -183,9 +380,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(omq_forest f, omq_w
   const int wave = tid / kWave;
   const int lane = lane_id();
   const int64_t tb = (int64_t)t * f.capacity;
-  const int MW = w.max_wave, MD = w.max_depth;
+  const int MW = w.max_wave, MD = w.max_depth_buf;
   const int64_t gmax = (int64_t)MW * MD;
-  int32_t* N = f.visit_counts;
+  int32_t* N = f.N;
   uint16_t* cnt_s = cnt_all + wave * OMQ_MAX_ROW;
 
   for (int s = tid; s < W; s += kSelThreads) {
@@ -228,8 +425,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(omq_forest f, omq_w
       }
 
       const int Np0 = N[tb + p];
-      const int k = f.num_children[tb + p];
-      const int first = f.first_child[tb + p];
+      const int k = f.nchild[tb + p];
+      const int first = f.first[tb + p];
       if (c.vl_atomic) {
         for (int r = lane; r < m; r += kWave) atomicAdd(&N[tb + p], c.vli);
       } else if (lane == 0) {
@@ -371,7 +568,28 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(select_kernel, dim3(f.num_trees), dim3(kSelThreads), lds, stream, f, w, c);
+  SelArgs a;
+  a.N = f.visit_counts;
+  a.W = f.value_sums;
+  a.P = f.priors;
+  a.first = f.first_child;
+  a.nchild = f.num_children;
+  a.paths = w.paths;
+  a.path_len = w.path_len;
+  a.leaves = w.leaves;
+  a.sim_uid = w.sim_uid;
+  a.uleaf = w.uleaf;
+  a.ufirst = w.ufirst;
+  a.ucount = w.ucount;
+  a.glog = w.glog;
+  a.gcount = w.gcount;
+  a.gmembers = w.gmembers;
+  a.stats = w.stats;
+  a.status = w.status;
+  a.capacity = f.capacity;
+  a.max_wave = w.max_wave;
+  a.max_depth_buf = w.max_depth;
+  hipLaunchKernelGGL(select_kernel, dim3(f.num_trees), dim3(kSelThreads), lds, stream, a, c);
   return hipGetLastError();
 }
 
