@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_HERE, LIB_NAME)
 ABI_VERSION = 1
 
 # constants of include/omq_tree_ops.h
-OMQ_OK = 0
+OMQ_OK, OMQ_E_ARG, OMQ_E_LAUNCH, OMQ_E_LIMIT = 0, -1, -2, -3
 OMQ_GAME_BOARD, OMQ_GAME_GO, OMQ_GAME_SPARSE = 0, 1, 2
 OMQ_EXPAND_FULL, OMQ_EXPAND_REFERENCE_PW = 0, 1
 OMQ_SIGN_LEAF_POSITIVE, OMQ_SIGN_ROOT_POSITIVE = 0, 1

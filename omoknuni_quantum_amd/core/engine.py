@@ -163,6 +163,50 @@ class WaveEngine:
                                         p.sign_mode, p.w_mode, self.stream_handle()),
                     "omq_backup")
 
+    def _tree_of(self, tree_of, n: int):
+        if tree_of is None:
+            return None
+        t = torch.as_tensor(tree_of, dtype=torch.int32, device=self.device).reshape(-1)
+        if t.numel() != n:
+            raise ValueError(f"tree_of has {t.numel()} entries for {n} rows")
+        return t.contiguous()
+
+    def apply_virtual_loss(self, nodes, tree_of=None, amount: int | None = None) -> None:
+        """N[tree_of[i], nodes[i]] += amount (default: the virtual loss) for every listed
+        node (csr_tree.py:759-763, mcts_kernels.cu batch_apply_virtual_loss)."""
+        delta = int(self.params.virtual_loss) if amount is None else int(amount)
+        self._virtual_loss(nodes, tree_of, delta)
+
+    def remove_virtual_loss(self, nodes, tree_of=None, amount: int | None = None) -> None:
+        delta = int(self.params.virtual_loss) if amount is None else int(amount)
+        self._virtual_loss(nodes, tree_of, -delta)
+
+    def _virtual_loss(self, nodes, tree_of, delta: int) -> None:
+        n = torch.as_tensor(nodes, dtype=torch.int32, device=self.device).reshape(-1).contiguous()
+        t = self._tree_of(tree_of, n.numel())
+        self._check(self.lib.omq_virtual_loss(self.forest_ref, n.data_ptr(),
+                                              None if t is None else t.data_ptr(), n.numel(),
+                                              delta, self.stream_handle()), "omq_virtual_loss")
+
+    def backup_paths(self, paths, path_lengths, values, tree_of=None) -> None:
+        """Reference vectorized_backup over an explicit [B, D] path matrix (root first, -1
+        padded): N[x] += 1 and W[x] += signed value along each path, float atomics
+        (torch_custom_ops.py:27-55, mcts_kernels.cu vectorized_backup)."""
+        p = torch.as_tensor(paths, dtype=torch.int32, device=self.device)
+        if p.dim() != 2:
+            raise ValueError("paths must be [batch, max_depth]")
+        B, D = p.shape
+        p = p.contiguous()
+        L = torch.as_tensor(path_lengths, dtype=torch.int32, device=self.device).reshape(-1).contiguous()
+        v = torch.as_tensor(values, dtype=torch.float32, device=self.device).reshape(-1).contiguous()
+        if L.numel() != B or v.numel() != B:
+            raise ValueError("path_lengths and values need one entry per path")
+        t = self._tree_of(tree_of, B)
+        self._check(self.lib.omq_paths_backup(self.forest_ref, p.data_ptr(), L.data_ptr(),
+                                              None if t is None else t.data_ptr(), v.data_ptr(),
+                                              B, D, self.params.sign_mode, self.stream_handle()),
+                    "omq_paths_backup")
+
     def run_wave(self, wave_size: int, evaluator, timer=None) -> None:
         """One wave in every tree: select, leaf info, evaluate, expand, backup.  With a
         PhaseTimer, every phase is bracketed by events on the launch stream."""

@@ -1,0 +1,275 @@
+"""MCTS: the search API of the reference over the HIP tree operations.
+
+Drop-in for python/mcts/core/mcts.py:43-2216 of cosmosapjw-quantum/omoknuni_quantum, GPU tree
+backend: ``MCTS(config, evaluator, game_interface=None, single_gpu_mode=False)`` with
+``search``, ``select_action``, ``update_root``, ``get_root_value``, ``clear``/``reset_tree``,
+``get_statistics``, ``warmup``, ``shutdown`` and the context-manager protocol, plus
+``search_batch`` for ``config.num_trees`` independent trees searched together.
+
+A search follows mcts.py:923-1063: the root is expanded first if it has no children (a
+one-simulation wave on the lone root; its value is backed up, mcts.py:1659-1691), then waves
+of min(max_wave_size, remaining) simulations run until num_simulations are done, and the
+policy is the root children's visit distribution (mcts.py:1069-1137).  Every wave runs on the
+device: selection with virtual loss, leaf evaluation, expansion, backup.
+
+Evaluators: a device-native evaluator (``evaluate_wave(engine)``, e.g. SyntheticEvaluator) is
+called with the wave engine; any other evaluator is called as in the reference,
+``evaluate_batch(features) -> (policies [B, A], values [B])``, on feature planes of the wave's
+unique leaves built on the device (core/features.py).
+"""
+from __future__ import annotations
+
+import logging
+import time
+from collections import defaultdict
+from typing import Any, Dict, Optional
+
+import numpy as np
+import torch
+
+from .. import _lib
+from ..synthetic import games
+from .engine import SearchParams, WaveEngine
+from .mcts_config import GameType, MCTSConfig
+
+logger = logging.getLogger(__name__)
+
+
+class _BatchEvaluatorAdapter:
+    """Runs a reference-protocol evaluator on the device-built features of the unique leaves
+    and writes its outputs into the engine's policy/value rows."""
+
+    def __init__(self, evaluator, builder):
+        self.evaluator = evaluator
+        self.builder = builder
+
+    def evaluate_wave(self, engine) -> None:
+        feats = self.builder.build()
+        pol, val = self.evaluator.evaluate_batch(feats)
+        pol = torch.as_tensor(pol, device=engine.device, dtype=torch.float32)
+        val = torch.as_tensor(val, device=engine.device, dtype=torch.float32).reshape(-1)
+        engine.policy.view(-1, engine.A).copy_(pol.view(-1, engine.A))
+        engine.values.copy_(val)
+
+
+class MCTS:
+    """High-level MCTS over the HIP wave tree operations (GPU tree backend)."""
+
+    def __init__(self, config: MCTSConfig, evaluator: Any, game_interface: Optional[Any] = None,
+                 single_gpu_mode: bool = False):
+        self.config = config
+        self.evaluator = evaluator
+        self.game_interface = game_interface
+        self.single_gpu_mode = single_gpu_mode
+        if config.backend != "gpu":
+            raise NotImplementedError(
+                f"backend '{config.backend}': this library implements the tree operations on the "
+                "GPU (backend='gpu'); the reference's Cython CPU tree is not part of it")
+        if game_interface is not None:
+            gt = getattr(game_interface, "game_type", None)
+            if gt is not None:
+                name = getattr(gt, "name", str(gt)).upper()
+                if name in GameType.__members__:
+                    config.game_type = GameType[name]
+            if getattr(game_interface, "board_size", None):
+                config.board_size = int(game_interface.board_size)
+        self.device = torch.device(config.device if config.device != "cuda" else "cuda:0")
+        self.model = self._game_model(config)
+        self.action_size = config.action_space_size()
+        self.wave = config.effective_wave_size()
+        if self.wave > _lib.OMQ_MAX_WAVE:
+            raise ValueError(f"max_wave_size {self.wave} exceeds the library limit "
+                             f"{_lib.OMQ_MAX_WAVE}")
+        self.params = SearchParams(
+            c_puct=float(config.c_puct), virtual_loss=config.effective_virtual_loss(),
+            max_depth=int(config.max_depth),
+            expand_policy=(_lib.OMQ_EXPAND_FULL if config.expansion_policy == "full"
+                           else _lib.OMQ_EXPAND_REFERENCE_PW),
+            sign_mode=(_lib.OMQ_SIGN_LEAF_POSITIVE if config.backup_sign == "leaf_positive"
+                       else _lib.OMQ_SIGN_ROOT_POSITIVE),
+            w_mode=(_lib.OMQ_WACC_ORDERED if config.w_accum == "ordered" else _lib.OMQ_WACC_ATOMIC),
+            vl_atomic=bool(config.vl_atomic), dirichlet_epsilon=float(config.dirichlet_epsilon))
+        self.engine = WaveEngine(self.model, config.num_trees, int(config.max_tree_nodes),
+                                 self.wave, int(config.max_depth), self.device, self.params)
+        self._roots_key: Optional[bytes] = None
+        self._boards: Optional[torch.Tensor] = None
+        self._eval = None
+        self._search_count = 0
+        self.last_selected_action = None
+        self._initialize_statistics()
+
+    # ---- setup ---------------------------------------------------------------------------
+    @staticmethod
+    def _game_model(config: MCTSConfig) -> games.GameModel:
+        if config.game_type == GameType.GOMOKU:
+            return games.gomoku(config.board_size)
+        if config.game_type == GameType.GO:
+            return games.go(config.board_size)
+        lo, hi = config.sparse_legal
+        return games.chess_sparse(config.action_space_size(), int(lo), int(hi))
+
+    def _initialize_statistics(self):
+        # mcts.py:783-796
+        self.stats = {
+            "total_searches": 0, "total_simulations": 0, "total_time": 0.0,
+            "avg_sims_per_second": 0.0, "peak_sims_per_second": 0.0,
+            "last_search_sims_per_second": 0.0, "tree_reuse_count": 0, "tree_reuse_nodes": 0,
+        }
+        self.stats_internal = defaultdict(float)
+
+    def _states_array(self, states) -> Optional[np.ndarray]:
+        if not self.model.is_board:
+            return None
+        bs = self.config.board_size
+        arr = np.asarray(states)
+        if arr.shape[-2:] != (bs, bs):
+            raise ValueError(f"Invalid state shape: {arr.shape}, expected {(bs, bs)}")
+        return arr.reshape(-1, bs, bs).astype(np.int8)
+
+    def _set_roots(self, boards: Optional[np.ndarray]) -> None:
+        T = self.engine.T
+        if boards is not None and boards.shape[0] != T:
+            raise ValueError(f"{boards.shape[0]} states given for {T} trees")
+        key = b"" if boards is None else boards.tobytes()
+        if key == self._roots_key and self._eval is not None:
+            return
+        keys = games.root_keys(self.config.seed, T)
+        legal = games.legal_masks(self.model, boards, T)
+        noise = None
+        if self.config.dirichlet_epsilon > 0:
+            if self.model.is_board:
+                counts = games.legal_counts(self.model, legal)
+            else:
+                counts = np.array([games.sparse_root_count(self.model, int(k)) for k in keys])
+            noise = games.dirichlet_noise(self.model, counts, float(self.config.dirichlet_alpha),
+                                          self.config.seed + 7919 * (self._search_count + 1))
+        self.engine.set_roots(keys, legal, noise)
+        self.engine.reset()
+        self._roots_key = key
+        self._boards = None if boards is None else torch.from_numpy(boards).to(self.device)
+        self._eval = self._make_evaluator()
+
+    def _make_evaluator(self):
+        if getattr(self.evaluator, "device_native", False) or hasattr(self.evaluator, "evaluate_wave"):
+            return self.evaluator
+        if not hasattr(self.evaluator, "evaluate_batch"):
+            raise TypeError("evaluator must provide evaluate_wave(engine) or evaluate_batch(states)")
+        if not self.model.is_board:
+            raise NotImplementedError("feature-plane evaluators need a board game model")
+        from .features import LeafFeatureBuilder
+        return _BatchEvaluatorAdapter(self.evaluator, LeafFeatureBuilder(self.engine, self._boards))
+
+    # ---- search --------------------------------------------------------------------------
+    def search(self, state: Any, num_simulations: Optional[int] = None) -> np.ndarray:
+        """Run the search from `state`; returns the root visit distribution [action_size]."""
+        if self.engine.T != 1:
+            raise ValueError("search() drives one tree; use search_batch() with num_trees > 1")
+        return self.search_batch(None if state is None else np.asarray(state)[None],
+                                 num_simulations)[0]
+
+    def search_batch(self, states: Any, num_simulations: Optional[int] = None) -> np.ndarray:
+        """Search num_trees independent trees together; returns [num_trees, action_size]."""
+        boards = None if states is None else self._states_array(states)
+        num_sims = self.config.num_simulations if num_simulations is None else int(num_simulations)
+        start = time.perf_counter()
+        if not self.config.enable_subtree_reuse:
+            self._roots_key = None
+        self._set_roots(boards)
+        if num_sims == 0:  # mcts.py:1022-1030
+            return np.full((self.engine.T, self.action_size), 1.0 / self.action_size)
+        eng = self.engine
+        if int(eng.nchild[0].item()) == 0 and int(eng.num_nodes[0].item()) == 1:
+            eng.run_wave(1, self._eval)  # root expansion with its own backup
+        done = 0
+        while done < num_sims:
+            w = min(self.wave, num_sims - done)
+            eng.run_wave(w, self._eval)
+            done += w
+        eng.check_status()
+        policy = eng.root_policies()
+        elapsed = time.perf_counter() - start
+        self._search_count += 1
+        self._update_statistics(num_sims * eng.T, elapsed)
+        return policy
+
+    def _update_statistics(self, num_simulations: int, elapsed_time: float):
+        # mcts.py:1442-1456
+        self.stats["total_searches"] += 1
+        self.stats["total_simulations"] += num_simulations
+        self.stats["total_time"] += elapsed_time
+        sps = num_simulations / elapsed_time if elapsed_time > 0 else 0
+        self.stats["last_search_sims_per_second"] = sps
+        self.stats["peak_sims_per_second"] = max(self.stats["peak_sims_per_second"], sps)
+        tt = self.stats["total_time"]
+        self.stats["avg_sims_per_second"] = self.stats["total_simulations"] / tt if tt > 0 else 0
+
+    # ---- actions and root ----------------------------------------------------------------
+    def select_action(self, state: Any, temperature: float = 1.0,
+                      policy: Optional[np.ndarray] = None) -> int:
+        """mcts.py:1167-1203: temperature 0 takes the first maximum; otherwise samples
+        policy^(1/T)."""
+        if policy is None:
+            policy = self.search(state)
+        if temperature == 0:
+            action = 0 if policy.max() == 0 else int(np.argmax(policy))
+        else:
+            p = np.power(policy, 1.0 / temperature)
+            p /= p.sum()
+            action = int(np.random.choice(len(policy), p=p))
+        self.last_selected_action = action
+        return action
+
+    def update_root(self, action: int, new_state: Any = None) -> None:
+        """mcts.py:1205-1245.  Validates the action; subtree reuse is not part of this build,
+        so the tree is reset (the reference's fallback, _efficient_tree_reset) and the new
+        state, if given, becomes the root."""
+        if action < 0 or action >= self.action_size:
+            raise ValueError(f"Invalid action {action}. Must be in range [0, {self.action_size})")
+        self._roots_key = None
+        if new_state is not None:
+            self._set_roots(self._states_array(np.asarray(new_state)[None]))
+
+    def update_with_move(self, move: int) -> None:
+        self.update_root(move, None)
+
+    def get_root_value(self) -> float:
+        """Q of the root, W/N (mcts.py:1139-1165, GPU tree branch)."""
+        n = int(self.engine.N[0].item())
+        return float(self.engine.W[0].item()) / n if n > 0 else 0.0
+
+    def clear(self) -> None:
+        self._roots_key = None
+        self.engine.reset()
+
+    def reset_tree(self) -> None:
+        self.clear()
+
+    def get_statistics(self) -> Dict[str, Any]:
+        st = dict(self.stats)
+        n = int(self.engine.num_nodes[0].item())
+        st.update({"num_nodes": n, "root_visits": int(self.engine.N[0].item()),
+                   "root_children": int(self.engine.nchild[0].item())})
+        st.update({f"op_{k}": v for k, v in self.engine.host_stats().items()})
+        st.update(self.stats_internal)
+        return st
+
+    def warmup(self, state: Any = None, num_simulations: int = 100) -> None:
+        if state is None and self.model.is_board:
+            state = np.zeros((self.config.board_size, self.config.board_size), dtype=np.int8)
+        if self.engine.T == 1:
+            self.search(state, num_simulations)
+        else:
+            self.search_batch(None if state is None else np.repeat(np.asarray(state)[None],
+                                                                   self.engine.T, 0),
+                              num_simulations)
+        self.clear()
+
+    def shutdown(self) -> None:
+        self.clear()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, exc_type, exc_val, exc_tb):
+        self.shutdown()
+        return False

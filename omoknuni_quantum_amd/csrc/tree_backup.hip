@@ -122,12 +122,13 @@ __global__ void paths_backup_kernel(omq_forest f, const int32_t* paths, const in
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= batch) return;
   const int t = tree_of ? tree_of[b] : 0;
+  if (t < 0 || t >= f.num_trees) return;  // entries naming no tree are skipped
   const int64_t tb = (int64_t)t * f.capacity;
-  const int L = plen[b];
+  const int L = min(plen[b], max_depth);
   const float v = values[b];
   for (int d = 0; d < L; ++d) {
     const int x = paths[(int64_t)b * max_depth + d];
-    if (x < 0) break;
+    if (x < 0 || x >= f.capacity) break;  // -1 padding (and anything out of range) ends a path
     const int e = sign_mode == OMQ_SIGN_LEAF_POSITIVE ? (L - 1 - d) : d;
     atomicAdd(&f.visit_counts[tb + x], 1);
     unsafeAtomicAdd(&f.value_sums[tb + x], (e & 1) ? -v : v);
@@ -140,7 +141,7 @@ __global__ void virtual_loss_kernel(omq_forest f, const int32_t* nodes, const in
   if (i >= count) return;
   const int t = tree_of ? tree_of[i] : 0;
   const int x = nodes[i];
-  if (x < 0) return;
+  if (x < 0 || x >= f.capacity || t < 0 || t >= f.num_trees) return;
   atomicAdd(&f.visit_counts[(int64_t)t * f.capacity + x], delta);
 }
 

@@ -20,19 +20,20 @@ class ParityError(AssertionError):
     pass
 
 
-def make_pair(wl, max_wave=None, w_mode=0, vl_atomic=False, device="cuda"):
+def make_pair(wl, max_wave=None, w_mode=0, vl_atomic=False, device="cuda", sign_mode=0):
     from omoknuni_quantum_amd.core.engine import SearchParams, WaveEngine
     from omoknuni_quantum_amd.synthetic.evaluator import SyntheticEvaluator
 
     MW = max_wave or wl.wave_size
     params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth,
                           expand_policy=EXPAND_CODES[wl.expand_policy], w_mode=w_mode,
+                          sign_mode=sign_mode,
                           vl_atomic=vl_atomic, dirichlet_epsilon=wl.dirichlet_epsilon)
     eng = WaveEngine(wl.model, wl.num_trees, wl.capacity, MW, wl.max_depth, device, params)
     keys, legal, noise = wl.root_inputs()
     eng.set_roots(keys, legal, noise)
     orc = Oracle(wl.model, wl.num_trees, wl.capacity, MW, wl.max_depth)
-    orc.set_params(wl.c_puct, wl.virtual_loss, EXPAND_CODES[wl.expand_policy], 0,
+    orc.set_params(wl.c_puct, wl.virtual_loss, EXPAND_CODES[wl.expand_policy], sign_mode,
                    wl.logit_scale, wl.dirichlet_epsilon)
     orc.set_roots(keys, legal, noise)
     return eng, orc, SyntheticEvaluator(wl.logit_scale)
@@ -92,12 +93,14 @@ def compare_wave(eng, orc, W, ctx, w_exact=True):
             raise ParityError(f"{c}: oracle edge array is not child[e] = e+1")
 
 
-def run_parity(wl, check_every=1, w_mode=0, vl_atomic=False, device="cuda", log=None):
+def run_parity(wl, check_every=1, w_mode=0, vl_atomic=False, device="cuda", log=None,
+               sign_mode=0):
     """Run the whole search on both sides; compare after every check_every-th wave and at
     the end.  Returns the number of waves compared."""
     import torch
 
-    eng, orc, ev = make_pair(wl, w_mode=w_mode, vl_atomic=vl_atomic, device=device)
+    eng, orc, ev = make_pair(wl, w_mode=w_mode, vl_atomic=vl_atomic, device=device,
+                             sign_mode=sign_mode)
     T = wl.num_trees
     eng.reset()
     for t in range(T):

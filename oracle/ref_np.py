@@ -1,0 +1,231 @@
+"""Independent numpy-float32 restatement of the reference CPU tree semantics, for tiny trees.
+
+TEST INFRASTRUCTURE ONLY (imported by tests/).  It pins the C oracle (oracle/tree_oracle.c):
+both are written from the reference's behaviour, separately, and must agree bit for bit.
+
+Reference behaviour restated (cosmosapjw-quantum/omoknuni_quantum):
+  init .............. python/mcts/cpu/cython_tree_optimized.pyx:92-100 (N[0]=1, P[0]=1)
+  best child ........ cython_tree_optimized.pyx:421-464
+  select_path ....... cython_tree_optimized.pyx:177-202 (+VL on arrival)
+  expand_node ....... cython_tree_optimized.pyx:232-277 (contiguous nodes and edges)
+  backup ............ VL revert of cython_tree_optimized.pyx:222, sign of
+                      python/mcts/cpu/optimized_wave_search.py:472-483 (leaf-positive) or
+                      cython_tree_optimized.pyx:216-224 (root-positive)
+  expansion policy .. optimized_wave_search.py:377-415 (legal renormalisation; 'full' or the
+                      reference's progressive widening)
+numpy float32 scalar arithmetic is IEEE binary32 with round-to-nearest-even, which is the
+arithmetic the reference's Cython tree performs in source order.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+F = np.float32
+
+
+def sum64(x) -> np.float32:
+    """Canonical 64-lane sum: lane l adds elements l, l+64, ... from +0 in order, then the xor
+    butterfly 32, 16, 8, 4, 2, 1."""
+    part = [F(0.0)] * 64
+    for i, v in enumerate(x):
+        part[i % 64] = F(part[i % 64] + F(v))
+    off = 32
+    while off >= 1:
+        part = [F(part[l] + part[l ^ off]) for l in range(64)]
+        off //= 2
+    return part[0]
+
+
+def sum64d(x) -> float:
+    part = [0.0] * 64
+    for i, v in enumerate(x):
+        part[i % 64] = part[i % 64] + float(v)
+    off = 32
+    while off >= 1:
+        part = [part[l] + part[l ^ off] for l in range(64)]
+        off //= 2
+    return part[0]
+
+
+class NpTree:
+    def __init__(self, cap: int, c_puct: float, vl: float):
+        self.cap = cap
+        self.c = F(c_puct)
+        self.vlf = F(vl)
+        self.vli = int(vl)
+        self.N = np.zeros(cap, np.int32)
+        self.W = np.zeros(cap, np.float32)
+        self.P = np.zeros(cap, np.float32)
+        self.parent = np.full(cap, -1, np.int32)
+        self.first = np.full(cap, -1, np.int32)
+        self.nchild = np.zeros(cap, np.int32)
+        self.action = np.zeros(cap, np.int32)
+        self.expanded = np.zeros(cap, bool)
+        self.children = np.zeros(cap, np.int32)
+        self.num_nodes = 1
+        self.num_edges = 0
+        self.N[0] = 1
+        self.P[0] = F(1.0)
+        self.action[0] = -1
+
+    def best_child(self, p: int, Np: int | None = None) -> int:
+        Np = int(self.N[p]) if Np is None else Np
+        f, k = int(self.first[p]), int(self.nchild[p])
+        if k == 0 or f < 0 or Np == 0:
+            return -1
+        s = F(math.sqrt(float(F(Np))))
+        best, arg = F(-1e9), -1
+        for i in range(k):
+            ch = int(self.children[f + i])
+            n = int(self.N[ch])
+            if n == 0:
+                return ch
+            q = F(self.W[ch] / F(F(n) + self.vlf))
+            u = F(F(F(self.c * self.P[ch]) * s) / F(1 + n))
+            sc = F(q + u)
+            if sc > best:
+                best, arg = sc, ch
+        return arg
+
+    def select_path(self, max_depth: int):
+        path, cur = [], 0
+        while True:
+            path.append(cur)
+            self.N[cur] += self.vli
+            if not self.expanded[cur] or self.nchild[cur] == 0 or len(path) == max_depth:
+                return path
+            c = self.best_child(cur)
+            if c < 0:
+                return path
+            cur = c
+
+    def expand(self, leaf: int, actions, priors) -> bool:
+        k = len(actions)
+        if self.expanded[leaf] or k == 0 or self.num_nodes + k > self.cap:
+            return False
+        fe, fc = self.num_edges, self.num_nodes
+        self.num_edges += k
+        self.num_nodes += k
+        self.first[leaf], self.nchild[leaf], self.expanded[leaf] = fe, k, True
+        for j in range(k):
+            c = fc + j
+            self.parent[c], self.P[c], self.action[c] = leaf, F(priors[j]), actions[j]
+            self.N[c], self.W[c] = 0, F(0.0)
+            self.children[fe + j] = c
+        return True
+
+    def backup(self, path, v: float, root_positive: bool = False):
+        L = len(path)
+        v = F(v)
+        for d, x in enumerate(path):
+            e = d if root_positive else L - 1 - d
+            self.N[x] = self.N[x] - self.vli + 1
+            self.W[x] = F(self.W[x] + (-v if e & 1 else v))
+
+
+def choose_children(legal, pol_row, is_root, policy, root_visits, noise=None, eps=0.0):
+    """Expansion of one leaf (optimized_wave_search.py:377-415): legal priors renormalised by
+    their canonical sum, Dirichlet at the root, 'full' or progressive widening; returns
+    (actions, priors) in ascending action order."""
+    legal = list(legal)
+    n = len(legal)
+    pf = [F(pol_row[a]) for a in legal]
+    S = sum64(pf)
+    pf = [F(p / S) for p in pf]
+    noisy = is_root and noise is not None and eps > 0
+    w32 = F(1.0 - eps)
+    pd = [float(F(w32 * p)) + eps * float(noise[i]) if noisy else float(p) for i, p in enumerate(pf)]
+    chosen = list(range(n))
+    k = n
+    if policy == "reference_pw":
+        if is_root:
+            m1 = min(n, int(10.0 * math.sqrt(float(root_visits))) + 1)
+            sel = max(5, min(m1, 15))
+        else:
+            sel = 3
+        if n > sel:
+            order = sorted(range(n), key=lambda i: (-pd[i], i))[:sel]
+            chosen = sorted(order)
+            if noisy:
+                Sd = sum64d([pd[i] for i in chosen])
+                for i in chosen:
+                    pd[i] = pd[i] / Sd
+            else:
+                Sf = sum64([F(pd[i]) for i in chosen])
+                for i in chosen:
+                    pd[i] = float(F(F(pd[i]) / Sf))
+        k = min(len(chosen), 8) if is_root else len(chosen)
+    chosen = chosen[:k]
+    return [legal[i] for i in chosen], [F(pd[i]) for i in chosen]
+
+
+def board_legal(root_empty, path_actions, pass_action=None):
+    taken = {a for a in path_actions if a != pass_action}
+    return [a for a in root_empty if a not in taken]
+
+
+def np_wave(tree: NpTree, W: int, max_depth: int, legal_of, pol_rows, vals, policy="full",
+            noise=None, eps=0.0, root_positive=False):
+    """One wave: W sequential select_paths, unique leaves in first-occurrence order evaluated
+    from pol_rows/vals (row u for the u-th unique leaf), expansion, then backup in order."""
+    paths = [tree.select_path(max_depth) for _ in range(W)]
+    leaves = [p[-1] for p in paths]
+    uniq = []
+    for l in leaves:
+        if l not in uniq:
+            uniq.append(l)
+    for u, leaf in enumerate(uniq):
+        if tree.expanded[leaf]:
+            continue
+        path = paths[leaves.index(leaf)]
+        legal = legal_of([int(tree.action[x]) for x in path[1:]])
+        if not legal:
+            continue
+        root_visits = int(tree.N[0]) - tree.vli * W
+        acts, pri = choose_children(legal, pol_rows[u], leaf == 0, policy, root_visits, noise, eps)
+        if len(acts) <= 512:
+            tree.expand(leaf, acts, pri)
+    for s, path in enumerate(paths):
+        tree.backup(path, vals[uniq.index(leaves[s])], root_positive)
+    return paths, uniq
+
+
+def grouped_select(tree: NpTree, W: int, max_depth: int):
+    """The device schedule of the selection, restated: level by level, the simulations at one
+    node form a group processed in simulation order, the r-th member seeing Np = N[p] + VL*r
+    and each child c with N[c] + VL*(members before it that chose c).  N is then advanced by
+    VL per path entry.  Returns the paths; must equal W sequential select_paths."""
+    paths = [[0] for _ in range(W)]
+    groups = {0: list(range(W))}
+    depth = 0
+    base = tree.N.copy()
+    while groups:
+        nxt = {}
+        for p, members in groups.items():
+            leaf = (not tree.expanded[p]) or tree.nchild[p] == 0 or depth == max_depth - 1
+            if leaf:
+                continue
+            extra = {}
+            saved = {}
+            f, k = int(tree.first[p]), int(tree.nchild[p])
+            for i in range(k):
+                saved[int(tree.children[f + i])] = int(tree.N[int(tree.children[f + i])])
+            for r, s in enumerate(members, start=1):
+                for c, n0 in saved.items():
+                    tree.N[c] = n0 + tree.vli * extra.get(c, 0)
+                c = tree.best_child(p, int(base[p]) + tree.vli * r)
+                if c < 0:
+                    continue
+                extra[c] = extra.get(c, 0) + 1
+                paths[s].append(c)
+                nxt.setdefault(c, []).append(s)
+            for c, n0 in saved.items():
+                tree.N[c] = n0
+        groups = nxt
+        depth += 1
+    for path in paths:
+        for x in path:
+            tree.N[x] += tree.vli
+    return paths

@@ -1,0 +1,176 @@
+"""The MCTS / MCTSConfig API over the HIP library, checked against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from omoknuni_quantum_amd.core.mcts import MCTS
+from omoknuni_quantum_amd.core.mcts_config import GameType, MCTSConfig
+from omoknuni_quantum_amd.synthetic import games
+from omoknuni_quantum_amd.synthetic.evaluator import SyntheticEvaluator
+from oracle.oracle import Oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _config(**kw):
+    base = dict(num_simulations=256, c_puct=1.4, virtual_loss=3.0, max_wave_size=32,
+                dirichlet_epsilon=0.0, max_tree_nodes=100_000, seed=7, board_size=15,
+                game_type=GameType.GOMOKU, device="cuda")
+    base.update(kw)
+    return MCTSConfig(**base)
+
+
+def _board(seed=1, stones=20):
+    return games.random_boards(1, 15, stones, seed, min_stones=stones)[0]
+
+
+def _oracle_for(cfg, boards, noise=None):
+    model = MCTS._game_model(cfg)
+    T = boards.shape[0] if boards is not None else cfg.num_trees
+    orc = Oracle(model, T, cfg.max_tree_nodes, cfg.max_wave_size, cfg.max_depth)
+    orc.set_params(cfg.c_puct, cfg.virtual_loss, 0 if cfg.expansion_policy == "full" else 1,
+                   0 if cfg.backup_sign == "leaf_positive" else 1, 1.0, cfg.dirichlet_epsilon)
+    orc.set_roots(games.root_keys(cfg.seed, T), games.legal_masks(model, boards, T), noise)
+    return orc
+
+
+def _assert_tree_equal(mcts, orc, t=0):
+    g = mcts.engine.host_tree(t)
+    o = orc.tree(t)
+    assert g["num_nodes"] == o["num_nodes"]
+    for k in ("N", "parent", "first", "nchild", "action"):
+        assert np.array_equal(g[k], o[k]), k
+    for k in ("W", "P"):
+        assert np.array_equal(g[k].view(np.int32), o[k].view(np.int32)), k
+
+
+def test_search_matches_oracle(device):
+    cfg = _config()
+    board = _board()
+    m = MCTS(cfg, SyntheticEvaluator())
+    pol = m.search(board)
+    orc = _oracle_for(cfg, board[None])
+    orc.search(256, 32)
+    assert pol.shape == (225,)
+    assert np.array_equal(pol, orc.root_policy(0))
+    _assert_tree_equal(m, orc)
+    assert abs(pol.sum() - 1.0) < 1e-12
+    assert np.all(pol[board.reshape(-1) != 0] == 0)  # occupied cells never visited
+
+
+def test_second_search_continues_tree(device):
+    cfg = _config(num_simulations=64)
+    board = _board()
+    m = MCTS(cfg, SyntheticEvaluator())
+    m.search(board)
+    m.search(board)
+    assert int(m.engine.N[0].item()) == 2 + 128
+    m.search(_board(seed=2))  # a different root resets the tree
+    assert int(m.engine.N[0].item()) == 2 + 64
+
+
+def test_zero_simulations_and_shape_check(device):
+    m = MCTS(_config(), SyntheticEvaluator())
+    pol = m.search(_board(), num_simulations=0)
+    assert np.allclose(pol, 1.0 / 225)
+    with pytest.raises(ValueError):
+        m.search(np.zeros((9, 9), np.int8))
+
+
+def test_select_action_update_root_root_value(device):
+    m = MCTS(_config(), SyntheticEvaluator())
+    board = _board()
+    pol = m.search(board)
+    assert m.select_action(board, temperature=0, policy=pol) == int(np.argmax(pol))
+    a = m.select_action(board, temperature=1.0, policy=pol)
+    assert pol[a] > 0
+    n, w = int(m.engine.N[0].item()), float(m.engine.W[0].item())
+    assert m.get_root_value() == pytest.approx(w / n)
+    with pytest.raises(ValueError):
+        m.update_root(-1)
+    with pytest.raises(ValueError):
+        m.update_root(225)
+    nb = board.copy()
+    nb.reshape(-1)[a] = 1
+    m.update_root(a, nb)
+    assert int(m.engine.num_nodes[0].item()) == 1
+    stats = m.get_statistics()
+    assert stats["total_searches"] == 1 and stats["total_simulations"] == 256
+    with MCTS(_config(), SyntheticEvaluator()) as m2:
+        m2.search(board, num_simulations=32)
+
+
+def test_search_batch_matches_oracle(device):
+    cfg = _config(num_trees=4, num_simulations=128, max_wave_size=64)
+    boards = games.random_boards(4, 15, 40, seed=9)
+    m = MCTS(cfg, SyntheticEvaluator())
+    pol = m.search_batch(boards)
+    orc = _oracle_for(cfg, boards)
+    orc.search(128, 64)
+    for t in range(4):
+        assert np.array_equal(pol[t], orc.root_policy(t))
+        _assert_tree_equal(m, orc, t)
+    with pytest.raises(ValueError):
+        m.search(boards[0])
+
+
+def test_root_dirichlet_noise_matches_oracle(device):
+    cfg = _config(dirichlet_epsilon=0.25, dirichlet_alpha=0.03, num_simulations=96)
+    board = _board()
+    m = MCTS(cfg, SyntheticEvaluator())
+    pol = m.search(board)
+    model = MCTS._game_model(cfg)
+    legal = games.legal_masks(model, board[None], 1)
+    noise = games.dirichlet_noise(model, games.legal_counts(model, legal), 0.03, cfg.seed + 7919)
+    orc = _oracle_for(cfg, board[None], noise)
+    orc.search(96, 32)
+    assert np.array_equal(pol, orc.root_policy(0))
+    _assert_tree_equal(m, orc)
+
+
+def test_reference_pw_and_root_positive_via_api(device):
+    cfg = _config(expansion_policy="reference_pw", backup_sign="root_positive",
+                  num_simulations=200)
+    board = _board()
+    m = MCTS(cfg, SyntheticEvaluator())
+    pol = m.search(board)
+    orc = _oracle_for(cfg, board[None])
+    orc.search(200, 32)
+    assert np.array_equal(pol, orc.root_policy(0))
+    _assert_tree_equal(m, orc)
+    assert int(m.engine.nchild[0].item()) == 8  # MAX_CHILDREN at the root
+
+
+class _RecordingEvaluator:
+    """A reference-protocol evaluator: features -> (policy, value) from a fixed random conv,
+    recording its outputs for replay into the oracle."""
+
+    def __init__(self, seed=0):
+        g = torch.Generator().manual_seed(seed)
+        self.w = (torch.randn(18, generator=g) * 0.5)
+        self.calls = []
+
+    def evaluate_batch(self, feats):
+        x = feats.float()
+        w = self.w.to(x.device)[None, :, None, None]
+        logits = (x * w).sum(dim=1).reshape(x.shape[0], -1) * 3
+        pol = torch.softmax(logits, dim=1)
+        val = torch.tanh(x[:, 0].mean(dim=(1, 2)) - x[:, 1].mean(dim=(1, 2)) + logits.mean(1))
+        self.calls.append((pol.cpu().numpy().copy(), val.cpu().numpy().copy()))
+        return pol, val
+
+
+def test_feature_evaluator_replay_parity(device):
+    cfg = _config(num_simulations=160)
+    board = _board(stones=30)
+    ev = _RecordingEvaluator()
+    m = MCTS(cfg, ev)
+    pol = m.search(board)
+    assert len(ev.calls) == 1 + 160 // 32
+    orc = _oracle_for(cfg, board[None])
+    orc.reset_tree(0)
+    sizes = [1] + [32] * 5
+    for (p, v), W in zip(ev.calls, sizes):
+        orc.wave(0, W, replay_policy=p[:32], replay_values=v[:32])
+    assert np.array_equal(pol, orc.root_policy(0))
+    _assert_tree_equal(m, orc)

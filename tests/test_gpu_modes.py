@@ -1,0 +1,137 @@
+"""Alternate modes of the wave operations and the reference-style primitives on the GPU."""
+import numpy as np
+import pytest
+import torch
+
+from omoknuni_quantum_amd import _lib
+from omoknuni_quantum_amd.core.engine import SearchParams, WaveEngine
+from omoknuni_quantum_amd.synthetic import games
+from omoknuni_quantum_amd.synthetic.evaluator import SyntheticEvaluator
+from omoknuni_quantum_amd.synthetic.workloads import get
+from oracle.parity import make_pair, run_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def test_root_positive_sign_parity(device):
+    wl = get("C1").scaled(name="C1-root_positive", num_simulations=480)
+    assert run_parity(wl, sign_mode=_lib.OMQ_SIGN_ROOT_POSITIVE, device=device) >= 2
+
+
+def test_atomic_virtual_loss_parity(device):
+    wl = get("C2").scaled(name="C2-vl_atomic", num_trees=2, num_simulations=512, wave_size=256,
+                          capacity=100_000)
+    assert run_parity(wl, vl_atomic=True, device=device) >= 2
+
+
+def test_atomic_w_within_tolerance(device):
+    """W accumulated with float atomics stays within 1e-5 relative of the ordered sum, wave by
+    wave; N is exact.  After each comparison the ordered W is copied over so the next selection
+    starts from the same tree."""
+    wl = get("C2").scaled(name="C2-atomic", num_trees=2, num_simulations=768, wave_size=256,
+                          capacity=100_000)
+    a, _, ev = make_pair(wl, w_mode=_lib.OMQ_WACC_ORDERED, device=device)
+    b, _, _ = make_pair(wl, w_mode=_lib.OMQ_WACC_ATOMIC, device=device)
+    a.reset()
+    b.reset()
+    for W in [1] + [256] * 3:
+        a.run_wave(W, ev)
+        b.run_wave(W, ev)
+        torch.cuda.synchronize()
+        assert torch.equal(a.N, b.N) and torch.equal(a.num_nodes, b.num_nodes)
+        assert torch.equal(a.P, b.P)
+        wa, wb = a.W.double(), b.W.double()
+        rel = ((wa - wb).abs() / wa.abs().clamp_min(1.0)).max().item()
+        assert rel <= 1e-5, rel
+        b.W.copy_(a.W)
+
+
+def _engine(T, cap, sign_mode=0, vl=3.0):
+    params = SearchParams(virtual_loss=vl, sign_mode=sign_mode)
+    return WaveEngine(games.gomoku(5), T, cap, 8, 16, "cuda", params)
+
+
+@pytest.mark.parametrize("sign_mode", [0, 1])
+def test_paths_backup_matches_numpy(device, sign_mode):
+    T, cap, B, D = 3, 1000, 500, 12
+    rng = np.random.default_rng(5 + sign_mode)
+    eng = _engine(T, cap, sign_mode)
+    paths = rng.integers(0, cap, (B, D)).astype(np.int32)
+    plen = rng.integers(0, D + 1, B).astype(np.int32)
+    for b in range(B):
+        paths[b, plen[b]:] = -1
+    paths[7, 2] = cap + 40          # out of range: the path ends there
+    plen[7] = max(plen[7], 5)
+    paths[7, :2] = [3, 4]
+    paths[7, 3:plen[7]] = 9
+    tree_of = rng.integers(0, T, B).astype(np.int32)
+    tree_of[11] = T + 2             # names no tree: skipped
+    values = (rng.integers(-8, 9, B) / 8.0).astype(np.float32)  # sums stay exact
+    N = np.zeros((T, cap), np.int64)
+    Wx = np.zeros((T, cap), np.float64)
+    for b in range(B):
+        t = tree_of[b]
+        if t >= T:
+            continue
+        L = plen[b]
+        for d in range(L):
+            x = paths[b, d]
+            if x < 0 or x >= cap:
+                break
+            e = (L - 1 - d) if sign_mode == 0 else d
+            N[t, x] += 1
+            Wx[t, x] += -values[b] if e & 1 else values[b]
+    eng.backup_paths(paths, plen, values, tree_of)
+    torch.cuda.synchronize()
+    assert np.array_equal(eng.N.view(T, cap).cpu().numpy(), N)
+    assert np.array_equal(eng.W.view(T, cap).cpu().numpy().astype(np.float64), Wx)
+    with pytest.raises(ValueError):
+        eng.backup_paths(paths[:, 0], plen, values)
+
+
+def test_virtual_loss_apply_revert(device):
+    T, cap = 2, 64
+    eng = _engine(T, cap, vl=3.0)
+    eng.reset()
+    base = eng.N.clone()
+    nodes = np.array([0, 5, 5, 5, 63, -1, 64, 7], np.int32)
+    tree_of = np.array([0, 1, 1, 0, 1, 0, 0, 9], np.int32)
+    eng.apply_virtual_loss(nodes, tree_of)
+    torch.cuda.synchronize()
+    want = base.view(T, cap).cpu().numpy().copy()
+    want[0, 0] += 3
+    want[1, 5] += 6
+    want[0, 5] += 3
+    want[1, 63] += 3
+    assert np.array_equal(eng.N.view(T, cap).cpu().numpy(), want)
+    eng.remove_virtual_loss(nodes, tree_of)
+    torch.cuda.synchronize()
+    assert torch.equal(eng.N, base)
+    eng.apply_virtual_loss([1, 2], amount=1)  # tree 0 when tree_of is omitted
+    torch.cuda.synchronize()
+    assert int(eng.N[1].item()) == int(base[1].item()) + 1
+
+
+@pytest.mark.parametrize("name", ["C3", "C4"])
+def test_synthetic_evaluator_rows_match_oracle(device, name):
+    """Leaf keys, legal counts and values of the synthetic evaluator equal the oracle's."""
+    wl = get(name).scaled(num_trees=2, num_simulations=128, wave_size=128, capacity=50_000)
+    eng, orc, ev = make_pair(wl, device=device)
+    eng.reset()
+    for t in range(wl.num_trees):
+        orc.reset_tree(t)
+    for W in (1, 128):
+        eng.run_wave(W, ev)
+        for t in range(wl.num_trees):
+            orc.wave(t, W)
+    torch.cuda.synchronize()
+    MW = eng.MW
+    for t in range(wl.num_trees):
+        lw = orc.last_wave(t, 128)
+        u = lw["ucount"]
+        assert int(eng.ucount[t].item()) == u
+        keys = eng.ukey[t * MW:t * MW + u].cpu().numpy().view(np.uint64)
+        assert np.array_equal(keys, lw["ukey"])
+        assert np.array_equal(eng.ulegal[t * MW:t * MW + u].cpu().numpy(), lw["ulegal"])
+        vals = eng.values[t * MW:t * MW + u].cpu().numpy()
+        assert np.array_equal(vals.view(np.int32), lw["values"].view(np.int32))

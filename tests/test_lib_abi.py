@@ -1,0 +1,102 @@
+"""The C-ABI library loads on a host without a GPU, exports every entry point that
+include/omq_tree_ops.h declares, and rejects invalid arguments before touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from omoknuni_quantum_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "omq_tree_ops.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(omq_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for n in ("omq_select", "omq_expand", "omq_backup", "omq_forest_reset", "omq_leaf_info",
+              "omq_synthetic_evaluate", "omq_paths_backup", "omq_virtual_loss",
+              "omq_last_error", "omq_abi_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+    assert lib.omq_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layout_matches_header():
+    # two int32 per 8 bytes, then pointers: offsets the C compiler uses
+    assert ctypes.sizeof(_lib.OmqForest) == 8 * 4 + 10 * 8
+    assert _lib.OmqForest.visit_counts.offset == 32
+    assert ctypes.sizeof(_lib.OmqWave) == 8 + 19 * 8
+    assert _lib.OmqWave.paths.offset == 8
+
+
+def _forest(**kw):
+    f = _lib.OmqForest()
+    f.num_trees, f.capacity, f.num_actions, f.game = 1, 16, 25, _lib.OMQ_GAME_BOARD
+    f.legal_words = 1
+    for name in ("visit_counts", "value_sums", "priors", "parents", "first_child",
+                 "num_children", "actions", "num_nodes", "root_keys", "root_legal"):
+        setattr(f, name, 8)  # never dereferenced: the calls below fail validation first
+    for k, v in kw.items():
+        setattr(f, k, v)
+    return f
+
+
+@pytest.mark.parametrize("bad,msg", [
+    ({"num_trees": 0}, "must be positive"),
+    ({"num_actions": 9000}, "num_actions"),
+    ({"game": 7}, "unknown game model"),
+    ({"legal_words": 3}, "legal_words"),
+    ({"num_actions": 600, "legal_words": 19}, "row limit"),
+    ({"game": _lib.OMQ_GAME_SPARSE, "min_legal": 10, "max_legal": 80}, "sparse legal range"),
+    ({"visit_counts": None}, "null array"),
+])
+def test_invalid_forest_rejected(bad, msg):
+    lib = _lib.load()
+    f = _forest(**bad)
+    rc = lib.omq_forest_reset(ctypes.byref(f), None)
+    assert rc == _lib.OMQ_E_ARG or rc == _lib.OMQ_E_LIMIT
+    assert msg in lib.omq_last_error().decode()
+    with pytest.raises(_lib.OmqError):
+        _lib.check(rc, "omq_forest_reset")
+
+
+def test_invalid_wave_arguments_rejected():
+    lib = _lib.load()
+    f = _forest()
+    w = _lib.OmqWave()
+    w.max_wave, w.max_depth = 8, 16
+    rc = lib.omq_select(ctypes.byref(f), ctypes.byref(w), 4, 1.4, 3.0, 16, 0, None)
+    assert rc == _lib.OMQ_E_ARG and "null array" in lib.omq_last_error().decode()
+    for name, _ in _lib.OmqWave._fields_[2:]:
+        setattr(w, name, 8)
+    assert lib.omq_select(ctypes.byref(f), ctypes.byref(w), 9, 1.4, 3.0, 16, 0, None) == _lib.OMQ_E_ARG
+    assert "wave_size" in lib.omq_last_error().decode()
+    assert lib.omq_select(ctypes.byref(f), ctypes.byref(w), 4, 1.4, -1.0, 16, 0, None) == _lib.OMQ_E_ARG
+    assert lib.omq_select(ctypes.byref(f), ctypes.byref(w), 4, 1.4, 3.0, 17, 0, None) == _lib.OMQ_E_ARG
+    w.max_wave = 5000
+    assert lib.omq_select(ctypes.byref(f), ctypes.byref(w), 4, 1.4, 3.0, 16, 0, None) == _lib.OMQ_E_LIMIT
+    w.max_wave = 8
+    assert lib.omq_expand(ctypes.byref(f), ctypes.byref(w), 4, 3.0, 5, None, 0.0, None) == _lib.OMQ_E_ARG
+    assert lib.omq_expand(ctypes.byref(f), ctypes.byref(w), 4, 3.0, 0, None, 2.0, None) == _lib.OMQ_E_ARG
+    assert lib.omq_backup(ctypes.byref(f), ctypes.byref(w), 4, 3.0, 9, 0, None) == _lib.OMQ_E_ARG
+    assert lib.omq_backup(ctypes.byref(f), ctypes.byref(w), 4, 3.0, 0, 9, None) == _lib.OMQ_E_ARG
+    assert lib.omq_paths_backup(ctypes.byref(f), None, None, None, None, 0, 4, 0, None) == 0
+    assert lib.omq_virtual_loss(ctypes.byref(f), None, None, -1, 3, None) == _lib.OMQ_E_ARG
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_lib.LibraryNotBuilt):
+        _lib.load(str(tmp_path / "absent.so"))
