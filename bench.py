@@ -50,6 +50,26 @@ def algorithmic_bytes(st: dict, sims: int) -> dict:
     }
 
 
+KERNEL_OF_PHASE = {"select": "select_kernel", "leaf_info": "leaf_info_kernel",
+                   "expand": "expand_write_kernel", "backup": "backup_groups_kernel"}
+
+
+def measured_traffic(workload: str, phase: str, args):
+    """HBM bytes per launch of the phase's main kernel from the committed rocprofv3 --pmc
+    summary (profiles/hbm_traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the
+    same counters of a plain copy of known size).  None when no profile covers this run's
+    workload and modes."""
+    path = os.path.join(_ROOT, "profiles", "hbm_traffic.json")
+    if args.w_mode != "ordered" or args.vl_atomic or args.trees or not os.path.exists(path):
+        return None, None
+    with open(path) as fh:
+        table = json.load(fh)
+    e = table.get(f"{workload}/{KERNEL_OF_PHASE[phase]}")
+    if not e:
+        return None, None
+    return int(e["bytes_per_dispatch"]), e["source"]
+
+
 def run(args) -> dict:
     import torch
 
@@ -72,6 +92,15 @@ def run(args) -> dict:
     eng.set_roots(keys, legal, noise)
     ev = SyntheticEvaluator(wl.logit_scale)
 
+    if args.copy_probe_mib > 0:
+        # one plain device copy of known size, outside the timed region: the reference point
+        # that scales the HBM counters (FETCH_SIZE / WRITE_SIZE) of a --pmc profile of this run
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        del src, dst
     for _ in range(args.warmup):
         eng.search(wl.num_simulations, wl.wave_size, ev)
     torch.cuda.synchronize(dev)
@@ -103,10 +132,13 @@ def run(args) -> dict:
     d_bytes = ab[dominant] / dn
     d_s = tot[dominant] / 1e3 / dn
     achieved = d_bytes / d_s / 1e9
+    traffic, traffic_src = measured_traffic(wl.name, dominant, args)
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 2),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                "traffic": None, "algorithmic_bytes_per_launch": int(d_bytes),
+                "traffic": traffic, "algorithmic_bytes_per_launch": int(d_bytes),
                 "us_per_launch": round(d_s * 1e6, 3)}
+    if traffic_src:
+        roofline["traffic_source"] = traffic_src
     whole_bytes = sum(ab.values())
     out = {
         "metric": METRIC,
@@ -140,25 +172,39 @@ def run(args) -> dict:
 
 
 def cpu_baseline(wl, eng, args):
-    """The C oracle timed on the host on the same workload (single thread), then its final
+    """The C oracle timed on the host on the same workload (one thread, then one tree per thread
+    on all threads), then its final
     trees compared bit for bit with the GPU's (state after the last timed search)."""
     from oracle.oracle import Oracle
     from oracle.parity import EXPAND_CODES
 
     T = wl.num_trees if args.cpu_trees <= 0 else min(args.cpu_trees, wl.num_trees)
-    orc = Oracle(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth)
+    keys, legal, noise = wl.root_inputs()
+    orc = Oracle(wl.model, T, wl.capacity, wl.wave_size, wl.max_depth)
     orc.set_params(wl.c_puct, wl.virtual_loss, EXPAND_CODES[wl.expand_policy], 0, wl.logit_scale,
                    wl.dirichlet_epsilon)
-    keys, legal, noise = wl.root_inputs()
-    orc.set_roots(keys, legal, noise)
+    orc.set_roots(keys[:T], None if legal is None else legal[:T],
+                  None if noise is None else noise[:T])
+    # single thread: the first tree(s), about 10 s of work at most
     t0 = time.perf_counter()
-    for t in range(T):
-        orc.lib.orc_search_tree(orc.f, t, wl.num_simulations, wl.wave_size, wl.max_depth)
+    t1 = 0
+    while t1 < T and (t1 == 0 or time.perf_counter() - t0 < 10.0):
+        orc.lib.orc_search_tree(orc.f, t1, wl.num_simulations, wl.wave_size, wl.max_depth)
+        t1 += 1
+    dt1 = time.perf_counter() - t0
+    single = t1 * wl.num_simulations / dt1
+    # all threads: every tree of the sample, one tree at a time per thread (trees independent)
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1, T)
+    t0 = time.perf_counter()
+    orc.search(wl.num_simulations, wl.wave_size, wl.max_depth, nthreads=threads)
     dt = time.perf_counter() - t0
-    cpu = {"value": round(T * wl.num_simulations / dt, 1), "unit": "simulations/s", "cores": 1,
-           "kind": "port",
+    cpu = {"value": round(T * wl.num_simulations / dt, 1), "unit": "simulations/s",
+           "cores": threads, "kind": "port",
            "sample": f"{T} of {wl.num_trees} trees x {wl.num_simulations} simulations of "
-                     f"{wl.name} ({dt:.2f} s, C oracle, gcc -O3, one thread)"}
+                     f"{wl.name} on {threads} threads, one tree per thread ({dt:.2f} s, C oracle, "
+                     f"gcc -O3); single thread: {single:.1f} sims/s over {t1} tree(s) "
+                     f"({dt1:.2f} s)",
+           "single_thread_value": round(single, 1)}
     ok = True
     mismatch = None
     w_exact = args.w_mode == "ordered"
@@ -193,6 +239,11 @@ def main():
     ap.add_argument("--cpu-baseline", choices=("auto", "skip"), default="auto")
     ap.add_argument("--cpu-trees", type=int, default=0,
                     help="trees of the CPU baseline sample (0 = all)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads of the CPU baseline (0 = min(16, cores, trees))")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run one plain device copy of this size before the search (counter "
+                         "calibration for --pmc profiles)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the trees of a workload are "

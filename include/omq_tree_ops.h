@@ -192,18 +192,21 @@ int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
                int32_t sign_mode, int32_t w_mode, void* stream);
 
 /* Reference-style path backup over an explicit path matrix (no group log needed):
- * paths[b*max_depth + d], d < path_len[b], root first; values[b] is the leaf value;
- * N[x] += 1, W[x] += sign * values[b] with float atomics; tree index tree_of[b] (tree 0 for
- * all when tree_of is NULL).  A path ends at its first entry outside [0, capacity); a row whose
- * tree index is outside [0, num_trees) is skipped.
+ * paths[b*max_depth + d], d < min(path_len[b], max_depth), root first; values[b] is the leaf
+ * value; N[x] += 1, W[x] += sign * values[b] with float atomics, the sign taken from the
+ * distance to the leaf (path_len[b]-1-d) or the depth d; tree index tree_of[b] (tree 0 for
+ * all when tree_of is NULL).  Entries outside [0, capacity) (-1 padding) are skipped, as in
+ * the reference kernel; a row whose tree index is outside [0, num_trees) is skipped.  Only
+ * num_trees, capacity, visit_counts and value_sums of the forest are read.
  * Replaces vectorized_backup (mcts_kernels.cu:121-158 / torch_custom_ops.py mcts::vectorized_backup). */
 int omq_paths_backup(const omq_forest* f, const int32_t* paths, const int32_t* path_len,
                      const int32_t* tree_of, const float* values, int32_t batch, int32_t max_depth,
                      int32_t sign_mode, void* stream);
 
 /* Reference-style virtual loss on a node list: visit_counts[tree_of[i]*capacity + nodes[i]]
- * += delta (atomic).  delta > 0 applies, delta < 0 reverts.  Entries whose node or tree index
- * is out of range (including -1 padding) are skipped.
+ * += delta (atomic).  delta > 0 applies, delta < 0 reverts (no clamp at zero: every revert
+ * pairs with an apply).  Entries whose node or tree index is out of range (including -1
+ * padding) are skipped.  Only num_trees, capacity and visit_counts of the forest are read.
  * Replaces batch_apply_virtual_loss / batch_remove_virtual_loss (mcts_kernels.cu:845-860,934-953). */
 int omq_virtual_loss(const omq_forest* f, const int32_t* nodes, const int32_t* tree_of,
                      int32_t count, int32_t delta, void* stream);

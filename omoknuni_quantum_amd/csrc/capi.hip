@@ -78,6 +78,17 @@ int check_forest(const omq_forest* f) {
   return OMQ_OK;
 }
 
+// The reference-style primitives touch visit_counts (and value_sums) only.
+int check_forest_nw(const omq_forest* f, bool need_w) {
+  if (!f) return fail(OMQ_E_ARG, "forest is null");
+  if (f->num_trees <= 0 || f->capacity <= 0)
+    return fail(OMQ_E_ARG, "num_trees (%d) and capacity (%d) must be positive", f->num_trees,
+                f->capacity);
+  if (!f->visit_counts || (need_w && !f->value_sums))
+    return fail(OMQ_E_ARG, "forest has a null array");
+  return OMQ_OK;
+}
+
 int check_wave(const omq_forest* f, const omq_wave* w, int wave_size) {
   if (!w) return fail(OMQ_E_ARG, "wave buffers are null");
   if (w->max_wave <= 0 || w->max_wave > OMQ_MAX_WAVE)
@@ -192,7 +203,7 @@ int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
 int omq_paths_backup(const omq_forest* f, const int32_t* paths, const int32_t* path_len,
                      const int32_t* tree_of, const float* values, int32_t batch,
                      int32_t max_depth, int32_t sign_mode, void* stream) {
-  int rc = check_forest(f);
+  int rc = check_forest_nw(f, true);
   if (rc) return rc;
   if (batch < 0 || max_depth <= 0) return fail(OMQ_E_ARG, "batch/max_depth out of range");
   if (batch == 0) return OMQ_OK;
@@ -206,7 +217,7 @@ int omq_paths_backup(const omq_forest* f, const int32_t* paths, const int32_t* p
 
 int omq_virtual_loss(const omq_forest* f, const int32_t* nodes, const int32_t* tree_of,
                      int32_t count, int32_t delta, void* stream) {
-  int rc = check_forest(f);
+  int rc = check_forest_nw(f, false);
   if (rc) return rc;
   if (count < 0) return fail(OMQ_E_ARG, "count %d < 0", count);
   if (count == 0) return OMQ_OK;

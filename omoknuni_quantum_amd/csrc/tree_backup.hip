@@ -128,7 +128,7 @@ __global__ void paths_backup_kernel(omq_forest f, const int32_t* paths, const in
   const float v = values[b];
   for (int d = 0; d < L; ++d) {
     const int x = paths[(int64_t)b * max_depth + d];
-    if (x < 0 || x >= f.capacity) break;  // -1 padding (and anything out of range) ends a path
+    if (x < 0 || x >= f.capacity) continue;  // -1 padding and out-of-range entries are skipped
     const int e = sign_mode == OMQ_SIGN_LEAF_POSITIVE ? (L - 1 - d) : d;
     atomicAdd(&f.visit_counts[tb + x], 1);
     unsafeAtomicAdd(&f.value_sums[tb + x], (e & 1) ? -v : v);

@@ -1,0 +1,118 @@
+"""torch.library operators over the C ABI, with the reference's operator signatures.
+
+The reference registers ``mcts::vectorized_backup`` (python/mcts/gpu/torch_custom_ops.py:26-55)
+and reaches ``batch_apply_virtual_loss`` / ``batch_remove_virtual_loss``
+(python/mcts/gpu/mcts_kernels.cu:845-860,934-953) through its pybind11 module.  The same
+operations are registered here in the ``omq`` namespace, mutating their tensor arguments in
+place on the caller's current HIP stream:
+
+    torch.ops.omq.vectorized_backup(paths, path_lengths, values, visit_counts, value_sums)
+    torch.ops.omq.batch_apply_virtual_loss(node_indices, virtual_loss_counts)
+    torch.ops.omq.batch_remove_virtual_loss(node_indices, virtual_loss_counts)
+
+``vectorized_backup`` follows the reference kernel (mcts_kernels.cu:121-158): for every path b
+and d < min(path_lengths[b], max_depth), node x = paths[b, d] in [0, num_nodes) gets
+visit_counts[x] += 1 and value_sums[x] += v * (-1)^(path_lengths[b]-1-d) (sign by distance
+from the leaf); other entries are skipped.  The virtual-loss operators add +1 / -1 per listed
+node (duplicates accumulate; indices outside the array are skipped).
+
+There is no CPU implementation: tensors must be on a HIP device, and a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+def _check_device(name: str, *tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(f"omq::{name}: tensors must be on a HIP device (got {dev})")
+    for t in tensors:
+        if t.device != dev:
+            raise RuntimeError(f"omq::{name}: all tensors must be on {dev}")
+        if not t.is_contiguous():
+            raise RuntimeError(f"omq::{name}: tensors must be contiguous")
+    return dev
+
+
+def _forest(counts: torch.Tensor, sums: torch.Tensor | None) -> _lib.OmqForest:
+    f = _lib.OmqForest()
+    f.num_trees = 1
+    f.capacity = counts.numel()
+    f.visit_counts = counts.data_ptr()
+    if sums is not None:
+        f.value_sums = sums.data_ptr()
+    return f
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+@torch.library.custom_op("omq::vectorized_backup", mutates_args=("visit_counts", "value_sums"))
+def vectorized_backup(paths: torch.Tensor, path_lengths: torch.Tensor, values: torch.Tensor,
+                      visit_counts: torch.Tensor, value_sums: torch.Tensor) -> None:
+    dev = _check_device("vectorized_backup", paths, path_lengths, values, visit_counts,
+                        value_sums)
+    if paths.dim() != 2 or paths.dtype != torch.int32 or path_lengths.dtype != torch.int32:
+        raise RuntimeError("omq::vectorized_backup: paths int32 [B, D], path_lengths int32 [B]")
+    if values.dtype != torch.float32 or visit_counts.dtype != torch.int32 or \
+            value_sums.dtype != torch.float32:
+        raise RuntimeError("omq::vectorized_backup: values/value_sums float32, visit_counts int32")
+    B, D = paths.shape
+    if path_lengths.numel() != B or values.numel() != B:
+        raise RuntimeError("omq::vectorized_backup: one length and one value per path")
+    if visit_counts.numel() != value_sums.numel():
+        raise RuntimeError("omq::vectorized_backup: visit_counts and value_sums differ in size")
+    if B == 0 or visit_counts.numel() == 0:
+        return
+    f = _forest(visit_counts, value_sums)
+    lib = _lib.load()
+    _lib.check(lib.omq_paths_backup(ctypes.byref(f), paths.data_ptr(), path_lengths.data_ptr(),
+                                    None, values.data_ptr(), B, max(D, 1),
+                                    _lib.OMQ_SIGN_LEAF_POSITIVE, _stream(dev)),
+               "omq_paths_backup")
+
+
+@vectorized_backup.register_fake
+def _(paths, path_lengths, values, visit_counts, value_sums) -> None:
+    return None
+
+
+def _virtual_loss(name: str, node_indices: torch.Tensor, counts: torch.Tensor, delta: int):
+    dev = _check_device(name, node_indices, counts)
+    if node_indices.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise RuntimeError(f"omq::{name}: node_indices and virtual_loss_counts must be int32")
+    n = node_indices.numel()
+    if n == 0 or counts.numel() == 0:
+        return
+    f = _forest(counts, None)
+    lib = _lib.load()
+    _lib.check(lib.omq_virtual_loss(ctypes.byref(f), node_indices.data_ptr(), None, n, delta,
+                                    _stream(dev)), "omq_virtual_loss")
+
+
+@torch.library.custom_op("omq::batch_apply_virtual_loss", mutates_args=("virtual_loss_counts",))
+def batch_apply_virtual_loss(node_indices: torch.Tensor,
+                             virtual_loss_counts: torch.Tensor) -> None:
+    _virtual_loss("batch_apply_virtual_loss", node_indices, virtual_loss_counts, 1)
+
+
+@batch_apply_virtual_loss.register_fake
+def _(node_indices, virtual_loss_counts) -> None:
+    return None
+
+
+@torch.library.custom_op("omq::batch_remove_virtual_loss", mutates_args=("virtual_loss_counts",))
+def batch_remove_virtual_loss(node_indices: torch.Tensor,
+                              virtual_loss_counts: torch.Tensor) -> None:
+    _virtual_loss("batch_remove_virtual_loss", node_indices, virtual_loss_counts, -1)
+
+
+@batch_remove_virtual_loss.register_fake
+def _(node_indices, virtual_loss_counts) -> None:
+    return None

@@ -60,7 +60,7 @@ def test_paths_backup_matches_numpy(device, sign_mode):
     plen = rng.integers(0, D + 1, B).astype(np.int32)
     for b in range(B):
         paths[b, plen[b]:] = -1
-    paths[7, 2] = cap + 40          # out of range: the path ends there
+    paths[7, 2] = cap + 40          # out of range: skipped, the path goes on
     plen[7] = max(plen[7], 5)
     paths[7, :2] = [3, 4]
     paths[7, 3:plen[7]] = 9
@@ -77,7 +77,7 @@ def test_paths_backup_matches_numpy(device, sign_mode):
         for d in range(L):
             x = paths[b, d]
             if x < 0 or x >= cap:
-                break
+                continue
             e = (L - 1 - d) if sign_mode == 0 else d
             N[t, x] += 1
             Wx[t, x] += -values[b] if e & 1 else values[b]
@@ -135,3 +135,39 @@ def test_synthetic_evaluator_rows_match_oracle(device, name):
         assert np.array_equal(eng.ulegal[t * MW:t * MW + u].cpu().numpy(), lw["ulegal"])
         vals = eng.values[t * MW:t * MW + u].cpu().numpy()
         assert np.array_equal(vals.view(np.int32), lw["values"].view(np.int32))
+
+
+def test_torch_ops_match_reference_kernel_semantics(device):
+    """torch.ops.omq.* with the reference operator signatures (torch_custom_ops.py:26-55,
+    mcts_kernels.cu:121-158,845-860,934-953)."""
+    from omoknuni_quantum_amd import torch_ops  # noqa: F401  (registers the operators)
+
+    rng = np.random.default_rng(3)
+    n, B, D = 300, 200, 9
+    paths = rng.integers(-1, n + 5, (B, D)).astype(np.int32)  # includes -1 and out-of-range
+    plen = rng.integers(0, D + 1, B).astype(np.int32)
+    vals = (rng.integers(-16, 17, B) / 16.0).astype(np.float32)
+    N = np.zeros(n, np.int64)
+    Wx = np.zeros(n, np.float64)
+    for b in range(B):
+        for d in range(min(plen[b], D)):
+            x = paths[b, d]
+            if 0 <= x < n:
+                N[x] += 1
+                Wx[x] += vals[b] if (plen[b] - 1 - d) % 2 == 0 else -vals[b]
+    vc = torch.zeros(n, dtype=torch.int32, device=device)
+    vs = torch.zeros(n, dtype=torch.float32, device=device)
+    torch.ops.omq.vectorized_backup(torch.from_numpy(paths).to(device),
+                                    torch.from_numpy(plen).to(device),
+                                    torch.from_numpy(vals).to(device), vc, vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(vc.cpu().numpy(), N)
+    assert np.array_equal(vs.cpu().numpy().astype(np.float64), Wx)
+    idx = torch.tensor([1, 1, 2, -1, n + 3, 7], dtype=torch.int32, device=device)
+    vl = torch.zeros(n, dtype=torch.int32, device=device)
+    torch.ops.omq.batch_apply_virtual_loss(idx, vl)
+    torch.cuda.synchronize()
+    assert vl[1].item() == 2 and vl[2].item() == 1 and vl[7].item() == 1 and int(vl.sum()) == 4
+    torch.ops.omq.batch_remove_virtual_loss(idx, vl)
+    torch.cuda.synchronize()
+    assert int(vl.abs().sum()) == 0

@@ -100,3 +100,31 @@ def test_invalid_wave_arguments_rejected():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_lib.LibraryNotBuilt):
         _lib.load(str(tmp_path / "absent.so"))
+
+
+def test_torch_ops_registered_and_refuse_host_tensors():
+    import torch
+
+    from omoknuni_quantum_amd import torch_ops  # noqa: F401
+
+    for name in ("vectorized_backup", "batch_apply_virtual_loss", "batch_remove_virtual_loss"):
+        assert hasattr(torch.ops.omq, name)
+    p = torch.zeros((2, 3), dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        torch.ops.omq.vectorized_backup(p, torch.zeros(2, dtype=torch.int32), torch.zeros(2),
+                                        torch.zeros(4, dtype=torch.int32), torch.zeros(4))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        torch.ops.omq.batch_apply_virtual_loss(torch.zeros(2, dtype=torch.int32),
+                                               torch.zeros(4, dtype=torch.int32))
+
+
+def test_primitives_need_only_counts():
+    """omq_paths_backup / omq_virtual_loss read only N (and W) of the forest."""
+    lib = _lib.load()
+    f = _lib.OmqForest()
+    f.num_trees, f.capacity = 1, 10
+    assert lib.omq_virtual_loss(ctypes.byref(f), None, None, 0, 1, None) == _lib.OMQ_E_ARG
+    f.visit_counts = 8
+    assert lib.omq_virtual_loss(ctypes.byref(f), None, None, 0, 1, None) == _lib.OMQ_OK
+    assert lib.omq_paths_backup(ctypes.byref(f), None, None, None, None, 1, 4, 0, None) == _lib.OMQ_E_ARG
+    assert "null" in lib.omq_last_error().decode()
