@@ -90,7 +90,12 @@ def run(args) -> dict:
     eng = WaveEngine(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth, dev, params)
     keys, legal, noise = wl.root_inputs()
     eng.set_roots(keys, legal, noise)
-    ev = SyntheticEvaluator(wl.logit_scale)
+    if wl.evaluator == "resnet":
+        from omoknuni_quantum_amd.synthetic.resnet_evaluator import ResNetEvaluator
+        boards = torch.from_numpy(wl.boards()).to(dev)
+        ev = ResNetEvaluator(eng, boards)
+    else:
+        ev = SyntheticEvaluator(wl.logit_scale)
 
     if args.copy_probe_mib > 0:
         # one plain device copy of known size, outside the timed region: the reference point
@@ -166,12 +171,26 @@ def run(args) -> dict:
         "phases": phases,
         "counters": st,
     }
+    if wl.evaluator == "resnet":
+        out["evaluator"] = (f"random-init ResNet {ev.net.blocks.__len__()} blocks x 128 channels, "
+                            "18 planes, bf16 autocast, one forward pass per wave over "
+                            f"{wl.num_trees} trees x {wl.wave_size} slots = "
+                            f"{wl.num_trees * wl.wave_size} positions")
+        out["tree_op_share"] = round(tree_ms / (tree_ms + eval_ms), 4)
+        out["end_to_end_gpu_sims_per_s"] = round(sims / ((tree_ms + eval_ms) / 1e3), 1)
     if args.cpu_baseline != "skip":
-        out["cpu_baseline"], out["parity_full_size"] = cpu_baseline(wl, eng, args)
+        replay = None
+        if wl.evaluator == "resnet":
+            # one more search with the evaluator outputs recorded, replayed into the oracle
+            ev.record = True
+            eng.search(wl.num_simulations, wl.wave_size, ev)
+            torch.cuda.synchronize(dev)
+            replay = ev.calls
+        out["cpu_baseline"], out["parity_full_size"] = cpu_baseline(wl, eng, args, replay)
     return out
 
 
-def cpu_baseline(wl, eng, args):
+def cpu_baseline(wl, eng, args, replay=None):
     """The C oracle timed on the host on the same workload (one thread, then one tree per thread
     on all threads), then its final
     trees compared bit for bit with the GPU's (state after the last timed search)."""
@@ -185,26 +204,46 @@ def cpu_baseline(wl, eng, args):
                    wl.dirichlet_epsilon)
     orc.set_roots(keys[:T], None if legal is None else legal[:T],
                   None if noise is None else noise[:T])
-    # single thread: the first tree(s), about 10 s of work at most
-    t0 = time.perf_counter()
-    t1 = 0
-    while t1 < T and (t1 == 0 or time.perf_counter() - t0 < 10.0):
-        orc.lib.orc_search_tree(orc.f, t1, wl.num_simulations, wl.wave_size, wl.max_depth)
-        t1 += 1
-    dt1 = time.perf_counter() - t0
-    single = t1 * wl.num_simulations / dt1
-    # all threads: every tree of the sample, one tree at a time per thread (trees independent)
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1, T)
-    t0 = time.perf_counter()
-    orc.search(wl.num_simulations, wl.wave_size, wl.max_depth, nthreads=threads)
-    dt = time.perf_counter() - t0
-    cpu = {"value": round(T * wl.num_simulations / dt, 1), "unit": "simulations/s",
-           "cores": threads, "kind": "port",
-           "sample": f"{T} of {wl.num_trees} trees x {wl.num_simulations} simulations of "
-                     f"{wl.name} on {threads} threads, one tree per thread ({dt:.2f} s, C oracle, "
-                     f"gcc -O3); single thread: {single:.1f} sims/s over {t1} tree(s) "
-                     f"({dt1:.2f} s)",
-           "single_thread_value": round(single, 1)}
+    if replay is not None:
+        # evaluator outputs recorded on the GPU, replayed wave by wave (one thread)
+        sizes = [1]
+        done = 0
+        while done < wl.num_simulations:
+            sizes.append(min(wl.wave_size, wl.num_simulations - done))
+            done += sizes[-1]
+        assert len(sizes) == len(replay)
+        t0 = time.perf_counter()
+        for t in range(T):
+            orc.reset_tree(t)
+            for (pol, val), W in zip(replay, sizes):
+                orc.wave(t, W, replay_policy=pol[t], replay_values=val[t])
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(T * wl.num_simulations / dt, 1), "unit": "simulations/s",
+               "cores": 1, "kind": "port",
+               "sample": f"{T} of {wl.num_trees} trees x {wl.num_simulations} simulations of "
+                         f"{wl.name}, tree operations only with the GPU run's evaluator outputs "
+                         f"replayed ({dt:.2f} s, C oracle, gcc -O3, one thread)"}
+    else:
+        # single thread: the first tree(s), about 10 s of work at most
+        t0 = time.perf_counter()
+        t1 = 0
+        while t1 < T and (t1 == 0 or time.perf_counter() - t0 < 10.0):
+            orc.lib.orc_search_tree(orc.f, t1, wl.num_simulations, wl.wave_size, wl.max_depth)
+            t1 += 1
+        dt1 = time.perf_counter() - t0
+        single = t1 * wl.num_simulations / dt1
+        # all threads: every tree of the sample, one tree at a time per thread
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1, T)
+        t0 = time.perf_counter()
+        orc.search(wl.num_simulations, wl.wave_size, wl.max_depth, nthreads=threads)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(T * wl.num_simulations / dt, 1), "unit": "simulations/s",
+               "cores": threads, "kind": "port",
+               "sample": f"{T} of {wl.num_trees} trees x {wl.num_simulations} simulations of "
+                         f"{wl.name} on {threads} threads, one tree per thread ({dt:.2f} s, C "
+                         f"oracle, gcc -O3); single thread: {single:.1f} sims/s over {t1} "
+                         f"tree(s) ({dt1:.2f} s)",
+               "single_thread_value": round(single, 1)}
     ok = True
     mismatch = None
     w_exact = args.w_mode == "ordered"

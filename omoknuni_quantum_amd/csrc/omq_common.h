@@ -134,13 +134,15 @@ __device__ inline float funkey(uint32_t k) {
 // row broadcasts 15,31 accumulate into lane 63; a lane whose DPP source is outside its row,
 // or whose row is masked off, reads its own value (max-neutral).
 __device__ inline uint32_t wave_max_u32(uint32_t x) {
+  // the DPP source of an invalid or masked lane reads 0, the identity of the max, so each
+  // step is one fused v_max_u32_dpp
   int v = (int)x;
-  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x111, 0xF, 0xF, false));
-  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x112, 0xF, 0xF, false));
-  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x114, 0xF, 0xF, false));
-  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x118, 0xF, 0xF, false));
-  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));
-  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, true));
+  v = (int)max((uint32_t)v, (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, true));
   return (uint32_t)__builtin_amdgcn_readlane(v, 63);
 }
 

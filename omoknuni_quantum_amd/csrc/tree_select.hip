@@ -83,6 +83,20 @@ __device__ inline uint32_t wave_max_rows(uint32_t x) {
   return max(max(r0, r1), max(r2, r3));
 }
 
+// Max of a float over the 64 lanes, made uniform: DPP row shifts 1,2,4,8 then row broadcasts
+// of lanes 15 and 31 (a lane whose DPP source is invalid keeps its value), read from lane 63.
+// NaN lanes are ignored unless every lane is NaN.
+__device__ inline float wave_max_bcast(float x) {
+  int v = __float_as_int(x);
+  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x111, 0xF, 0xF, false))));
+  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x112, 0xF, 0xF, false))));
+  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x114, 0xF, 0xF, false))));
+  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x118, 0xF, 0xF, false))));
+  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false))));
+  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false))));
+  return __int_as_float(__builtin_amdgcn_readlane(v, 63));
+}
+
 // Serial chain of row-argmaxes for one group (whole wave).  ch[r] receives, for the r-th
 // member, (child index << 16) | rank among the members that chose the same child, or
 // kNoChild.  Child counts are left in cnt_s[0..k).  Returns the first rank without a child
@@ -90,28 +104,33 @@ __device__ inline uint32_t wave_max_rows(uint32_t x) {
 //
 // Exact score (the reference's fp32 expression):
 //     sc = Q + ((c*P)*s)/d,   Q = W/((float)N + VL),  d = (float)(1+N),  s = sqrt((float)Np)
-// Each lane keeps, per child, qa = W*r' and a = (c*P)*r, with r and r' Newton-refined
-// reciprocals of d and of (float)N + VL (|r*d - 1| <= 2^-24(1+eps)), and each step ranks the
-// children by ap = fma(s, a, qa).  With U = s*(c*P)/d: |qa - Q| <= |Q|*2^-22.4,
-// |ap - (Q + U)| <= U*2^-23 + |Q|*2^-22.4 + |ap|*2^-24 and |sc - (Q + U)| <= U*2^-23 + |sc|*2^-24;
-// since U <= |ap| + |Q| + tiny, |ap - sc| <= (|ap| + QB) * 2^-21 with QB >= max |Q| a running
-// bound.  Let A = max ap and E = (|A| + QB) * 2^-20.5.  The child with ap = A has exact score
-// >= A - E; a child w whose exact score reaches the maximum then has ap_w >= A - 2E
-// (|ap_w| <= |A| + 2E keeps e_w <= E).  So the exact argmax is among the candidates
-// ap >= T = A - (|A| + QB) * 2^-19 (a further factor 2^0.5 of margin).  A single candidate is
-// the exact argmax (A is checked above -1e8, so its exact score is above the -1e9 start
-// value); otherwise the candidates are scored exactly (two correctly rounded divisions each)
-// and compared in scalar registers.  No candidate (NaN or infinite scores) or a negative c*P
-// scores every child exactly.
+// Lane l holds children l, l+64, ... (slot j holds child j*64 + l).  Each lane keeps, per child,
+// qa = W*r' and a = (c*P)*r, with r and r' Newton-refined reciprocals of d and of (float)N + VL
+// (|r*d - 1| <= 2^-24(1+eps)), and each step ranks the children by ap = fma(s, a, qa).  With
+// U = s*(c*P)/d: |qa - Q| <= |Q|*2^-22.4, |ap - (Q + U)| <= U*2^-23 + |Q|*2^-22.4 + |ap|*2^-24
+// and |sc - (Q + U)| <= U*2^-23 + |sc|*2^-24; since U <= |ap| + |Q| + tiny,
+// |ap - sc| <= (|ap| + QB) * 2^-21 with QB >= max |Q|.  Let A = max ap and
+// E = (|A| + QB) * 2^-20.5.  The child with ap = A has exact score >= A - E; a child w whose
+// exact score reaches the maximum then has ap_w >= A - 2E (|ap_w| <= |A| + 2E keeps e_w <= E).
+// So the exact argmax is among the candidates ap >= T = A - (|A| + QB) * 2^-19 (a further
+// factor 2^0.5 of margin).  A single candidate is the exact argmax (A is checked above -1e8,
+// so its exact score is above the -1e9 start value); otherwise the candidates are scored
+// exactly (two correctly rounded divisions each) and compared in scalar registers.  No
+// candidate (NaN or infinite scores) or a negative c*P scores every child exactly.
+//
+// QB is fixed for the whole chain: W does not change during selection and N only grows, so
+// |Q| = |W|/((float)N + VL) of every later state is at most its value at the start (the
+// approximation error of qa, 2^-22.4 relative, is absorbed by the 2^0.5 margin above).
 //
 // An unvisited child i (N == 0) carries qa = (1024 - i) * 2^90 and a = 0: it dominates every
 // visited child, and a lower index dominates a higher one by a factor >= 1 + 2^-10, so the
 // lowest-index unvisited child is the single candidate, as the reference's first-unvisited
 // rule requires.  A padding child (index >= k) carries qa = -inf, a = 0.  Every child's state
 // after its next pick is kept too, so a pick is a register select; the state after the
-// following pick is computed at the start of the next step.  Ranks are counted per child in
-// registers.  The parent's sqrt for ranks r0..r0+63 is computed once per 64 steps (lane l
-// holds rank r0+l); the 64 records of a block are kept one per lane and stored together.
+// following pick is computed at the start of the next step, off the pick's dependency chain.
+// Ranks are counted per child in registers.  The parent's sqrt for ranks r0..r0+63 is computed
+// once per 64 steps (lane l holds rank r0+l); the 64 records of a block are kept one per lane
+// and stored together.
 __device__ inline float refined_rcp(float d) {
   const float r = __builtin_amdgcn_rcpf(d);
   return __builtin_fmaf(r, __builtin_fmaf(-d, r, 1.0f), r);
@@ -129,6 +148,53 @@ __device__ inline bool child_state(float d, float w, float cp, int i, float vlf,
   return vis;
 }
 
+// Exact argmax of the step among the candidate children (all children when `all`), or -1 when
+// no child scores above -1e9: exact scores as order-preserving keys, compared in scalar
+// registers, lowest index on ties; an unvisited child ranks above every visited one, lower
+// index first.
+template <int R>
+__device__ inline int exact_pick(const float* den, const float* wv,
+                                                    const float* cp, uint32_t bits, bool all,
+                                                    int k, float s, float vlf) {
+  const int lane = lane_id();
+  uint32_t kx[R];
+  uint64_t cj[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int i = j * kWave + lane;
+    const bool cand = all ? (i < k) : (((bits >> j) & 1u) != 0);
+    cj[j] = __ballot(cand);
+    kx[j] = 0u;
+    if (cand) {
+      if (den[j] == 1.0f) {
+        kx[j] = 0xFFFF0000u | (uint32_t)(0xFFFF - i);
+      } else {
+        const float qe = wv[j] / ((den[j] - 1.0f) + vlf);
+        float sc = qe + (cp[j] * s) / den[j];
+        sc = sc + 0.0f;  // -0 -> +0, so that equal scores compare equal
+        kx[j] = (sc > -1e9f) ? fkey(sc) : 0u;
+      }
+    }
+  }
+  uint32_t bk = 0u;
+  int bidx = 0x7FFFFFFF;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    uint64_t rest = cj[j];
+    while (rest) {
+      const int l = lowest_lane(rest);
+      rest &= rest - 1;
+      const uint32_t kv = (uint32_t)readlane_i((int)kx[j], l);
+      const int idx = j * kWave + l;
+      if (kv > bk || (kv == bk && kv != 0u && idx < bidx)) {
+        bk = kv;
+        bidx = idx;
+      }
+    }
+  }
+  return bk != 0u ? bidx : -1;
+}
+
 template <int R>
 __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
                          const SelCfg& c, uint32_t* ch, uint16_t* cnt_s) {
@@ -136,13 +202,12 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
   const float vlf = c.vlf;
   const float fvl = (float)c.vli;
   float wv[R], cp[R], den[R], q[R], ar[R], qn[R], arn[R];
-  int cnt[R];
   float qbl = 0.0f;
   bool negcp = false;
 #pragma unroll
   for (int j = 0; j < R; ++j) {
-    const int i = lane * R + j;
-    cnt[j] = 0;
+    const int i = j * kWave + lane;
+    if (i < k) cnt_s[i] = 0;
     if (i < k) {
       const int64_t node = tb + first + 1 + i;  // child of edge first+i is node first+i+1
       const int n = f.N[node];
@@ -152,8 +217,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
       negcp = negcp || !(cp[j] >= 0.0f);
       if (child_state(den[j], wv[j], cp[j], i, vlf, &q[j], &ar[j]))
         qbl = fmaxf(qbl, __builtin_fabsf(q[j]));
-      if (child_state(den[j] + fvl, wv[j], cp[j], i, vlf, &qn[j], &arn[j]))
-        qbl = fmaxf(qbl, __builtin_fabsf(qn[j]));
+      child_state(den[j] + fvl, wv[j], cp[j], i, vlf, &qn[j], &arn[j]);
     } else {
       wv[j] = 0.0f;
       cp[j] = 0.0f;
@@ -162,8 +226,8 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
       ar[j] = arn[j] = 0.0f;
     }
   }
-  // |qa| bound on |Q|: qa = Q*(1 +- 2^-22.4); the margin of T absorbs the difference
-  uint32_t QBb = wave_max_rows(__float_as_uint(qbl));  // bits of QB (non-negative)
+  const uint32_t QBb = wave_max_rows(__float_as_uint(qbl));  // bits of QB (non-negative)
+  const float qbt = __uint_as_float(QBb) * (-1.0f / 524288.0f);
   const bool exact_only = __ballot(negcp) != 0;
   if (Np0 == 0 && c.vli == 0) {
     // N is never negative: Np = 0 at every step, the reference returns no child
@@ -185,12 +249,13 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
         float dw = den[0], ww = wv[0], cw = cp[0];
 #pragma unroll
         for (int j = 1; j < R; ++j) {
-          dw = (j == pjj) ? den[j] : dw;
-          ww = (j == pjj) ? wv[j] : ww;
-          cw = (j == pjj) ? cp[j] : cw;
+          const bool sel = j == pjj;
+          dw = sel ? den[j] : dw;
+          ww = sel ? wv[j] : ww;
+          cw = sel ? cp[j] : cw;
         }
         float qx, ax;
-        const bool vis = child_state(dw + fvl, ww, cw, lane * R + pjj, vlf, &qx, &ax);
+        child_state(dw + fvl, ww, cw, pjj * kWave + lane, vlf, &qx, &ax);
         const bool mine = lane == powner;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
@@ -198,10 +263,6 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
           qn[j] = hit ? qx : qn[j];
           arn[j] = hit ? ax : arn[j];
         }
-        // |qx| enters QB before the state becomes current (one step later at the earliest)
-        const uint32_t qo =
-            (uint32_t)readlane_i(vis ? (int)__float_as_uint(__builtin_fabsf(qx)) : 0, max(powner, 0));
-        QBb = max(QBb, powner < 0 ? 0u : qo);
       }
       const float s = readlane_f(svec, rr);
       float ap[R];
@@ -220,98 +281,83 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
           for (int j = 0; j + w < R; j += 2 * w) t[j] = fmaxf(t[j], t[j + w]);
         lm = t[0];
       }
+#if defined(OMQ_STEP_V4)
+      const uint32_t Ak = wave_max_u32(fkey(lm));
+      const float A = funkey(Ak);
+      const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt;
+      const bool aok = Ak > 0x334143DFu;
+#elif defined(OMQ_STEP_V3)
+      const float A = wave_max_bcast(lm);
+      // T = A - |A| * 2^-19 - QB * 2^-19
+      const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt;
+      // A > -1e8 keeps the exact score of a single candidate above -1e9; as bits: every
+      // non-negative A and every negative A of magnitude below 1e8 lies below bits(-1e8)
+      const bool aok = __float_as_uint(A) < 0xCCBEBC20u;
+#else
       const uint32_t Ak = wave_max_rows(fkey(lm));
       const float A = funkey(Ak);
       // T = A - (|A| + QB) * 2^-19 = A * (1 -+ 2^-19) - QB * 2^-19 (key MSB set: A >= 0)
       const float T = __builtin_fmaf(A, (Ak & 0x80000000u) ? 0.99999809265136719f
-                                                           : 1.0000019073486328f,
-                                     __uint_as_float(QBb) * (-1.0f / 524288.0f));
+                                                           : 1.0000019073486328f, qbt);
+      const bool aok = Ak > 0x334143DFu;
+#endif
       uint32_t bits = 0;
 #pragma unroll
       for (int j = 0; j < R; ++j) bits |= (ap[j] >= T) ? (1u << j) : 0u;
       const uint64_t cm = __ballot(bits != 0);
-      const uint64_t mm = (R > 1) ? __ballot((bits & (bits - 1)) != 0) : 0ull;
-      int win = -1;
       // A > -1e8 (key 0x334143DF) keeps the exact score of a single candidate above -1e9
-      if (!exact_only && cm != 0 && (cm & (cm - 1)) == 0 && mm == 0 && Ak > 0x334143DFu) {
+      bool single = !exact_only && __popcll(cm) == 1 && aok;
+      if (R > 1) single = single && __ballot((bits & (bits - 1)) != 0) == 0ull;
+      int win;
+      if (single) {
         const int l = lowest_lane(cm);
-        win = (R == 1) ? l : l * R + (__ffs((unsigned)readlane_i((int)bits, l)) - 1);
+        win = (R == 1) ? l : (__ffs((unsigned)readlane_i((int)bits, l)) - 1) * kWave + l;
       } else {
-        // exact scores of the candidates (every child if there is none or c*P < 0), compared
-        // as order-preserving keys in scalar registers, lowest index on ties; an unvisited
-        // child ranks above every visited one, lower index first
-        const bool all = exact_only || cm == 0;
-        uint32_t kx[R];
-        uint64_t cj[R];
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-          const int i = lane * R + j;
-          const bool cand = all ? (i < k) : (((bits >> j) & 1u) != 0);
-          cj[j] = __ballot(cand);
-          kx[j] = 0u;
-          if (cand) {
-            if (den[j] == 1.0f) {
-              kx[j] = 0xFFFF0000u | (uint32_t)(0xFFFF - i);
-            } else {
-              const float qe = wv[j] / ((den[j] - 1.0f) + vlf);
-              float sc = qe + (cp[j] * s) / den[j];
-              sc = sc + 0.0f;  // -0 -> +0, so that equal scores compare equal
-              kx[j] = (sc > -1e9f) ? fkey(sc) : 0u;
-            }
-          }
-        }
-        uint32_t bk = 0u;
-        int bidx = 0x7FFFFFFF;
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-          uint64_t rest = cj[j];
-          while (rest) {
-            const int l = lowest_lane(rest);
-            rest &= rest - 1;
-            const uint32_t kv = (uint32_t)readlane_i((int)kx[j], l);
-            const int idx = l * R + j;
-            if (kv > bk || (kv == bk && kv != 0u && idx < bidx)) {
-              bk = kv;
-              bidx = idx;
-            }
-          }
-        }
-        if (bk != 0u) win = bidx;
+        win = exact_pick<R>(den, wv, cp, bits, exact_only || cm == 0, k, s, vlf);
+        win = __builtin_amdgcn_readfirstlane(win);
+        if (win < 0 && first_end < 0) first_end = r0 + rr;
       }
-      win = __builtin_amdgcn_readfirstlane(win);
-      uint32_t rv = kNoChild;
       if (win >= 0) {
-        const int owner = win / R;
-        const int jj = win - owner * R;
+        const int owner = win & (kWave - 1);
+        const int jj = win / kWave;
         const bool mine = lane == owner;
-        int cw = cnt[0];
-#pragma unroll
-        for (int j = 1; j < R; ++j) cw = (j == jj) ? cnt[j] : cw;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
           const bool hit = mine && j == jj;
           q[j] = hit ? qn[j] : q[j];
           ar[j] = hit ? arn[j] : ar[j];
           den[j] = hit ? den[j] + fvl : den[j];
-          cnt[j] += hit ? 1 : 0;
         }
-        rv = ((uint32_t)win << 16) | (uint32_t)readlane_i(cw, owner);
-        powner = __builtin_amdgcn_readfirstlane(owner);
-        pjj = __builtin_amdgcn_readfirstlane(jj);
+        powner = owner;
+        pjj = jj;
       } else {
         powner = -1;
-        if (first_end < 0) first_end = r0 + rr;
       }
-      rec = (lane == rr) ? rv : rec;
+      rec = (lane == rr) ? (uint32_t)win : rec;
     }
-    if (lane < rend) ch[r0 + lane] = rec;
+    // ranks of the block's picks: count of the child before the block (cnt_s) plus the number
+    // of earlier picks of the same child within the block
+    const bool valid = lane < rend && rec != kNoChild;
+    const uint32_t key = valid ? rec : 0u;
+    const uint32_t base = valid ? (uint32_t)cnt_s[key] : 0u;
+    uint64_t pend = __ballot(valid);
+    uint32_t inb = 0;
+    bool last = false;
+    while (pend) {
+      const uint32_t kk = (uint32_t)readlane_i((int)key, lowest_lane(pend));
+      const bool eq = valid && key == kk;
+      const uint64_t same = __ballot(eq);
+      if (eq) {
+        inb = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+        last = (same >> lane) == 1ull;
+      }
+      pend &= ~same;
+    }
+    if (valid && last) cnt_s[key] = (uint16_t)(base + inb + 1);
+    if (lane < rend) ch[r0 + lane] = valid ? ((key << 16) | (base + inb)) : kNoChild;
+    wave_sync();
   }
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    const int i = lane * R + j;
-    if (i < k) cnt_s[i] = (uint16_t)cnt[j];
-  }
-  wave_sync();
   return first_end;
 }
 

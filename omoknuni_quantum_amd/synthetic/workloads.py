@@ -37,6 +37,7 @@ class Workload:
     max_depth: int = 100
     expand_policy: str = "full"  # "full" | "reference_pw"
     seed: int = 20260101
+    evaluator: str = "synthetic"  # "synthetic" | "resnet"
 
     def scaled(self, **kw) -> "Workload":
         return replace(self, **kw)
@@ -69,7 +70,8 @@ WORKLOADS = {
     "C3": Workload("C3", games.go(19), 32, 10_000, 1024, 2_000_000, max_stones=112,
                    logit_scale=2.0, dirichlet_alpha=0.03, dirichlet_epsilon=0.25),
     "C4": Workload("C4", games.chess_sparse(4672, 20, 45), 16, 20_000, 2048, 1_000_000),
-    "C5": Workload("C5", games.gomoku(15), 32, 1600, 16, 400_000, max_stones=60),
+    "C5": Workload("C5", games.gomoku(15), 32, 1600, 16, 400_000, max_stones=60,
+                   evaluator="resnet"),
 }
 
 

@@ -1,0 +1,53 @@
+"""Workload C5: the tree operations driven by the bf16 ResNet evaluator, with the evaluator's
+outputs replayed into the oracle (bit-exact trees)."""
+import numpy as np
+import pytest
+import torch
+
+from omoknuni_quantum_amd.core.engine import SearchParams, WaveEngine
+from omoknuni_quantum_amd.synthetic.resnet_evaluator import ResNetEvaluator
+from omoknuni_quantum_amd.synthetic.workloads import get
+from oracle.oracle import Oracle
+
+
+@pytest.mark.gpu
+def test_c5_resnet_replay_parity(device):
+    wl = get("C5").scaled(num_trees=4, num_simulations=96, capacity=50_000)
+    params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth)
+    eng = WaveEngine(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth, device,
+                     params)
+    keys, legal, noise = wl.root_inputs()
+    eng.set_roots(keys, legal, noise)
+    boards = torch.from_numpy(wl.boards()).to(device)
+    ev = ResNetEvaluator(eng, boards, num_blocks=2, channels=32, record=True)
+    eng.search(wl.num_simulations, wl.wave_size, ev)
+    torch.cuda.synchronize()
+    sizes = [1] + [wl.wave_size] * (wl.num_simulations // wl.wave_size)
+    assert len(ev.calls) == len(sizes)
+    pol0 = ev.calls[1][0]
+    assert np.allclose(pol0.sum(axis=2), 1.0, atol=1e-3)  # probabilities over all 225 slots
+    orc = Oracle(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth)
+    orc.set_params(wl.c_puct, wl.virtual_loss, 0, 0, 1.0, 0.0)
+    orc.set_roots(keys, legal, noise)
+    for t in range(wl.num_trees):
+        orc.reset_tree(t)
+        for (pol, val), W in zip(ev.calls, sizes):
+            orc.wave(t, W, replay_policy=pol[t], replay_values=val[t])
+        g, o = eng.host_tree(t), orc.tree(t)
+        assert g["num_nodes"] == o["num_nodes"]
+        for k in ("N", "parent", "first", "nchild", "action"):
+            assert np.array_equal(g[k], o[k]), (t, k)
+        for k in ("W", "P"):
+            assert np.array_equal(g[k].view(np.int32), o[k].view(np.int32)), (t, k)
+
+
+def test_resnet_architecture_shapes():
+    from omoknuni_quantum_amd.synthetic.resnet_evaluator import AlphaZeroResNet
+
+    net = AlphaZeroResNet(15, 225, num_blocks=10, channels=128).eval()
+    n_params = sum(p.numel() for p in net.parameters())
+    assert 3_100_000 < n_params < 3_300_000  # 20 convs of 3x3x128x128 (2.95 M) + heads
+    with torch.no_grad():
+        lp, v = net(torch.zeros(2, 18, 15, 15))
+    assert lp.shape == (2, 225) and v.shape == (2,)
+    assert torch.allclose(lp.exp().sum(1), torch.ones(2), atol=1e-5)
