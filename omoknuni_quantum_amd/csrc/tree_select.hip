@@ -83,19 +83,17 @@ __device__ inline uint32_t wave_max_rows(uint32_t x) {
   return max(max(r0, r1), max(r2, r3));
 }
 
-// Max of a float over the 64 lanes, made uniform: DPP row shifts 1,2,4,8 then row broadcasts
-// of lanes 15 and 31 (a lane whose DPP source is invalid keeps its value), read from lane 63.
-// NaN lanes are ignored unless every lane is NaN.
-__device__ inline float wave_max_bcast(float x) {
-  int v = __float_as_int(x);
-  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x111, 0xF, 0xF, false))));
-  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x112, 0xF, 0xF, false))));
-  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x114, 0xF, 0xF, false))));
-  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x118, 0xF, 0xF, false))));
-  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false))));
-  v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false))));
-  return __int_as_float(__builtin_amdgcn_readlane(v, 63));
-}
+// One step of a wave max over order-preserving keys: the DPP source of an out-of-row or
+// masked lane reads 0, the identity of the max, so each step is one fused v_max_u32_dpp.
+#define OMQ_DPP_MAX(v, ctrl, rmask)                                                        \
+  v = (int)max((uint32_t)(v),                                                             \
+               (uint32_t)__builtin_amdgcn_update_dpp(0, (v), (ctrl), (rmask), 0xF, true))
+// Keeps the instruction scheduler from moving instructions across this point (used to
+// interleave two independent dependency chains by hand).
+#define OMQ_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+// Materialises a value at this point (an empty asm that reads and rewrites the register), so
+// that the compiler cannot sink its computation towards its later use.
+#define OMQ_PIN(x) asm volatile("" : "+v"(x))
 
 // Serial chain of row-argmaxes for one group (whole wave).  ch[r] receives, for the r-th
 // member, (child index << 16) | rank among the members that chose the same child, or
@@ -113,24 +111,35 @@ __device__ inline float wave_max_bcast(float x) {
 // E = (|A| + QB) * 2^-20.5.  The child with ap = A has exact score >= A - E; a child w whose
 // exact score reaches the maximum then has ap_w >= A - 2E (|ap_w| <= |A| + 2E keeps e_w <= E).
 // So the exact argmax is among the candidates ap >= T = A - (|A| + QB) * 2^-19 (a further
-// factor 2^0.5 of margin).  A single candidate is the exact argmax (A is checked above -1e8,
-// so its exact score is above the -1e9 start value); otherwise the candidates are scored
-// exactly (two correctly rounded divisions each) and compared in scalar registers.  No
-// candidate (NaN or infinite scores) or a negative c*P scores every child exactly.
+// factor 2^0.5 of margin).  A single candidate is the exact argmax; otherwise the candidates
+// are scored exactly (two correctly rounded divisions each) and compared in scalar registers.
+// No candidate (NaN or infinite scores), a negative c*P or QB >= 1e8 scores every child
+// exactly.
 //
 // QB is fixed for the whole chain: W does not change during selection and N only grows, so
 // |Q| = |W|/((float)N + VL) of every later state is at most its value at the start (the
-// approximation error of qa, 2^-22.4 relative, is absorbed by the 2^0.5 margin above).
+// approximation error of qa, 2^-22.4 relative, is absorbed by the 2^0.5 margin above).  With
+// QB < 1e8, c*P >= 0 and s >= 0 every real child has ap >= -QB > -1e8, so the exact score of a
+// single candidate is above the reference's -1e9 start value.
 //
 // An unvisited child i (N == 0) carries qa = (1024 - i) * 2^90 and a = 0: it dominates every
 // visited child, and a lower index dominates a higher one by a factor >= 1 + 2^-10, so the
 // lowest-index unvisited child is the single candidate, as the reference's first-unvisited
 // rule requires.  A padding child (index >= k) carries qa = -inf, a = 0.  Every child's state
 // after its next pick is kept too, so a pick is a register select; the state after the
-// following pick is computed at the start of the next step, off the pick's dependency chain.
-// Ranks are counted per child in registers.  The parent's sqrt for ranks r0..r0+63 is computed
-// once per 64 steps (lane l holds rank r0+l); the 64 records of a block are kept one per lane
-// and stored together.
+// following pick is computed during the next step's wave max, off the pick's dependency chain.
+// The parent's sqrt for ranks r0..r0+63 is computed once per 64 steps (lane l holds rank
+// r0+l); the 64 picks of a block are kept one per lane, and their ranks are counted after the
+// block.
+//
+// Rows of more than 64 children run most steps on a window of at most 64 contenders, one per
+// lane: the children with the largest ap at the window's first step.  A non-contender keeps its
+// state during the window and its ap only grows with s, so fma(s_end, a, qa) at the last rank
+// of the block bounds it for the whole window; a step whose threshold T exceeds that bound has
+// the same candidates (and maximum) over the contenders as over the whole row, so the window
+// takes the step.  The first step where T does not exceed the bound ends the window before it
+// is taken.  Contenders keep their index order in the lanes, so lowest-lane ties remain
+// lowest-index ties.
 __device__ inline float refined_rcp(float d) {
   const float r = __builtin_amdgcn_rcpf(d);
   return __builtin_fmaf(r, __builtin_fmaf(-d, r, 1.0f), r);
@@ -151,11 +160,10 @@ __device__ inline bool child_state(float d, float w, float cp, int i, float vlf,
 // Exact argmax of the step among the candidate children (all children when `all`), or -1 when
 // no child scores above -1e9: exact scores as order-preserving keys, compared in scalar
 // registers, lowest index on ties; an unvisited child ranks above every visited one, lower
-// index first.
+// index first.  Lane l, slot j holds the child of order j*64 + l.
 template <int R>
-__device__ inline int exact_pick(const float* den, const float* wv,
-                                                    const float* cp, uint32_t bits, bool all,
-                                                    int k, float s, float vlf) {
+__device__ inline int exact_pick(const float* den, const float* wv, const float* cp,
+                                 uint32_t bits, bool all, int k, float s, float vlf) {
   const int lane = lane_id();
   uint32_t kx[R];
   uint64_t cj[R];
@@ -195,145 +203,422 @@ __device__ inline int exact_pick(const float* den, const float* wv,
   return bk != 0u ? bidx : -1;
 }
 
+// Selection state of the children held by a lane (R slots).
+template <int R>
+struct Row {
+  float q[R], ar[R];    // current approximate state (qa, a)
+  float qn[R], arn[R];  // state after the next pick
+  float den[R];         // (float)(1 + N) including this chain's picks
+  float wv[R], cp[R];   // W and c_puct * P
+  bool pb[R];           // the previous step's pick, whose next state is still pending
+};
+
+// Computes the pending next state of the previous pick now (leaves no pick pending).
+template <int R>
+__device__ inline void settle_pending(Row<R>& x, float fvl, float vlf) {
+  float dw = x.den[0], ww = x.wv[0], cw = x.cp[0];
+#pragma unroll
+  for (int j = 1; j < R; ++j) {
+    dw = x.pb[j] ? x.den[j] : dw;
+    ww = x.pb[j] ? x.wv[j] : ww;
+    cw = x.pb[j] ? x.cp[j] : cw;
+  }
+  const float d2 = dw + fvl;
+  const float qx = ww * refined_rcp((d2 - 1.0f) + vlf);
+  const float ax = cw * refined_rcp(d2);
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    x.qn[j] = x.pb[j] ? qx : x.qn[j];
+    x.arn[j] = x.pb[j] ? ax : x.arn[j];
+    x.pb[j] = false;
+  }
+}
+
+// One step over the row held in x.  Returns the pick as j*64 + lane, -1 when no child can be
+// picked, or -2 (window mode only) when the step must be taken over the whole row: the
+// threshold does not exceed `ubnc` or there is no candidate.  Nothing is changed on -2.
+// `idx` is the row index of the child in slot 0 (for the unvisited marker).
+template <int R>
+__device__ inline int select_step(Row<R>& x, float s, float fvl, float vlf, float qbt_eff,
+                                  bool exact_only, int k, int idx0, bool window, float ubnc) {
+  const int lane = lane_id();
+  float ap[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) ap[j] = __builtin_fmaf(s, x.ar[j], x.q[j]);
+  float lm;
+  if (R == 1) {
+    lm = ap[0];
+  } else {
+    float t[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) t[j] = ap[j];
+#pragma unroll
+    for (int w = 1; w < R; w <<= 1)
+#pragma unroll
+      for (int j = 0; j + w < R; j += 2 * w) t[j] = fmaxf(t[j], t[j + w]);
+    lm = t[0];
+  }
+  // The wave max of the keys (6 dependent DPP steps) is interleaved with the state after
+  // the next pick of the previous step's child, which is independent of it (each
+  // independent instruction takes the place of a DPP hazard wait).
+  int v = (int)fkey(lm);
+  float dw = x.den[0], ww = x.wv[0], cw = x.cp[0];
+#pragma unroll
+  for (int j = 1; j < R; ++j) {
+    dw = x.pb[j] ? x.den[j] : dw;
+    ww = x.pb[j] ? x.wv[j] : ww;
+    cw = x.pb[j] ? x.cp[j] : cw;
+  }
+  float d2 = dw + fvl;
+  float e2 = (d2 - 1.0f) + vlf;
+  OMQ_PIN(d2);
+  OMQ_PIN(e2);
+  OMQ_SCHED_FENCE();
+  OMQ_DPP_MAX(v, 0x111, 0xF);  // row_shr:1
+  float r1 = __builtin_amdgcn_rcpf(e2);
+  float r2 = __builtin_amdgcn_rcpf(d2);
+  OMQ_PIN(r1);
+  OMQ_PIN(r2);
+  OMQ_SCHED_FENCE();
+  OMQ_DPP_MAX(v, 0x112, 0xF);  // row_shr:2
+  float t1 = __builtin_fmaf(-e2, r1, 1.0f);
+  float t2 = __builtin_fmaf(-d2, r2, 1.0f);
+  OMQ_PIN(t1);
+  OMQ_PIN(t2);
+  OMQ_SCHED_FENCE();
+  OMQ_DPP_MAX(v, 0x114, 0xF);  // row_shr:4
+  r1 = __builtin_fmaf(r1, t1, r1);
+  r2 = __builtin_fmaf(r2, t2, r2);
+  OMQ_PIN(r1);
+  OMQ_PIN(r2);
+  OMQ_SCHED_FENCE();
+  OMQ_DPP_MAX(v, 0x118, 0xF);  // row_shr:8
+  // a picked child is visited afterwards (virtual loss >= 1 here)
+  float qx = ww * r1;
+  float ax = cw * r2;
+  OMQ_PIN(qx);
+  OMQ_PIN(ax);
+  OMQ_SCHED_FENCE();
+  OMQ_DPP_MAX(v, 0x142, 0xA);  // row_bcast:15
+  float qnv[R], arnv[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    qnv[j] = x.pb[j] ? qx : x.qn[j];
+    arnv[j] = x.pb[j] ? ax : x.arn[j];
+    OMQ_PIN(qnv[j]);
+    OMQ_PIN(arnv[j]);
+  }
+  OMQ_SCHED_FENCE();
+  OMQ_DPP_MAX(v, 0x143, 0xC);  // row_bcast:31
+  const uint32_t Ak = (uint32_t)__builtin_amdgcn_readlane(v, 63);
+  const float A = funkey(Ak);
+  // T = A - (|A| + QB) * 2^-19
+  const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt_eff;
+  bool b[R];
+  uint64_t cm = 0;
+  int tot = 0;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    b[j] = ap[j] >= T;
+    const uint64_t mj = __ballot(b[j]);
+    cm |= mj;
+    tot += __popcll(mj);
+  }
+  if (window && (tot == 0 || !(T > ubnc))) return -2;
+  // the pending state is final now
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    x.qn[j] = qnv[j];
+    x.arn[j] = arnv[j];
+  }
+  // The candidates' next states are taken as if the single candidate were the pick; the
+  // exact comparison below undoes this when there is not exactly one candidate.
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    x.q[j] = b[j] ? x.qn[j] : x.q[j];
+    x.ar[j] = b[j] ? x.arn[j] : x.ar[j];
+    x.den[j] = b[j] ? x.den[j] + fvl : x.den[j];
+    x.pb[j] = b[j];
+  }
+  int win;
+  if (__builtin_expect(tot == 1, 1)) {
+    const int l = lowest_lane(cm);
+    if (R == 1) {
+      win = l;
+    } else {
+      int jv = 0;
+#pragma unroll
+      for (int j = 1; j < R; ++j) jv = b[j] ? j : jv;
+      win = readlane_i(jv, l) * kWave + l;
+    }
+  } else {
+    uint32_t bits = 0;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      bits |= b[j] ? (1u << j) : 0u;
+      // restore the candidates' states (the step's candidates were advanced above)
+      const float dr = b[j] ? x.den[j] - fvl : x.den[j];
+      float qr, ar0;
+      child_state(dr, x.wv[j], x.cp[j], idx0 + j * kWave, vlf, &qr, &ar0);
+      x.q[j] = b[j] ? qr : x.q[j];
+      x.ar[j] = b[j] ? ar0 : x.ar[j];
+      x.den[j] = dr;
+    }
+    win = exact_pick<R>(x.den, x.wv, x.cp, bits, exact_only || tot == 0, k, s, vlf);
+    win = __builtin_amdgcn_readfirstlane(win);
+    const bool mine = win >= 0 && lane == (win & (kWave - 1));
+    const int jj = win >> 6;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const bool hit = mine && j == jj;
+      x.q[j] = hit ? x.qn[j] : x.q[j];
+      x.ar[j] = hit ? x.arn[j] : x.ar[j];
+      x.den[j] = hit ? x.den[j] + fvl : x.den[j];
+      x.pb[j] = hit;
+    }
+  }
+  return win;
+}
+
+// State of a row of more than 64 children held R slots per lane, for steps over the whole row
+// (the steps between contender windows): no next states are kept, a pick recomputes the
+// picked child's state.
+template <int R>
+struct WideRow {
+  float q[R], ar[R], den[R], wv[R], cp[R];
+};
+
+// One step over the whole row (see select_step); returns j*64 + lane of the pick or -1.
+template <int R>
+__device__ inline int wide_step(WideRow<R>& x, float s, float fvl, float vlf, float qbt_eff,
+                                bool exact_only, int k) {
+  const int lane = lane_id();
+  float ap[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) ap[j] = __builtin_fmaf(s, x.ar[j], x.q[j]);
+  float t[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) t[j] = ap[j];
+#pragma unroll
+  for (int w = 1; w < R; w <<= 1)
+#pragma unroll
+    for (int j = 0; j + w < R; j += 2 * w) t[j] = fmaxf(t[j], t[j + w]);
+  const float A = funkey(wave_max_u32(fkey(t[0])));
+  const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt_eff;
+  uint32_t bits = 0;
+  uint64_t cm = 0;
+  int tot = 0;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const bool bj = ap[j] >= T;
+    const uint64_t mj = __ballot(bj);
+    bits |= bj ? (1u << j) : 0u;
+    cm |= mj;
+    tot += __popcll(mj);
+  }
+  int win;
+  if (tot == 1) {
+    const int l = lowest_lane(cm);
+    win = (__ffs((unsigned)readlane_i((int)bits, l)) - 1) * kWave + l;
+  } else {
+    win = exact_pick<R>(x.den, x.wv, x.cp, bits, exact_only || tot == 0, k, s, vlf);
+    win = __builtin_amdgcn_readfirstlane(win);
+  }
+  if (win >= 0) {
+    const bool mine = lane == (win & (kWave - 1));
+    const int jj = win >> 6;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      if (j == jj) {
+        const float d = mine ? x.den[j] + fvl : x.den[j];
+        float qv, av;
+        child_state(d, x.wv[j], x.cp[j], j * kWave + lane, vlf, &qv, &av);
+        x.den[j] = d;
+        x.q[j] = mine ? qv : x.q[j];
+        x.ar[j] = mine ? av : x.ar[j];
+      }
+    }
+  }
+  return win;
+}
+
+// Wave max of a float as order-preserving keys (made uniform).
+__device__ inline float wave_max_key(float x) { return funkey(wave_max_u32(fkey(x))); }
+
+// Smallest key threshold t with at most 64 of the row's keys >= t (bisection on the keys).
+template <int R>
+__device__ inline uint32_t top64_threshold(const uint32_t* key) {
+  uint64_t lo = 0, hi = 1ull << 32;  // count(>= lo) > 64 >= count(>= hi)
+  for (int it = 0; it < 32; ++it) {
+    const uint64_t mid = (lo + hi) >> 1;
+    const uint32_t mt = (uint32_t)mid;
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < R; ++j) cnt += __popcll(__ballot(key[j] >= mt));
+    if (cnt <= kWave) hi = mid; else lo = mid;
+  }
+  return (uint32_t)hi;
+}
+
 template <int R>
 __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
-                         const SelCfg& c, uint32_t* ch, uint16_t* cnt_s) {
+                         const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr) {
   const int lane = lane_id();
   const float vlf = c.vlf;
   const float fvl = (float)c.vli;
-  float wv[R], cp[R], den[R], q[R], ar[R], qn[R], arn[R];
+  // R == 1 keeps next states (Row<1>); wider rows keep the wide state between windows
+  Row<1> y;
+  WideRow<R> x;
   float qbl = 0.0f;
   bool negcp = false;
 #pragma unroll
   for (int j = 0; j < R; ++j) {
     const int i = j * kWave + lane;
     if (i < k) cnt_s[i] = 0;
+    float d = 2.0f, w = 0.0f, cpv = 0.0f, qv = -__builtin_inff(), av = 0.0f;
     if (i < k) {
       const int64_t node = tb + first + 1 + i;  // child of edge first+i is node first+i+1
       const int n = f.N[node];
-      wv[j] = f.W[node];
-      cp[j] = c.c_puct * f.P[node];
-      den[j] = (float)(1 + n);
-      negcp = negcp || !(cp[j] >= 0.0f);
-      if (child_state(den[j], wv[j], cp[j], i, vlf, &q[j], &ar[j]))
-        qbl = fmaxf(qbl, __builtin_fabsf(q[j]));
-      child_state(den[j] + fvl, wv[j], cp[j], i, vlf, &qn[j], &arn[j]);
-    } else {
-      wv[j] = 0.0f;
-      cp[j] = 0.0f;
-      den[j] = 2.0f;
-      q[j] = qn[j] = -__builtin_inff();
-      ar[j] = arn[j] = 0.0f;
+      w = f.W[node];
+      cpv = c.c_puct * f.P[node];
+      d = (float)(1 + n);
+      negcp = negcp || !(cpv >= 0.0f);
+      if (child_state(d, w, cpv, i, vlf, &qv, &av)) qbl = fmaxf(qbl, __builtin_fabsf(qv));
     }
+    x.den[j] = d;
+    x.wv[j] = w;
+    x.cp[j] = cpv;
+    x.q[j] = qv;
+    x.ar[j] = av;
   }
   const uint32_t QBb = wave_max_rows(__float_as_uint(qbl));  // bits of QB (non-negative)
   const float qbt = __uint_as_float(QBb) * (-1.0f / 524288.0f);
-  const bool exact_only = __ballot(negcp) != 0;
-  if (Np0 == 0 && c.vli == 0) {
-    // N is never negative: Np = 0 at every step, the reference returns no child
-    for (int r = lane; r < m; r += kWave) ch[r] = kNoChild;
-    for (int i = lane; i < k; i += kWave) cnt_s[i] = 0;
+  const bool exact_only = __ballot(negcp) != 0 || !(__uint_as_float(QBb) < 1e8f);
+  if (c.vli == 0) {
+    // Without an integer virtual loss a pick changes no visit count: every rank sees the same
+    // row and the same parent count, so every rank takes the first rank's choice.
+    int win = -1;
+    if (Np0 != 0) {  // Np = 0: sqrt(0) exploration, the reference returns no child
+      win = exact_pick<R>(x.den, x.wv, x.cp, 0u, true, k, sqrtf((float)Np0), vlf);
+      win = __builtin_amdgcn_readfirstlane(win);
+    }
+    for (int r = lane; r < m; r += kWave)
+      ch[r] = win >= 0 ? (((uint32_t)win << 16) | (uint32_t)r) : kNoChild;
+    if (lane == 0 && win >= 0) cnt_s[win] = (uint16_t)m;
     wave_sync();
-    return m > 0 ? 0 : -1;
+    return (win < 0 && m > 0) ? 0 : -1;
+  }
+  if (R == 1) {
+    y.den[0] = x.den[0];
+    y.wv[0] = x.wv[0];
+    y.cp[0] = x.cp[0];
+    y.q[0] = x.q[0];
+    y.ar[0] = x.ar[0];
+    y.pb[0] = false;
+    if (lane < k) {
+      child_state(y.den[0] + fvl, y.wv[0], y.cp[0], lane, vlf, &y.qn[0], &y.arn[0]);
+    } else {
+      y.qn[0] = -__builtin_inff();
+      y.arn[0] = 0.0f;
+    }
   }
   int first_end = -1;
-  int powner = -1, pjj = 0;  // the previous step's pick, whose next state is pending
+  // a NaN threshold sends every step to the exact comparison
+  const float qbt_eff = exact_only ? __builtin_nanf("") : qbt;
   for (int r0 = 0; r0 < m; r0 += kWave) {
     const int Npl = Np0 + c.vli * (r0 + lane + 1);
     const float svec = sqrtf((float)Npl);
-    const int rend = min(kWave, m - r0);
+    const int rend = __builtin_amdgcn_readfirstlane(min(kWave, m - r0));
     uint32_t rec = kNoChild;
-    for (int rr = 0; rr < rend; ++rr) {
-      // state after the next pick of the child picked in the previous step
-      {
-        float dw = den[0], ww = wv[0], cw = cp[0];
-#pragma unroll
-        for (int j = 1; j < R; ++j) {
-          const bool sel = j == pjj;
-          dw = sel ? den[j] : dw;
-          ww = sel ? wv[j] : ww;
-          cw = sel ? cp[j] : cw;
-        }
-        float qx, ax;
-        child_state(dw + fvl, ww, cw, pjj * kWave + lane, vlf, &qx, &ax);
-        const bool mine = lane == powner;
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-          const bool hit = mine && j == pjj;
-          qn[j] = hit ? qx : qn[j];
-          arn[j] = hit ? ax : arn[j];
-        }
-      }
-      const float s = readlane_f(svec, rr);
-      float ap[R];
-#pragma unroll
-      for (int j = 0; j < R; ++j) ap[j] = __builtin_fmaf(s, ar[j], q[j]);
-      float lm;
-      if (R == 1) {
-        lm = ap[0];
-      } else {
-        float t[R];
-#pragma unroll
-        for (int j = 0; j < R; ++j) t[j] = ap[j];
-#pragma unroll
-        for (int w = 1; w < R; w <<= 1)
-#pragma unroll
-          for (int j = 0; j + w < R; j += 2 * w) t[j] = fmaxf(t[j], t[j + w]);
-        lm = t[0];
-      }
-#if defined(OMQ_STEP_V4)
-      const uint32_t Ak = wave_max_u32(fkey(lm));
-      const float A = funkey(Ak);
-      const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt;
-      const bool aok = Ak > 0x334143DFu;
-#elif defined(OMQ_STEP_V3)
-      const float A = wave_max_bcast(lm);
-      // T = A - |A| * 2^-19 - QB * 2^-19
-      const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt;
-      // A > -1e8 keeps the exact score of a single candidate above -1e9; as bits: every
-      // non-negative A and every negative A of magnitude below 1e8 lies below bits(-1e8)
-      const bool aok = __float_as_uint(A) < 0xCCBEBC20u;
-#else
-      const uint32_t Ak = wave_max_rows(fkey(lm));
-      const float A = funkey(Ak);
-      // T = A - (|A| + QB) * 2^-19 = A * (1 -+ 2^-19) - QB * 2^-19 (key MSB set: A >= 0)
-      const float T = __builtin_fmaf(A, (Ak & 0x80000000u) ? 0.99999809265136719f
-                                                           : 1.0000019073486328f, qbt);
-      const bool aok = Ak > 0x334143DFu;
-#endif
-      uint32_t bits = 0;
-#pragma unroll
-      for (int j = 0; j < R; ++j) bits |= (ap[j] >= T) ? (1u << j) : 0u;
-      const uint64_t cm = __ballot(bits != 0);
-      // A > -1e8 (key 0x334143DF) keeps the exact score of a single candidate above -1e9
-      bool single = !exact_only && __popcll(cm) == 1 && aok;
-      if (R > 1) single = single && __ballot((bits & (bits - 1)) != 0) == 0ull;
-      int win;
-      if (single) {
-        const int l = lowest_lane(cm);
-        win = (R == 1) ? l : (__ffs((unsigned)readlane_i((int)bits, l)) - 1) * kWave + l;
-      } else {
-        win = exact_pick<R>(den, wv, cp, bits, exact_only || cm == 0, k, s, vlf);
-        win = __builtin_amdgcn_readfirstlane(win);
+    if (R == 1) {
+#pragma unroll 2
+      for (int rr = 0; rr < rend; ++rr) {
+        const float s = readlane_f(svec, rr);
+        const int win = select_step<1>(y, s, fvl, vlf, qbt_eff, exact_only, k, lane, false, 0.0f);
         if (win < 0 && first_end < 0) first_end = r0 + rr;
+        asm volatile("s_mov_b32 m0, %2\n\tv_writelane_b32 %0, %1, m0"
+                     : "+v"(rec) : "s"(win), "s"(rr) : "m0");
       }
-      if (win >= 0) {
-        const int owner = win & (kWave - 1);
-        const int jj = win / kWave;
-        const bool mine = lane == owner;
+    } else {
+      int rr = 0;
+      bool try_window = !exact_only;
+      while (rr < rend) {
+        if (try_window && rend - rr >= 8) {
+          // ---- contender window: the top 64 children by ap at its first rank ----
+          const float s0 = readlane_f(svec, rr);
+          const float s_end = readlane_f(svec, rend - 1);
+          uint32_t key[R];
 #pragma unroll
-        for (int j = 0; j < R; ++j) {
-          const bool hit = mine && j == jj;
-          q[j] = hit ? qn[j] : q[j];
-          ar[j] = hit ? arn[j] : ar[j];
-          den[j] = hit ? den[j] + fvl : den[j];
+          for (int j = 0; j < R; ++j) key[j] = fkey(__builtin_fmaf(s0, x.ar[j], x.q[j]));
+          const uint32_t tau = top64_threshold<R>(key);
+          uint64_t cmask[R];
+          int base = 0;
+          float ub = -__builtin_inff();
+#pragma unroll
+          for (int j = 0; j < R; ++j) {
+            const int i = j * kWave + lane;
+            const bool con = i < k && key[j] >= tau;
+            cmask[j] = __ballot(con);
+            const int dest = base + (int)__builtin_amdgcn_mbcnt_hi(
+                                        (uint32_t)(cmask[j] >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)cmask[j], 0u));
+            if (con) cscr[dest] = make_float4(x.den[j], x.wv[j], x.cp[j], __int_as_float(i));
+            if (i < k && !con) ub = fmaxf(ub, __builtin_fmaf(s_end, x.ar[j], x.q[j]));
+            base += __popcll(cmask[j]);
+          }
+          const float ubnc = wave_max_key(ub);
+          const int ncon = base;
+          wave_sync();
+          const float4 e = lane < ncon ? cscr[lane] : make_float4(2.0f, 0.0f, 0.0f, 0.0f);
+          const int cidx = __float_as_int(e.w);
+          y.den[0] = e.x;
+          y.wv[0] = e.y;
+          y.cp[0] = e.z;
+          y.pb[0] = false;
+          if (lane < ncon) {
+            child_state(y.den[0], y.wv[0], y.cp[0], cidx, vlf, &y.q[0], &y.ar[0]);
+            child_state(y.den[0] + fvl, y.wv[0], y.cp[0], cidx, vlf, &y.qn[0], &y.arn[0]);
+          } else {
+            y.q[0] = y.qn[0] = -__builtin_inff();
+            y.ar[0] = y.arn[0] = 0.0f;
+          }
+          const int rr0 = rr;
+          while (rr < rend) {
+            const float s = readlane_f(svec, rr);
+            const int wl = select_step<1>(y, s, fvl, vlf, qbt_eff, false, ncon, cidx, true, ubnc);
+            if (wl == -2) break;
+            const int win = wl >= 0 ? readlane_i(cidx, wl) : -1;
+            if (win < 0 && first_end < 0) first_end = r0 + rr;
+            rec = (lane == rr) ? (uint32_t)win : rec;
+            ++rr;
+          }
+          // write back the contenders' counts; every state follows from its count
+          wave_sync();
+          if (lane < ncon) cscr[lane].x = y.den[0];
+          wave_sync();
+          base = 0;
+#pragma unroll
+          for (int j = 0; j < R; ++j) {
+            const int i = j * kWave + lane;
+            const bool con = ((cmask[j] >> lane) & 1ull) != 0;
+            const int dest = base + (int)__builtin_amdgcn_mbcnt_hi(
+                                        (uint32_t)(cmask[j] >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)cmask[j], 0u));
+            if (con) x.den[j] = cscr[dest].x;
+            if (i < k) child_state(x.den[j], x.wv[j], x.cp[j], i, vlf, &x.q[j], &x.ar[j]);
+            base += __popcll(cmask[j]);
+          }
+          wave_sync();
+          if (rr - rr0 < 8) try_window = false;  // no more windows in this block
+          continue;
         }
-        powner = owner;
-        pjj = jj;
-      } else {
-        powner = -1;
+        // ---- one step over the whole row ----
+        const float s = readlane_f(svec, rr);
+        const int win = wide_step<R>(x, s, fvl, vlf, qbt_eff, exact_only, k);
+        if (win < 0 && first_end < 0) first_end = r0 + rr;
+        rec = (lane == rr) ? (uint32_t)win : rec;
+        ++rr;
       }
-      rec = (lane == rr) ? (uint32_t)win : rec;
     }
     // ranks of the block's picks: count of the child before the block (cnt_s) plus the number
     // of earlier picks of the same child within the block
@@ -361,18 +646,21 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
   return first_end;
 }
 
+// Chain of a row of k children, instantiated up to RMAX slots per lane (rows of at most
+// 64*RMAX children): a kernel holds only the widths its game model can produce, which keeps
+// its register demand within the 128 VGPRs of a 1024-thread workgroup.
+template <int RMAX>
 __device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0,
-                                     int m, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s) {
-  switch ((k + kWave - 1) / kWave) {  // k <= OMQ_MAX_ROW = 512
-    case 1: return run_chain<1>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-    case 2: return run_chain<2>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-    case 3: return run_chain<3>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-    case 4: return run_chain<4>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-    case 5: return run_chain<5>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-    case 6: return run_chain<6>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-    case 7: return run_chain<7>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-    default: return run_chain<8>(f, tb, first, k, Np0, m, c, ch, cnt_s);
-  }
+                                     int m, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s,
+                                     float4* cscr) {
+  const int r = (k + kWave - 1) / kWave;  // 1 <= r <= RMAX (checked by the caller)
+  if (RMAX <= 1 || r <= 1) return run_chain<1>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
+  if (RMAX >= 2 && r == 2) return run_chain<(RMAX >= 2 ? 2 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
+  if (RMAX >= 3 && r == 3) return run_chain<(RMAX >= 3 ? 3 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
+  if (RMAX >= 4 && r == 4) return run_chain<(RMAX >= 4 ? 4 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
+  if (RMAX >= 5 && r == 5) return run_chain<(RMAX >= 5 ? 5 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
+  if (RMAX >= 6 && r == 6) return run_chain<(RMAX >= 6 ? 6 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
+  return run_chain<(RMAX >= 8 ? 8 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
 }
 
 // Block-wide exclusive scan of a[0..n) in place (n <= 4 * kSelThreads); returns the total.
@@ -404,11 +692,13 @@ __device__ int block_excl_scan(int32_t* a, int n, int* s_wtot) {
   return total;
 }
 
+template <int RMAX>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c) {
   SelArgs& w = f;
   extern __shared__ __align__(16) unsigned char smem[];
   const int W = c.W;
-  uint32_t* choice = reinterpret_cast<uint32_t*>(smem);       // [W]
+  float4* cscr_all = reinterpret_cast<float4*>(smem);         // [kSelWaves * 64] (16-aligned)
+  uint32_t* choice = reinterpret_cast<uint32_t*>(cscr_all + kSelWaves * kWave);  // [W]
   int32_t* lflag = reinterpret_cast<int32_t*>(choice + W);    // [W] leaf-first flags, then scan
   uint32_t* gnode = reinterpret_cast<uint32_t*>(lflag + W);   // [2W] group node per level
   uint32_t* gsl = gnode + 2 * W;                              // [2W] seg | len << 16
@@ -430,6 +720,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   const int64_t gmax = (int64_t)MW * MD;
   int32_t* N = f.N;
   uint16_t* cnt_s = cnt_all + wave * OMQ_MAX_ROW;
+  float4* cscr = cscr_all + wave * kWave;  // contender window scratch of this wave
 
   for (int s = tid; s < W; s += kSelThreads) {
     buf[s] = (uint16_t)s;
@@ -481,7 +772,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       if (lane == 0) atomicAdd(&s_st[OMQ_ST_PATHNODES], 1ull);
 
       bool leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
-      if (!leaf && k > OMQ_MAX_ROW) {
+      if (!leaf && k > RMAX * kWave) {
         if (lane == 0) atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
         leaf = true;
       }
@@ -501,7 +792,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       }
 
       uint32_t* ch = choice + seg;
-      const int fe = dispatch_chain(f, tb, first, k, Np0, m, c, ch, cnt_s);
+      const int fe = dispatch_chain<RMAX>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
       if (lane == 0) {
         atomicAdd(&s_st[OMQ_ST_INTERNAL], 1ull);
         atomicAdd(&s_st[OMQ_ST_ROWSUM], (unsigned long long)k);
@@ -592,7 +883,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
 namespace omq {
 
 size_t select_lds_bytes(int W) {
-  return (size_t)W * (4 + 4 + 8 + 8) + (size_t)W * (4 + 2) +
+  return (size_t)kSelWaves * kWave * 16 + (size_t)W * (4 + 4 + 8 + 8) + (size_t)W * (4 + 2) +
          (size_t)kSelWaves * OMQ_MAX_ROW * 2;
 }
 
@@ -606,13 +897,27 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   c.max_depth = max_depth;
   c.vl_atomic = vl_atomic;
   const size_t lds = select_lds_bytes(W);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)select_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+  // widest row the game model can produce: every legal action (board games) or max_legal
+  const int max_row = f.game == OMQ_GAME_SPARSE ? f.max_legal : f.num_actions;
+  int rmax = (max_row + kWave - 1) / kWave;
+  if (rmax > 6) rmax = 8;
+  const void* kern = nullptr;
+  switch (rmax) {
+    case 0:
+    case 1: kern = (const void*)select_kernel<1>; break;
+    case 2: kern = (const void*)select_kernel<2>; break;
+    case 3: kern = (const void*)select_kernel<3>; break;
+    case 4: kern = (const void*)select_kernel<4>; break;
+    case 5: kern = (const void*)select_kernel<5>; break;
+    case 6: kern = (const void*)select_kernel<6>; break;
+    default: kern = (const void*)select_kernel<8>; break;
+  }
+  static bool attr_set[9] = {};
+  if (!attr_set[rmax]) {
+    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)select_lds_bytes(OMQ_MAX_WAVE));
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_set[rmax] = true;
   }
   SelArgs a;
   a.N = f.visit_counts;
@@ -635,7 +940,9 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   a.capacity = f.capacity;
   a.max_wave = w.max_wave;
   a.max_depth_buf = w.max_depth;
-  hipLaunchKernelGGL(select_kernel, dim3(f.num_trees), dim3(kSelThreads), lds, stream, a, c);
+  void* args[] = {&a, &c};
+  hipError_t e = hipLaunchKernel(kern, dim3(f.num_trees), dim3(kSelThreads), args, lds, stream);
+  if (e != hipSuccess) return e;
   return hipGetLastError();
 }
 
