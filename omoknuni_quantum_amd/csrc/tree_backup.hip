@@ -29,20 +29,29 @@ __global__ void sim_value_kernel(omq_forest f, omq_wave w, int W, int sign_mode)
   w.sim_value[wb + s] = neg ? -v : v;
 }
 
+// Groups are dealt to the lanes of all waves in a strided order (lane l of wave w takes groups
+// w + (l + 64*i) * waves), so the few big groups of a level -- they are logged next to each
+// other -- land in different waves.  A small group is folded by its lane after all of its
+// member values have been fetched (the loads of a lane are issued together); a big group is
+// folded by its wave: the member values are staged in LDS 64 at a time and lane 0 adds them in
+// order from registers.
 __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_forest f, omq_wave w,
                                                                        int vli) {
+  __shared__ __align__(16) float stage[kBackupThreads / kWave][kWave];
   const int t = blockIdx.y;
   const int lane = lane_id();
+  const int wib = threadIdx.x / kWave;
   const int64_t tb = (int64_t)t * f.capacity;
   const int64_t wb = (int64_t)t * w.max_wave;
   const int MW = w.max_wave, MD = w.max_depth;
   const int64_t gmax = (int64_t)MW * MD;
   const int G = w.gcount[t];
   const int waves_total = gridDim.x * (kBackupThreads / kWave);
-  const int wave_global = blockIdx.x * (kBackupThreads / kWave) + threadIdx.x / kWave;
+  const int wave_global = blockIdx.x * (kBackupThreads / kWave) + wib;
   const float* sv = w.sim_value + wb;
-  for (int g0 = wave_global * kWave; g0 < G; g0 += waves_total * kWave) {
-    const int g = g0 + lane;
+  float* st = stage[wib];
+  for (int i0 = 0; wave_global + i0 * waves_total < G; i0 += kWave) {
+    const int g = wave_global + (i0 + lane) * waves_total;
     int p = 0, d = 0, seg = 0, m = 0;
     if (g < G) {
       const int4 rec = *reinterpret_cast<const int4*>(w.glog + ((int64_t)t * gmax + g) * 4);
@@ -51,23 +60,16 @@ __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_fores
       seg = rec.z;
       m = rec.w;
     }
-    const uint16_t* mem = w.gmembers + ((int64_t)t * MD + d) * MW + seg;
     if (g < G && m <= kBigGroup) {
+      const uint16_t* mem = w.gmembers + ((int64_t)t * MD + d) * MW + seg;
+      float vals[kBigGroup];
+#pragma unroll
+      for (int i = 0; i < kBigGroup; ++i) vals[i] = i < m ? sv[mem[i]] : 0.0f;
       float acc = f.value_sums[tb + p];
       const bool odd = d & 1;
-      int i = 0;
-      for (; i + 4 <= m; i += 4) {
-        const float c0 = sv[mem[i]], c1 = sv[mem[i + 1]], c2 = sv[mem[i + 2]],
-                    c3 = sv[mem[i + 3]];
-        acc = acc + (odd ? -c0 : c0);
-        acc = acc + (odd ? -c1 : c1);
-        acc = acc + (odd ? -c2 : c2);
-        acc = acc + (odd ? -c3 : c3);
-      }
-      for (; i < m; ++i) {
-        const float c0 = sv[mem[i]];
-        acc = acc + (odd ? -c0 : c0);
-      }
+#pragma unroll
+      for (int i = 0; i < kBigGroup; ++i)
+        if (i < m) acc = acc + (odd ? -vals[i] : vals[i]);
       f.value_sums[tb + p] = acc;
       f.visit_counts[tb + p] += m - vli * m;
     }
@@ -81,14 +83,36 @@ __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_fores
       const uint16_t* bmem = w.gmembers + ((int64_t)t * MD + bd) * MW + bseg;
       const bool odd = bd & 1;
       float acc = f.value_sums[tb + bp];
-      for (int c = 0; c < bm; c += kWave) {
-        float x = 0.0f;
-        if (c + lane < bm) {
-          const float v = sv[bmem[c + lane]];
-          x = odd ? -v : v;
+      // fetch 4 chunks of 64 ahead, then fold each chunk in order on lane 0
+      for (int c0 = 0; c0 < bm; c0 += 4 * kWave) {
+        float x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int c = c0 + u * kWave + lane;
+          const float v = c < bm ? sv[bmem[c]] : 0.0f;
+          x[u] = odd ? -v : v;
         }
-        const int lim = min(kWave, bm - c);
-        for (int j = 0; j < lim; ++j) acc = acc + readlane_f(x, j);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int cb = c0 + u * kWave;
+          if (cb >= bm) break;
+          st[lane] = x[u];
+          wave_sync();
+          if (lane == 0) {
+            const int lim = min(kWave, bm - cb);
+            const float4* s4 = reinterpret_cast<const float4*>(st);
+            int j = 0;
+            for (; j + 4 <= lim; j += 4) {
+              const float4 q = s4[j >> 2];
+              acc = acc + q.x;
+              acc = acc + q.y;
+              acc = acc + q.z;
+              acc = acc + q.w;
+            }
+            for (; j < lim; ++j) acc = acc + st[j];
+          }
+          wave_sync();
+        }
       }
       if (lane == 0) {
         f.value_sums[tb + bp] = acc;
