@@ -692,11 +692,17 @@ __device__ int block_excl_scan(int32_t* a, int n, int* s_wtot) {
   return total;
 }
 
-// Single-member groups of level d, one per lane: the member's next node is the reference's
-// best child (first unvisited child, else the strict argmax of the exact score) at the parent
-// count N + VL, scanned in row order by the lane.
+// Groups of at most kSmallGroup members at level d, one group per lane.  Each member in turn
+// takes the reference's best child (first unvisited child, else the strict argmax of the
+// exact score) at the parent count N + VL*(rank+1), the children picked by earlier members
+// carrying their virtual loss; the lane scans the row in order, exactly as
+// CythonLockFreeTree.select_best_child_nogil does.  The members of each picked child are
+// placed in the parent's segment, children in order of their first pick, members in rank
+// order.
+constexpr int kSmallGroup = 1;
+
 template <int RMAX>
-__device__ inline void single_member_groups(
+__device__ inline void small_groups(
     const SelArgs& f, const SelCfg& c, int t, int d, int ng, int W, int64_t tb, int64_t gmax,
     uint32_t* gnode, uint32_t* gsl, uint16_t* buf, uint16_t* lfs, int32_t* lflag, int* s_gcount,
     int* s_glog, unsigned long long* s_st) {
@@ -709,77 +715,113 @@ __device__ inline void single_member_groups(
   for (int g0 = wave * kWave; g0 < ng; g0 += kSelThreads) {
     const int gi = g0 + lane;
     const uint32_t sl = gi < ng ? gsl[cur * W + gi] : 0u;
-    if ((sl >> 16) != 1u) continue;
-      const int p = (int)gnode[cur * W + gi];
-      const int seg = (int)(sl & 0xFFFFu);
-      const int sm = buf[cur * W + seg];
-      const int gid = atomicAdd(s_glog, 1);
-      *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, 1);
-      w.paths[((int64_t)t * MW + sm) * MD + d] = p;
-      w.gmembers[((int64_t)t * MD + d) * MW + seg] = (uint16_t)sm;
-      const int Np0 = N[tb + p];
-      const int k = f.nchild[tb + p];
-      const int first = f.first[tb + p];
-      if (c.vl_atomic)
-        atomicAdd(&N[tb + p], c.vli);
-      else
-        N[tb + p] = Np0 + c.vli;
-      atomicAdd(&s_st[OMQ_ST_PATHNODES], 1ull);
-      bool leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
-      if (!leaf && k > RMAX * kWave) {
-        atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
-        leaf = true;
-      }
-      int pick = -1;
-      if (!leaf) {
-        const int Np = Np0 + c.vli;
-        atomicAdd(&s_st[OMQ_ST_INTERNAL], 1ull);
-        atomicAdd(&s_st[OMQ_ST_ROWSUM], (unsigned long long)k);
-        atomicAdd(&s_st[OMQ_ST_STEPS], 1ull);
-        if (Np != 0) {
-          const float sp = sqrtf((float)Np);
-          float best = -1e9f;
-          int unv = -1;
-#pragma unroll 1
-          for (int i = 0; i < k; ++i) {
-            const int64_t node = tb + first + 1 + i;
-            const int n = N[node];
-            const float wvv = f.W[node];
-            const float pv = f.P[node];
-            if (n == 0) {
-              unv = unv < 0 ? i : unv;
-            } else {
-              const float q = wvv / ((float)n + c.vlf);
-              const float u = ((c.c_puct * pv) * sp) / (float)(1 + n);
-              const float sc = q + u;
-              if (sc > best) {
-                best = sc;
-                pick = i;
-              }
-            }
-          }
-          pick = unv >= 0 ? unv : pick;
-        }
-        if (pick < 0) atomicOr(&w.status[0], OMQ_STATUS_NOCHILD);
-      }
-      if (pick >= 0) {
-        const int g = atomicAdd(&s_gcount[nxt], 1);
-        gnode[nxt * W + g] = (uint32_t)(first + 1 + pick);
-        gsl[nxt * W + g] = (uint32_t)seg | (1u << 16);
-        buf[nxt * W + seg] = (uint16_t)sm;
-      } else {
-        w.path_len[(int64_t)t * MW + sm] = d + 1;
-        w.leaves[(int64_t)t * MW + sm] = p;
-        lfs[sm] = (uint16_t)sm;
-        lflag[sm] = 1;
-        atomicAdd(&s_st[OMQ_ST_PATHENTRIES], (unsigned long long)(d + 1));
+    const int m = (int)(sl >> 16);
+    if (m < 1 || m > kSmallGroup) continue;
+    const int p = (int)gnode[cur * W + gi];
+    const int seg = (int)(sl & 0xFFFFu);
+    int mem[kSmallGroup];
+#pragma unroll
+    for (int r = 0; r < kSmallGroup; ++r) mem[r] = r < m ? (int)buf[cur * W + seg + r] : 0;
+    const int gid = atomicAdd(s_glog, 1);
+    *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, m);
+#pragma unroll
+    for (int r = 0; r < kSmallGroup; ++r) {
+      if (r < m) {
+        w.paths[((int64_t)t * MW + mem[r]) * MD + d] = p;
+        w.gmembers[((int64_t)t * MD + d) * MW + seg + r] = (uint16_t)mem[r];
       }
     }
+    const int Np0 = N[tb + p];
+    const int k = f.nchild[tb + p];
+    const int first = f.first[tb + p];
+    if (c.vl_atomic)
+      atomicAdd(&N[tb + p], c.vli * m);
+    else
+      N[tb + p] = Np0 + c.vli * m;
+    atomicAdd(&s_st[OMQ_ST_PATHNODES], 1ull);
+    bool leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
+    if (!leaf && k > RMAX * kWave) {
+      atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
+      leaf = true;
+    }
+    int pick[kSmallGroup];
+#pragma unroll
+    for (int r = 0; r < kSmallGroup; ++r) pick[r] = -1;
+    if (!leaf) {
+      atomicAdd(&s_st[OMQ_ST_INTERNAL], 1ull);
+      atomicAdd(&s_st[OMQ_ST_ROWSUM], (unsigned long long)k);
+      atomicAdd(&s_st[OMQ_ST_STEPS], (unsigned long long)m);
+#pragma unroll
+      for (int r = 0; r < kSmallGroup; ++r) {
+        if (r >= m) break;
+        const int Np = Np0 + c.vli * (r + 1);
+        if (Np == 0) continue;  // the reference returns no child for a parent count of 0
+        const float sp = sqrtf((float)Np);
+        float best = -1e9f;
+        int bi = -1, unv = -1;
+        for (int i = 0; i < k; ++i) {
+          const int64_t node = tb + first + 1 + i;
+          int n = N[node];
+#pragma unroll
+          for (int r2 = 0; r2 < kSmallGroup - 1; ++r2)
+            if (r2 < r && pick[r2] == i) n += c.vli;
+          const float wvv = f.W[node];
+          const float pv = f.P[node];
+          if (n == 0) {
+            unv = unv < 0 ? i : unv;
+          } else {
+            const float q = wvv / ((float)n + c.vlf);
+            const float u = ((c.c_puct * pv) * sp) / (float)(1 + n);
+            const float sc = q + u;
+            if (sc > best) {
+              best = sc;
+              bi = i;
+            }
+          }
+        }
+        pick[r] = unv >= 0 ? unv : bi;
+        if (pick[r] < 0) atomicOr(&w.status[0], OMQ_STATUS_NOCHILD);
+      }
+    }
+    // children in order of first pick; members of a child contiguous, in rank order
+    int pos = seg;
+    int s_end = -1;
+#pragma unroll
+    for (int r = 0; r < kSmallGroup; ++r) {
+      if (r >= m) break;
+      if (pick[r] < 0) {
+        if (s_end < 0) s_end = mem[r];
+        w.path_len[(int64_t)t * MW + mem[r]] = d + 1;
+        w.leaves[(int64_t)t * MW + mem[r]] = p;
+        lfs[mem[r]] = (uint16_t)s_end;
+        atomicAdd(&s_st[OMQ_ST_PATHENTRIES], (unsigned long long)(d + 1));
+        continue;
+      }
+      bool seen = false;
+#pragma unroll
+      for (int r2 = 0; r2 < kSmallGroup - 1; ++r2)
+        if (r2 < r && pick[r2] == pick[r]) seen = true;
+      if (seen) continue;
+      int cntc = 0;
+#pragma unroll
+      for (int r2 = 0; r2 < kSmallGroup; ++r2) {
+        if (r2 < m && pick[r2] == pick[r]) {
+          buf[nxt * W + pos + cntc] = (uint16_t)mem[r2];
+          ++cntc;
+        }
+      }
+      const int g = atomicAdd(&s_gcount[nxt], 1);
+      gnode[nxt * W + g] = (uint32_t)(first + 1 + pick[r]);
+      gsl[nxt * W + g] = (uint32_t)pos | ((uint32_t)cntc << 16);
+      pos += cntc;
+    }
+    if (s_end >= 0) lflag[s_end] = 1;
+  }
 }
 
 template <int RMAX>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c) {
-  // single-member groups one per lane; kept out of the widest kernels, whose chains need every
+  // small groups one per lane; kept out of the widest kernels, whose chains need every
   // register
   constexpr bool kLanePass = RMAX <= 3;
   SelArgs& w = f;
@@ -833,7 +875,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       const uint32_t sl = gsl[cur * W + gi];
       const int seg = (int)(sl & 0xFFFFu);
       const int m = (int)(sl >> 16);
-      if (kLanePass && m == 1) continue;  // single-member groups: one per lane, below
+      if (kLanePass && m <= kSmallGroup) continue;  // small groups: one per lane, below
       const uint16_t* mem = buf + cur * W + seg;
 
       // log the group and record the path entries
@@ -939,8 +981,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       wave_sync();
     }
     if (kLanePass)
-      single_member_groups<RMAX>(f, c, t, d, ng, W, tb, gmax, gnode, gsl, buf, lfs, lflag,
-                                 s_gcount, &s_glog, s_st);
+      small_groups<RMAX>(f, c, t, d, ng, W, tb, gmax, gnode, gsl, buf, lfs, lflag, s_gcount,
+                         &s_glog, s_st);
     __syncthreads();
     if (tid == 0) s_gcount[cur] = 0;
     __syncthreads();
