@@ -13,10 +13,11 @@
 // the group is processed as a chain in simulation order, the r-th member (1-based) seeing
 // Np = N[p] + VL*r and each child c with N[c] + VL*(members before it that chose c).  Groups
 // are independent of each other.  A workgroup per tree takes the groups level by level, one
-// wavefront per group; the chain keeps the row (N, W, c*P, Q) in registers, lane l holding
-// children [l*R, l*R+R), so the winning lane order is the index order.  The members of a
-// group are kept in simulation order in LDS and partitioned among the chosen children by a
-// counting scatter, which yields the groups of the next level.
+// wavefront per group; the chain keeps the row's selection state in registers, slot j of lane
+// l holding child j*64 + l.  In the kernels for rows of at most 192 children, groups of one
+// member are taken one per lane instead (small_groups).  The members of a group are kept in
+// simulation order in LDS and partitioned among the chosen children by a counting scatter,
+// which yields the groups of the next level.
 //
 // Virtual loss is materialised once per group (N[p] += VL*m, p is owned by one group per
 // wave), or with one atomic per path entry when vl_atomic is set.
