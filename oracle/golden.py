@@ -1,0 +1,292 @@
+"""Known-answer cases for the selection chain and small whole searches.
+
+TEST INFRASTRUCTURE ONLY (tests/ and tests/golden/make_golden.py).
+
+Two kinds of case:
+
+* **Crafted rows.** A root with k unexpanded children whose N, W and P are chosen to stress the
+  selection. The cases include exact ties, priors one ulp apart, unvisited children at high
+  indices, |Q| above 1e8, negative priors, c_puct = 0, VL = 0 and fractional VL. The root
+  takes m simulations of one wave. Each simulation's path is [root, child], so the expected
+  output is the child picked by each of the m simulations, plus the visit counts after the
+  wave. The answer follows select_path / select_best_child_nogil
+  (python/mcts/cpu/cython_tree_optimized.pyx:177-202,421-464).
+* **Small searches.** Whole searches on tiny boards, with evaluator rows (policy, value) drawn
+  from a seeded generator and replayed. The expected output is every wave's paths and the
+  final tree (optimized_wave_search.py:299-483 for expansion and backup).
+
+Both kinds are computed twice, by the numpy-float32 restatement (oracle/ref_np.py) and by the
+C oracle (oracle/tree_oracle.c). The fixture generator refuses to write a case on which the two
+differ.
+"""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+
+from omoknuni_quantum_amd.synthetic import games
+
+from . import ref_np
+from .oracle import Oracle
+
+F32 = np.float32
+
+
+def model_from_name(name: str) -> games.GameModel:
+    kind, _, arg = name.partition(":")
+    if kind == "gomoku":
+        return games.gomoku(int(arg))
+    if kind == "go":
+        return games.go(int(arg))
+    if kind == "sparse":
+        return games.chess_sparse()
+    raise ValueError(name)
+
+
+# ---- crafted rows -----------------------------------------------------------------------
+
+def _model_for_width(k: int) -> str:
+    for bound, name in ((45, "sparse"), (121, "gomoku:11"), (169, "gomoku:13"), (225, "gomoku:15"),
+                        (362, "go:19"), (441, "gomoku:21")):
+        if k <= bound:
+            return name
+    raise ValueError(k)
+
+
+def crafted_row_cases(seed: int = 2024) -> list[dict]:
+    """The crafted-row cases: dicts with model, k, m, c, vl, N0 and the child arrays N, W, P."""
+    rng = np.random.default_rng(seed)
+    cases = []
+
+    def add(kind, k, m, c=1.4, vl=3.0, N0=None, Nc=None, Wc=None, Pc=None, model=None):
+        if Nc is None:
+            Nc = rng.integers(0, 40, k)
+        Nc = np.asarray(Nc, np.int32)
+        if Wc is None:
+            Wc = (Nc * rng.uniform(-1, 1, k)).astype(F32)
+        if Pc is None:
+            Pc = rng.dirichlet([0.3] * k).astype(F32)
+        if N0 is None:
+            N0 = int(Nc.sum()) + 1
+        cases.append({"kind": kind, "model": model or _model_for_width(k), "k": int(k),
+                      "m": int(m), "c": float(F32(c)), "vl": float(vl), "N0": int(N0),
+                      "N": Nc.astype(np.int32), "W": np.asarray(Wc, F32),
+                      "P": np.asarray(Pc, F32)})
+
+    # random rows of every chain width, with a few unvisited children
+    for k, m in ((1, 5), (3, 9), (20, 64), (45, 130), (64, 65), (65, 200), (121, 256),
+                 (128, 129), (169, 300), (200, 256), (225, 512), (300, 700), (362, 1024),
+                 (441, 600)):
+        add("random", k, m)
+    # all visited: the chain runs on scores only from the first step
+    for k, m in ((40, 256), (225, 256), (362, 1024)):
+        add("visited", k, m, Nc=rng.integers(1, 30, k))
+    # exact ties everywhere: identical children, every step a tie broken by index
+    for k, m in ((8, 40), (64, 128), (225, 300)):
+        add("ties", k, m, Nc=np.full(k, 5), Wc=np.full(k, 1.25, F32), Pc=np.full(k, 1.0 / k, F32))
+    # priors one ulp apart, equal N and W: the approximate scores cannot separate the children
+    for k, m in ((30, 90), (200, 256)):
+        p = F32(0.01)
+        Pc = np.array([np.nextafter(p, F32(1), dtype=F32) if j % 3 == 1 else p for j in range(k)],
+                      F32)
+        add("ulp", k, m, Nc=np.full(k, 7), Wc=np.full(k, -0.5, F32), Pc=Pc)
+    # values one ulp apart
+    for k, m in ((50, 100),):
+        w0 = F32(0.75)
+        Wc = np.array([np.nextafter(w0, F32(2), dtype=F32) if j % 4 == 2 else w0 for j in range(k)],
+                      F32)
+        add("ulpW", k, m, Nc=np.full(k, 3), Wc=Wc, Pc=np.full(k, F32(1.0 / k), F32))
+    # unvisited children only at high indices (first unvisited rule late in the row)
+    for k, m in ((60, 64), (225, 64), (362, 128)):
+        Nc = rng.integers(1, 20, k)
+        Nc[[k - 1, k - 3]] = 0
+        add("late_unvisited", k, m, Nc=Nc)
+    # all unvisited
+    add("all_unvisited", 100, 150, Nc=np.zeros(100, np.int64), Wc=np.zeros(100, F32))
+    # |Q| beyond 1e8: every step compares exactly
+    for k, m in ((40, 80), (225, 256)):
+        Nc = rng.integers(1, 9, k)
+        add("bigQ", k, m, Nc=Nc, Wc=(rng.uniform(-1, 1, k) * 1e12).astype(F32))
+    # negative priors: exact comparison as well
+    for k, m in ((40, 80), (150, 200)):
+        Pc = rng.uniform(-0.02, 0.05, k).astype(F32)
+        add("negP", k, m, Pc=Pc, Nc=rng.integers(1, 9, k))
+    # c_puct = 0: pure value ranking with ties among equal Q
+    add("c0", 64, 100, c=0.0, Nc=np.full(64, 4), Wc=np.round(rng.uniform(-4, 4, 64)).astype(F32))
+    # large c_puct
+    add("c50", 225, 256, c=50.0)
+    # VL = 0 (every rank takes the first rank's choice), VL = 1, fractional VL = 2.5
+    add("vl0", 225, 64, vl=0.0)
+    add("vl0_np0", 10, 5, vl=0.0, N0=0)
+    add("vl1", 100, 256, vl=1.0)
+    add("vl2.5", 225, 256, vl=2.5)
+    # single members under each narrow kernel (per-lane best-child scan) and under wide kernels
+    for k in (1, 17, 45, 100, 160, 225, 362):
+        add("single", k, 1)
+    # narrow rows under the wide kernels
+    add("narrow_in_wide", 30, 200, model="gomoku:15")
+    add("narrow_in_go", 64, 300, model="go:19")
+    add("small_in_8", 100, 130, model="gomoku:21")
+    return cases
+
+
+def crafted_expected_np(case: dict) -> tuple[np.ndarray, np.ndarray]:
+    """Picks (child index or -1 per simulation) and N after the wave, from the numpy restatement."""
+    k = case["k"]
+    t = ref_np.NpTree(k + 1, case["c"], case["vl"])
+    t.expand(0, list(range(k)), [F32(x) for x in case["P"]])
+    t.N[0] = case["N0"]
+    t.N[1:k + 1] = case["N"]
+    t.W[1:k + 1] = case["W"]
+    picks = []
+    for _ in range(case["m"]):
+        path = t.select_path(100)
+        picks.append(path[1] - 1 if len(path) > 1 else -1)
+    return np.array(picks, np.int32), t.N[:k + 1].copy()
+
+
+def crafted_expected_oracle(case: dict) -> tuple[np.ndarray, np.ndarray]:
+    """The same from the C oracle, on the crafted state written into its arrays."""
+    k, m = case["k"], case["m"]
+    model = model_from_name(case["model"])
+    orc = Oracle(model, 1, k + 1, m, 100)
+    orc.set_params(case["c"], case["vl"], 0, 0, 1.0, 0.0)
+    orc.set_roots(games.root_keys(1, 1))
+    orc.reset_tree(0)
+    orc.write("N", np.concatenate([[case["N0"]], case["N"]]).astype(np.int32))
+    orc.write("W", np.concatenate([[0.0], case["W"]]).astype(F32))
+    orc.write("P", np.concatenate([[1.0], case["P"]]).astype(F32))
+    orc.write("parent", np.array([-1] + [0] * k, np.int32))
+    orc.write("first", np.array([0] + [-1] * k, np.int32))
+    orc.write("nchild", np.array([k] + [0] * k, np.int32))
+    orc.write("action", np.array([-1] + list(range(k)), np.int32))
+    orc.write("expanded", np.array([1] + [0] * k, np.uint8))
+    orc.write("children", np.arange(1, k + 1, dtype=np.int32))
+    orc.write("child_actions", np.arange(k, dtype=np.int32))
+    orc.write("num_nodes", np.array([k + 1], np.int32))
+    orc.write("num_edges", np.array([k], np.int32))
+    orc.lib.orc_wave_select(orc.f, 0, m, 100)
+    lw = orc.last_wave(0, m)
+    picks = np.array([p[1] - 1 if len(p) > 1 else -1 for p in lw["paths"]], np.int32)
+    return picks, orc.array("N", k + 1)
+
+
+def pack_crafted(cases: list[dict], picks: list[np.ndarray], n_after: list[np.ndarray]) -> dict:
+    """Flatten the cases into arrays for an npz file (no object arrays)."""
+    meta = [{key: c[key] for key in ("kind", "model", "k", "m", "c", "vl", "N0")} for c in cases]
+    koff = np.concatenate([[0], np.cumsum([c["k"] for c in cases])]).astype(np.int64)
+    moff = np.concatenate([[0], np.cumsum([c["m"] for c in cases])]).astype(np.int64)
+    noff = np.concatenate([[0], np.cumsum([c["k"] + 1 for c in cases])]).astype(np.int64)
+    return {
+        "meta": np.array(json.dumps(meta)),
+        "koff": koff, "moff": moff, "noff": noff,
+        "N": np.concatenate([c["N"] for c in cases]).astype(np.int32),
+        "W": np.concatenate([c["W"] for c in cases]).astype(F32),
+        "P": np.concatenate([c["P"] for c in cases]).astype(F32),
+        "picks": np.concatenate(picks).astype(np.int32),
+        "N_after": np.concatenate(n_after).astype(np.int32),
+    }
+
+
+def unpack_crafted(z) -> list[dict]:
+    meta = json.loads(str(z["meta"]))
+    out = []
+    for i, c in enumerate(meta):
+        a, b = int(z["koff"][i]), int(z["koff"][i + 1])
+        ma, mb = int(z["moff"][i]), int(z["moff"][i + 1])
+        na, nb = int(z["noff"][i]), int(z["noff"][i + 1])
+        c = dict(c)
+        c.update(N=z["N"][a:b], W=z["W"][a:b], P=z["P"][a:b], picks=z["picks"][ma:mb],
+                 N_after=z["N_after"][na:nb])
+        out.append(c)
+    return out
+
+
+# ---- small whole searches with replayed evaluator rows ----------------------------------
+
+SEARCH_CASES = [
+    {"name": "gomoku4_full", "model": "gomoku:4", "policy": "full", "sign": 0, "eps": 0.0,
+     "vl": 3.0, "W": 8, "sims": 96, "seed": 11, "stones": 3},
+    {"name": "gomoku5_pw_rootpos_noise", "model": "gomoku:5", "policy": "reference_pw", "sign": 1,
+     "eps": 0.25, "vl": 3.0, "W": 8, "sims": 96, "seed": 12, "stones": 4},
+    {"name": "go4_full_vl1", "model": "go:4", "policy": "full", "sign": 0, "eps": 0.0,
+     "vl": 1.0, "W": 5, "sims": 60, "seed": 13, "stones": 2},
+    {"name": "gomoku4_vl0_ties", "model": "gomoku:4", "policy": "full", "sign": 0, "eps": 0.0,
+     "vl": 0.0, "W": 3, "sims": 45, "seed": 14, "stones": 0},
+]
+CAPACITY = 4000
+C_PUCT = 1.4
+
+
+def search_inputs(case: dict) -> dict:
+    """Root board, legal mask, keys, noise and the evaluator rows of every wave (seeded)."""
+    model = model_from_name(case["model"])
+    A, cells = model.num_actions, model.cells
+    rng = np.random.default_rng(case["seed"])
+    board = np.zeros(cells, np.int8)
+    s = case["stones"]
+    board[rng.permutation(cells)[:s]] = np.where(np.arange(s) % 2 == 0, 1, 2)
+    legal = games.legal_masks(model, board.reshape(1, model.board_size, model.board_size), 1)
+    root_legal = [a for a in range(A) if (int(legal[0, a // 32]) >> (a % 32)) & 1]
+    noise = None
+    if case["eps"] > 0:
+        noise = np.zeros((1, A))
+        noise[0, :len(root_legal)] = rng.dirichlet([0.3] * len(root_legal))
+    W = case["W"]
+    waves = [1] + [W] * (case["sims"] // W)
+    pols, vals = [], []
+    for wi in range(len(waves)):
+        pol = rng.random((W, A)).astype(F32) + F32(0.01)
+        val = (rng.random(W) * 2 - 1).astype(F32)
+        if wi % 5 == 3:  # a wave of identical priors and values: exact ties
+            pol[:] = F32(0.5)
+            val[:] = F32(0.25)
+        pols.append(pol)
+        vals.append(val)
+    return {"model": model, "board": board, "legal": legal, "root_legal": root_legal,
+            "keys": games.root_keys(case["seed"], 1), "noise": noise, "waves": waves,
+            "policy": np.stack(pols), "values": np.stack(vals)}
+
+
+def search_expected(case: dict) -> dict:
+    """Run the case on the C oracle and on the numpy restatement; both must agree.  Returns
+    the per-wave paths (flattened) and the final tree."""
+    inp = search_inputs(case)
+    model = inp["model"]
+    pass_action = model.num_actions - 1 if model.kind == "go" else None
+    orc = Oracle(model, 1, CAPACITY, case["W"], 100)
+    orc.set_params(C_PUCT, case["vl"], 1 if case["policy"] == "reference_pw" else 0, case["sign"],
+                   1.0, case["eps"])
+    orc.set_roots(inp["keys"], inp["legal"], inp["noise"])
+    orc.reset_tree(0)
+    npt = ref_np.NpTree(CAPACITY, C_PUCT, case["vl"])
+    legal_of = lambda pacts: ref_np.board_legal(inp["root_legal"], pacts, pass_action)  # noqa: E731
+    plens, pflat = [], []
+    for wi, w in enumerate(inp["waves"]):
+        pol, val = inp["policy"][wi], inp["values"][wi]
+        orc.wave(0, w, replay_policy=pol, replay_values=val)
+        paths, _ = ref_np.np_wave(npt, w, 100, legal_of, pol, val, case["policy"],
+                                  None if inp["noise"] is None else inp["noise"][0], case["eps"],
+                                  case["sign"] == 1)
+        lw = orc.last_wave(0, w)
+        for s in range(w):
+            if list(lw["paths"][s]) != paths[s]:
+                raise AssertionError(f"{case['name']} wave {wi} sim {s}: oracle "
+                                     f"{list(lw['paths'][s])} numpy {paths[s]}")
+            plens.append(len(paths[s]))
+            pflat.extend(paths[s])
+    tr = orc.tree(0)
+    n = tr["num_nodes"]
+    if n != npt.num_nodes:
+        raise AssertionError(f"{case['name']}: node count {n} vs {npt.num_nodes}")
+    for key in ("N", "parent", "first", "nchild", "action"):
+        if not np.array_equal(tr[key], getattr(npt, key)[:n]):
+            raise AssertionError(f"{case['name']}: {key} differs")
+    for key in ("W", "P"):
+        if not np.array_equal(tr[key].view(np.int32), getattr(npt, key)[:n].view(np.int32)):
+            raise AssertionError(f"{case['name']}: {key} differs")
+    out = {key: tr[key] for key in ("N", "W", "P", "parent", "first", "nchild", "action")}
+    out["path_len"] = np.array(plens, np.int32)
+    out["paths"] = np.array(pflat, np.int32)
+    return out

@@ -126,6 +126,14 @@ class Oracle:
         buf = (ctypes.c_char * ((offset + count) * dt.itemsize)).from_address(ptr)
         return np.frombuffer(buf, dtype=dt, count=count, offset=offset * dt.itemsize).copy()
 
+    def write(self, name: str, values, offset: int = 0) -> None:
+        """Overwrite entries [offset, offset + len(values)) of an oracle array (crafted states
+        for the known-answer tests)."""
+        dt = np.dtype(_DT[name])
+        v = np.ascontiguousarray(values, dtype=dt)
+        ptr = getattr(self.lib, "orc_" + name)(self.f)
+        ctypes.memmove(ptr + offset * dt.itemsize, v.ctypes.data, v.nbytes)
+
     def num_nodes(self, t: int) -> int:
         return int(self.array("num_nodes", 1, t)[0])
 
