@@ -66,6 +66,17 @@ extern "C" {
 #define OMQ_WACC_ORDERED 0  /* per node, contributions added in simulation order (deterministic) */
 #define OMQ_WACC_ATOMIC 1   /* hardware float atomics per path entry (order not fixed) */
 
+/* Gomoku rules of omq_gomoku_terminal */
+#define OMQ_RULE_FREESTYLE 0  /* five or more in a row win */
+#define OMQ_RULE_RENJU 1      /* as FREESTYLE, but an overline of player 1 does not win (the
+                                 reference's simplified renju: no other forbidden moves) */
+
+/* terminal codes of omq_gomoku_terminal */
+#define OMQ_TERM_NONE 0
+#define OMQ_TERM_WIN1 1  /* player 1 has five */
+#define OMQ_TERM_WIN2 2  /* player 2 has five */
+#define OMQ_TERM_DRAW 3  /* full board without five */
+
 /* limits of this build */
 #define OMQ_MAX_WAVE 4096   /* simulations per tree per wave */
 #define OMQ_MAX_ROW 512     /* children per node (a selection row is held in registers) */
@@ -190,6 +201,28 @@ int omq_expand(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
  * vectorized_backup / batch_remove_virtual_loss (mcts_kernels.cu:121-158,934-953). */
 int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float virtual_loss,
                int32_t sign_mode, int32_t w_mode, void* stream);
+
+/* Gomoku terminal check of every unique leaf of the wave; call it after omq_leaf_info and
+ * before omq_expand.  Needs an OMQ_GAME_BOARD forest with num_actions = bs*bs.
+ * - Position.  A leaf's position is the root board root_boards[t*num_actions + cell] (int8:
+ *   0 empty, 1 and 2 stones) with the moves of the leaf's path played in alternating colours.
+ *   The first move is played by root_player[t]. When root_player is NULL, it is player 1 if the
+ *   root board holds an even number of stones, else player 2 (python/mcts/core/mcts.py:1506).
+ * - Scan.  The position is scanned as FastTerminalChecker._check_gomoku_terminal_cpu scans it
+ *   (python/mcts/utils/fast_terminal_check.py:132-232): cells in row-major order, directions
+ *   horizontal, vertical, down-right and down-left. The first cell that starts a five names the
+ *   winner. Under OMQ_RULE_RENJU an overline of player 1 does not count, and it ends that
+ *   cell's scan as in the reference. A full board without a five is a draw.
+ * - Terminal leaves.  A terminal leaf gets ulegal = 0, so omq_expand leaves it unexpanded
+ *   (python/mcts/cpu/optimized_wave_search.py:374-376). Its value is still the evaluator's. The
+ *   root (a path of length 1) is never terminal.
+ * - Output.  uterminal, when not NULL, is [T*max_wave] and receives OMQ_TERM_* per unique leaf.
+ * Replaces the terminal detection run by CPUGameStates.apply_actions
+ * (python/mcts/cpu/cpu_game_states.py:352-412) and the GPU Gomoku terminal kernels
+ * (python/mcts/gpu/gomoku_kernels.py:14-160). */
+int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
+                        const int32_t* root_player, int32_t rule, int32_t* uterminal,
+                        void* stream);
 
 /* Reference-style path backup over an explicit path matrix (no group log needed):
  * paths[b*max_depth + d], d < min(path_len[b], max_depth), root first; values[b] is the leaf

@@ -28,6 +28,8 @@ STAT_NAMES = [
     "sims", "steps", "capfail",
 ]
 OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT = 1, 2
+OMQ_RULE_FREESTYLE, OMQ_RULE_RENJU = 0, 1
+OMQ_TERM_NONE, OMQ_TERM_WIN1, OMQ_TERM_WIN2, OMQ_TERM_DRAW = 0, 1, 2, 3
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -67,6 +69,7 @@ SIGNATURES = {
     "omq_backup": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _i32, _p]),
     "omq_paths_backup": (ctypes.c_int, [_FP, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "omq_virtual_loss": (ctypes.c_int, [_FP, _p, _p, _i32, _i32, _p]),
+    "omq_gomoku_terminal": (ctypes.c_int, [_FP, _WP, _p, _p, _i32, _p, _p]),
 }
 
 

@@ -95,6 +95,11 @@ class WaveEngine:
         self.status = z(4, i32)
         self.noise = z(T * A, torch.float64)
         self.has_noise = False
+        # Gomoku rules (terminal leaves are not expanded), off until set_gomoku_rules
+        self.uterm = z(T * MW, i32)
+        self.rule: int | None = None
+        self.root_boards: torch.Tensor | None = None
+        self.root_player: torch.Tensor | None = None
 
         f = _lib.OmqForest()
         f.num_trees, f.capacity, f.num_actions, f.game = T, cap, A, model.code
@@ -132,6 +137,28 @@ class WaveEngine:
         if noise is not None:
             self.noise.copy_(torch.from_numpy(np.ascontiguousarray(noise, dtype=np.float64).reshape(-1)))
 
+    def set_gomoku_rules(self, boards, rule: int = _lib.OMQ_RULE_FREESTYLE,
+                         root_player=None) -> None:
+        """Turn on the Gomoku terminal check of every wave's leaves.  boards: int8 [T, bs, bs]
+        root positions (0 empty, 1/2 stones); root_player: [T] player of the first path move
+        (default: 1 for an even stone count, else 2).  boards=None turns the check off."""
+        if boards is None:
+            self.rule, self.root_boards, self.root_player = None, None, None
+            return
+        if self.model.kind != "gomoku":
+            raise ValueError("the Gomoku terminal rule needs a gomoku game model")
+        b = torch.as_tensor(np.ascontiguousarray(boards, dtype=np.int8)).reshape(-1)
+        if b.numel() != self.T * self.A:
+            raise ValueError(f"boards hold {b.numel()} cells, expected {self.T} x {self.A}")
+        self.root_boards = b.to(self.device)
+        self.root_player = None
+        if root_player is not None:
+            rp = torch.as_tensor(np.ascontiguousarray(root_player, dtype=np.int32)).reshape(-1)
+            if rp.numel() != self.T:
+                raise ValueError("one root player per tree")
+            self.root_player = rp.to(self.device)
+        self.rule = int(rule)
+
     def _check(self, rc: int, what: str) -> None:
         _lib.check(rc, what)
 
@@ -147,8 +174,15 @@ class WaveEngine:
                                         self.stream_handle()), "omq_select")
 
     def leaf_info(self) -> None:
+        """Keys and legal counts of the unique leaves; with the Gomoku rule on, also the
+        terminal check (terminal leaves get no legal action, so they are not expanded)."""
         self._check(self.lib.omq_leaf_info(self.forest_ref, self.wave_ref, self.stream_handle()),
                     "omq_leaf_info")
+        if self.rule is not None:
+            self._check(self.lib.omq_gomoku_terminal(
+                self.forest_ref, self.wave_ref, self.root_boards.data_ptr(),
+                None if self.root_player is None else self.root_player.data_ptr(), self.rule,
+                self.uterm.data_ptr(), self.stream_handle()), "omq_gomoku_terminal")
 
     def expand(self, wave_size: int) -> None:
         p = self.params

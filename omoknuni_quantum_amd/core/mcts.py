@@ -144,10 +144,24 @@ class MCTS:
             noise = games.dirichlet_noise(self.model, counts, float(self.config.dirichlet_alpha),
                                           self.config.seed + 7919 * (self._search_count + 1))
         self.engine.set_roots(keys, legal, noise)
+        rule = self._gomoku_rule()
+        if rule is not None:
+            b = boards if boards is not None else np.zeros(
+                (T, self.config.board_size, self.config.board_size), np.int8)
+            self.engine.set_gomoku_rules(b, rule)
         self.engine.reset()
         self._roots_key = key
         self._boards = None if boards is None else torch.from_numpy(boards).to(self.device)
         self._eval = self._make_evaluator()
+
+    def _gomoku_rule(self) -> Optional[int]:
+        """Terminal rule of Gomoku leaves: the config's, renju when the game interface says
+        use_renju (fast_terminal_check.py:34-40 reads it there); None for other games."""
+        if self.model.kind != "gomoku" or self.config.gomoku_rules == "off":
+            return None
+        if self.config.gomoku_rules == "renju" or getattr(self.game_interface, "use_renju", False):
+            return _lib.OMQ_RULE_RENJU
+        return _lib.OMQ_RULE_FREESTYLE
 
     def _make_evaluator(self):
         if getattr(self.evaluator, "device_native", False) or hasattr(self.evaluator, "evaluate_wave"):

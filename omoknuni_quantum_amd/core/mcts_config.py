@@ -20,6 +20,11 @@ New fields of this build:
   num_trees         independent trees searched together (search_batch)
   seed              seeds root keys and root Dirichlet noise
   sparse_legal      (min, max) legal actions per node for the chess-shaped synthetic model
+  gomoku_rules      'freestyle' (five or more win), 'renju' (an overline of player 1 does
+                    not win) or 'off': the terminal check of Gomoku leaves, as the
+                    reference's game states run it after every move
+                    (python/mcts/utils/fast_terminal_check.py:132-232); terminal leaves are
+                    not expanded
 """
 from __future__ import annotations
 
@@ -71,6 +76,7 @@ hybrid_num_buffers use_tensorrt
 _EXPANSION = ("full", "reference_pw")
 _SIGNS = ("leaf_positive", "root_positive")
 _WACC = ("ordered", "atomic")
+_RULES = ("freestyle", "renju", "off")
 
 
 @dataclass
@@ -115,6 +121,7 @@ class _ConfigFields:
     num_trees: int = 1
     seed: int = 0
     sparse_legal: tuple = (20, 45)
+    gomoku_rules: str = "freestyle"
     extra: Dict[str, Any] = field(default_factory=dict)
 
 
@@ -150,6 +157,8 @@ class MCTSConfig(_ConfigFields):
             raise ValueError(f"w_accum must be one of {_WACC}")
         if self.num_trees < 1:
             raise ValueError("num_trees must be >= 1")
+        if self.gomoku_rules not in _RULES:
+            raise ValueError(f"gomoku_rules must be one of {_RULES}")
 
     # effective values ---------------------------------------------------------------------
     def effective_wave_size(self) -> int:

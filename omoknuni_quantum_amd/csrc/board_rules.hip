@@ -1,0 +1,116 @@
+// Gomoku terminal check of the unique leaves of a wave (gfx950).
+//
+// The reference decides after every move whether a child state is terminal.
+// CPUGameStates.apply_actions (python/mcts/cpu/cpu_game_states.py:352-412) calls
+// FastTerminalChecker._check_gomoku_terminal_cpu with last_move=None, which is a full-board
+// scan (python/mcts/utils/fast_terminal_check.py:132-232):
+//   - cells are visited in row-major order; at an occupied cell, the directions horizontal,
+//     vertical, down-right and down-left are tried in that order;
+//   - a direction counts when there is room for five cells (col <= bs-5 / row <= bs-5 / both /
+//     row <= bs-5 and col >= 4) and all five belong to the cell's player;
+//   - the first cell with a counting direction names the winner;
+//   - with use_renju, a five of player 1 that continues on either side (an overline) does not
+//     count, and it ends the scan of that cell: the reference's `continue` skips the
+//     remaining directions of the cell;
+//   - a full board without a five is a draw.
+// The driver does not expand a terminal leaf (python/mcts/cpu/optimized_wave_search.py:374-376),
+// but it still backs up the evaluator's value for it.
+//
+// Here a leaf's position is never stored.  It is rebuilt in LDS from the root board and the
+// moves on the leaf's path: one wavefront per unique leaf, colours alternating from the
+// root's player to move.  The leaf is then scanned cell-parallel: lane l takes cells
+// l, l+64, ..., and a wave min over the winning cells reproduces the row-major first.  A
+// terminal leaf gets ulegal = 0, which keeps omq_expand from expanding it.
+#include "omq_common.h"
+
+namespace omq {
+
+__global__ void gomoku_terminal_kernel(omq_forest f, omq_wave w, const int8_t* root_boards,
+                                       const int32_t* root_player, int rule, int bs,
+                                       int32_t* uterm) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int cells = bs * bs;
+  const int stride = (cells + 15) & ~15;
+  const int t = blockIdx.y;
+  const int wave = threadIdx.x / kWave;
+  const int u = blockIdx.x * (blockDim.x / kWave) + wave;
+  const int lane = lane_id();
+  const int64_t wb = (int64_t)t * w.max_wave;
+  if (u >= w.ucount[t]) return;
+  int8_t* b = reinterpret_cast<int8_t*>(smem + (size_t)wave * stride);
+  const int8_t* rb = root_boards + (int64_t)t * cells;
+  int stones = 0;
+  for (int i = lane; i < cells; i += kWave) {
+    const int8_t v = rb[i];
+    b[i] = v;
+    stones += v != 0;
+  }
+  stones = wave_sum_i(stones);
+  const int s0 = w.ufirst[wb + u];
+  int a_lo, a_hi;
+  const int L = load_path_actions(f, w, t, s0, &a_lo, &a_hi);
+  if (L <= 1) {  // the root position itself is not checked (the reference never flags it)
+    if (uterm != nullptr && lane == 0) uterm[wb + u] = OMQ_TERM_NONE;
+    return;
+  }
+  const int rp = root_player != nullptr ? root_player[t] : ((stones & 1) == 0 ? 1 : 2);
+  wave_sync();
+  // move j (0-based, depth j+1) is played by rp when j is even; lane l holds moves l and l+64
+  const int8_t mine = (int8_t)((lane & 1) == 0 ? rp : 3 - rp);
+  if (lane + 1 < L && a_lo >= 0 && a_lo < cells) b[a_lo] = mine;
+  if (lane + 65 < L && a_hi >= 0 && a_hi < cells) b[a_hi] = mine;
+  wave_sync();
+
+  constexpr int dr[4] = {0, 1, 1, 1};
+  constexpr int dc[4] = {1, 0, 1, -1};
+  int win = 0x7FFFFFFF;
+  int empty = 0;
+  for (int cell = lane; cell < cells; cell += kWave) {
+    const int p = b[cell];
+    if (p == 0) {
+      ++empty;
+      continue;
+    }
+    const int r = cell / bs, c = cell - (cell / bs) * bs;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int re = r + 4 * dr[d], ce = c + 4 * dc[d];
+      if (re >= bs || ce < 0 || ce >= bs) continue;  // no room for five in this direction
+      bool five = true;
+#pragma unroll
+      for (int k = 1; k < 5; ++k) five = five && b[(r + k * dr[d]) * bs + c + k * dc[d]] == p;
+      if (!five) continue;
+      if (rule == OMQ_RULE_RENJU && p == 1) {
+        const int rn = r + 5 * dr[d], cn = c + 5 * dc[d];
+        const int rq = r - dr[d], cq = c - dc[d];
+        const bool after = rn < bs && cn >= 0 && cn < bs && b[rn * bs + cn] == p;
+        const bool before = rq >= 0 && cq >= 0 && cq < bs && b[rq * bs + cq] == p;
+        if (after || before) break;  // overline: the reference skips the rest of this cell
+      }
+      win = min(win, cell);
+      break;
+    }
+  }
+  win = (int)~wave_max_u32(~(uint32_t)win);  // wave min
+  empty = wave_sum_i(empty);
+  int code = OMQ_TERM_NONE;
+  if (win != 0x7FFFFFFF) code = b[win];
+  else if (empty == 0) code = OMQ_TERM_DRAW;
+  if (lane == 0) {
+    if (code != OMQ_TERM_NONE) w.ulegal[wb + u] = 0;
+    if (uterm != nullptr) uterm[wb + u] = code;
+  }
+}
+
+hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const int8_t* boards,
+                                  const int32_t* root_player, int rule, int bs, int32_t* uterm,
+                                  hipStream_t st) {
+  constexpr int wpb = 4;
+  const size_t lds = (size_t)(((bs * bs) + 15) & ~15) * wpb;
+  dim3 grid((w.max_wave + wpb - 1) / wpb, f.num_trees);
+  hipLaunchKernelGGL(gomoku_terminal_kernel, grid, dim3(wpb * kWave), lds, st, f, w, boards,
+                     root_player, rule, bs, uterm);
+  return hipGetLastError();
+}
+
+}  // namespace omq

@@ -25,6 +25,9 @@ hipError_t launch_paths_backup(const omq_forest& f, const int32_t* paths, const 
 hipError_t launch_virtual_loss(const omq_forest& f, const int32_t* nodes, const int32_t* tree_of,
                                int count, int delta, hipStream_t st);
 hipError_t launch_reset(const omq_forest& f, hipStream_t st);
+hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const int8_t* boards,
+                                  const int32_t* root_player, int rule, int bs, int32_t* uterm,
+                                  hipStream_t st);
 size_t leaf_lds_per_wave_host(const omq_forest& f);
 }  // namespace omq
 
@@ -152,6 +155,27 @@ int omq_leaf_info(const omq_forest* f, const omq_wave* w, void* stream) {
   if (rc) return rc;
   return hip_status(omq::launch_leaf_info(*f, *w, w->max_wave, (hipStream_t)stream),
                     "omq_leaf_info");
+}
+
+int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
+                        const int32_t* root_player, int32_t rule, int32_t* uterminal,
+                        void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  rc = check_wave(f, w, w ? w->max_wave : 1);
+  if (rc) return rc;
+  if (f->game != OMQ_GAME_BOARD)
+    return fail(OMQ_E_ARG, "omq_gomoku_terminal needs a board forest (game %d)", f->game);
+  int bs = 0;
+  while ((bs + 1) * (bs + 1) <= f->num_actions) ++bs;
+  if (bs * bs != f->num_actions)
+    return fail(OMQ_E_ARG, "num_actions %d is not a square board", f->num_actions);
+  if (!root_boards) return fail(OMQ_E_ARG, "root_boards is null");
+  if (rule != OMQ_RULE_FREESTYLE && rule != OMQ_RULE_RENJU)
+    return fail(OMQ_E_ARG, "unknown gomoku rule %d", rule);
+  return hip_status(omq::launch_gomoku_terminal(*f, *w, root_boards, root_player, rule, bs,
+                                                uterminal, (hipStream_t)stream),
+                    "omq_gomoku_terminal");
 }
 
 int omq_synthetic_evaluate(const omq_forest* f, const omq_wave* w, float logit_scale,

@@ -64,6 +64,8 @@ def load() -> ctypes.CDLL:
         "orc_exp_cw": (fl, [fl]),
         "orc_sum64": (fl, [P, i]),
         "orc_sum64d": (d, [P, i]),
+        "orc_set_gomoku_rules": (None, [P, i, i, P, P]),
+        "orc_gomoku_terminal": (i, [P, i, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -72,7 +74,7 @@ def load() -> ctypes.CDLL:
     for name in ("N", "W", "P", "parent", "first", "nchild", "action", "expanded", "children",
                  "child_actions", "num_nodes", "num_edges", "paths", "path_len", "leaves",
                  "sim_uid", "uleaf", "ufirst", "ucount", "ukey", "ulegal", "uexpanded", "policy",
-                 "values"):
+                 "values", "uterm"):
         fn = getattr(lib, "orc_" + name)
         fn.restype = P
         fn.argtypes = [P]
@@ -85,7 +87,8 @@ _DT = {"N": np.int32, "W": np.float32, "P": np.float32, "parent": np.int32, "fir
        "child_actions": np.int32, "num_nodes": np.int32, "num_edges": np.int32,
        "paths": np.int32, "path_len": np.int32, "leaves": np.int32, "sim_uid": np.int32,
        "uleaf": np.int32, "ufirst": np.int32, "ucount": np.int32, "ukey": np.uint64,
-       "ulegal": np.int32, "uexpanded": np.int32, "policy": np.float32, "values": np.float32}
+       "ulegal": np.int32, "uexpanded": np.int32, "policy": np.float32, "values": np.float32,
+       "uterm": np.int32}
 
 
 class Oracle:
@@ -125,6 +128,17 @@ class Oracle:
         dt = np.dtype(_DT[name])
         buf = (ctypes.c_char * ((offset + count) * dt.itemsize)).from_address(ptr)
         return np.frombuffer(buf, dtype=dt, count=count, offset=offset * dt.itemsize).copy()
+
+    def set_gomoku_rules(self, boards, rule: int = 0, root_player=None) -> None:
+        """Gomoku terminal checks on the leaves (boards: int8 [T, bs, bs] root positions);
+        boards=None switches them off."""
+        if boards is None:
+            self.lib.orc_set_gomoku_rules(self.f, 0, 0, None, None)
+            return
+        self._boards = np.ascontiguousarray(boards, dtype=np.int8).reshape(self.T, self.A)
+        self._rp = None if root_player is None else np.ascontiguousarray(root_player, np.int32)
+        self.lib.orc_set_gomoku_rules(self.f, 1, rule, self._boards.ctypes.data,
+                                      None if self._rp is None else self._rp.ctypes.data)
 
     def write(self, name: str, values, offset: int = 0) -> None:
         """Overwrite entries [offset, offset + len(values)) of an oracle array (crafted states
@@ -180,6 +194,7 @@ class Oracle:
             "ukey": self.array("ukey", nu, wb),
             "ulegal": self.array("ulegal", nu, wb),
             "values": self.array("values", nu, wb),
+            "uterm": self.array("uterm", nu, wb),
             "ucount": nu,
         }
 

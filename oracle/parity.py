@@ -20,7 +20,10 @@ class ParityError(AssertionError):
     pass
 
 
-def make_pair(wl, max_wave=None, w_mode=0, vl_atomic=False, device="cuda", sign_mode=0):
+def make_pair(wl, max_wave=None, w_mode=0, vl_atomic=False, device="cuda", sign_mode=0,
+              rule=None):
+    """Engine and oracle for the workload; rule (0 freestyle, 1 renju) turns the Gomoku
+    terminal check on for both, from the workload's root boards."""
     from omoknuni_quantum_amd.core.engine import SearchParams, WaveEngine
     from omoknuni_quantum_amd.synthetic.evaluator import SyntheticEvaluator
 
@@ -36,6 +39,12 @@ def make_pair(wl, max_wave=None, w_mode=0, vl_atomic=False, device="cuda", sign_
     orc.set_params(wl.c_puct, wl.virtual_loss, EXPAND_CODES[wl.expand_policy], sign_mode,
                    wl.logit_scale, wl.dirichlet_epsilon)
     orc.set_roots(keys, legal, noise)
+    if rule is not None:
+        boards = wl.boards()
+        if boards is None:
+            boards = np.zeros((wl.num_trees, wl.model.board_size, wl.model.board_size), np.int8)
+        eng.set_gomoku_rules(boards, rule)
+        orc.set_gomoku_rules(boards, rule)
     return eng, orc, SyntheticEvaluator(wl.logit_scale)
 
 
@@ -74,6 +83,9 @@ def compare_wave(eng, orc, W, ctx, w_exact=True):
         if ucount[t] != lw["ucount"]:
             raise ParityError(f"{c}: unique leaves {ucount[t]} != oracle {lw['ucount']}")
         _cmp("uleaf", uleaf_all[t, :ucount[t]], lw["uleaf"], c)
+        if eng.rule is not None:
+            _cmp("uterm", eng.uterm.view(T, MW)[t, :ucount[t]].cpu().numpy(), lw["uterm"], c)
+            _cmp("ulegal", eng.ulegal.view(T, MW)[t, :ucount[t]].cpu().numpy(), lw["ulegal"], c)
         g = eng.host_tree(t)
         o = orc.tree(t)
         if g["num_nodes"] != o["num_nodes"]:
@@ -94,13 +106,14 @@ def compare_wave(eng, orc, W, ctx, w_exact=True):
 
 
 def run_parity(wl, check_every=1, w_mode=0, vl_atomic=False, device="cuda", log=None,
-               sign_mode=0):
+               sign_mode=0, rule=None, stats=None):
     """Run the whole search on both sides; compare after every check_every-th wave and at
-    the end.  Returns the number of waves compared."""
+    the end.  Returns the number of waves compared.  With a Gomoku rule, stats (a dict)
+    receives the number of terminal unique leaves met."""
     import torch
 
     eng, orc, ev = make_pair(wl, w_mode=w_mode, vl_atomic=vl_atomic, device=device,
-                             sign_mode=sign_mode)
+                             sign_mode=sign_mode, rule=rule)
     T = wl.num_trees
     eng.reset()
     for t in range(T):
@@ -116,6 +129,10 @@ def run_parity(wl, check_every=1, w_mode=0, vl_atomic=False, device="cuda", log=
         eng.run_wave(W, ev)
         for t in range(T):
             orc.wave(t, W)
+        if stats is not None and rule is not None:
+            for t in range(T):
+                stats["terminal"] = stats.get("terminal", 0) + int(
+                    (orc.last_wave(t, W)["uterm"] != 0).sum())
         if i % check_every == 0 or i == len(sizes) - 1:
             torch.cuda.synchronize()
             compare_wave(eng, orc, W, f"{wl.name} wave {i} (W={W})", w_exact=(w_mode == 0))

@@ -161,15 +161,58 @@ def choose_children(legal, pol_row, is_root, policy, root_visits, noise=None, ep
     return [legal[i] for i in chosen], [F(pd[i]) for i in chosen]
 
 
+def gomoku_terminal(board, renju: bool = False) -> int:
+    """Full-board Gomoku scan of FastTerminalChecker._check_gomoku_terminal_cpu without a last
+    move (python/mcts/utils/fast_terminal_check.py:132-232), on a [bs, bs] board of 0/1/2.
+
+    All five-windows are found with array slices, per direction in the reference's order
+    (horizontal, vertical, down-right, down-left).  The cells are then visited in row-major
+    order.  At each occupied cell, the first direction whose window is full decides: an
+    overline of player 1 under renju skips the cell, anything else returns the player.
+    Returns 1 or 2 for a win, 3 for a full board without a five, 0 otherwise."""
+    b = np.asarray(board, dtype=np.int64)
+    bs = b.shape[0]
+    dirs = ((0, 1), (1, 0), (1, 1), (1, -1))
+    full = np.zeros((4, bs, bs), bool)
+    over = np.zeros((4, bs, bs), bool)
+
+    def at(r, c):
+        return b[r, c] if 0 <= r < bs and 0 <= c < bs else -1
+
+    for d, (dr, dc) in enumerate(dirs):
+        for r in range(bs):
+            for c in range(bs):
+                re, ce = r + 4 * dr, c + 4 * dc
+                if not (re < bs and 0 <= ce < bs) or b[r, c] == 0:
+                    continue
+                cells = [b[r + k * dr, c + k * dc] for k in range(5)]
+                if all(x == b[r, c] for x in cells):
+                    full[d, r, c] = True
+                    over[d, r, c] = (at(r + 5 * dr, c + 5 * dc) == b[r, c]
+                                     or at(r - dr, c - dc) == b[r, c])
+    for r in range(bs):
+        for c in range(bs):
+            ds = np.flatnonzero(full[:, r, c])
+            if len(ds) == 0:
+                continue
+            d = int(ds[0])
+            if renju and b[r, c] == 1 and over[d, r, c]:
+                continue
+            return int(b[r, c])
+    return 3 if np.all(b != 0) else 0
+
+
 def board_legal(root_empty, path_actions, pass_action=None):
     taken = {a for a in path_actions if a != pass_action}
     return [a for a in root_empty if a not in taken]
 
 
 def np_wave(tree: NpTree, W: int, max_depth: int, legal_of, pol_rows, vals, policy="full",
-            noise=None, eps=0.0, root_positive=False):
+            noise=None, eps=0.0, root_positive=False, terminal_of=None):
     """One wave: W sequential select_paths, unique leaves in first-occurrence order evaluated
-    from pol_rows/vals (row u for the u-th unique leaf), expansion, then backup in order."""
+    from pol_rows/vals (row u for the u-th unique leaf), expansion, then backup in order.
+    terminal_of(path actions), when given, names the terminal leaves, which are evaluated and
+    backed up but not expanded (optimized_wave_search.py:374-376); the root never is."""
     paths = [tree.select_path(max_depth) for _ in range(W)]
     leaves = [p[-1] for p in paths]
     uniq = []
@@ -180,7 +223,10 @@ def np_wave(tree: NpTree, W: int, max_depth: int, legal_of, pol_rows, vals, poli
         if tree.expanded[leaf]:
             continue
         path = paths[leaves.index(leaf)]
-        legal = legal_of([int(tree.action[x]) for x in path[1:]])
+        pacts = [int(tree.action[x]) for x in path[1:]]
+        if terminal_of is not None and pacts and terminal_of(pacts):
+            continue
+        legal = legal_of(pacts)
         if not legal:
             continue
         root_visits = int(tree.N[0]) - tree.vli * W

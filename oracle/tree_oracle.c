@@ -35,6 +35,10 @@
 #define ORC_EXPAND_REFERENCE_PW 1
 #define ORC_SIGN_LEAF_POSITIVE 0
 #define ORC_SIGN_ROOT_POSITIVE 1
+#define ORC_RULE_FREESTYLE 0
+#define ORC_RULE_RENJU 1
+#define ORC_TERM_NONE 0
+#define ORC_TERM_DRAW 3
 
 typedef struct orc_forest {
   /* shape */
@@ -61,6 +65,11 @@ typedef struct orc_forest {
   int32_t *ulegal, *uexpanded;
   float *policy, *values; /* [T*max_wave*A] (legal slots written), [T*max_wave] */
   int32_t *seen;          /* [T*cap] unique-leaf index of a node during a wave, else -1 */
+  /* Gomoku rules (terminal leaves are not expanded); off unless orc_set_gomoku_rules */
+  int rules_on, rule;
+  int8_t *root_boards;    /* [T*A] 0 empty, 1/2 stones */
+  int32_t *root_player;   /* [T] player of the first path move */
+  int32_t *uterm;         /* [T*max_wave] ORC_TERM_* of each unique leaf */
 } orc_forest;
 
 /* ---- synthetic workload (same specification as the device code) ---------------------- */
@@ -232,10 +241,12 @@ orc_forest *orc_create(int T, int cap, int A, int game, int min_legal, int max_l
   f->uexpanded = (int32_t *)calloc(nw, 4);
   f->policy = (float *)calloc(nw * (size_t)A, 4);
   f->values = (float *)calloc(nw, 4);
+  f->uterm = (int32_t *)calloc(nw, 4);
   f->seen = (int32_t *)malloc(nc * 4);
   if (f->seen) memset(f->seen, 0xFF, nc * 4);
   if (!f->seen || !f->N || !f->W || !f->P || !f->parent || !f->first || !f->nchild || !f->action ||
-      !f->expanded || !f->children || !f->child_actions || !f->paths || !f->policy) {
+      !f->expanded || !f->children || !f->child_actions || !f->paths || !f->policy ||
+      !f->uterm) {
     return NULL;
   }
   return f;
@@ -247,7 +258,7 @@ void orc_destroy(orc_forest *f) {
                   f->children, f->child_actions, f->num_nodes, f->num_edges, f->root_keys,
                   f->root_legal, f->paths, f->path_len, f->leaves, f->sim_uid, f->uleaf,
                   f->ufirst, f->ucount, f->ukey, f->ulegal, f->uexpanded, f->policy, f->values,
-                  f->root_noise, f->seen};
+                  f->root_noise, f->seen, f->uterm, f->root_boards, f->root_player};
   for (size_t i = 0; i < sizeof ptrs / sizeof ptrs[0]; ++i) free(ptrs[i]);
   free(f);
 }
@@ -272,6 +283,120 @@ void orc_set_roots(orc_forest *f, const uint64_t *keys, const uint32_t *legal,
     f->root_noise = (double *)malloc(sizeof(double) * (size_t)f->T * f->A);
     memcpy(f->root_noise, noise, sizeof(double) * (size_t)f->T * f->A);
   }
+}
+
+/* Gomoku rules for the leaves of later waves: boards [T*A] (0 empty, 1/2 stones) are the root
+   positions; root_player[T] is the player of the first path move, or NULL for 1 when the root
+   board holds an even number of stones, else 2 (mcts.py:1506).  enable=0 switches them off. */
+void orc_set_gomoku_rules(orc_forest *f, int enable, int rule, const int8_t *boards,
+                          const int32_t *root_player) {
+  free(f->root_boards);
+  free(f->root_player);
+  f->root_boards = NULL;
+  f->root_player = NULL;
+  f->rules_on = 0;
+  if (!enable) return;
+  f->rule = rule;
+  f->root_boards = (int8_t *)malloc((size_t)f->T * f->A);
+  f->root_player = (int32_t *)malloc(sizeof(int32_t) * (size_t)f->T);
+  memcpy(f->root_boards, boards, (size_t)f->T * f->A);
+  for (int t = 0; t < f->T; ++t) {
+    if (root_player) {
+      f->root_player[t] = root_player[t];
+    } else {
+      int stones = 0;
+      for (int a = 0; a < f->A; ++a) stones += boards[(size_t)t * f->A + a] != 0;
+      f->root_player[t] = stones % 2 == 0 ? 1 : 2;
+    }
+  }
+  f->rules_on = 1;
+}
+
+/* FastTerminalChecker._check_gomoku_terminal_cpu without last_move
+   (python/mcts/utils/fast_terminal_check.py:132-232), literally: for each occupied cell in
+   row-major order, the horizontal, vertical, '\' and '/' windows of five starting there are
+   tried in turn; a renju overline of player 1 skips the rest of the cell (the reference's
+   `continue` of its column loop); the first full window returns its player.  A full board
+   without a five is a draw.  Returns the player (1, 2), ORC_TERM_DRAW or ORC_TERM_NONE. */
+int orc_gomoku_terminal(const int8_t *board, int bs, int rule) {
+  const int renju = rule == ORC_RULE_RENJU;
+#define CELL(r, c) board[(r) * bs + (c)]
+  for (int row = 0; row < bs; ++row) {
+    for (int col = 0; col < bs; ++col) {
+      const int player = CELL(row, col);
+      if (player == 0) continue;
+      int skip = 0;
+      /* horizontal */
+      if (col <= bs - 5) {
+        int all = 1;
+        for (int i = 0; i < 5; ++i) all &= CELL(row, col + i) == player;
+        if (all) {
+          if (renju && player == 1) {
+            if (col + 5 < bs && CELL(row, col + 5) == player) skip = 1;
+            else if (col > 0 && CELL(row, col - 1) == player) skip = 1;
+          }
+          if (skip) continue;
+          return player;
+        }
+      }
+      /* vertical */
+      if (row <= bs - 5) {
+        int all = 1;
+        for (int i = 0; i < 5; ++i) all &= CELL(row + i, col) == player;
+        if (all) {
+          if (renju && player == 1) {
+            if (row + 5 < bs && CELL(row + 5, col) == player) skip = 1;
+            else if (row > 0 && CELL(row - 1, col) == player) skip = 1;
+          }
+          if (skip) continue;
+          return player;
+        }
+      }
+      /* diagonal down-right */
+      if (row <= bs - 5 && col <= bs - 5) {
+        int all = 1;
+        for (int i = 0; i < 5; ++i) all &= CELL(row + i, col + i) == player;
+        if (all) {
+          if (renju && player == 1) {
+            if (row + 5 < bs && col + 5 < bs && CELL(row + 5, col + 5) == player) skip = 1;
+            else if (row > 0 && col > 0 && CELL(row - 1, col - 1) == player) skip = 1;
+          }
+          if (skip) continue;
+          return player;
+        }
+      }
+      /* diagonal down-left */
+      if (row <= bs - 5 && col >= 4) {
+        int all = 1;
+        for (int i = 0; i < 5; ++i) all &= CELL(row + i, col - i) == player;
+        if (all) {
+          if (renju && player == 1) {
+            if (row + 5 < bs && col - 5 >= 0 && CELL(row + 5, col - 5) == player) skip = 1;
+            else if (row > 0 && col < bs - 1 && CELL(row - 1, col + 1) == player) skip = 1;
+          }
+          if (skip) continue;
+          return player;
+        }
+      }
+    }
+  }
+  for (int i = 0; i < bs * bs; ++i)
+    if (board[i] == 0) return ORC_TERM_NONE;
+  return ORC_TERM_DRAW;
+#undef CELL
+}
+
+/* terminal code of a leaf reached by the path moves acts[0..np) (np >= 1) */
+static int leaf_terminal(const orc_forest *f, int t, const int *acts, int np) {
+  int8_t board[8192];
+  const int A = f->A;
+  int bs = 0;
+  while ((bs + 1) * (bs + 1) <= A) ++bs;
+  memcpy(board, f->root_boards + (size_t)t * A, (size_t)A);
+  const int rp = f->root_player[t];
+  for (int q = 0; q < np; ++q)
+    if (acts[q] >= 0 && acts[q] < A) board[acts[q]] = (int8_t)(q % 2 == 0 ? rp : 3 - rp);
+  return orc_gomoku_terminal(board, bs, f->rule);
 }
 
 /* CythonLockFreeTree.__cinit__ / reset: one node, N[0]=1, P[0]=1 (pyx:92-100, 537-558) */
@@ -381,6 +506,11 @@ static void leaves_info(orc_forest *f, int t, int W) {
     for (int q = 0; q < np; ++q) k = orc_child_key(k, acts[q]);
     f->ukey[wb + u] = k;
     f->ulegal[wb + u] = legal_list(f, t, acts, np, k, list);
+    f->uterm[wb + u] = ORC_TERM_NONE;
+    if (f->rules_on && np >= 1) {  /* the root itself is never flagged */
+      f->uterm[wb + u] = leaf_terminal(f, t, acts, np);
+      if (f->uterm[wb + u] != ORC_TERM_NONE) f->ulegal[wb + u] = 0;
+    }
   }
 }
 
@@ -428,6 +558,7 @@ static void expand_leaves(orc_forest *f, int t, int W) {
     const int leaf = f->uleaf[wb + u];
     f->uexpanded[wb + u] = 0;
     if (f->expanded[b + leaf]) continue;
+    if (f->uterm[wb + u] != ORC_TERM_NONE) continue; /* terminal: not expanded (:374-376) */
     const int s0 = f->ufirst[wb + u];
     const int np = path_actions(f, t, s0, acts);
     const int n = legal_list(f, t, acts, np, f->ukey[wb + u], list);
@@ -623,5 +754,6 @@ ORC_GET(ucount, int32_t)
 ORC_GET(ukey, uint64_t)
 ORC_GET(ulegal, int32_t)
 ORC_GET(uexpanded, int32_t)
+ORC_GET(uterm, int32_t)
 ORC_GET(policy, float)
 ORC_GET(values, float)

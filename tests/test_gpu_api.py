@@ -31,6 +31,9 @@ def _oracle_for(cfg, boards, noise=None):
     orc.set_params(cfg.c_puct, cfg.virtual_loss, 0 if cfg.expansion_policy == "full" else 1,
                    0 if cfg.backup_sign == "leaf_positive" else 1, 1.0, cfg.dirichlet_epsilon)
     orc.set_roots(games.root_keys(cfg.seed, T), games.legal_masks(model, boards, T), noise)
+    if model.kind == "gomoku" and cfg.gomoku_rules != "off":
+        b = boards if boards is not None else np.zeros((T, cfg.board_size, cfg.board_size), np.int8)
+        orc.set_gomoku_rules(b, 1 if cfg.gomoku_rules == "renju" else 0)
     return orc
 
 

@@ -22,7 +22,7 @@ def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("omq_select", "omq_expand", "omq_backup", "omq_forest_reset", "omq_leaf_info",
               "omq_synthetic_evaluate", "omq_paths_backup", "omq_virtual_loss",
-              "omq_last_error", "omq_abi_version"):
+              "omq_gomoku_terminal", "omq_last_error", "omq_abi_version"):
         assert n in names
 
 
@@ -95,6 +95,20 @@ def test_invalid_wave_arguments_rejected():
     assert lib.omq_backup(ctypes.byref(f), ctypes.byref(w), 4, 3.0, 0, 9, None) == _lib.OMQ_E_ARG
     assert lib.omq_paths_backup(ctypes.byref(f), None, None, None, None, 0, 4, 0, None) == 0
     assert lib.omq_virtual_loss(ctypes.byref(f), None, None, -1, 3, None) == _lib.OMQ_E_ARG
+    # gomoku terminal check: square board forests only, a board array, a known rule
+    assert lib.omq_gomoku_terminal(ctypes.byref(f), ctypes.byref(w), None, None, 0, None,
+                                   None) == _lib.OMQ_E_ARG
+    assert "root_boards" in lib.omq_last_error().decode()
+    assert lib.omq_gomoku_terminal(ctypes.byref(f), ctypes.byref(w), 8, None, 5, None,
+                                   None) == _lib.OMQ_E_ARG
+    assert "rule" in lib.omq_last_error().decode()
+    g = _forest(num_actions=24)
+    assert lib.omq_gomoku_terminal(ctypes.byref(g), ctypes.byref(w), 8, None, 0, None,
+                                   None) == _lib.OMQ_E_ARG
+    assert "square" in lib.omq_last_error().decode()
+    g = _forest(game=_lib.OMQ_GAME_GO, num_actions=26)
+    assert lib.omq_gomoku_terminal(ctypes.byref(g), ctypes.byref(w), 8, None, 0, None,
+                                   None) == _lib.OMQ_E_ARG
 
 
 def test_missing_library_fails_loudly(tmp_path):
