@@ -187,6 +187,83 @@ def run(args) -> dict:
             torch.cuda.synchronize(dev)
             replay = ev.calls
         out["cpu_baseline"], out["parity_full_size"] = cpu_baseline(wl, eng, args, replay)
+    if args.next_rows != "skip":
+        out["next_rows"] = next_rows(wl, eng, ev)
+    return out
+
+
+def next_rows(wl, eng, ev) -> dict:
+    """The operations beside the wave path, timed once on the searched trees (after the
+    parity check, outside the timed region): the Gomoku terminal check of one wave's leaves
+    and the subtree reuse of every tree."""
+    import torch
+
+    from omoknuni_quantum_amd import _lib
+
+    out = {}
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if wl.model.kind == "gomoku":
+        # one more wave selected and its leaves looked up; the terminal check is then timed
+        # alone over those leaves (repeated calls give the same result)
+        boards = wl.boards()
+        if boards is None:
+            boards = np.zeros((wl.num_trees, wl.model.board_size, wl.model.board_size), np.int8)
+        eng.set_gomoku_rules(boards, _lib.OMQ_RULE_FREESTYLE)
+        eng.select(wl.wave_size)
+        eng.leaf_info()
+        reps = 20
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            eng.leaf_info_terminal_only()
+        stop.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(stop) * 1e3 / reps
+        nu = int(eng.ucount.sum().item())
+        plen = eng.path_len.view(eng.T, eng.MW)
+        first = eng.ufirst.view(eng.T, eng.MW).to(torch.int64).clamp_(0, eng.MW - 1)
+        ucnt = eng.ucount.to(torch.int64)
+        valid = torch.arange(eng.MW, device=eng.device)[None, :] < ucnt[:, None]
+        moves = int(torch.where(valid, torch.gather(plen, 1, first) - 1, 0).sum().item())
+        nterm = int((torch.where(valid, eng.uterm.view(eng.T, eng.MW), 0) != 0).sum().item())
+        # per unique leaf: its root board (A bytes), 4 B per path move, 8 B written
+        ab = nu * (wl.model.num_actions + 8) + 4 * moves
+        out["gomoku_terminal"] = {
+            "us_per_launch": round(us, 3), "unique_leaves": nu, "terminal_leaves": nterm,
+            "algorithmic_bytes": ab, "algorithmic_GBps": round(ab / (us * 1e-6) / 1e9, 2),
+            "launch": f"one wave of {wl.wave_size} simulations per tree after the timed "
+                      f"searches, freestyle rule, {reps} launches averaged"}
+        eng.set_gomoku_rules(None)
+    # subtree reuse: every tree moves to its most visited root child
+    T, cap = eng.T, eng.cap
+    roots = torch.arange(T, device=eng.device, dtype=torch.int64) * cap
+    first = eng.first[roots].to(torch.int64)
+    k = eng.nchild[roots].to(torch.int64)
+    new_roots = np.full(T, -1, np.int32)
+    kmax = int(k.max().item())
+    if kmax > 0:
+        j = torch.arange(kmax, device=eng.device)
+        idx = roots[:, None] + first[:, None] + 1 + j[None, :]
+        valid = j[None, :] < k[:, None]
+        n = torch.where(valid, eng.N[torch.where(valid, idx, roots[:, None])], -1)
+        best = n.argmax(dim=1)
+        new_roots = (first + 1 + best).to(torch.int32).cpu().numpy()
+        new_roots[(k == 0).cpu().numpy()] = -1
+    before = int(eng.num_nodes.sum().item())
+    eng.shift_roots(np.zeros(T, np.int32))  # workspace allocated outside the timed launch
+    torch.cuda.synchronize()
+    start.record()
+    eng.shift_roots(new_roots)
+    stop.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) * 1e3
+    kept = int(eng.num_nodes.sum().item())
+    # per kept node: 24 B read (row, N, W, P, action) + 28 B written (the compacted record)
+    ab = 52 * kept
+    out["shift_root"] = {
+        "us_per_launch": round(us, 3), "nodes_before": before, "nodes_kept": kept,
+        "algorithmic_bytes": ab, "algorithmic_GBps": round(ab / (us * 1e-6) / 1e9, 2),
+        "launch": "one launch, every tree moves to its most visited root child"}
     return out
 
 
@@ -280,6 +357,8 @@ def main():
                     help="trees of the CPU baseline sample (0 = all)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads of the CPU baseline (0 = min(16, cores, trees))")
+    ap.add_argument("--next-rows", choices=("auto", "skip"), default="auto",
+                    help="also time the Gomoku terminal check and the subtree reuse once")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one plain device copy of this size before the search (counter "
                          "calibration for --pmc profiles)")

@@ -77,6 +77,9 @@ extern "C" {
 #define OMQ_TERM_WIN2 2  /* player 2 has five */
 #define OMQ_TERM_DRAW 3  /* full board without five */
 
+/* workspace of omq_shift_root: int32 entries per node of capacity, per tree */
+#define OMQ_SHIFT_WORKSPACE_PER_NODE 8
+
 /* limits of this build */
 #define OMQ_MAX_WAVE 4096   /* simulations per tree per wave */
 #define OMQ_MAX_ROW 512     /* children per node (a selection row is held in registers) */
@@ -223,6 +226,26 @@ int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
 int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
                         const int32_t* root_player, int32_t rule, int32_t* uterminal,
                         void* stream);
+
+/* Subtree reuse.  For every tree t with 0 < new_roots[t] < num_nodes[t], node new_roots[t]
+ * becomes the root, and its subtree is kept. Other values leave tree t unchanged.
+ * - Numbering.  Kept nodes are renumbered breadth-first from the new root, children in row
+ *   order. This is the order in which CSRTree.shift_root assigns the new indices.
+ * - Copied fields.  N, W and P are copied, and parents and rows are remapped. The new root has
+ *   parent -1 and action -1 and keeps its N, W and P.
+ * - Dropped nodes.  Every other node is dropped, and num_nodes[t] becomes the subtree size.
+ * - Layout.  Children stay consecutive (child of edge e = node e+1), so the tree is ready for
+ *   the next omq_select.
+ * - Inconsistent trees.  A tree with a row outside [0, num_nodes) is left unchanged.
+ * - Workspace.  A device array of at least
+ *   OMQ_SHIFT_WORKSPACE_PER_NODE * num_trees * capacity int32 entries, owned by the caller.
+ * The caller updates what lives outside the forest arrays: the root key, the root legal mask
+ * and the root board.
+ * Replaces CSRTree.shift_root (python/mcts/gpu/csr_tree.py:1020-1229) as used by
+ * TreeOperations.apply_subtree_reuse (python/mcts/core/tree_operations.py:53-133) and the
+ * reuse kernels of mcts_kernels.cu:2095-2337. */
+int omq_shift_root(const omq_forest* f, const int32_t* new_roots, int32_t* workspace,
+                   int64_t workspace_ints, void* stream);
 
 /* Reference-style path backup over an explicit path matrix (no group log needed):
  * paths[b*max_depth + d], d < min(path_len[b], max_depth), root first; values[b] is the leaf

@@ -30,6 +30,7 @@ STAT_NAMES = [
 OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT = 1, 2
 OMQ_RULE_FREESTYLE, OMQ_RULE_RENJU = 0, 1
 OMQ_TERM_NONE, OMQ_TERM_WIN1, OMQ_TERM_WIN2, OMQ_TERM_DRAW = 0, 1, 2, 3
+OMQ_SHIFT_WORKSPACE_PER_NODE = 8
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -70,6 +71,7 @@ SIGNATURES = {
     "omq_paths_backup": (ctypes.c_int, [_FP, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "omq_virtual_loss": (ctypes.c_int, [_FP, _p, _p, _i32, _i32, _p]),
     "omq_gomoku_terminal": (ctypes.c_int, [_FP, _WP, _p, _p, _i32, _p, _p]),
+    "omq_shift_root": (ctypes.c_int, [_FP, _p, _p, ctypes.c_int64, _p]),
 }
 
 

@@ -100,6 +100,7 @@ class WaveEngine:
         self.rule: int | None = None
         self.root_boards: torch.Tensor | None = None
         self.root_player: torch.Tensor | None = None
+        self._shift_ws: torch.Tensor | None = None  # subtree-reuse workspace, made on first use
 
         f = _lib.OmqForest()
         f.num_trees, f.capacity, f.num_actions, f.game = T, cap, A, model.code
@@ -179,6 +180,11 @@ class WaveEngine:
         self._check(self.lib.omq_leaf_info(self.forest_ref, self.wave_ref, self.stream_handle()),
                     "omq_leaf_info")
         if self.rule is not None:
+            self.leaf_info_terminal_only()
+
+    def leaf_info_terminal_only(self) -> None:
+        """The Gomoku terminal check alone, over the unique leaves already looked up."""
+        if self.rule is not None:
             self._check(self.lib.omq_gomoku_terminal(
                 self.forest_ref, self.wave_ref, self.root_boards.data_ptr(),
                 None if self.root_player is None else self.root_player.data_ptr(), self.rule,
@@ -196,6 +202,21 @@ class WaveEngine:
         self._check(self.lib.omq_backup(self.forest_ref, self.wave_ref, wave_size, p.virtual_loss,
                                         p.sign_mode, p.w_mode, self.stream_handle()),
                     "omq_backup")
+
+    def shift_roots(self, new_roots) -> None:
+        """Subtree reuse (CSRTree.shift_root): node new_roots[t] of tree t becomes its root
+        and keeps its subtree, renumbered breadth-first; -1 (or 0) leaves a tree unchanged.
+        Root keys, legal masks and boards are the caller's to update."""
+        nr = np.ascontiguousarray(new_roots, dtype=np.int32).reshape(-1)
+        if nr.size != self.T:
+            raise ValueError(f"{nr.size} new roots for {self.T} trees")
+        need = _lib.OMQ_SHIFT_WORKSPACE_PER_NODE * self.T * self.cap
+        if self._shift_ws is None or self._shift_ws.numel() < need:
+            self._shift_ws = torch.empty(need, dtype=torch.int32, device=self.device)
+        d = torch.from_numpy(nr).to(self.device)
+        self._check(self.lib.omq_shift_root(self.forest_ref, d.data_ptr(),
+                                            self._shift_ws.data_ptr(), self._shift_ws.numel(),
+                                            self.stream_handle()), "omq_shift_root")
 
     def _tree_of(self, tree_of, n: int):
         if tree_of is None:

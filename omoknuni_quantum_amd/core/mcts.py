@@ -135,23 +135,36 @@ class MCTS:
             return
         keys = games.root_keys(self.config.seed, T)
         legal = games.legal_masks(self.model, boards, T)
-        noise = None
-        if self.config.dirichlet_epsilon > 0:
-            if self.model.is_board:
-                counts = games.legal_counts(self.model, legal)
-            else:
-                counts = np.array([games.sparse_root_count(self.model, int(k)) for k in keys])
-            noise = games.dirichlet_noise(self.model, counts, float(self.config.dirichlet_alpha),
-                                          self.config.seed + 7919 * (self._search_count + 1))
-        self.engine.set_roots(keys, legal, noise)
+        self._install_roots(keys, legal, boards)
+        self.engine.reset()
+
+    def _root_noise(self, keys: np.ndarray, legal: np.ndarray) -> Optional[np.ndarray]:
+        if self.config.dirichlet_epsilon <= 0:
+            return None
+        if self.model.is_board:
+            counts = games.legal_counts(self.model, legal)
+        else:
+            counts = np.array([games.sparse_root_count(self.model, int(k)) for k in keys])
+        return games.dirichlet_noise(self.model, counts, float(self.config.dirichlet_alpha),
+                                     self.config.seed + 7919 * (self._search_count + 1))
+
+    def _install_roots(self, keys: np.ndarray, legal: np.ndarray,
+                       boards: Optional[np.ndarray]) -> None:
+        """Root inputs of every tree on the device (keys, legal masks, noise, Gomoku boards)
+        and the evaluator built on them; the tree arrays are left as they are."""
+        T = self.engine.T
+        self._root_keys_host = np.asarray(keys, dtype=np.uint64).copy()
+        self._root_legal_host = np.asarray(legal, dtype=np.uint32).copy()
+        self._root_boards_host = None if boards is None else np.asarray(boards, np.int8).copy()
+        self.engine.set_roots(keys, legal, self._root_noise(keys, legal))
         rule = self._gomoku_rule()
         if rule is not None:
             b = boards if boards is not None else np.zeros(
                 (T, self.config.board_size, self.config.board_size), np.int8)
             self.engine.set_gomoku_rules(b, rule)
-        self.engine.reset()
-        self._roots_key = key
-        self._boards = None if boards is None else torch.from_numpy(boards).to(self.device)
+        self._roots_key = b"" if boards is None else np.ascontiguousarray(boards, np.int8).tobytes()
+        self._boards = None if boards is None else torch.from_numpy(
+            np.ascontiguousarray(boards, np.int8)).to(self.device)
         self._eval = self._make_evaluator()
 
     def _gomoku_rule(self) -> Optional[int]:
@@ -234,14 +247,81 @@ class MCTS:
         return action
 
     def update_root(self, action: int, new_state: Any = None) -> None:
-        """mcts.py:1205-1245.  Validates the action; subtree reuse is not part of this build,
-        so the tree is reset (the reference's fallback, _efficient_tree_reset) and the new
-        state, if given, becomes the root."""
-        if action < 0 or action >= self.action_size:
-            raise ValueError(f"Invalid action {action}. Must be in range [0, {self.action_size})")
+        """mcts.py:1205-1245.  Validates the action, then reuses the subtree of the root's
+        child for `action` when enable_subtree_reuse is set and that child has at least
+        subtree_reuse_min_visits visits (default 10; tree_operations.py:53-133).  Otherwise
+        the tree is reset (_efficient_tree_reset) and the new state, if given, becomes the
+        root."""
+        if self.engine.T != 1:
+            raise ValueError("update_root() drives one tree; use update_roots() with num_trees > 1")
+        self.update_roots([action], None if new_state is None else np.asarray(new_state)[None])
+
+    def update_roots(self, actions, new_states: Any = None) -> bool:
+        """update_root for every tree at once (actions[t] played in tree t).  Returns whether
+        the subtrees were reused (all trees or none)."""
+        actions = [int(a) for a in np.asarray(actions).reshape(-1)]
+        if len(actions) != self.engine.T:
+            raise ValueError(f"{len(actions)} actions for {self.engine.T} trees")
+        for a in actions:
+            if a < 0 or a >= self.action_size:
+                raise ValueError(f"Invalid action {a}. Must be in range [0, {self.action_size})")
+        boards = None if new_states is None else self._states_array(new_states)
+        if self.config.enable_subtree_reuse and self._roots_key is not None:
+            kept = self._reuse_subtrees(actions, boards)
+            if kept is not None:
+                self.stats["tree_reuse_count"] += 1
+                self.stats["tree_reuse_nodes"] += kept
+                return True
         self._roots_key = None
-        if new_state is not None:
-            self._set_roots(self._states_array(np.asarray(new_state)[None]))
+        self.engine.reset()
+        if boards is not None:
+            self._set_roots(boards)
+        return False
+
+    def _reuse_subtrees(self, actions, boards: Optional[np.ndarray]) -> Optional[int]:
+        """Shift every tree's root to its child for actions[t] (CSRTree.shift_root on the
+        device).  None, with nothing changed, when some tree lacks that child or the child has
+        fewer than subtree_reuse_min_visits visits."""
+        eng = self.engine
+        T, cap = eng.T, eng.cap
+        min_visits = int(self.config.extra.get("subtree_reuse_min_visits", 10))
+        roots = torch.arange(T, device=eng.device, dtype=torch.int64) * cap
+        first = eng.first[roots].cpu().numpy()
+        k = eng.nchild[roots].cpu().numpy()
+        new_roots = np.full(T, -1, np.int32)
+        for t, a in enumerate(actions):
+            if k[t] <= 0:
+                return None
+            lo = t * cap + int(first[t]) + 1
+            acts = eng.action[lo:lo + int(k[t])].cpu().numpy()
+            hit = np.flatnonzero(acts == a)
+            if hit.size == 0:
+                return None
+            node = int(first[t]) + 1 + int(hit[0])
+            if int(eng.N[t * cap + node].item()) < min_visits:
+                return None
+            new_roots[t] = node
+        eng.shift_roots(new_roots)
+        keys = np.array([games.child_key(int(key), a)
+                         for key, a in zip(self._root_keys_host, actions)], np.uint64)
+        legal = self._root_legal_host.copy()
+        if self.model.is_board:
+            pass_action = self.action_size - 1 if self.model.kind == "go" else -1
+            for t, a in enumerate(actions):
+                if a != pass_action:  # Go's pass stays legal
+                    legal[t, a // 32] &= np.uint32(~(1 << (a % 32)) & 0xFFFFFFFF)
+            if boards is None:
+                prev = self._root_boards_host
+                if prev is None:
+                    bs = self.config.board_size
+                    prev = np.zeros((T, bs, bs), np.int8)
+                boards = prev.copy()
+                for t, a in enumerate(actions):
+                    flat = boards[t].reshape(-1)
+                    if a < flat.size:  # Go's pass occupies no cell
+                        flat[a] = 1 if int((boards[t] != 0).sum()) % 2 == 0 else 2
+        self._install_roots(keys, legal, boards)
+        return int(eng.num_nodes.sum().item())
 
     def update_with_move(self, move: int) -> None:
         self.update_root(move, None)

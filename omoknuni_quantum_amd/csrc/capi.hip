@@ -25,6 +25,8 @@ hipError_t launch_paths_backup(const omq_forest& f, const int32_t* paths, const 
 hipError_t launch_virtual_loss(const omq_forest& f, const int32_t* nodes, const int32_t* tree_of,
                                int count, int delta, hipStream_t st);
 hipError_t launch_reset(const omq_forest& f, hipStream_t st);
+hipError_t launch_shift_root(const omq_forest& f, const int32_t* new_roots, int32_t* ws,
+                             hipStream_t st);
 hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const int8_t* boards,
                                   const int32_t* root_player, int rule, int bs, int32_t* uterm,
                                   hipStream_t st);
@@ -176,6 +178,19 @@ int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* ro
   return hip_status(omq::launch_gomoku_terminal(*f, *w, root_boards, root_player, rule, bs,
                                                 uterminal, (hipStream_t)stream),
                     "omq_gomoku_terminal");
+}
+
+int omq_shift_root(const omq_forest* f, const int32_t* new_roots, int32_t* workspace,
+                   int64_t workspace_ints, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  if (!new_roots || !workspace) return fail(OMQ_E_ARG, "new_roots and workspace are required");
+  const int64_t need = (int64_t)OMQ_SHIFT_WORKSPACE_PER_NODE * f->num_trees * f->capacity;
+  if (workspace_ints < need)
+    return fail(OMQ_E_ARG, "workspace holds %lld int32, omq_shift_root needs %lld",
+                (long long)workspace_ints, (long long)need);
+  return hip_status(omq::launch_shift_root(*f, new_roots, workspace, (hipStream_t)stream),
+                    "omq_shift_root");
 }
 
 int omq_synthetic_evaluate(const omq_forest* f, const omq_wave* w, float logit_scale,

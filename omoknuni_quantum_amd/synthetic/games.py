@@ -33,6 +33,11 @@ def splitmix64(x: int) -> int:
     return z ^ (z >> 31)
 
 
+def child_key(key: int, action: int) -> int:
+    """Key of the child reached from a node with key `key` by `action`."""
+    return splitmix64((key ^ (((action + 1) * GOLDEN) & MASK64)) & MASK64)
+
+
 def root_keys(seed: int, num_trees: int) -> np.ndarray:
     return np.array([splitmix64((seed ^ t) & MASK64) for t in range(num_trees)], dtype=np.uint64)
 

@@ -66,6 +66,7 @@ def load() -> ctypes.CDLL:
         "orc_sum64d": (d, [P, i]),
         "orc_set_gomoku_rules": (None, [P, i, i, P, P]),
         "orc_gomoku_terminal": (i, [P, i, i]),
+        "orc_shift_root": (i, [P, i, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -139,6 +140,11 @@ class Oracle:
         self._rp = None if root_player is None else np.ascontiguousarray(root_player, np.int32)
         self.lib.orc_set_gomoku_rules(self.f, 1, rule, self._boards.ctypes.data,
                                       None if self._rp is None else self._rp.ctypes.data)
+
+    def shift_root(self, t: int, node: int) -> int:
+        """Subtree reuse on tree t (CSRTree.shift_root); returns the kept node count (0 when
+        the tree is unchanged)."""
+        return int(self.lib.orc_shift_root(self.f, t, node))
 
     def write(self, name: str, values, offset: int = 0) -> None:
         """Overwrite entries [offset, offset + len(values)) of an oracle array (crafted states

@@ -116,6 +116,50 @@ class NpTree:
             self.children[fe + j] = c
         return True
 
+    def shift_root(self, r: int) -> dict:
+        """CSRTree.shift_root (python/mcts/gpu/csr_tree.py:1020-1229): breadth-first from r
+        over each node's children (its row, in order), new index = discovery order; node
+        data copied, parents remapped, the root's parent and action cleared; rows rebuilt
+        node by node in the new order.  Returns the old -> new mapping."""
+        if r == 0 or not (0 < r < self.num_nodes):
+            return {i: i for i in range(self.num_nodes)}
+        order, new_of = [r], {r: 0}
+        head = 0
+        while head < len(order):
+            cur = order[head]
+            head += 1
+            f, k = int(self.first[cur]), int(self.nchild[cur])
+            for ch in (self.children[f:f + k] if f >= 0 else []):
+                ch = int(ch)
+                if ch not in new_of:
+                    new_of[ch] = len(order)
+                    order.append(ch)
+        old = {k: getattr(self, k)[order].copy() for k in ("N", "W", "P", "action", "expanded")}
+        old_par = self.parent[order].copy()
+        rows = [[new_of[int(c)] for c in (self.children[int(self.first[o]):int(self.first[o]) +
+                                                          int(self.nchild[o])]
+                                          if self.first[o] >= 0 else [])] for o in order]
+        n = len(order)
+        n_old = self.num_nodes
+        # the reference resets the whole tree before writing the kept nodes back
+        self.N[:n_old], self.W[:n_old], self.P[:n_old] = 0, F(0.0), F(0.0)
+        self.parent[:n_old], self.first[:n_old], self.nchild[:n_old] = -1, -1, 0
+        self.action[:n_old], self.expanded[:n_old], self.children[:n_old] = 0, False, 0
+        for k, v in old.items():
+            getattr(self, k)[:n] = v
+        self.parent[:n] = [new_of.get(int(p), -1) if p >= 0 else -1 for p in old_par]
+        self.parent[0] = -1
+        self.action[0] = -1
+        e = 0
+        for i, row in enumerate(rows):
+            self.first[i] = e if row else -1
+            self.nchild[i] = len(row)
+            for c in row:
+                self.children[e] = c
+                e += 1
+        self.num_nodes, self.num_edges = n, e
+        return new_of
+
     def backup(self, path, v: float, root_positive: bool = False):
         L = len(path)
         v = F(v)

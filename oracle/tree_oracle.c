@@ -399,6 +399,106 @@ static int leaf_terminal(const orc_forest *f, int t, const int *acts, int np) {
   return orc_gomoku_terminal(board, bs, f->rule);
 }
 
+/* CSRTree.shift_root (python/mcts/gpu/csr_tree.py:1020-1229) on tree t: breadth-first queue
+   from node r over the children in row order, visited-marked; new index = queue position;
+   N, W, P, expanded flag and action copied, parents remapped (root: -1, action -1); the edge
+   arrays rebuilt node by node in the new order.  Returns the number of kept nodes (the tree
+   is unchanged and 0 is returned when r is 0 or out of range). */
+int orc_shift_root(orc_forest *f, int t, int r) {
+  const size_t b = (size_t)t * f->cap;
+  const int n_old = f->num_nodes[t];
+  if (r <= 0 || r >= n_old) return 0;
+  int32_t *queue = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_old);
+  int32_t *new_of = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_old);
+  if (!queue || !new_of) {
+    free(queue);
+    free(new_of);
+    return 0;
+  }
+  for (int i = 0; i < n_old; ++i) new_of[i] = -1;
+  int kept = 0, rd = 0;
+  queue[kept] = r;
+  new_of[r] = kept++;
+  while (rd < kept) {
+    const int cur = queue[rd++];
+    if (f->first[b + cur] < 0) continue;
+    for (int j = 0; j < f->nchild[b + cur]; ++j) {
+      const int c = f->children[b + f->first[b + cur] + j];
+      if (new_of[c] < 0) {
+        new_of[c] = kept;
+        queue[kept++] = c;
+      }
+    }
+  }
+  /* copies of the kept nodes in the new order, and their children's new ids row by row,
+     all read before the tree is overwritten */
+  int32_t *N = (int32_t *)malloc(4 * (size_t)kept), *par = (int32_t *)malloc(4 * (size_t)kept);
+  int32_t *act = (int32_t *)malloc(4 * (size_t)kept), *kids = (int32_t *)malloc(4 * (size_t)kept);
+  int32_t *kid_new = (int32_t *)malloc(4 * (size_t)kept);
+  float *W = (float *)malloc(4 * (size_t)kept), *P = (float *)malloc(4 * (size_t)kept);
+  uint8_t *ex = (uint8_t *)malloc((size_t)kept);
+  int nk = 0;
+  for (int i = 0; i < kept; ++i) {
+    const int o = queue[i];
+    N[i] = f->N[b + o];
+    W[i] = f->W[b + o];
+    P[i] = f->P[b + o];
+    ex[i] = f->expanded[b + o];
+    act[i] = f->action[b + o];
+    par[i] = f->parent[b + o] >= 0 ? new_of[f->parent[b + o]] : -1;
+    kids[i] = 0;
+    if (f->first[b + o] < 0) continue;
+    for (int j = 0; j < f->nchild[b + o]; ++j) {
+      const int c = new_of[f->children[b + f->first[b + o] + j]];
+      if (c >= 0 && nk < kept) { /* a child reached earlier from another row is not kept twice */
+        kid_new[nk++] = c;
+        kids[i] += 1;
+      }
+    }
+  }
+  par[0] = -1;
+  act[0] = -1;
+  int e = 0;
+  for (int i = 0; i < kept; ++i) {
+    f->N[b + i] = N[i];
+    f->W[b + i] = W[i];
+    f->P[b + i] = P[i];
+    f->parent[b + i] = par[i];
+    f->action[b + i] = act[i];
+    f->expanded[b + i] = ex[i];
+    f->first[b + i] = kids[i] > 0 ? e : -1;
+    f->nchild[b + i] = kids[i];
+    for (int j = 0; j < kids[i]; ++j, ++e) {
+      f->children[b + e] = kid_new[e];
+      f->child_actions[b + e] = act[kid_new[e]];
+    }
+  }
+  /* the reference resets the tree before writing the kept nodes back: clear the rest */
+  for (int i = kept; i < n_old; ++i) {
+    f->N[b + i] = 0;
+    f->W[b + i] = 0.0f;
+    f->P[b + i] = 0.0f;
+    f->parent[b + i] = -1;
+    f->first[b + i] = -1;
+    f->nchild[b + i] = 0;
+    f->action[b + i] = 0;
+    f->expanded[b + i] = 0;
+  }
+  f->num_nodes[t] = kept;
+  f->num_edges[t] = e;
+  free(N);
+  free(par);
+  free(act);
+  free(kids);
+  free(kid_new);
+  free(W);
+  free(P);
+  free(ex);
+  free(queue);
+  free(new_of);
+  return kept;
+}
+
 /* CythonLockFreeTree.__cinit__ / reset: one node, N[0]=1, P[0]=1 (pyx:92-100, 537-558) */
 void orc_reset_tree(orc_forest *f, int t) {
   size_t b = (size_t)t * f->cap;
