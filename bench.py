@@ -178,6 +178,8 @@ def run(args) -> dict:
                             f"{wl.num_trees * wl.wave_size} positions")
         out["tree_op_share"] = round(tree_ms / (tree_ms + eval_ms), 4)
         out["end_to_end_gpu_sims_per_s"] = round(sims / ((tree_ms + eval_ms) / 1e3), 1)
+    if args.graph and wl.evaluator == "synthetic":
+        out["graph"] = graph_replay(wl, eng, ev, args)
     if args.cpu_baseline != "skip":
         replay = None
         if wl.evaluator == "resnet":
@@ -190,6 +192,28 @@ def run(args) -> dict:
     if args.next_rows != "skip":
         out["next_rows"] = next_rows(wl, eng, ev)
     return out
+
+
+def graph_replay(wl, eng, ev, args) -> dict:
+    """The whole search recorded once as a HIP graph and replayed: end-to-end time per search
+    (tree operations and the synthetic evaluator), beside the eager end-to-end time."""
+    import torch
+
+    g = eng.capture_search(wl.num_simulations, wl.wave_size, ev)
+    for _ in range(args.warmup):
+        g.replay()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    return {"ms_per_search": round(ms, 4),
+            "end_to_end_sims_per_s": round(wl.num_trees * wl.num_simulations / (ms / 1e3), 1),
+            "what": "select, leaf info, synthetic evaluator, expand and backup of every wave "
+                    "of one search, replayed from one HIP graph"}
 
 
 def next_rows(wl, eng, ev) -> dict:
@@ -357,6 +381,8 @@ def main():
                     help="trees of the CPU baseline sample (0 = all)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads of the CPU baseline (0 = min(16, cores, trees))")
+    ap.add_argument("--graph", action="store_true",
+                    help="also time the search replayed from one HIP graph")
     ap.add_argument("--next-rows", choices=("auto", "skip"), default="auto",
                     help="also time the Gomoku terminal check and the subtree reuse once")
     ap.add_argument("--copy-probe-mib", type=int, default=0,

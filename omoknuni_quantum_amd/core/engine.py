@@ -291,6 +291,26 @@ class WaveEngine:
             self.run_wave(w, evaluator, timer)
             done += w
 
+    def capture_search(self, num_simulations: int, wave_size: int, evaluator):
+        """Record one whole search (reset, root expansion, every wave) as a HIP graph; each
+        g.replay() then runs it again with one launch from the host.  The evaluator must be
+        device-native and free of host synchronisation (the synthetic evaluator is).  The
+        search is run once eagerly first, on the capture's side stream, so that every kernel
+        attribute is set before recording."""
+        import torch
+
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.search(num_simulations, wave_size, evaluator)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.search(num_simulations, wave_size, evaluator)
+        torch.cuda.synchronize(self.device)
+        return g
+
     # ---- results ----------------------------------------------------------------------
     def check_status(self) -> None:
         st = int(self.status[0].item())
