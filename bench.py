@@ -258,6 +258,30 @@ def next_rows(wl, eng, ev) -> dict:
             "launch": f"one wave of {wl.wave_size} simulations per tree after the timed "
                       f"searches, freestyle rule, {reps} launches averaged"}
         eng.set_gomoku_rules(None)
+    # per-move root operations: policy rows, a move per tree at temperature 1, root noise
+    def timed(fn, reps=20):
+        fn()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) * 1e3 / reps
+
+    pol = eng.root_policies(device=True)
+    acts = torch.empty(eng.T, dtype=torch.int32, device=eng.device)
+    us_pol = timed(lambda: eng.lib.omq_root_policy(eng.forest_ref, pol.data_ptr(),
+                                                    eng.stream_handle()))
+    us_smp = timed(lambda: eng.lib.omq_sample_actions(eng.forest_ref, pol.data_ptr(), 1.0, 5, 1,
+                                                       acts.data_ptr(), eng.stream_handle()))
+    us_dir = timed(lambda: eng.lib.omq_root_dirichlet(eng.forest_ref, 0.3, 5, 1,
+                                                       eng.noise.data_ptr(), eng.stream_handle()))
+    out["root_ops"] = {
+        "root_policy_us": round(us_pol, 3), "sample_actions_us": round(us_smp, 3),
+        "root_dirichlet_us": round(us_dir, 3), "trees": eng.T, "actions": eng.A,
+        "what": "one launch each over every tree (policy rows, one move per tree at "
+                "temperature 1, Dirichlet(0.3) root noise), 20 launches averaged"}
     # subtree reuse: every tree moves to its most visited root child
     T, cap = eng.T, eng.cap
     roots = torch.arange(T, device=eng.device, dtype=torch.int64) * cap

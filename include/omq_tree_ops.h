@@ -247,6 +247,38 @@ int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* ro
 int omq_shift_root(const omq_forest* f, const int32_t* new_roots, int32_t* workspace,
                    int64_t workspace_ints, void* stream);
 
+/* Root visit-count policy of every tree into policy[t*num_actions + a] (double):
+ * N(child_a) / (sum of the root's children's N). When the root has no children, the policy
+ * is uniform over the action space. When it has children but no visits, it is uniform over
+ * the children's actions.
+ * Replaces MCTS._extract_policy (python/mcts/core/mcts.py:1069-1137). */
+int omq_root_policy(const omq_forest* f, double* policy, void* stream);
+
+/* Move selection per tree from policy rows (as omq_root_policy writes them) into actions[t].
+ * - temperature 0 takes the first maximum.
+ * - Otherwise w_a = p_a^(1/temperature), with w = p at temperature 1 and 0 where p = 0. The
+ *   action is the first a whose normalised cumulative sum of w_a / sum(w) exceeds a uniform
+ *   draw u in [0, 1).
+ * u comes from a SplitMix64 stream keyed by (seed, counter, tree), in place of numpy's global
+ * generator; one (seed, counter) pair gives one reproducible draw per tree. The power is
+ * evaluated as exp(log(p)/T) with the library's own log and exp.
+ * Replaces MCTS.select_action (python/mcts/core/mcts.py:1167-1203). */
+int omq_sample_actions(const omq_forest* f, const double* policy, double temperature,
+                       uint64_t seed, uint64_t counter, int32_t* actions, void* stream);
+
+/* Root Dirichlet noise on the device. Row t of noise ([T*num_actions], double) receives a
+ * Dirichlet(alpha, ..., alpha) draw over the root's L legal actions: entry i belongs to the
+ * i-th legal action (the layout omq_expand reads), and entries i >= L are 0. L is the root
+ * legal mask's popcount for board models and the sparse-model count of the root key otherwise.
+ * - Gamma variates: Marsaglia-Tsang. Shape < 1 is boosted by U^(1/alpha).
+ * - Normal variates: Marsaglia's polar method.
+ * - log and exp: the library's own.
+ * - Uniforms: a SplitMix64 stream keyed by (seed, counter, tree, action index).
+ * Replaces np.random.dirichlet at root expansion (python/mcts/cpu/optimized_wave_search.py:387-392)
+ * and the Dirichlet kernel of mcts_kernels.cu:649-754. */
+int omq_root_dirichlet(const omq_forest* f, double alpha, uint64_t seed, uint64_t counter,
+                       double* noise, void* stream);
+
 /* Reference-style path backup over an explicit path matrix (no group log needed):
  * paths[b*max_depth + d], d < min(path_len[b], max_depth), root first; values[b] is the leaf
  * value; N[x] += 1, W[x] += sign * values[b] with float atomics, the sign taken from the

@@ -72,6 +72,11 @@ SIGNATURES = {
     "omq_virtual_loss": (ctypes.c_int, [_FP, _p, _p, _i32, _i32, _p]),
     "omq_gomoku_terminal": (ctypes.c_int, [_FP, _WP, _p, _p, _i32, _p, _p]),
     "omq_shift_root": (ctypes.c_int, [_FP, _p, _p, ctypes.c_int64, _p]),
+    "omq_root_policy": (ctypes.c_int, [_FP, _p, _p]),
+    "omq_sample_actions": (ctypes.c_int, [_FP, _p, ctypes.c_double, ctypes.c_uint64,
+                                          ctypes.c_uint64, _p, _p]),
+    "omq_root_dirichlet": (ctypes.c_int, [_FP, ctypes.c_double, ctypes.c_uint64,
+                                          ctypes.c_uint64, _p, _p]),
 }
 
 

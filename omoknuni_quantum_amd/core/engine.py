@@ -101,6 +101,7 @@ class WaveEngine:
         self.root_boards: torch.Tensor | None = None
         self.root_player: torch.Tensor | None = None
         self._shift_ws: torch.Tensor | None = None  # subtree-reuse workspace, made on first use
+        self._policy: torch.Tensor | None = None    # root policies [T, A] float64
 
         f = _lib.OmqForest()
         f.num_trees, f.capacity, f.num_actions, f.game = T, cap, A, model.code
@@ -318,26 +319,35 @@ class WaveEngine:
             raise _lib.OmqError(f"a node has more than {_lib.OMQ_MAX_ROW} legal actions; "
                                 "its expansion was refused by the library")
 
-    def root_policies(self) -> np.ndarray:
-        """pi[t, a] = N(child_a) / sum N over root children (mcts.py:1069-1137); uniform over
-        the action space for a tree whose root has no children."""
-        T, cap, A = self.T, self.cap, self.A
-        roots = torch.arange(T, device=self.device, dtype=torch.int64) * cap
-        first = self.first[roots].to(torch.int64)
-        k = self.nchild[roots].to(torch.int64)
-        kmax = int(k.max().item()) if T > 0 else 0
-        pol = torch.zeros((T, A), dtype=torch.float64, device=self.device)
-        if kmax > 0:
-            j = torch.arange(kmax, device=self.device, dtype=torch.int64)
-            valid = j[None, :] < k[:, None]
-            idx = roots[:, None] + first[:, None] + 1 + j[None, :]
-            idx = torch.where(valid, idx, roots[:, None])
-            visits = torch.where(valid, self.N[idx], 0).to(torch.float64)
-            acts = torch.where(valid, self.action[idx], 0).to(torch.int64)
-            pol.scatter_add_(1, acts, visits)
-        tot = pol.sum(dim=1, keepdim=True)
-        out = torch.where(tot > 0, pol / torch.where(tot > 0, tot, 1.0), 1.0 / A)
+    def root_policies(self, device: bool = False):
+        """pi[t, a] = N(child_a) / sum N over the root's children (mcts.py:1069-1137): uniform
+        over the children's actions when they have no visits, uniform over the action space
+        for a root without children.  float64 [T, A], as numpy (or the device tensor)."""
+        if self._policy is None:
+            self._policy = torch.empty((self.T, self.A), dtype=torch.float64, device=self.device)
+        self._check(self.lib.omq_root_policy(self.forest_ref, self._policy.data_ptr(),
+                                             self.stream_handle()), "omq_root_policy")
+        return self._policy if device else self._policy.cpu().numpy()
+
+    def sample_actions(self, temperature: float, seed: int, counter: int) -> np.ndarray:
+        """One move per tree from the root policies (MCTS.select_action): the first maximum at
+        temperature 0, else a draw from p^(1/T) keyed by (seed, counter, tree)."""
+        pol = self.root_policies(device=True)
+        out = torch.empty(self.T, dtype=torch.int32, device=self.device)
+        self._check(self.lib.omq_sample_actions(self.forest_ref, pol.data_ptr(), float(temperature),
+                                                int(seed) & (2**64 - 1), int(counter) & (2**64 - 1),
+                                                out.data_ptr(), self.stream_handle()),
+                    "omq_sample_actions")
         return out.cpu().numpy()
+
+    def device_root_noise(self, alpha: float, seed: int, counter: int) -> None:
+        """Root Dirichlet noise drawn on the device into the noise rows that omq_expand mixes at
+        root expansion (entry i of row t: i-th legal root action)."""
+        self._check(self.lib.omq_root_dirichlet(self.forest_ref, float(alpha),
+                                                int(seed) & (2**64 - 1), int(counter) & (2**64 - 1),
+                                                self.noise.data_ptr(), self.stream_handle()),
+                    "omq_root_dirichlet")
+        self.has_noise = True
 
     def host_tree(self, t: int) -> dict:
         """Copy of tree t's used prefix (tests and debugging)."""

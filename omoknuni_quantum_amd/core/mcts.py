@@ -139,7 +139,7 @@ class MCTS:
         self.engine.reset()
 
     def _root_noise(self, keys: np.ndarray, legal: np.ndarray) -> Optional[np.ndarray]:
-        if self.config.dirichlet_epsilon <= 0:
+        if self.config.dirichlet_epsilon <= 0 or self.config.root_noise_source == "device":
             return None
         if self.model.is_board:
             counts = games.legal_counts(self.model, legal)
@@ -157,6 +157,9 @@ class MCTS:
         self._root_legal_host = np.asarray(legal, dtype=np.uint32).copy()
         self._root_boards_host = None if boards is None else np.asarray(boards, np.int8).copy()
         self.engine.set_roots(keys, legal, self._root_noise(keys, legal))
+        if self.config.dirichlet_epsilon > 0 and self.config.root_noise_source == "device":
+            self.engine.device_root_noise(float(self.config.dirichlet_alpha), self.config.seed,
+                                          self._search_count + 1)
         rule = self._gomoku_rule()
         if rule is not None:
             b = boards if boards is not None else np.zeros(
@@ -245,6 +248,16 @@ class MCTS:
             action = int(np.random.choice(len(policy), p=p))
         self.last_selected_action = action
         return action
+
+    def select_actions(self, temperature: float = 1.0, seed: Optional[int] = None) -> np.ndarray:
+        """One move per tree from the current root policies, on the device
+        (omq_sample_actions): temperature 0 takes the first maximum, as select_action does;
+        otherwise each tree draws from p^(1/temperature) with a counter-based stream keyed by
+        the seed and a per-call counter (in place of numpy's global generator)."""
+        self._sample_count = getattr(self, "_sample_count", 0) + 1
+        return self.engine.sample_actions(temperature,
+                                          self.config.seed if seed is None else seed,
+                                          self._sample_count)
 
     def update_root(self, action: int, new_state: Any = None) -> None:
         """mcts.py:1205-1245.  Validates the action, then reuses the subtree of the root's

@@ -25,6 +25,9 @@ New fields of this build:
                     reference's game states run it after every move
                     (python/mcts/utils/fast_terminal_check.py:132-232); terminal leaves are
                     not expanded
+  root_noise_source 'host' (numpy PCG64 Dirichlet, per tree seed + t) or 'device'
+                    (omq_root_dirichlet: Marsaglia-Tsang gamma variates from a counter-based
+                    SplitMix64 stream keyed by seed and search count)
 """
 from __future__ import annotations
 
@@ -122,6 +125,7 @@ class _ConfigFields:
     seed: int = 0
     sparse_legal: tuple = (20, 45)
     gomoku_rules: str = "freestyle"
+    root_noise_source: str = "host"
     extra: Dict[str, Any] = field(default_factory=dict)
 
 
@@ -159,6 +163,8 @@ class MCTSConfig(_ConfigFields):
             raise ValueError("num_trees must be >= 1")
         if self.gomoku_rules not in _RULES:
             raise ValueError(f"gomoku_rules must be one of {_RULES}")
+        if self.root_noise_source not in ("host", "device"):
+            raise ValueError("root_noise_source must be 'host' or 'device'")
 
     # effective values ---------------------------------------------------------------------
     def effective_wave_size(self) -> int:

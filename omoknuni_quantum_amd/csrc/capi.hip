@@ -27,6 +27,12 @@ hipError_t launch_virtual_loss(const omq_forest& f, const int32_t* nodes, const 
 hipError_t launch_reset(const omq_forest& f, hipStream_t st);
 hipError_t launch_shift_root(const omq_forest& f, const int32_t* new_roots, int32_t* ws,
                              hipStream_t st);
+hipError_t launch_root_policy(const omq_forest& f, double* pol, hipStream_t st);
+hipError_t launch_sample_actions(const omq_forest& f, const double* pol, double temperature,
+                                 uint64_t seed, uint64_t counter, int32_t* actions,
+                                 hipStream_t st);
+hipError_t launch_root_dirichlet(const omq_forest& f, double alpha, uint64_t seed,
+                                 uint64_t counter, double* noise, hipStream_t st);
 hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const int8_t* boards,
                                   const int32_t* root_player, int rule, int bs, int32_t* uterm,
                                   hipStream_t st);
@@ -191,6 +197,36 @@ int omq_shift_root(const omq_forest* f, const int32_t* new_roots, int32_t* works
                 (long long)workspace_ints, (long long)need);
   return hip_status(omq::launch_shift_root(*f, new_roots, workspace, (hipStream_t)stream),
                     "omq_shift_root");
+}
+
+int omq_root_policy(const omq_forest* f, double* policy, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  if (!policy) return fail(OMQ_E_ARG, "policy is null");
+  return hip_status(omq::launch_root_policy(*f, policy, (hipStream_t)stream), "omq_root_policy");
+}
+
+int omq_sample_actions(const omq_forest* f, const double* policy, double temperature,
+                       uint64_t seed, uint64_t counter, int32_t* actions, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  if (!policy || !actions) return fail(OMQ_E_ARG, "policy and actions are required");
+  if (!(temperature >= 0.0) || temperature > 1e6)
+    return fail(OMQ_E_ARG, "temperature %g outside [0, 1e6]", temperature);
+  return hip_status(omq::launch_sample_actions(*f, policy, temperature, seed, counter, actions,
+                                               (hipStream_t)stream),
+                    "omq_sample_actions");
+}
+
+int omq_root_dirichlet(const omq_forest* f, double alpha, uint64_t seed, uint64_t counter,
+                       double* noise, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  if (!noise) return fail(OMQ_E_ARG, "noise is null");
+  if (!(alpha > 0.0) || alpha > 1e6) return fail(OMQ_E_ARG, "alpha %g outside (0, 1e6]", alpha);
+  return hip_status(omq::launch_root_dirichlet(*f, alpha, seed, counter, noise,
+                                               (hipStream_t)stream),
+                    "omq_root_dirichlet");
 }
 
 int omq_synthetic_evaluate(const omq_forest* f, const omq_wave* w, float logit_scale,

@@ -67,6 +67,11 @@ def load() -> ctypes.CDLL:
         "orc_set_gomoku_rules": (None, [P, i, i, P, P]),
         "orc_gomoku_terminal": (i, [P, i, i]),
         "orc_shift_root": (i, [P, i, i]),
+        "orc_exp_d": (d, [d]),
+        "orc_log_d": (d, [d]),
+        "orc_gamma": (d, [d, u64, u64, i, i]),
+        "orc_root_dirichlet": (None, [P, i, d, u64, u64, P]),
+        "orc_sample_action": (i, [P, i, d, u64, u64, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -205,11 +210,24 @@ class Oracle:
         }
 
     def root_policy(self, t: int) -> np.ndarray:
+        """MCTS._extract_policy (mcts.py:1069-1137): visits / total over the root's children;
+        uniform over the children's actions when they have no visits, uniform over the action
+        space when the root has no children."""
         tr = self.tree(t)
         pol = np.zeros(self.A)
         f, k = tr["first"][0], tr["nchild"][0]
-        if k > 0:
-            kids = tr["children"][f:f + k]
-            pol[tr["child_actions"][f:f + k]] = tr["N"][kids]
-        s = pol.sum()
-        return pol / s if s > 0 else np.full(self.A, 1.0 / self.A)
+        if k <= 0:
+            return np.full(self.A, 1.0 / self.A)
+        kids = tr["children"][f:f + k]
+        acts = tr["child_actions"][f:f + k]
+        tot = int(tr["N"][kids].sum())
+        if tot == 0:
+            pol[acts] = 1.0 / k
+            return pol
+        pol[acts] = tr["N"][kids] / tot
+        return pol
+
+    def root_dirichlet(self, t: int, alpha: float, seed: int, counter: int) -> np.ndarray:
+        row = np.zeros(self.A, np.float64)
+        self.lib.orc_root_dirichlet(self.f, t, alpha, seed, counter, row.ctypes.data)
+        return row

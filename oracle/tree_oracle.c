@@ -399,6 +399,169 @@ static int leaf_terminal(const orc_forest *f, int t, const int *acts, int np) {
   return orc_gomoku_terminal(board, bs, f->rule);
 }
 
+/* ---- per-move root operations ------------------------------------------------------------
+   Restated from their specification: the visit-count policy (mcts.py:1069-1137), move
+   selection with a temperature (mcts.py:1167-1203, np.random.choice semantics) and root
+   Dirichlet noise, with the draws taken from a SplitMix64 stream keyed by (seed, counter, tree,
+   item).  Gamma variates by Marsaglia and Tsang (ACM TOMS 26(3), 2000; shape < 1 boosted by
+   U^(1/alpha)), normal variates by Marsaglia's polar method, log and exp by textbook methods
+   (Cody-Waite reduction + Taylor polynomial; exponent split + atanh series), all in IEEE double
+   with +, -, *, /, sqrt and floor only. */
+static double orc_pow2i(int k) {
+  const uint64_t b = (uint64_t)(k + 1023) << 52;
+  double d;
+  memcpy(&d, &b, 8);
+  return d;
+}
+
+double orc_exp_d(double x) {
+  static const double ln2_hi = 0x1.62e42feep-1, ln2_lo = 0x1.a39ef35793c76p-33;
+  if (x < -745.0) return 0.0;
+  if (x > 709.0) return INFINITY;
+  const double kf = floor(x * (1.0 / 0.6931471805599453) + 0.5);
+  const int k = (int)kf;
+  const double r = (x - kf * ln2_hi) - kf * ln2_lo;
+  /* e^r = sum r^n / n!, n = 0..13, by Horner from the top */
+  static const double fact[14] = {1.0, 1.0, 2.0, 6.0, 24.0, 120.0, 720.0, 5040.0, 40320.0,
+                                  362880.0, 3628800.0, 39916800.0, 479001600.0, 6227020800.0};
+  double p = 1.0 / fact[13];
+  for (int n = 12; n >= 0; --n) p = p * r + 1.0 / fact[n];
+  if (k < -1021) return (p * orc_pow2i(k + 1000)) * orc_pow2i(-1000);
+  return p * orc_pow2i(k);
+}
+
+double orc_log_d(double x) {
+  static const double ln2_hi = 0x1.62e42feep-1, ln2_lo = 0x1.a39ef35793c76p-33;
+  uint64_t b;
+  memcpy(&b, &x, 8);
+  int e = 0;
+  if ((b >> 52) == 0) {
+    x = x * 0x1p54;
+    memcpy(&b, &x, 8);
+    e = -54;
+  }
+  e += (int)((b >> 52) & 0x7FF) - 1023;
+  const uint64_t mb = (b & 0x000FFFFFFFFFFFFFull) | 0x3FF0000000000000ull;
+  double m;
+  memcpy(&m, &mb, 8);
+  if (m > 0x1.6a09e667f3bcdp+0) {
+    m = m * 0.5;
+    e += 1;
+  }
+  const double s = (m - 1.0) / (m + 1.0);
+  const double z = s * s;
+  /* atanh series: log m = 2 s (1 + z/3 + z^2/5 + ... + z^11/23) */
+  double p = 1.0 / 23.0;
+  for (int n = 21; n >= 1; n -= 2) p = p * z + 1.0 / (double)n;
+  const double ed = (double)e;
+  return (ed * ln2_lo + 2.0 * s * p) + ed * ln2_hi;
+}
+
+typedef struct {
+  uint64_t base, j;
+} orc_stream;
+
+static orc_stream orc_make_stream(uint64_t seed, uint64_t counter, int t, int item) {
+  orc_stream s;
+  const uint64_t tag = ((uint64_t)(uint32_t)t << 32) | (uint32_t)item;
+  s.base = orc_splitmix64(orc_splitmix64(orc_splitmix64(seed) ^ counter) ^ tag);
+  s.j = 0;
+  return s;
+}
+
+static double orc_uniform_open(orc_stream *s) {
+  const uint64_t b = orc_splitmix64(s->base + s->j * GOLDEN);
+  s->j += 1;
+  return ((double)(b >> 11) + 0.5) * 0x1p-53;
+}
+
+static double orc_normal_polar(orc_stream *s) {
+  for (;;) {
+    const double u = 2.0 * orc_uniform_open(s) - 1.0;
+    const double v = 2.0 * orc_uniform_open(s) - 1.0;
+    const double q = u * u + v * v;
+    if (q > 0.0 && q < 1.0) return u * sqrt(-2.0 * orc_log_d(q) / q);
+  }
+}
+
+static double orc_gamma_s(double alpha, orc_stream *s) {
+  const int boost = alpha < 1.0;
+  const double a = boost ? alpha + 1.0 : alpha;
+  const double d = a - 1.0 / 3.0;
+  const double c = 1.0 / sqrt(9.0 * d);
+  double x, v;
+  for (;;) {
+    do {
+      x = orc_normal_polar(s);
+      v = 1.0 + c * x;
+    } while (v <= 0.0);
+    v = v * v * v;
+    const double u = orc_uniform_open(s);
+    const double x2 = x * x;
+    if (u < 1.0 - 0.0331 * (x2 * x2)) break;
+    if (orc_log_d(u) < 0.5 * x2 + d * (1.0 - v + orc_log_d(v))) break;
+  }
+  double g = d * v;
+  if (boost) g = g * orc_exp_d(orc_log_d(orc_uniform_open(s)) / alpha);
+  return g;
+}
+
+double orc_gamma(double alpha, uint64_t seed, uint64_t counter, int t, int item) {
+  orc_stream s = orc_make_stream(seed, counter, t, item);
+  return orc_gamma_s(alpha, &s);
+}
+
+/* Dirichlet(alpha) over the L legal root actions of tree t into row[0..A) (zeros past L) */
+void orc_root_dirichlet(const orc_forest *f, int t, double alpha, uint64_t seed,
+                        uint64_t counter, double *row) {
+  int L = 0;
+  if (f->game == ORC_GAME_SPARSE) {
+    L = sparse_count(f, f->root_keys[t]);
+  } else {
+    for (int w = 0; w < f->legal_words; ++w)
+      L += __builtin_popcount(f->root_legal[(size_t)t * f->legal_words + w]);
+  }
+  for (int i = 0; i < f->A; ++i) row[i] = 0.0;
+  for (int i = 0; i < L; ++i) row[i] = orc_gamma(alpha, seed, counter, t, i);
+  const double S = orc_sum64d(row, L);
+  for (int i = 0; i < L; ++i) row[i] = S > 0.0 ? row[i] / S : 1.0 / (double)L;
+}
+
+/* select_action on one policy row: first maximum at temperature 0; otherwise the normalised
+   cumulative sums of p^(1/T) / sum against u in [0, 1) (first entry above u) */
+int orc_sample_action(const double *p, int A, double temperature, uint64_t seed,
+                      uint64_t counter, int t) {
+  if (temperature == 0.0) {
+    int best = 0;
+    for (int a = 1; a < A; ++a)
+      if (p[a] > p[best]) best = a;
+    return best;
+  }
+  const double inv_t = 1.0 / temperature;
+  const int unit = temperature == 1.0;
+  double *w = (double *)malloc(sizeof(double) * (size_t)A);
+  double S = 0.0;
+  for (int a = 0; a < A; ++a) {
+    w[a] = p[a] > 0.0 ? (unit ? p[a] : orc_exp_d(orc_log_d(p[a]) * inv_t)) : 0.0;
+    S = S + w[a];
+  }
+  double last = 0.0;
+  for (int a = 0; a < A; ++a) last = last + w[a] / S;
+  const orc_stream st = orc_make_stream(seed, counter, t, -1);
+  const double u = (double)(orc_splitmix64(st.base) >> 11) * 0x1p-53;
+  double c = 0.0;
+  int pick = A - 1;
+  for (int a = 0; a < A; ++a) {
+    c = c + w[a] / S;
+    if (c / last > u) {
+      pick = a;
+      break;
+    }
+  }
+  free(w);
+  return pick;
+}
+
 /* CSRTree.shift_root (python/mcts/gpu/csr_tree.py:1020-1229) on tree t: breadth-first queue
    from node r over the children in row order, visited-marked; new index = queue position;
    N, W, P, expanded flag and action copied, parents remapped (root: -1, action -1); the edge
