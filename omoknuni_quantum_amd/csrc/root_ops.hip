@@ -177,42 +177,76 @@ __global__ __launch_bounds__(kRootThreads) void root_policy_kernel(omq_forest f,
 }
 
 // ---- move selection -------------------------------------------------------------------------
-// One thread per tree: temperature 0 takes the first maximum; otherwise w = p^(1/T) (w = p for
-// T = 1, 0 for p = 0), S = sum of w in action order, cdf_a = (w_0/S + ... + w_a/S) / cdf_last,
-// and the action is the first a with cdf_a > u.
-__global__ void sample_actions_kernel(omq_forest f, const double* pol, double temperature,
-                                      uint64_t seed, uint64_t counter, int32_t* actions) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= f.num_trees) return;
+// One wavefront per tree.  Temperature 0 takes the first maximum (a wave reduction on
+// (value, lowest index)).  Otherwise the lanes compute w = p^(1/T) (w = p for T = 1, 0 for
+// p = 0) into LDS, and lane 0 runs the order-dependent part in action order: S = sum of w,
+// cdf_a = (w_0/S + ... + w_a/S) / cdf_last, the action is the first a with cdf_a > u.
+__global__ __launch_bounds__(kWave) void sample_actions_kernel(omq_forest f, const double* pol,
+                                                               double temperature,
+                                                               uint64_t seed, uint64_t counter,
+                                                               int32_t* actions) {
+  extern __shared__ __align__(16) double w[];  // [num_actions]
+  const int t = blockIdx.x;
+  const int lane = lane_id();
   const int A = f.num_actions;
   const double* p = pol + (int64_t)t * A;
   if (temperature == 0.0) {
-    int best = 0;
-    for (int a = 1; a < A; ++a)
-      if (p[a] > p[best]) best = a;
-    actions[t] = best;
+    double bv = -1.0;
+    int bi = 0x7FFFFFFF;
+    for (int a = lane; a < A; a += kWave) {
+      const double x = p[a];
+      if (x > bv) {  // ascending within the lane: the first maximum of the lane
+        bv = x;
+        bi = a;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const double ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) actions[t] = bi;
     return;
   }
   const double inv_t = 1.0 / temperature;
   const bool unit = temperature == 1.0;
-  double S = 0.0;
-  for (int a = 0; a < A; ++a) {
+  for (int a = lane; a < A; a += kWave) {
     const double x = p[a];
-    S = S + (x > 0.0 ? (unit ? x : exp_cw_d(log_cw_d(x) * inv_t)) : 0.0);
+    w[a] = x > 0.0 ? (unit ? x : exp_cw_d(log_cw_d(x) * inv_t)) : 0.0;
   }
+  wave_sync();
+  double S = 0.0;
+  if (lane == 0) {
+#pragma unroll 16
+    for (int a = 0; a < A; ++a) S = S + w[a];
+  }
+  S = __shfl(S, 0, 64);
+  for (int a = lane; a < A; a += kWave) w[a] = w[a] / S;  // the quotients, once, in parallel
+  wave_sync();
+  if (lane != 0) return;
+  double last = 0.0;
+#pragma unroll 16
+  for (int a = 0; a < A; ++a) last = last + w[a];
   Stream st = make_stream(seed, counter, t, -1);
   const double u = (double)(splitmix64(st.base) >> 11) * 0x1p-53;  // [0, 1)
-  // cumulative sums of w/S, normalised by the last (np.random.choice)
-  double last = 0.0;
-  for (int a = 0; a < A; ++a) {
-    const double x = p[a];
-    last = last + (x > 0.0 ? (unit ? x : exp_cw_d(log_cw_d(x) * inv_t)) : 0.0) / S;
-  }
+  // the first a whose cumulative sum, divided by the total, exceeds u; c / last is monotone
+  // in a, so blocks of 16 are skipped while their last cumulative sum stays at or below u
   double c = 0.0;
+  int a = 0;
+  for (; a + 16 <= A; a += 16) {
+    double cb = c;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) cb = cb + w[a + e];
+    if (cb / last > u) break;
+    c = cb;
+  }
   int pick = A - 1;
-  for (int a = 0; a < A; ++a) {
-    const double x = p[a];
-    c = c + (x > 0.0 ? (unit ? x : exp_cw_d(log_cw_d(x) * inv_t)) : 0.0) / S;
+  for (; a < A; ++a) {
+    c = c + w[a];
     if (c / last > u) {
       pick = a;
       break;
@@ -264,8 +298,9 @@ hipError_t launch_root_policy(const omq_forest& f, double* pol, hipStream_t st) 
 hipError_t launch_sample_actions(const omq_forest& f, const double* pol, double temperature,
                                  uint64_t seed, uint64_t counter, int32_t* actions,
                                  hipStream_t st) {
-  hipLaunchKernelGGL(sample_actions_kernel, dim3((f.num_trees + 63) / 64), dim3(64), 0, st, f,
-                     pol, temperature, seed, counter, actions);
+  const size_t lds = (size_t)f.num_actions * sizeof(double);
+  hipLaunchKernelGGL(sample_actions_kernel, dim3(f.num_trees), dim3(kWave), lds, st, f, pol,
+                     temperature, seed, counter, actions);
   return hipGetLastError();
 }
 

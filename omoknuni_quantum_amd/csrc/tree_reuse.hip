@@ -14,9 +14,10 @@
 //
 // One workgroup per tree walks the subtree level by level. A level is a contiguous range of
 // new ids. A block-wide scan of the level's row lengths gives each node the new id of its
-// first child, so a level costs one scan and one pass of writes. The new arrays are built in
-// a workspace and then copied over the front of the tree. The workspace holds eight int32
-// arrays of `capacity` entries per tree.
+// first child, and all threads then write the level's children together. Two grid-wide
+// kernels follow: one gathers the kept nodes' fields into a workspace, the other writes them
+// over the front of the tree. The workspace holds eight int32 arrays of `capacity` entries
+// per tree.
 #include "omq_common.h"
 
 namespace omq {
@@ -43,65 +44,91 @@ __device__ inline int shift_block_scan(int v, int* s_wtot, int* total) {
   return base + wex;
 }
 
-__global__ __launch_bounds__(kShiftThreads) void shift_root_kernel(omq_forest f,
-                                                                   const int32_t* new_roots,
-                                                                   int32_t* ws) {
+// Breadth-first numbering of tree t's kept nodes (one workgroup per tree).  Writes, for new
+// id i: old_of_new[i], npar[i], nfirst[i], nnch[i]; then num_nodes[t] = kept count.  npar[0]
+// is -1 for a tree to move and -2 for a tree left unchanged (no shift, or an inconsistent row:
+// a row that leaves [0, num_nodes), or more kept nodes than num_nodes, as from a cycle).
+// A level is taken in chunks of kShiftPer consecutive nodes per thread, so that the row loads
+// of a chunk are in flight together.
+constexpr int kShiftPer = 4;
+constexpr int kShiftChunk = kShiftThreads * kShiftPer;
+
+__global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f,
+                                                                    const int32_t* new_roots,
+                                                                    int32_t* ws) {
   __shared__ int s_wtot[kShiftWaves];
+  __shared__ int s_ex[kShiftChunk];
+  __shared__ int s_of[kShiftChunk];
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
   const int cap = f.capacity;
   const int64_t tb = (int64_t)t * cap;
-  const int r = new_roots[t];
-  const int n_old = f.num_nodes[t];
-  if (r <= 0 || r >= n_old) return;  // tree unchanged (0: already the root; -1: no shift)
-
   int32_t* old_of_new = ws + (int64_t)t * cap * 8;
   int32_t* npar = old_of_new + cap;
   int32_t* nfirst = old_of_new + 2 * (int64_t)cap;
   int32_t* nnch = old_of_new + 3 * (int64_t)cap;
-  int32_t* nN = old_of_new + 4 * (int64_t)cap;
-  float* nW = reinterpret_cast<float*>(old_of_new + 5 * (int64_t)cap);
-  float* nP = reinterpret_cast<float*>(old_of_new + 6 * (int64_t)cap);
-  int32_t* nA = old_of_new + 7 * (int64_t)cap;
-
-  if (tid == 0) {
-    old_of_new[0] = r;
-    npar[0] = -1;
+  const int r = new_roots[t];
+  const int n_old = f.num_nodes[t];
+  if (r <= 0 || r >= n_old) {  // 0: already the root; -1: no shift
+    if (tid == 0) npar[0] = -2;
+    return;
   }
+  if (tid == 0) old_of_new[0] = r;
   __syncthreads();
-  // breadth-first numbering: level [lo, hi) of new ids; its children get [hi, next).  A row
-  // that leaves [0, num_nodes), or more kept nodes than num_nodes (a cycle), marks the tree
-  // inconsistent: it is then left unchanged, and no access leaves the tree's arrays.
+  // level [lo, hi) of new ids; its children get [hi, next)
   int lo = 0, hi = 1, next = 1;
   bool bad = false;
   while (lo < hi && !bad) {
-    for (int c0 = lo; c0 < hi; c0 += kShiftThreads) {
-      const int i = c0 + tid;
-      int k = 0, old = 0, of = 0;
+    for (int c0 = lo; c0 < hi; c0 += kShiftChunk) {
+      const int i0 = c0 + tid * kShiftPer;  // this thread's nodes: i0 .. i0+kShiftPer-1
+      int k[kShiftPer], of[kShiftPer];
       bool row_bad = false;
-      if (i < hi) {
-        old = old_of_new[i];
-        k = f.num_children[tb + old];
-        of = f.first_child[tb + old];
-        if (k < 0 || (k > 0 && (of < 0 || (int64_t)of + k >= n_old))) {
-          row_bad = true;
-          k = 0;
+      int mine = 0;
+#pragma unroll
+      for (int e = 0; e < kShiftPer; ++e) {
+        k[e] = 0;
+        of[e] = 0;
+        if (i0 + e < hi) {
+          const int old = old_of_new[i0 + e];
+          k[e] = f.num_children[tb + old];
+          of[e] = f.first_child[tb + old];
+          if (k[e] < 0 || (k[e] > 0 && (of[e] < 0 || (int64_t)of[e] + k[e] >= n_old))) {
+            row_bad = true;
+            k[e] = 0;
+          }
         }
+        mine += k[e];
       }
       int tot;
-      const int ex = shift_block_scan(k, s_wtot, &tot);
+      int ex = shift_block_scan(mine, s_wtot, &tot);
       if (__syncthreads_or(row_bad) || next + tot > n_old) {
         bad = true;
         break;
       }
-      if (i < hi) {
-        const int base = next + ex;
-        nnch[i] = k;
-        nfirst[i] = k > 0 ? base - 1 : -1;
-        for (int j = 0; j < k; ++j) {
-          old_of_new[base + j] = of + 1 + j;  // child of edge of+j is node of+j+1
-          npar[base + j] = i;
+#pragma unroll
+      for (int e = 0; e < kShiftPer; ++e) {
+        const int i = i0 + e;
+        if (i < hi) {
+          nnch[i] = k[e];
+          nfirst[i] = k[e] > 0 ? next + ex - 1 : -1;
         }
+        // non-decreasing over the chunk; a childless node repeats its successor's offset
+        s_ex[tid * kShiftPer + e] = ex;
+        s_of[tid * kShiftPer + e] = of[e];
+        ex += k[e];
+      }
+      __syncthreads();
+      // the chunk's children, written by all threads: output q belongs to the last node j of
+      // the chunk with s_ex[j] <= q (binary search), as its child q - s_ex[j]
+      for (int q = tid; q < tot; q += kShiftThreads) {
+        int a = 0, b = kShiftChunk - 1;
+        while (a < b) {
+          const int mid = (a + b + 1) >> 1;
+          if (s_ex[mid] <= q) a = mid;
+          else b = mid - 1;
+        }
+        old_of_new[next + q] = s_of[a] + 1 + (q - s_ex[a]);  // child of edge of+j is node of+j+1
+        npar[next + q] = c0 + a;
       }
       next += tot;
       __syncthreads();
@@ -109,17 +136,50 @@ __global__ __launch_bounds__(kShiftThreads) void shift_root_kernel(omq_forest f,
     lo = hi;
     hi = next;
   }
-  if (bad) return;
-  const int n_new = next;
-  for (int i = tid; i < n_new; i += kShiftThreads) {
+  if (tid == 0) {
+    npar[0] = bad ? -2 : -1;
+    if (!bad) f.num_nodes[t] = next;
+  }
+}
+
+// Gathers the kept nodes' N, W, P and action into the workspace (grid-stride over new ids).
+__global__ void shift_gather_kernel(omq_forest f, int32_t* ws) {
+  const int t = blockIdx.y;
+  const int cap = f.capacity;
+  const int64_t tb = (int64_t)t * cap;
+  const int32_t* old_of_new = ws + (int64_t)t * cap * 8;
+  const int32_t* npar = old_of_new + cap;
+  if (npar[0] != -1) return;
+  int32_t* nN = const_cast<int32_t*>(old_of_new) + 4 * (int64_t)cap;
+  float* nW = reinterpret_cast<float*>(nN + cap);
+  float* nP = reinterpret_cast<float*>(nN + 2 * (int64_t)cap);
+  int32_t* nA = nN + 3 * (int64_t)cap;
+  const int n_new = f.num_nodes[t];
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_new; i += gridDim.x * blockDim.x) {
     const int64_t o = tb + old_of_new[i];
     nN[i] = f.visit_counts[o];
     nW[i] = f.value_sums[o];
     nP[i] = f.priors[o];
     nA[i] = i == 0 ? -1 : f.actions[o];
   }
-  __syncthreads();
-  for (int i = tid; i < n_new; i += kShiftThreads) {
+}
+
+// Writes the compacted tree over the front of the tree's arrays.
+__global__ void shift_write_kernel(omq_forest f, const int32_t* ws) {
+  const int t = blockIdx.y;
+  const int cap = f.capacity;
+  const int64_t tb = (int64_t)t * cap;
+  const int32_t* base = ws + (int64_t)t * cap * 8;
+  const int32_t* npar = base + cap;
+  if (npar[0] != -1) return;
+  const int32_t* nfirst = base + 2 * (int64_t)cap;
+  const int32_t* nnch = base + 3 * (int64_t)cap;
+  const int32_t* nN = base + 4 * (int64_t)cap;
+  const float* nW = reinterpret_cast<const float*>(nN + cap);
+  const float* nP = reinterpret_cast<const float*>(nN + 2 * (int64_t)cap);
+  const int32_t* nA = nN + 3 * (int64_t)cap;
+  const int n_new = f.num_nodes[t];
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_new; i += gridDim.x * blockDim.x) {
     const int64_t d = tb + i;
     f.visit_counts[d] = nN[i];
     f.value_sums[d] = nW[i];
@@ -129,13 +189,19 @@ __global__ __launch_bounds__(kShiftThreads) void shift_root_kernel(omq_forest f,
     f.num_children[d] = nnch[i];
     f.actions[d] = nA[i];
   }
-  if (tid == 0) f.num_nodes[t] = n_new;
 }
 
 hipError_t launch_shift_root(const omq_forest& f, const int32_t* new_roots, int32_t* ws,
                              hipStream_t st) {
-  hipLaunchKernelGGL(shift_root_kernel, dim3(f.num_trees), dim3(kShiftThreads), 0, st, f,
+  hipLaunchKernelGGL(shift_order_kernel, dim3(f.num_trees), dim3(kShiftThreads), 0, st, f,
                      new_roots, ws);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int blocks = (int)std::min<int64_t>(64, ((int64_t)f.capacity + 255) / 256);
+  hipLaunchKernelGGL(shift_gather_kernel, dim3(blocks, f.num_trees), dim3(256), 0, st, f, ws);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(shift_write_kernel, dim3(blocks, f.num_trees), dim3(256), 0, st, f, ws);
   return hipGetLastError();
 }
 
