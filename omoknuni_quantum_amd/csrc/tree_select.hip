@@ -212,6 +212,7 @@ struct Row {
   float den[R];         // (float)(1 + N) including this chain's picks
   float wv[R], cp[R];   // W and c_puct * P
   bool pb[R];           // the previous step's pick, whose next state is still pending
+  int cn[R];            // picks of the child in this chain so far
 };
 
 // Computes the pending next state of the previous pick now (leaves no pick pending).
@@ -339,6 +340,7 @@ __device__ inline int select_step(Row<R>& x, float s, float fvl, float vlf, floa
     x.q[j] = b[j] ? x.qn[j] : x.q[j];
     x.ar[j] = b[j] ? x.arn[j] : x.ar[j];
     x.den[j] = b[j] ? x.den[j] + fvl : x.den[j];
+    x.cn[j] = b[j] ? x.cn[j] + 1 : x.cn[j];
     x.pb[j] = b[j];
   }
   int win;
@@ -364,6 +366,7 @@ __device__ inline int select_step(Row<R>& x, float s, float fvl, float vlf, floa
       x.q[j] = b[j] ? qr : x.q[j];
       x.ar[j] = b[j] ? ar0 : x.ar[j];
       x.den[j] = dr;
+      x.cn[j] = b[j] ? x.cn[j] - 1 : x.cn[j];
     }
     win = exact_pick<R>(x.den, x.wv, x.cp, bits, exact_only || tot == 0, k, s, vlf);
     win = __builtin_amdgcn_readfirstlane(win);
@@ -375,6 +378,7 @@ __device__ inline int select_step(Row<R>& x, float s, float fvl, float vlf, floa
       x.q[j] = hit ? x.qn[j] : x.q[j];
       x.ar[j] = hit ? x.arn[j] : x.ar[j];
       x.den[j] = hit ? x.den[j] + fvl : x.den[j];
+      x.cn[j] = hit ? x.cn[j] + 1 : x.cn[j];
       x.pb[j] = hit;
     }
   }
@@ -516,6 +520,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     y.q[0] = x.q[0];
     y.ar[0] = x.ar[0];
     y.pb[0] = false;
+    y.cn[0] = 0;
     if (lane < k) {
       child_state(y.den[0] + fvl, y.wv[0], y.cp[0], lane, vlf, &y.qn[0], &y.arn[0]);
     } else {
@@ -530,15 +535,21 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     const int Npl = Np0 + c.vli * (r0 + lane + 1);
     const float svec = sqrtf((float)Npl);
     const int rend = __builtin_amdgcn_readfirstlane(min(kWave, m - r0));
+    // lane rr of rec / rnk: the child picked at rank r0+rr and its rank among the chain's
+    // picks of that child (the picked lane's count before the pick)
     uint32_t rec = kNoChild;
+    uint32_t rnk = 0;
     if (R == 1) {
 #pragma unroll 2
       for (int rr = 0; rr < rend; ++rr) {
         const float s = readlane_f(svec, rr);
         const int win = select_step<1>(y, s, fvl, vlf, qbt_eff, exact_only, k, lane, false, 0.0f);
         if (win < 0 && first_end < 0) first_end = r0 + rr;
-        asm volatile("s_mov_b32 m0, %2\n\tv_writelane_b32 %0, %1, m0"
-                     : "+v"(rec) : "s"(win), "s"(rr) : "m0");
+        const int rk = readlane_i(y.cn[0], win & (kWave - 1)) - 1;
+        // lane rr := win / rk; the lane select goes through m0, which the "{m0}" operand hands
+        // to the compiler (v_writelane may read only one SGPR besides m0)
+        asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(rec) : "s"(win), "{m0}"(rr));
+        asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(rnk) : "s"(rk), "{m0}"(rr));
       }
     } else {
       int rr = 0;
@@ -576,6 +587,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
           y.wv[0] = e.y;
           y.cp[0] = e.z;
           y.pb[0] = false;
+          y.cn[0] = lane < ncon ? (int)cnt_s[cidx] : 0;
           if (lane < ncon) {
             child_state(y.den[0], y.wv[0], y.cp[0], cidx, vlf, &y.q[0], &y.ar[0]);
             child_state(y.den[0] + fvl, y.wv[0], y.cp[0], cidx, vlf, &y.qn[0], &y.arn[0]);
@@ -584,18 +596,26 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
             y.ar[0] = y.arn[0] = 0.0f;
           }
           const int rr0 = rr;
-          while (rr < rend) {
+          // window steps record the picked lane; the lanes become child indices below.  A
+          // window step always picks (no candidate or an unsafe threshold aborts it first).
+          for (; rr < rend; ++rr) {
             const float s = readlane_f(svec, rr);
             const int wl = select_step<1>(y, s, fvl, vlf, qbt_eff, false, ncon, cidx, true, ubnc);
-            if (wl == -2) break;
-            const int win = wl >= 0 ? readlane_i(cidx, wl) : -1;
-            if (win < 0 && first_end < 0) first_end = r0 + rr;
-            rec = (lane == rr) ? (uint32_t)win : rec;
-            ++rr;
+            if (wl < 0) break;
+            const int rk = readlane_i(y.cn[0], wl) - 1;
+            asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(rec) : "s"(wl), "{m0}"(rr));
+            asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(rnk) : "s"(rk), "{m0}"(rr));
+          }
+          {
+            const int ci = __shfl(cidx, (int)(rec & 63u), 64);
+            if (lane >= rr0 && lane < rr) rec = (uint32_t)ci;
           }
           // write back the contenders' counts; every state follows from its count
           wave_sync();
-          if (lane < ncon) cscr[lane].x = y.den[0];
+          if (lane < ncon) {
+            cscr[lane].x = y.den[0];
+            cnt_s[cidx] = (uint16_t)y.cn[0];
+          }
           wave_sync();
           base = 0;
 #pragma unroll
@@ -617,33 +637,23 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
         const float s = readlane_f(svec, rr);
         const int win = wide_step<R>(x, s, fvl, vlf, qbt_eff, exact_only, k);
         if (win < 0 && first_end < 0) first_end = r0 + rr;
+        int rk = 0;
+        if (win >= 0) {
+          rk = cnt_s[win];
+          wave_sync();
+          if (lane == 0) cnt_s[win] = (uint16_t)(rk + 1);
+          wave_sync();
+        }
         rec = (lane == rr) ? (uint32_t)win : rec;
+        rnk = (lane == rr) ? (uint32_t)rk : rnk;
         ++rr;
       }
     }
-    // ranks of the block's picks: count of the child before the block (cnt_s) plus the number
-    // of earlier picks of the same child within the block
-    const bool valid = lane < rend && rec != kNoChild;
-    const uint32_t key = valid ? rec : 0u;
-    const uint32_t base = valid ? (uint32_t)cnt_s[key] : 0u;
-    uint64_t pend = __ballot(valid);
-    uint32_t inb = 0;
-    bool last = false;
-    while (pend) {
-      const uint32_t kk = (uint32_t)readlane_i((int)key, lowest_lane(pend));
-      const bool eq = valid && key == kk;
-      const uint64_t same = __ballot(eq);
-      if (eq) {
-        inb = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32),
-                                        __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
-        last = (same >> lane) == 1ull;
-      }
-      pend &= ~same;
-    }
-    if (valid && last) cnt_s[key] = (uint16_t)(base + inb + 1);
-    if (lane < rend) ch[r0 + lane] = valid ? ((key << 16) | (base + inb)) : kNoChild;
-    wave_sync();
+    if (lane < rend) ch[r0 + lane] = rec != kNoChild ? ((rec << 16) | rnk) : kNoChild;
   }
+  // the chain's pick counts per child (R == 1 keeps them in the lanes until here)
+  if (R == 1 && lane < k) cnt_s[lane] = (uint16_t)y.cn[0];
+  wave_sync();
   return first_end;
 }
 
