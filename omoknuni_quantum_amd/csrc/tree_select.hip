@@ -715,17 +715,19 @@ constexpr int kSmallGroup = 1;
 template <int RMAX>
 __device__ inline void small_groups(
     const SelArgs& f, const SelCfg& c, int t, int d, int ng, int W, int64_t tb, int64_t gmax,
-    uint32_t* gnode, uint32_t* gsl, uint16_t* buf, uint16_t* lfs, int32_t* lflag, int* s_gcount,
-    int* s_glog, unsigned long long* s_st) {
+    uint32_t* gnode, uint32_t* gsl, uint16_t* buf, uint16_t* lfs, int32_t* lflag,
+    int* s_glog, unsigned long long* s_st, int* s_nbig, int* s_nsmall) {
   const SelArgs& w = f;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int cur = d & 1, nxt = cur ^ 1;
   const int MW = w.max_wave, MD = w.max_depth_buf;
   int32_t* N = f.N;
-  for (int g0 = wave * kWave; g0 < ng; g0 += kSelThreads) {
-    const int gi = g0 + lane;
-    const uint32_t sl = gi < ng ? gsl[cur * W + gi] : 0u;
+  // the small groups of the level sit at the top of the group arrays: [W - ns, W)
+  const int ns = s_nsmall[cur];
+  for (int g0 = wave * kWave; g0 < ns; g0 += kSelThreads) {
+    const int gi = W - 1 - (g0 + lane);
+    const uint32_t sl = g0 + lane < ns ? gsl[cur * W + gi] : 0u;
     const int m = (int)(sl >> 16);
     if (m < 1 || m > kSmallGroup) continue;
     const int p = (int)gnode[cur * W + gi];
@@ -821,7 +823,8 @@ __device__ inline void small_groups(
           ++cntc;
         }
       }
-      const int g = atomicAdd(&s_gcount[nxt], 1);
+      const int g = cntc > kSmallGroup ? atomicAdd(&s_nbig[nxt], 1)
+                                       : W - 1 - atomicAdd(&s_nsmall[nxt], 1);
       gnode[nxt * W + g] = (uint32_t)(first + 1 + pick[r]);
       gsl[nxt * W + g] = (uint32_t)pos | ((uint32_t)cntc << 16);
       pos += cntc;
@@ -847,7 +850,11 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   uint16_t* lfs = buf + 2 * W;                                // [W] first sim of own leaf group
   uint16_t* cnt_all = lfs + W;                                // [kSelWaves * OMQ_MAX_ROW]
 
-  __shared__ int s_gcount[2];
+  // Groups of a level: those a wave runs as a chain at [0, nbig), those the lane pass takes
+  // (kernels with a lane pass) at [W - nsmall, W) of the level's group arrays.
+  __shared__ int s_nbig[2];
+  __shared__ int s_nsmall[2];
+  __shared__ int s_next[2];  // next chain group to take at the level (dynamic deal)
   __shared__ int s_glog;
   __shared__ int s_wtot[kSelWaves];
   __shared__ unsigned long long s_st[OMQ_NSTATS];
@@ -869,24 +876,42 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   }
   if (tid < OMQ_NSTATS) s_st[tid] = 0;
   if (tid == 0) {
-    gnode[0] = 0;
-    gsl[0] = 0u | ((uint32_t)W << 16);
-    s_gcount[0] = 1;
-    s_gcount[1] = 0;
+    // the root group is a chain unless the lane pass takes it
+    const bool root_big = !kLanePass || W > kSmallGroup;
+    const int g0 = root_big ? 0 : W - 1;
+    gnode[g0] = 0;
+    gsl[g0] = 0u | ((uint32_t)W << 16);
+    s_nbig[0] = root_big ? 1 : 0;
+    s_nsmall[0] = root_big ? 0 : 1;
+    s_nbig[1] = 0;
+    s_nsmall[1] = 0;
+    s_next[0] = 0;
+    s_next[1] = 0;
     s_glog = 0;
   }
   __syncthreads();
 
   for (int d = 0; d < c.max_depth; ++d) {
     const int cur = d & 1, nxt = cur ^ 1;
-    const int ng = s_gcount[cur];
+    const int nb = s_nbig[cur];
+    const int ng = nb + s_nsmall[cur];
     if (ng == 0) break;
-    for (int gi = wave; gi < ng; gi += kSelWaves) {
+    // The chain groups are dealt dynamically: each wave takes the next index from an LDS
+    // counter, so a wave that finishes a short chain takes the next group at once.  The next
+    // index is requested when a group starts, so that the answer is back by its end.  Every
+    // fetch advances the counter, so a wave sees an index >= nb after at most nb + 1
+    // fetches; the loop bound states this (it never ends the loop early).  No barrier is
+    // inside the loop.
+    int gnext = 0;
+    if (lane == 0) gnext = atomicAdd(&s_next[cur], 1);
+    for (int it = 0; it <= nb; ++it) {
+      const int gi = readlane_i(gnext, 0);
+      if (gi >= nb) break;
+      if (lane == 0) gnext = atomicAdd(&s_next[cur], 1);
       const int p = (int)gnode[cur * W + gi];
       const uint32_t sl = gsl[cur * W + gi];
       const int seg = (int)(sl & 0xFFFFu);
       const int m = (int)(sl >> 16);
-      if (kLanePass && m <= kSmallGroup) continue;  // small groups: one per lane, below
       const uint16_t* mem = buf + cur * W + seg;
 
       // log the group and record the path entries
@@ -945,22 +970,30 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       // the groups of the next level
       const int B = (k + kWave - 1) / kWave;
       const int lo = lane * B, hi = min(lo + B, k);
-      int sum = 0, nz = 0;
+      // (chain groups go to the bottom of the next level's group arrays, the lane pass's
+      // groups to the top)
+      int sum = 0, nbg = 0, nsm = 0;
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         sum += v;
-        nz += v > 0;
+        const bool big = !kLanePass || v > kSmallGroup;
+        nbg += v > 0 && big;
+        nsm += v > 0 && !big;
       }
-      int tot_sum, tot_nz;
+      int tot_sum, tot_bg, tot_sm;
       int run = wave_excl_scan(sum, &tot_sum);
-      int gpos = wave_excl_scan(nz, &tot_nz);
-      int gbase = 0;
-      if (lane == 0 && tot_nz > 0) gbase = atomicAdd(&s_gcount[nxt], tot_nz);
-      gbase = readlane_i(gbase, 0);
+      int pbg = wave_excl_scan(nbg, &tot_bg);
+      int psm = wave_excl_scan(nsm, &tot_sm);
+      int bbase = 0, sbase = 0;
+      if (lane == 0 && tot_bg > 0) bbase = atomicAdd(&s_nbig[nxt], tot_bg);
+      if (lane == 0 && tot_sm > 0) sbase = atomicAdd(&s_nsmall[nxt], tot_sm);
+      bbase = readlane_i(bbase, 0);
+      sbase = readlane_i(sbase, 0);
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         if (v > 0) {
-          const int g = gbase + gpos++;
+          const bool big = !kLanePass || v > kSmallGroup;
+          const int g = big ? bbase + pbg++ : W - 1 - (sbase + psm++);
           gnode[nxt * W + g] = (uint32_t)(first + 1 + i);
           gsl[nxt * W + g] = (uint32_t)(seg + run) | ((uint32_t)v << 16);
         }
@@ -992,10 +1025,14 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       wave_sync();
     }
     if (kLanePass)
-      small_groups<RMAX>(f, c, t, d, ng, W, tb, gmax, gnode, gsl, buf, lfs, lflag, s_gcount,
-                         &s_glog, s_st);
+      small_groups<RMAX>(f, c, t, d, ng, W, tb, gmax, gnode, gsl, buf, lfs, lflag, &s_glog, s_st,
+                         s_nbig, s_nsmall);
     __syncthreads();
-    if (tid == 0) s_gcount[cur] = 0;
+    if (tid == 0) {
+      s_nbig[cur] = 0;
+      s_nsmall[cur] = 0;
+      s_next[cur] = 0;
+    }
     __syncthreads();
   }
 
