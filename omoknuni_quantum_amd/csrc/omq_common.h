@@ -197,13 +197,24 @@ __device__ inline int sparse_legal_list(const omq_forest& f, uint64_t k, int* li
   const int lane = lane_id();
   const int A = f.num_actions;
   const int n = sparse_legal_count(f, k);
-  int mine = -1;  // lane i holds the i-th sampled value
-  for (int i = 0; i < n; ++i) {
-    const int j = A - n + i;
-    const uint32_t r =
-        (uint32_t)(splitmix64(k ^ ((uint64_t)(j + 1) * kSaltFloyd)) >> 32) % (uint32_t)(j + 1);
-    const bool hit = __ballot(lane < i && mine == (int)r) != 0;
-    if (lane == i) mine = hit ? j : (int)r;
+  // lane i draws step i's value r_i in [0, j_i], j_i = A - n + i (the draws are independent)
+  const int jl = A - n + lane;
+  int r = -1;
+  if (lane < n)
+    r = (int)((uint32_t)(splitmix64(k ^ ((uint64_t)(jl + 1) * kSaltFloyd)) >> 32) %
+              (uint32_t)(jl + 1));
+  // With no two equal draws, every step adds its own draw; otherwise the steps are replayed
+  // in order, a draw already taken being replaced by j_i.
+  bool dup = false;
+  for (int i = 0; i < n; ++i) dup = dup || (lane > i && readlane_i(r, i) == r);
+  int mine = r;  // lane i holds the i-th sampled value
+  if (__ballot(dup && lane < n) != 0) {
+    mine = -1;
+    for (int i = 0; i < n; ++i) {
+      const int ri = readlane_i(r, i);
+      const bool hit = __ballot(lane < i && mine == ri) != 0;
+      if (lane == i) mine = hit ? A - n + i : ri;
+    }
   }
   // rank sort (values are distinct)
   int rank = 0;
