@@ -15,6 +15,7 @@ namespace omq {
 
 constexpr int kBackupThreads = 256;
 constexpr int kBigGroup = 32;
+constexpr int kBigChunk = 4;  // member values per lane held per chunk of a big group
 
 // signed value per simulation: v(leaf), negated when the leaf depth is odd in leaf-positive
 // mode, so that the contribution at depth d is (d odd ? -sv : sv)
@@ -33,11 +34,10 @@ __global__ void sim_value_kernel(omq_forest f, omq_wave w, int W, int sign_mode)
 // w + (l + 64*i) * waves), so the few big groups of a level -- they are logged next to each
 // other -- land in different waves.  A small group is folded by its lane after all of its
 // member values have been fetched (the loads of a lane are issued together); a big group is
-// folded by its wave: the member values are staged in LDS 64 at a time and lane 0 adds them in
-// order from registers.
+// folded by its wave: 64 member values at a time, one per lane, are read into scalar
+// registers and added in order (the loads of the next 256 are in flight meanwhile).
 __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_forest f, omq_wave w,
                                                                        int vli) {
-  __shared__ __align__(16) float stage[kBackupThreads / kWave][kWave];
   const int t = blockIdx.y;
   const int lane = lane_id();
   const int wib = threadIdx.x / kWave;
@@ -49,7 +49,6 @@ __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_fores
   const int waves_total = gridDim.x * (kBackupThreads / kWave);
   const int wave_global = blockIdx.x * (kBackupThreads / kWave) + wib;
   const float* sv = w.sim_value + wb;
-  float* st = stage[wib];
   for (int i0 = 0; wave_global + i0 * waves_total < G; i0 += kWave) {
     const int g = wave_global + (i0 + lane) * waves_total;
     int p = 0, d = 0, seg = 0, m = 0;
@@ -83,36 +82,37 @@ __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_fores
       const uint16_t* bmem = w.gmembers + ((int64_t)t * MD + bd) * MW + bseg;
       const bool odd = bd & 1;
       float acc = f.value_sums[tb + bp];
-      // fetch 4 chunks of 64 ahead, then fold each chunk in order on lane 0
-      for (int c0 = 0; c0 < bm; c0 += 4 * kWave) {
-        float x[4];
+      // chunks of kBigChunk*64 members: the next chunk's values are loaded while the current
+      // one is folded in order
+      float xa[kBigChunk], xb[kBigChunk];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int c = c0 + u * kWave + lane;
-          const float v = c < bm ? sv[bmem[c]] : 0.0f;
-          x[u] = odd ? -v : v;
+      for (int u = 0; u < kBigChunk; ++u) {
+        const int c = u * kWave + lane;
+        xa[u] = c < bm ? sv[bmem[c]] : 0.0f;
+      }
+      for (int c0 = 0; c0 < bm; c0 += kBigChunk * kWave) {
+        const int cn = c0 + kBigChunk * kWave;
+#pragma unroll
+        for (int u = 0; u < kBigChunk; ++u) {
+          const int c = cn + u * kWave + lane;
+          xb[u] = c < bm ? sv[bmem[c]] : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kBigChunk; ++u) {
           const int cb = c0 + u * kWave;
           if (cb >= bm) break;
-          st[lane] = x[u];
-          wave_sync();
-          if (lane == 0) {
-            const int lim = min(kWave, bm - cb);
-            const float4* s4 = reinterpret_cast<const float4*>(st);
-            int j = 0;
-            for (; j + 4 <= lim; j += 4) {
-              const float4 q = s4[j >> 2];
-              acc = acc + q.x;
-              acc = acc + q.y;
-              acc = acc + q.z;
-              acc = acc + q.w;
-            }
-            for (; j < lim; ++j) acc = acc + st[j];
+          // lanes 0..63 hold members cb..cb+63: add them in order from scalar registers (the
+          // reads are independent, only the adds form a chain)
+          const float x = odd ? -xa[u] : xa[u];
+          if (bm - cb >= kWave) {
+#pragma unroll
+            for (int l = 0; l < kWave; ++l) acc = acc + readlane_f(x, l);
+          } else {
+            for (int l = 0; l < bm - cb; ++l) acc = acc + readlane_f(x, l);
           }
-          wave_sync();
         }
+#pragma unroll
+        for (int u = 0; u < kBigChunk; ++u) xa[u] = xb[u];
       }
       if (lane == 0) {
         f.value_sums[tb + bp] = acc;
