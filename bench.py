@@ -173,7 +173,8 @@ def run(args) -> dict:
     }
     if wl.evaluator == "resnet":
         out["evaluator"] = (f"random-init ResNet {ev.net.blocks.__len__()} blocks x 128 channels, "
-                            "18 planes, bf16 autocast, one forward pass per wave over "
+                            "18 planes, bf16 weights and activations, batch norm folded, "
+                            "channels-last, one forward pass per wave over "
                             f"{wl.num_trees} trees x {wl.wave_size} slots = "
                             f"{wl.num_trees * wl.wave_size} positions")
         out["tree_op_share"] = round(tree_ms / (tree_ms + eval_ms), 4)
@@ -218,8 +219,8 @@ def graph_replay(wl, eng, ev, args) -> dict:
 
 def next_rows(wl, eng, ev) -> dict:
     """The operations beside the wave path, timed once on the searched trees (after the
-    parity check, outside the timed region): the Gomoku terminal check of one wave's leaves
-    and the subtree reuse of every tree."""
+    parity check, outside the timed region): the Gomoku terminal check and the feature planes
+    of one wave's leaves, the per-move root operations and the subtree reuse of every tree."""
     import torch
 
     from omoknuni_quantum_amd import _lib
@@ -257,6 +258,27 @@ def next_rows(wl, eng, ev) -> dict:
             "algorithmic_bytes": ab, "algorithmic_GBps": round(ab / (us * 1e-6) / 1e9, 2),
             "launch": f"one wave of {wl.wave_size} simulations per tree after the timed "
                       f"searches, freestyle rule, {reps} launches averaged"}
+        # feature planes of the same wave's slots: bfloat16 channels-last (the ResNet's input)
+        # and float32 NCHW with the reference's 19 planes
+        dev_boards = torch.from_numpy(boards.reshape(-1).copy()).to(eng.device)
+        feats = {}
+        for name, planes, dtype, nhwc in (("bf16_nhwc_18", 18, torch.bfloat16, True),
+                                          ("f32_nchw_19", 19, torch.float32, False)):
+            buf = torch.empty(eng.T * eng.MW * planes * eng.A, dtype=dtype, device=eng.device)
+            eng.leaf_features(buf, dev_boards, planes, nhwc=nhwc)
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(reps):
+                eng.leaf_features(buf, dev_boards, planes, nhwc=nhwc)
+            stop.record()
+            torch.cuda.synchronize()
+            us = start.elapsed_time(stop) * 1e3 / reps
+            # every slot's planes written; per unique leaf its root board and path moves read
+            ab = buf.numel() * buf.element_size() + nu * wl.model.num_actions + 4 * moves
+            feats[name] = {"us_per_launch": round(us, 3), "algorithmic_bytes": ab,
+                           "algorithmic_GBps": round(ab / (us * 1e-6) / 1e9, 2)}
+        out["leaf_features"] = dict(feats, slots=eng.T * eng.MW, unique_leaves=nu,
+                                    launch=f"the same wave's slots, {reps} launches averaged")
         eng.set_gomoku_rules(None)
     # per-move root operations: policy rows, a move per tree at temperature 1, root noise
     def timed(fn, reps=20):

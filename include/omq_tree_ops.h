@@ -80,6 +80,12 @@ extern "C" {
 /* workspace of omq_shift_root: int32 entries per node of capacity, per tree */
 #define OMQ_SHIFT_WORKSPACE_PER_NODE 8
 
+/* output of omq_leaf_features */
+#define OMQ_DTYPE_F32 0   /* float32 planes */
+#define OMQ_DTYPE_BF16 1  /* bfloat16 planes, rounded to nearest even */
+#define OMQ_LAYOUT_NCHW 0 /* [slot][plane][cell] */
+#define OMQ_LAYOUT_NHWC 1 /* [slot][cell][plane] (channels-last) */
+
 /* limits of this build */
 #define OMQ_MAX_WAVE 4096   /* simulations per tree per wave */
 #define OMQ_MAX_ROW 512     /* children per node (a selection row is held in registers) */
@@ -226,6 +232,25 @@ int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
 int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
                         const int32_t* root_player, int32_t rule, int32_t* uterminal,
                         void* stream);
+
+/* Neural-network feature planes of every wave slot of a Gomoku forest; call it after
+ * omq_leaf_info.  Needs an OMQ_GAME_BOARD forest with num_actions = bs*bs.
+ * - Slots.  out holds num_trees*max_wave slots of planes*bs*bs values (slot t*max_wave+u).
+ *   Slot u < ucount[t] receives the position of unique leaf u; the other slots receive zeros.
+ * - Position.  As in omq_gomoku_terminal: the root board with the path's moves in alternating
+ *   colours from root_player[t] (NULL: 1 when the root board holds an even number of stones,
+ *   else 2). The leaf's move count is root_moves[t] (NULL: the root board's stone count) plus
+ *   the moves on the path (python/mcts/core/mcts.py:1503-1508, cpu_game_states.py:352-412).
+ * - Planes (planes = 18 or 19).  0 stones of the player to move; 1 the opponent's stones;
+ *   2-15 zero; 16 ones when player 1 is to move; 17 move count / 100; 18 ones (19 planes only).
+ *   This is CPUGameStates.get_nn_features 'basic' (python/mcts/cpu/cpu_game_states.py:430-494);
+ *   18 planes leaves out its last, all-ones plane.
+ * - dtype OMQ_DTYPE_F32 or OMQ_DTYPE_BF16; layout OMQ_LAYOUT_NCHW or OMQ_LAYOUT_NHWC.
+ * Replaces the per-state feature extraction of CPUGameStates.get_nn_features and the GPU
+ * feature builder of GPUGameStates (python/mcts/gpu/gpu_game_states.py:534-664). */
+int omq_leaf_features(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
+                      const int32_t* root_player, const int32_t* root_moves, int32_t planes,
+                      int32_t dtype, int32_t layout, void* out, void* stream);
 
 /* Subtree reuse.  For every tree t with 0 < new_roots[t] < num_nodes[t], node new_roots[t]
  * becomes the root, and its subtree is kept. Other values leave tree t unchanged.

@@ -31,6 +31,8 @@ OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT = 1, 2
 OMQ_RULE_FREESTYLE, OMQ_RULE_RENJU = 0, 1
 OMQ_TERM_NONE, OMQ_TERM_WIN1, OMQ_TERM_WIN2, OMQ_TERM_DRAW = 0, 1, 2, 3
 OMQ_SHIFT_WORKSPACE_PER_NODE = 8
+OMQ_DTYPE_F32, OMQ_DTYPE_BF16 = 0, 1
+OMQ_LAYOUT_NCHW, OMQ_LAYOUT_NHWC = 0, 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -72,6 +74,7 @@ SIGNATURES = {
     "omq_virtual_loss": (ctypes.c_int, [_FP, _p, _p, _i32, _i32, _p]),
     "omq_gomoku_terminal": (ctypes.c_int, [_FP, _WP, _p, _p, _i32, _p, _p]),
     "omq_shift_root": (ctypes.c_int, [_FP, _p, _p, ctypes.c_int64, _p]),
+    "omq_leaf_features": (ctypes.c_int, [_FP, _WP, _p, _p, _p, _i32, _i32, _i32, _p, _p]),
     "omq_root_policy": (ctypes.c_int, [_FP, _p, _p]),
     "omq_sample_actions": (ctypes.c_int, [_FP, _p, ctypes.c_double, ctypes.c_uint64,
                                           ctypes.c_uint64, _p, _p]),

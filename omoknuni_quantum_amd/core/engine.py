@@ -191,6 +191,33 @@ class WaveEngine:
                 None if self.root_player is None else self.root_player.data_ptr(), self.rule,
                 self.uterm.data_ptr(), self.stream_handle()), "omq_gomoku_terminal")
 
+    def leaf_features(self, out: torch.Tensor, boards: torch.Tensor, planes: int = 18,
+                      root_player: torch.Tensor | None = None,
+                      root_moves: torch.Tensor | None = None, nhwc: bool = False) -> None:
+        """Feature planes of every wave slot (omq_leaf_features) into out: float32 or bfloat16,
+        T*max_wave*planes*A values on the engine's device; boards: int8 [T*A] root positions;
+        root_player / root_moves: optional int32 [T]."""
+        if out.dtype == torch.float32:
+            dt = _lib.OMQ_DTYPE_F32
+        elif out.dtype == torch.bfloat16:
+            dt = _lib.OMQ_DTYPE_BF16
+        else:
+            raise ValueError(f"feature planes are float32 or bfloat16, not {out.dtype}")
+        if out.numel() != self.T * self.MW * planes * self.A or not out.is_contiguous():
+            raise ValueError("out must be a contiguous buffer of T*max_wave*planes*A values")
+        for name, x, n, dty in (("boards", boards, self.T * self.A, torch.int8),
+                                ("root_player", root_player, self.T, torch.int32),
+                                ("root_moves", root_moves, self.T, torch.int32)):
+            if x is not None and (x.dtype != dty or x.numel() != n or not x.is_contiguous()
+                                  or x.device != out.device):
+                raise ValueError(f"{name} must be contiguous {dty} [{n}] on {out.device}")
+        self._check(self.lib.omq_leaf_features(
+            self.forest_ref, self.wave_ref, boards.data_ptr(),
+            None if root_player is None else root_player.data_ptr(),
+            None if root_moves is None else root_moves.data_ptr(), planes, dt,
+            _lib.OMQ_LAYOUT_NHWC if nhwc else _lib.OMQ_LAYOUT_NCHW, out.data_ptr(),
+            self.stream_handle()), "omq_leaf_features")
+
     def expand(self, wave_size: int) -> None:
         p = self.params
         noise = self.noise.data_ptr() if (self.has_noise and p.dirichlet_epsilon > 0) else None

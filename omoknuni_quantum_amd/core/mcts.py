@@ -35,6 +35,20 @@ from .mcts_config import GameType, MCTSConfig
 logger = logging.getLogger(__name__)
 
 
+def _input_planes(evaluator) -> int:
+    """Feature planes a reference-protocol evaluator takes: the 19 of the reference's 'basic'
+    representation (cpu_game_states.py:452-494, ResNetConfig.input_channels = 19 in
+    neural_networks/resnet_model.py:21), or 18 when the evaluator or its network says
+    input_channels = 18."""
+    for obj in (evaluator, getattr(evaluator, "model", None), getattr(evaluator, "network", None)):
+        ch = getattr(obj, "input_channels", None)
+        if ch is not None:
+            if int(ch) not in (18, 19):
+                raise ValueError(f"evaluator input_channels {ch}: feature planes are 18 or 19")
+            return int(ch)
+    return 19
+
+
 class _BatchEvaluatorAdapter:
     """Runs a reference-protocol evaluator on the device-built features of the unique leaves
     and writes its outputs into the engine's policy/value rows."""
@@ -187,7 +201,9 @@ class MCTS:
         if not self.model.is_board:
             raise NotImplementedError("feature-plane evaluators need a board game model")
         from .features import LeafFeatureBuilder
-        return _BatchEvaluatorAdapter(self.evaluator, LeafFeatureBuilder(self.engine, self._boards))
+        planes = _input_planes(self.evaluator)
+        return _BatchEvaluatorAdapter(self.evaluator,
+                                      LeafFeatureBuilder(self.engine, self._boards, planes))
 
     # ---- search --------------------------------------------------------------------------
     def search(self, state: Any, num_simulations: Optional[int] = None) -> np.ndarray:

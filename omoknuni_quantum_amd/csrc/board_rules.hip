@@ -1,4 +1,4 @@
-// Gomoku terminal check of the unique leaves of a wave (gfx950).
+// Gomoku positions of the unique leaves of a wave: terminal check and feature planes (gfx950).
 //
 // The reference decides after every move whether a child state is terminal.
 // CPUGameStates.apply_actions (python/mcts/cpu/cpu_game_states.py:352-412) calls
@@ -25,6 +25,39 @@
 
 namespace omq {
 
+// Rebuilds the position of unique leaf u of tree t into the wave's LDS board b: the root board
+// with the path's moves played in alternating colours from the root's player to move.  Returns
+// the path length L (the leaf has L-1 moves on it).  *rp_out receives the root's player to
+// move: root_player[t], or 1 when the root board holds an even number of stones, else 2
+// (python/mcts/core/mcts.py:1503-1508); *stones_out the root board's stone count.
+__device__ inline int rebuild_leaf_board(const omq_forest& f, const omq_wave& w,
+                                         const int8_t* root_boards, const int32_t* root_player,
+                                         int t, int u, int cells, int8_t* b, int* rp_out,
+                                         int* stones_out) {
+  const int lane = lane_id();
+  const int8_t* rb = root_boards + (int64_t)t * cells;
+  int stones = 0;
+  for (int i = lane; i < cells; i += kWave) {
+    const int8_t v = rb[i];
+    b[i] = v;
+    stones += v != 0;
+  }
+  stones = wave_sum_i(stones);
+  const int s0 = w.ufirst[(int64_t)t * w.max_wave + u];
+  int a_lo, a_hi;
+  const int L = load_path_actions(f, w, t, s0, &a_lo, &a_hi);
+  const int rp = root_player != nullptr ? root_player[t] : ((stones & 1) == 0 ? 1 : 2);
+  wave_sync();
+  // move j (0-based, depth j+1) is played by rp when j is even; lane l holds moves l and l+64
+  const int8_t mine = (int8_t)((lane & 1) == 0 ? rp : 3 - rp);
+  if (lane + 1 < L && a_lo >= 0 && a_lo < cells) b[a_lo] = mine;
+  if (lane + 65 < L && a_hi >= 0 && a_hi < cells) b[a_hi] = mine;
+  wave_sync();
+  *rp_out = rp;
+  *stones_out = stones;
+  return L;
+}
+
 __global__ void gomoku_terminal_kernel(omq_forest f, omq_wave w, const int8_t* root_boards,
                                        const int32_t* root_player, int rule, int bs,
                                        int32_t* uterm) {
@@ -38,28 +71,12 @@ __global__ void gomoku_terminal_kernel(omq_forest f, omq_wave w, const int8_t* r
   const int64_t wb = (int64_t)t * w.max_wave;
   if (u >= w.ucount[t]) return;
   int8_t* b = reinterpret_cast<int8_t*>(smem + (size_t)wave * stride);
-  const int8_t* rb = root_boards + (int64_t)t * cells;
-  int stones = 0;
-  for (int i = lane; i < cells; i += kWave) {
-    const int8_t v = rb[i];
-    b[i] = v;
-    stones += v != 0;
-  }
-  stones = wave_sum_i(stones);
-  const int s0 = w.ufirst[wb + u];
-  int a_lo, a_hi;
-  const int L = load_path_actions(f, w, t, s0, &a_lo, &a_hi);
+  int rp, stones;
+  const int L = rebuild_leaf_board(f, w, root_boards, root_player, t, u, cells, b, &rp, &stones);
   if (L <= 1) {  // the root position itself is not checked (the reference never flags it)
     if (uterm != nullptr && lane == 0) uterm[wb + u] = OMQ_TERM_NONE;
     return;
   }
-  const int rp = root_player != nullptr ? root_player[t] : ((stones & 1) == 0 ? 1 : 2);
-  wave_sync();
-  // move j (0-based, depth j+1) is played by rp when j is even; lane l holds moves l and l+64
-  const int8_t mine = (int8_t)((lane & 1) == 0 ? rp : 3 - rp);
-  if (lane + 1 < L && a_lo >= 0 && a_lo < cells) b[a_lo] = mine;
-  if (lane + 65 < L && a_hi >= 0 && a_hi < cells) b[a_hi] = mine;
-  wave_sync();
 
   constexpr int dr[4] = {0, 1, 1, 1};
   constexpr int dc[4] = {1, 0, 1, -1};
@@ -110,6 +127,90 @@ hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const 
   dim3 grid((w.max_wave + wpb - 1) / wpb, f.num_trees);
   hipLaunchKernelGGL(gomoku_terminal_kernel, grid, dim3(wpb * kWave), lds, st, f, w, boards,
                      root_player, rule, bs, uterm);
+  return hipGetLastError();
+}
+
+// Feature planes of every wave slot (one wavefront per slot u of tree t).  Slot u < ucount[t]
+// holds the position of unique leaf u; the other slots are written with zeros.  Planes follow
+// CPUGameStates.get_nn_features, representation 'basic' (python/mcts/cpu/cpu_game_states.py:
+// 430-494), with the leaf's player to move and move count as CPUGameStates.apply_actions
+// (cpu_game_states.py:352-412) leaves them after the path's moves:
+//   0 stones of the player to move, 1 stones of the opponent, 2-15 zero (history, unused by
+//   the reference), 16 ones when player 1 is to move, 17 move count / 100 (the reference's
+//   int16 count divided in double, stored as float), 18 ones (only with 19 planes).
+// The slot's planes are one contiguous block of C*cells values; lane l writes elements
+// l, l+64, ... of it, so a wave's stores cover consecutive addresses.
+template <typename OutT>
+__device__ inline OutT plane_value(float v);
+template <>
+__device__ inline float plane_value<float>(float v) {
+  return v;
+}
+template <>
+__device__ inline uint16_t plane_value<uint16_t>(float v) {  // bfloat16, round to nearest even
+  const uint32_t x = __float_as_uint(v);
+  return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+}
+
+template <typename OutT>
+__global__ void leaf_features_kernel(omq_forest f, omq_wave w, const int8_t* root_boards,
+                                     const int32_t* root_player, const int32_t* root_moves,
+                                     int bs, int planes, int nhwc, OutT* out) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int cells = bs * bs;
+  const int stride = (cells + 15) & ~15;
+  const int t = blockIdx.y;
+  const int wave = threadIdx.x / kWave;
+  const int u = blockIdx.x * (blockDim.x / kWave) + wave;
+  const int lane = lane_id();
+  if (u >= w.max_wave) return;
+  const int per = planes * cells;
+  OutT* o = out + ((int64_t)t * w.max_wave + u) * per;
+  if (u >= w.ucount[t]) {
+    for (int i = lane; i < per; i += kWave) o[i] = plane_value<OutT>(0.0f);
+    return;
+  }
+  int8_t* b = reinterpret_cast<int8_t*>(smem + (size_t)wave * stride);
+  int rp, stones;
+  const int L = rebuild_leaf_board(f, w, root_boards, root_player, t, u, cells, b, &rp, &stones);
+  const int moves = L - 1;
+  const int tm = (moves & 1) == 0 ? rp : 3 - rp;  // player to move at the leaf
+  const int mc = (root_moves != nullptr ? root_moves[t] : stones) + moves;
+  const float mcv = (float)((double)mc / 100.0);
+  const float colour = tm == 1 ? 1.0f : 0.0f;
+  for (int i = lane; i < per; i += kWave) {
+    int c, cell;
+    if (nhwc) {
+      cell = i / planes;
+      c = i - cell * planes;
+    } else {
+      c = i / cells;
+      cell = i - c * cells;
+    }
+    float v = 0.0f;
+    if (c == 0) v = b[cell] == tm ? 1.0f : 0.0f;
+    else if (c == 1) v = b[cell] == 3 - tm ? 1.0f : 0.0f;
+    else if (c == 16) v = colour;
+    else if (c == 17) v = mcv;
+    else if (c == 18) v = 1.0f;
+    o[i] = plane_value<OutT>(v);
+  }
+}
+
+hipError_t launch_leaf_features(const omq_forest& f, const omq_wave& w, const int8_t* boards,
+                                const int32_t* root_player, const int32_t* root_moves, int bs,
+                                int planes, int dtype, int nhwc, void* out, hipStream_t st) {
+  constexpr int wpb = 4;
+  const size_t lds = (size_t)(((bs * bs) + 15) & ~15) * wpb;
+  dim3 grid((w.max_wave + wpb - 1) / wpb, f.num_trees);
+  if (dtype == OMQ_DTYPE_BF16)
+    hipLaunchKernelGGL(leaf_features_kernel<uint16_t>, grid, dim3(wpb * kWave), lds, st, f, w,
+                       boards, root_player, root_moves, bs, planes, nhwc,
+                       static_cast<uint16_t*>(out));
+  else
+    hipLaunchKernelGGL(leaf_features_kernel<float>, grid, dim3(wpb * kWave), lds, st, f, w,
+                       boards, root_player, root_moves, bs, planes, nhwc,
+                       static_cast<float*>(out));
   return hipGetLastError();
 }
 

@@ -36,6 +36,9 @@ hipError_t launch_root_dirichlet(const omq_forest& f, double alpha, uint64_t see
 hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const int8_t* boards,
                                   const int32_t* root_player, int rule, int bs, int32_t* uterm,
                                   hipStream_t st);
+hipError_t launch_leaf_features(const omq_forest& f, const omq_wave& w, const int8_t* boards,
+                                const int32_t* root_player, const int32_t* root_moves, int bs,
+                                int planes, int dtype, int nhwc, void* out, hipStream_t st);
 size_t leaf_lds_per_wave_host(const omq_forest& f);
 }  // namespace omq
 
@@ -184,6 +187,31 @@ int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* ro
   return hip_status(omq::launch_gomoku_terminal(*f, *w, root_boards, root_player, rule, bs,
                                                 uterminal, (hipStream_t)stream),
                     "omq_gomoku_terminal");
+}
+
+int omq_leaf_features(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
+                      const int32_t* root_player, const int32_t* root_moves, int32_t planes,
+                      int32_t dtype, int32_t layout, void* out, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  rc = check_wave(f, w, w ? w->max_wave : 1);
+  if (rc) return rc;
+  if (f->game != OMQ_GAME_BOARD)
+    return fail(OMQ_E_ARG, "omq_leaf_features needs a board forest (game %d)", f->game);
+  int bs = 0;
+  while ((bs + 1) * (bs + 1) <= f->num_actions) ++bs;
+  if (bs * bs != f->num_actions)
+    return fail(OMQ_E_ARG, "num_actions %d is not a square board", f->num_actions);
+  if (!root_boards || !out) return fail(OMQ_E_ARG, "root_boards and out are required");
+  if (planes != 18 && planes != 19) return fail(OMQ_E_ARG, "planes %d is not 18 or 19", planes);
+  if (dtype != OMQ_DTYPE_F32 && dtype != OMQ_DTYPE_BF16)
+    return fail(OMQ_E_ARG, "unknown feature dtype %d", dtype);
+  if (layout != OMQ_LAYOUT_NCHW && layout != OMQ_LAYOUT_NHWC)
+    return fail(OMQ_E_ARG, "unknown feature layout %d", layout);
+  return hip_status(omq::launch_leaf_features(*f, *w, root_boards, root_player, root_moves, bs,
+                                              planes, dtype, layout == OMQ_LAYOUT_NHWC, out,
+                                              (hipStream_t)stream),
+                    "omq_leaf_features");
 }
 
 int omq_shift_root(const omq_forest* f, const int32_t* new_roots, int32_t* workspace,

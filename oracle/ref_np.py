@@ -246,6 +246,41 @@ def gomoku_terminal(board, renju: bool = False) -> int:
     return 3 if np.all(b != 0) else 0
 
 
+def leaf_position(root_board, path_actions, root_player=None, root_moves=None):
+    """Position after the moves of a path, as CPUGameStates.apply_actions leaves it
+    (python/mcts/cpu/cpu_game_states.py:372-384): each move puts the current player's stone on
+    cell (a // bs, a % bs), switches the player and adds one to the move count.  The root's
+    player and move count are those MCTS gives an ndarray root (python/mcts/core/mcts.py:
+    1503-1508): player 1 when the stone count is even, else 2, and the stone count.
+    Returns (board int8 [bs, bs], player to move, move count)."""
+    b = np.array(root_board, dtype=np.int8, copy=True)
+    bs = b.shape[0]
+    stones = int(np.count_nonzero(b))
+    player = (1 if stones % 2 == 0 else 2) if root_player is None else int(root_player)
+    count = stones if root_moves is None else int(root_moves)
+    for a in path_actions:
+        b[a // bs, a % bs] = player
+        player = 3 - player
+        count += 1
+    return b, player, count
+
+
+def nn_features(board, player, move_count, planes: int = 19):
+    """CPUGameStates.get_nn_features, representation 'basic' (python/mcts/cpu/
+    cpu_game_states.py:452-494), of one position: float32 [planes, bs, bs] with
+    0 the player's stones, 1 the opponent's, 2-15 zero, 16 ones when player 1 is to move,
+    17 move_count / 100 (int16 count over a Python float: a double division, stored as
+    float32), 18 ones.  planes=18 leaves out the last plane."""
+    bs = board.shape[0]
+    f = np.zeros((19, bs, bs), dtype=np.float32)
+    f[0] = (board == player).astype(np.float32)
+    f[1] = (board == 3 - player).astype(np.float32)
+    f[16] = float(player == 1)
+    f[17] = np.int16(move_count) / 100.0
+    f[18] = 1.0
+    return f[:planes]
+
+
 def board_legal(root_empty, path_actions, pass_action=None):
     taken = {a for a in path_actions if a != pass_action}
     return [a for a in root_empty if a not in taken]

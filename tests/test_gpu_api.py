@@ -8,6 +8,7 @@ from omoknuni_quantum_amd.core.mcts_config import GameType, MCTSConfig
 from omoknuni_quantum_amd.synthetic import games
 from omoknuni_quantum_amd.synthetic.evaluator import SyntheticEvaluator
 from oracle.oracle import Oracle
+from oracle.ref_np import leaf_position, nn_features
 
 pytestmark = pytest.mark.gpu
 
@@ -150,10 +151,12 @@ class _RecordingEvaluator:
 
     def __init__(self, seed=0):
         g = torch.Generator().manual_seed(seed)
-        self.w = (torch.randn(18, generator=g) * 0.5)
+        self.w = (torch.randn(19, generator=g) * 0.5)
         self.calls = []
+        self.feats = []
 
     def evaluate_batch(self, feats):
+        self.feats.append(feats.cpu().numpy().copy())
         x = feats.float()
         w = self.w.to(x.device)[None, :, None, None]
         logits = (x * w).sum(dim=1).reshape(x.shape[0], -1) * 3
@@ -170,6 +173,11 @@ def test_feature_evaluator_replay_parity(device):
     m = MCTS(cfg, ev)
     pol = m.search(board)
     assert len(ev.calls) == 1 + 160 // 32
+    # reference 'basic' planes; the root wave's one leaf is the root position itself
+    assert ev.feats[0].shape[1:] == (19, 15, 15)
+    b, player, count = leaf_position(board, [])
+    assert np.array_equal(ev.feats[0][0], nn_features(b, player, count, 19))
+    assert not ev.feats[0][1:].any()
     orc = _oracle_for(cfg, board[None])
     orc.reset_tree(0)
     sizes = [1] + [32] * 5

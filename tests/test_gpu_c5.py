@@ -51,3 +51,22 @@ def test_resnet_architecture_shapes():
         lp, v = net(torch.zeros(2, 18, 15, 15))
     assert lp.shape == (2, 225) and v.shape == (2,)
     assert torch.allclose(lp.exp().sum(1), torch.ones(2), atol=1e-5)
+
+
+def test_batch_norm_folding_is_exact_in_float32():
+    import copy
+
+    from omoknuni_quantum_amd.synthetic.resnet_evaluator import AlphaZeroResNet, fold_batch_norm
+
+    torch.manual_seed(0)
+    net = AlphaZeroResNet(9, 81, num_blocks=2, channels=16).eval()
+    for m in net.modules():  # non-trivial running statistics
+        if isinstance(m, torch.nn.BatchNorm2d):
+            m.running_mean.uniform_(-0.5, 0.5)
+            m.running_var.uniform_(0.5, 2.0)
+    x = torch.rand(4, 18, 9, 9)
+    with torch.no_grad():
+        lp, v = net(x)
+        lp2, v2 = fold_batch_norm(copy.deepcopy(net))(x)
+    assert not any(isinstance(m, torch.nn.BatchNorm2d) for m in fold_batch_norm(net).modules())
+    assert torch.allclose(lp, lp2, atol=1e-5) and torch.allclose(v, v2, atol=1e-5)

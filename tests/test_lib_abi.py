@@ -22,7 +22,8 @@ def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("omq_select", "omq_expand", "omq_backup", "omq_forest_reset", "omq_leaf_info",
               "omq_synthetic_evaluate", "omq_paths_backup", "omq_virtual_loss",
-              "omq_gomoku_terminal", "omq_last_error", "omq_abi_version"):
+              "omq_gomoku_terminal", "omq_leaf_features", "omq_last_error",
+              "omq_abi_version"):
         assert n in names
 
 
@@ -109,6 +110,21 @@ def test_invalid_wave_arguments_rejected():
     g = _forest(game=_lib.OMQ_GAME_GO, num_actions=26)
     assert lib.omq_gomoku_terminal(ctypes.byref(g), ctypes.byref(w), 8, None, 0, None,
                                    None) == _lib.OMQ_E_ARG
+    # feature planes: square board forests, boards and output, 18 or 19 planes, known formats
+    assert lib.omq_leaf_features(ctypes.byref(f), ctypes.byref(w), None, None, None, 19, 0, 0,
+                                 8, None) == _lib.OMQ_E_ARG
+    assert "root_boards" in lib.omq_last_error().decode()
+    assert lib.omq_leaf_features(ctypes.byref(f), ctypes.byref(w), 8, None, None, 17, 0, 0, 8,
+                                 None) == _lib.OMQ_E_ARG
+    assert "planes" in lib.omq_last_error().decode()
+    assert lib.omq_leaf_features(ctypes.byref(f), ctypes.byref(w), 8, None, None, 18, 2, 0, 8,
+                                 None) == _lib.OMQ_E_ARG
+    assert "dtype" in lib.omq_last_error().decode()
+    assert lib.omq_leaf_features(ctypes.byref(f), ctypes.byref(w), 8, None, None, 18, 1, 3, 8,
+                                 None) == _lib.OMQ_E_ARG
+    assert "layout" in lib.omq_last_error().decode()
+    assert lib.omq_leaf_features(ctypes.byref(g), ctypes.byref(w), 8, None, None, 18, 0, 0, 8,
+                                 None) == _lib.OMQ_E_ARG
 
 
 def test_missing_library_fails_loudly(tmp_path):
