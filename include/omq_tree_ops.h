@@ -245,9 +245,12 @@ int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* ro
  *   2-15 zero; 16 ones when player 1 is to move; 17 move count / 100; 18 ones (19 planes only).
  *   This is CPUGameStates.get_nn_features 'basic' (python/mcts/cpu/cpu_game_states.py:430-494);
  *   18 planes leaves out its last, all-ones plane.
- * - dtype OMQ_DTYPE_F32 or OMQ_DTYPE_BF16; layout OMQ_LAYOUT_NCHW or OMQ_LAYOUT_NHWC.
- * Replaces the per-state feature extraction of CPUGameStates.get_nn_features and the GPU
- * feature builder of GPUGameStates (python/mcts/gpu/gpu_game_states.py:534-664). */
+ * - dtype OMQ_DTYPE_F32 or OMQ_DTYPE_BF16; layout OMQ_LAYOUT_NCHW or OMQ_LAYOUT_NHWC. out is
+ *   aligned to two elements (8 bytes for float32, 4 for bfloat16).
+ * Replaces the per-state feature extraction of CPUGameStates.get_nn_features, which the CPU
+ * driver feeds its evaluator (python/mcts/cpu/optimized_wave_search.py:337). The reference's
+ * GPU builder, GPUGameStates.get_nn_features (python/mcts/gpu/gpu_game_states.py:534-664),
+ * has the same role with another plane layout. */
 int omq_leaf_features(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
                       const int32_t* root_player, const int32_t* root_moves, int32_t planes,
                       int32_t dtype, int32_t layout, void* out, void* stream);

@@ -130,88 +130,132 @@ hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const 
   return hipGetLastError();
 }
 
-// Feature planes of every wave slot (one wavefront per slot u of tree t).  Slot u < ucount[t]
-// holds the position of unique leaf u; the other slots are written with zeros.  Planes follow
-// CPUGameStates.get_nn_features, representation 'basic' (python/mcts/cpu/cpu_game_states.py:
-// 430-494), with the leaf's player to move and move count as CPUGameStates.apply_actions
-// (cpu_game_states.py:352-412) leaves them after the path's moves:
+// Feature planes of every wave slot (one 256-thread workgroup per slot u of tree t).  Slot
+// u < ucount[t] holds the position of unique leaf u; the other slots are written with zeros.
+// Planes follow CPUGameStates.get_nn_features, representation 'basic'
+// (python/mcts/cpu/cpu_game_states.py:430-494), with the leaf's player to move and move count
+// as CPUGameStates.apply_actions (cpu_game_states.py:352-412) leaves them after the path:
 //   0 stones of the player to move, 1 stones of the opponent, 2-15 zero (history, unused by
 //   the reference), 16 ones when player 1 is to move, 17 move count / 100 (the reference's
 //   int16 count divided in double, stored as float), 18 ones (only with 19 planes).
-// The slot's planes are one contiguous block of C*cells values; lane l writes elements
-// l, l+64, ... of it, so a wave's stores cover consecutive addresses.
-template <typename OutT>
-__device__ inline OutT plane_value(float v);
-template <>
-__device__ inline float plane_value<float>(float v) {
-  return v;
-}
-template <>
-__device__ inline uint16_t plane_value<uint16_t>(float v) {  // bfloat16, round to nearest even
-  const uint32_t x = __float_as_uint(v);
-  return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
-}
+// Wave 0 rebuilds the leaf's board in LDS; then the whole workgroup writes the slot's planes,
+// one contiguous block of PLANES*cells values, element i by thread i mod 256, two values per
+// store where the block has an even length.
+constexpr int kFeatThreads = 256;
 
 template <typename OutT>
-__global__ void leaf_features_kernel(omq_forest f, omq_wave w, const int8_t* root_boards,
-                                     const int32_t* root_player, const int32_t* root_moves,
-                                     int bs, int planes, int nhwc, OutT* out) {
+struct PlaneStore;
+template <>
+struct PlaneStore<float> {
+  using Pair = float2;
+  __device__ static float one(float v) { return v; }
+  __device__ static float2 two(float a, float b) { return make_float2(a, b); }
+};
+template <>
+struct PlaneStore<uint16_t> {  // bfloat16, rounded to nearest even
+  using Pair = uint32_t;
+  __device__ static uint16_t one(float v) {
+    const uint32_t x = __float_as_uint(v);
+    return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+  }
+  __device__ static uint32_t two(float a, float b) {
+    return (uint32_t)one(a) | ((uint32_t)one(b) << 16);
+  }
+};
+
+template <typename OutT, int PLANES, bool NHWC>
+__global__ __launch_bounds__(kFeatThreads) void leaf_features_kernel(
+    omq_forest f, omq_wave w, const int8_t* root_boards, const int32_t* root_player,
+    const int32_t* root_moves, int bs, OutT* out) {
+  using S = PlaneStore<OutT>;
+  using Pair = typename S::Pair;
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float s_val[4];  // player to move is 1, move count / 100, player to move
   const int cells = bs * bs;
-  const int stride = (cells + 15) & ~15;
   const int t = blockIdx.y;
-  const int wave = threadIdx.x / kWave;
-  const int u = blockIdx.x * (blockDim.x / kWave) + wave;
-  const int lane = lane_id();
-  if (u >= w.max_wave) return;
-  const int per = planes * cells;
+  const int u = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int per = PLANES * cells;
   OutT* o = out + ((int64_t)t * w.max_wave + u) * per;
+  const bool pairs = (per & 1) == 0;  // then every slot starts on a pair boundary
   if (u >= w.ucount[t]) {
-    for (int i = lane; i < per; i += kWave) o[i] = plane_value<OutT>(0.0f);
+    if (pairs) {
+      Pair* o2 = reinterpret_cast<Pair*>(o);
+      for (int i = tid; i < per / 2; i += kFeatThreads) o2[i] = S::two(0.0f, 0.0f);
+    } else {
+      for (int i = tid; i < per; i += kFeatThreads) o[i] = S::one(0.0f);
+    }
     return;
   }
-  int8_t* b = reinterpret_cast<int8_t*>(smem + (size_t)wave * stride);
-  int rp, stones;
-  const int L = rebuild_leaf_board(f, w, root_boards, root_player, t, u, cells, b, &rp, &stones);
-  const int moves = L - 1;
-  const int tm = (moves & 1) == 0 ? rp : 3 - rp;  // player to move at the leaf
-  const int mc = (root_moves != nullptr ? root_moves[t] : stones) + moves;
-  const float mcv = (float)((double)mc / 100.0);
-  const float colour = tm == 1 ? 1.0f : 0.0f;
-  for (int i = lane; i < per; i += kWave) {
+  int8_t* b = reinterpret_cast<int8_t*>(smem);
+  if (tid < kWave) {
+    int rp, stones;
+    const int L = rebuild_leaf_board(f, w, root_boards, root_player, t, u, cells, b, &rp,
+                                     &stones);
+    if (tid == 0) {
+      const int moves = L - 1;
+      const int tm = (moves & 1) == 0 ? rp : 3 - rp;  // player to move at the leaf
+      const int mc = (root_moves != nullptr ? root_moves[t] : stones) + moves;
+      s_val[0] = tm == 1 ? 1.0f : 0.0f;
+      s_val[1] = (float)((double)mc / 100.0);
+      s_val[2] = (float)tm;
+    }
+  }
+  __syncthreads();
+  const float colour = s_val[0], mcv = s_val[1];
+  const int tm = (int)s_val[2];
+  auto value = [&](int i) -> float {
     int c, cell;
-    if (nhwc) {
-      cell = i / planes;
-      c = i - cell * planes;
+    if (NHWC) {
+      cell = i / PLANES;
+      c = i - cell * PLANES;
     } else {
       c = i / cells;
       cell = i - c * cells;
     }
-    float v = 0.0f;
-    if (c == 0) v = b[cell] == tm ? 1.0f : 0.0f;
-    else if (c == 1) v = b[cell] == 3 - tm ? 1.0f : 0.0f;
-    else if (c == 16) v = colour;
-    else if (c == 17) v = mcv;
-    else if (c == 18) v = 1.0f;
-    o[i] = plane_value<OutT>(v);
+    if (c == 0) return b[cell] == tm ? 1.0f : 0.0f;
+    if (c == 1) return b[cell] == 3 - tm ? 1.0f : 0.0f;
+    if (c == 16) return colour;
+    if (c == 17) return mcv;
+    if (c == 18) return 1.0f;
+    return 0.0f;
+  };
+  if (pairs) {
+    Pair* o2 = reinterpret_cast<Pair*>(o);
+    for (int i = tid; i < per / 2; i += kFeatThreads) o2[i] = S::two(value(2 * i), value(2 * i + 1));
+  } else {
+    for (int i = tid; i < per; i += kFeatThreads) o[i] = S::one(value(i));
   }
+}
+
+template <typename OutT>
+hipError_t launch_leaf_features_t(const omq_forest& f, const omq_wave& w, const int8_t* boards,
+                                  const int32_t* root_player, const int32_t* root_moves, int bs,
+                                  int planes, bool nhwc, OutT* out, hipStream_t st) {
+  const size_t lds = (size_t)(((bs * bs) + 15) & ~15);
+  dim3 grid(w.max_wave, f.num_trees);
+#define OMQ_FEAT_LAUNCH(P, NH)                                                                  \
+  hipLaunchKernelGGL((leaf_features_kernel<OutT, P, NH>), grid, dim3(kFeatThreads), lds, st, f, \
+                     w, boards, root_player, root_moves, bs, out)
+  if (planes == 18) {
+    if (nhwc) OMQ_FEAT_LAUNCH(18, true);
+    else OMQ_FEAT_LAUNCH(18, false);
+  } else {
+    if (nhwc) OMQ_FEAT_LAUNCH(19, true);
+    else OMQ_FEAT_LAUNCH(19, false);
+  }
+#undef OMQ_FEAT_LAUNCH
+  return hipGetLastError();
 }
 
 hipError_t launch_leaf_features(const omq_forest& f, const omq_wave& w, const int8_t* boards,
                                 const int32_t* root_player, const int32_t* root_moves, int bs,
                                 int planes, int dtype, int nhwc, void* out, hipStream_t st) {
-  constexpr int wpb = 4;
-  const size_t lds = (size_t)(((bs * bs) + 15) & ~15) * wpb;
-  dim3 grid((w.max_wave + wpb - 1) / wpb, f.num_trees);
   if (dtype == OMQ_DTYPE_BF16)
-    hipLaunchKernelGGL(leaf_features_kernel<uint16_t>, grid, dim3(wpb * kWave), lds, st, f, w,
-                       boards, root_player, root_moves, bs, planes, nhwc,
-                       static_cast<uint16_t*>(out));
-  else
-    hipLaunchKernelGGL(leaf_features_kernel<float>, grid, dim3(wpb * kWave), lds, st, f, w,
-                       boards, root_player, root_moves, bs, planes, nhwc,
-                       static_cast<float*>(out));
-  return hipGetLastError();
+    return launch_leaf_features_t(f, w, boards, root_player, root_moves, bs, planes, nhwc != 0,
+                                  static_cast<uint16_t*>(out), st);
+  return launch_leaf_features_t(f, w, boards, root_player, root_moves, bs, planes, nhwc != 0,
+                                static_cast<float*>(out), st);
 }
 
 }  // namespace omq

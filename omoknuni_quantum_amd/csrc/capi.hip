@@ -208,6 +208,9 @@ int omq_leaf_features(const omq_forest* f, const omq_wave* w, const int8_t* root
     return fail(OMQ_E_ARG, "unknown feature dtype %d", dtype);
   if (layout != OMQ_LAYOUT_NCHW && layout != OMQ_LAYOUT_NHWC)
     return fail(OMQ_E_ARG, "unknown feature layout %d", layout);
+  const uintptr_t align = dtype == OMQ_DTYPE_F32 ? 8 : 4;
+  if ((uintptr_t)out % align != 0)
+    return fail(OMQ_E_ARG, "out must be aligned to %d bytes", (int)align);
   return hip_status(omq::launch_leaf_features(*f, *w, root_boards, root_player, root_moves, bs,
                                               planes, dtype, layout == OMQ_LAYOUT_NHWC, out,
                                               (hipStream_t)stream),

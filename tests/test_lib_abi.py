@@ -125,6 +125,9 @@ def test_invalid_wave_arguments_rejected():
     assert "layout" in lib.omq_last_error().decode()
     assert lib.omq_leaf_features(ctypes.byref(g), ctypes.byref(w), 8, None, None, 18, 0, 0, 8,
                                  None) == _lib.OMQ_E_ARG
+    assert lib.omq_leaf_features(ctypes.byref(f), ctypes.byref(w), 8, None, None, 18, 0, 0, 12,
+                                 None) == _lib.OMQ_E_ARG
+    assert "aligned" in lib.omq_last_error().decode()
 
 
 def test_missing_library_fails_loudly(tmp_path):
