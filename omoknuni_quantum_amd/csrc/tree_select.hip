@@ -833,11 +833,107 @@ __device__ inline void small_groups(
   }
 }
 
+// Single-member groups of level d in the kernels without a lane pass.  Such a group's node is
+// usually a leaf, which needs only the node's header (visit count, row offset, row length): all
+// threads take one group each, so the header loads of the whole level are in flight together,
+// and the leaves are finished here as the chain groups finish theirs.  The groups that are not
+// leaves join the level's chain groups.  Every single-member group's entry is read before the
+// barrier, and the chain entries are appended after it, so an appended entry may overwrite a
+// single-member entry that has been read.  Called by every thread of the workgroup.
+constexpr int kLeafPer = (OMQ_MAX_WAVE + kSelThreads - 1) / kSelThreads;
+
+template <int RMAX>
+__device__ inline void leaf_pass(const SelArgs& f, const SelCfg& c, int t, int d, int W,
+                                 int64_t tb, int64_t gmax, uint32_t* gnode, uint32_t* gsl,
+                                 const uint16_t* buf, uint16_t* lfs, int32_t* lflag, int* s_glog,
+                                 unsigned long long* s_st, int* s_nbig, int ns) {
+  const SelArgs& w = f;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int cur = d & 1;
+  const int MW = w.max_wave, MD = w.max_depth_buf;
+  int32_t* N = f.N;
+  uint32_t kp[kLeafPer], ksl[kLeafPer];
+  bool keep[kLeafPer];
+#pragma unroll
+  for (int e = 0; e < kLeafPer; ++e) {
+    const int x = tid + e * kSelThreads;
+    keep[e] = false;
+    kp[e] = 0;
+    ksl[e] = 0;
+    bool leaf = false;
+    int p = 0, seg = 0, s = 0, Np0 = 0;
+    if (x < ns) {
+      const int gi = W - 1 - x;
+      const uint32_t sl = gsl[cur * W + gi];
+      p = (int)gnode[cur * W + gi];
+      seg = (int)(sl & 0xFFFFu);
+      s = buf[cur * W + seg];
+      Np0 = N[tb + p];
+      const int k = f.nchild[tb + p];
+      const int first = f.first[tb + p];
+      leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
+      if (!leaf && k > RMAX * kWave) {
+        atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
+        leaf = true;
+      }
+      keep[e] = !leaf;
+      kp[e] = (uint32_t)p;
+      ksl[e] = sl;
+    }
+    // the leaves: group log, path entry, the arrival's virtual loss, end of the path
+    const uint64_t lm = __ballot(leaf);
+    if (lm == 0) continue;
+    const int nl = __popcll(lm);
+    int gbase = 0;
+    if (lane == 0) {
+      gbase = atomicAdd(s_glog, nl);
+      atomicAdd(&s_st[OMQ_ST_PATHNODES], (unsigned long long)nl);
+      atomicAdd(&s_st[OMQ_ST_PATHENTRIES], (unsigned long long)nl * (d + 1));
+    }
+    gbase = readlane_i(gbase, 0);
+    if (leaf) {
+      const int gid = gbase + (int)__builtin_amdgcn_mbcnt_hi(
+                                  (uint32_t)(lm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)lm, 0u));
+      *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, 1);
+      w.paths[((int64_t)t * MW + s) * MD + d] = p;
+      w.gmembers[((int64_t)t * MD + d) * MW + seg] = (uint16_t)s;
+      if (c.vl_atomic)
+        atomicAdd(&N[tb + p], c.vli);
+      else
+        N[tb + p] = Np0 + c.vli;
+      w.path_len[(int64_t)t * MW + s] = d + 1;
+      w.leaves[(int64_t)t * MW + s] = p;
+      lfs[s] = (uint16_t)s;
+      lflag[s] = 1;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < kLeafPer; ++e) {
+    const uint64_t km = __ballot(keep[e]);
+    if (km == 0) continue;
+    int gbase = 0;
+    if (lane == 0) gbase = atomicAdd(s_nbig, __popcll(km));
+    gbase = readlane_i(gbase, 0);
+    if (keep[e]) {
+      const int g = gbase + (int)__builtin_amdgcn_mbcnt_hi(
+                                (uint32_t)(km >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)km, 0u));
+      gnode[cur * W + g] = kp[e];
+      gsl[cur * W + g] = ksl[e];
+    }
+  }
+}
+
 template <int RMAX>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c) {
   // small groups one per lane; kept out of the widest kernels, whose chains need every
   // register
   constexpr bool kLanePass = RMAX <= 3;
+  // single-member groups through the leaf pass: the kernel of 4 slots per lane (the wider
+  // kernels keep every group a chain: the pass's registers would add spills to their chains)
+  constexpr bool kLeafPass = RMAX == 4;
+  constexpr bool kSingles = kLanePass || kLeafPass;  // single-member groups kept apart
   SelArgs& w = f;
   extern __shared__ __align__(16) unsigned char smem[];
   const int W = c.W;
@@ -877,7 +973,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   if (tid < OMQ_NSTATS) s_st[tid] = 0;
   if (tid == 0) {
     // the root group is a chain unless the lane pass takes it
-    const bool root_big = !kLanePass || W > kSmallGroup;
+    const bool root_big = !kSingles || W > kSmallGroup;
     const int g0 = root_big ? 0 : W - 1;
     gnode[g0] = 0;
     gsl[g0] = 0u | ((uint32_t)W << 16);
@@ -893,9 +989,17 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
 
   for (int d = 0; d < c.max_depth; ++d) {
     const int cur = d & 1, nxt = cur ^ 1;
-    const int nb = s_nbig[cur];
-    const int ng = nb + s_nsmall[cur];
+    const int ng = s_nbig[cur] + s_nsmall[cur];
     if (ng == 0) break;
+    if (kLeafPass) {
+      // single-member groups: leaves finished by all threads at once, the rest become chains
+      if (s_nsmall[cur] > 0) {
+        leaf_pass<RMAX>(f, c, t, d, W, tb, gmax, gnode, gsl, buf, lfs, lflag, &s_glog, s_st,
+                        &s_nbig[cur], s_nsmall[cur]);
+        __syncthreads();
+      }
+    }
+    const int nb = s_nbig[cur];
     // The chain groups are dealt dynamically: each wave takes the next index from an LDS
     // counter, so a wave that finishes a short chain takes the next group at once.  The next
     // index is requested when a group starts, so that the answer is back by its end.  Every
@@ -976,7 +1080,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         sum += v;
-        const bool big = !kLanePass || v > kSmallGroup;
+        const bool big = !kSingles || v > kSmallGroup;
         nbg += v > 0 && big;
         nsm += v > 0 && !big;
       }
@@ -992,7 +1096,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         if (v > 0) {
-          const bool big = !kLanePass || v > kSmallGroup;
+          const bool big = !kSingles || v > kSmallGroup;
           const int g = big ? bbase + pbg++ : W - 1 - (sbase + psm++);
           gnode[nxt * W + g] = (uint32_t)(first + 1 + i);
           gsl[nxt * W + g] = (uint32_t)(seg + run) | ((uint32_t)v << 16);
