@@ -833,15 +833,14 @@ __device__ inline void small_groups(
   }
 }
 
-// Single-member groups of level d in the kernels without a lane pass.  Such a group's node is
-// usually a leaf, which needs only the node's header (visit count, row offset, row length): all
-// threads take one group each, so the header loads of the whole level are in flight together,
-// and the leaves are finished here as the chain groups finish theirs.  The groups that are not
-// leaves join the level's chain groups.  Every single-member group's entry is read before the
-// barrier, and the chain entries are appended after it, so an appended entry may overwrite a
-// single-member entry that has been read.  Called by every thread of the workgroup.
-constexpr int kLeafPer = (OMQ_MAX_WAVE + kSelThreads - 1) / kSelThreads;
-
+// Single-member groups of level d in the kernels without a lane pass, for waves of at most
+// kSelThreads simulations.  Such a group's node is usually a leaf, which needs only the node's
+// header (visit count, row offset, row length): every thread takes one group, so the header
+// loads of the whole level are in flight together, and the leaves are finished here as the
+// chain groups finish theirs.  The groups that are not leaves join the level's chain groups.
+// Every single-member group's entry is read before the barrier, and the chain entries are
+// appended after it, so an appended entry may overwrite only entries already read.  Called by
+// every thread of the workgroup.
 template <int RMAX>
 __device__ inline void leaf_pass(const SelArgs& f, const SelCfg& c, int t, int d, int W,
                                  int64_t tb, int64_t gmax, uint32_t* gnode, uint32_t* gsl,
@@ -853,37 +852,28 @@ __device__ inline void leaf_pass(const SelArgs& f, const SelCfg& c, int t, int d
   const int cur = d & 1;
   const int MW = w.max_wave, MD = w.max_depth_buf;
   int32_t* N = f.N;
-  uint32_t kp[kLeafPer], ksl[kLeafPer];
-  bool keep[kLeafPer];
-#pragma unroll
-  for (int e = 0; e < kLeafPer; ++e) {
-    const int x = tid + e * kSelThreads;
-    keep[e] = false;
-    kp[e] = 0;
-    ksl[e] = 0;
-    bool leaf = false;
-    int p = 0, seg = 0, s = 0, Np0 = 0;
-    if (x < ns) {
-      const int gi = W - 1 - x;
-      const uint32_t sl = gsl[cur * W + gi];
-      p = (int)gnode[cur * W + gi];
-      seg = (int)(sl & 0xFFFFu);
-      s = buf[cur * W + seg];
-      Np0 = N[tb + p];
-      const int k = f.nchild[tb + p];
-      const int first = f.first[tb + p];
-      leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
-      if (!leaf && k > RMAX * kWave) {
-        atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
-        leaf = true;
-      }
-      keep[e] = !leaf;
-      kp[e] = (uint32_t)p;
-      ksl[e] = sl;
+  bool keep = false, leaf = false;
+  uint32_t sl = 0;
+  int p = 0, seg = 0, s = 0, Np0 = 0;
+  if (tid < ns) {
+    const int gi = W - 1 - tid;
+    sl = gsl[cur * W + gi];
+    p = (int)gnode[cur * W + gi];
+    seg = (int)(sl & 0xFFFFu);
+    s = buf[cur * W + seg];
+    Np0 = N[tb + p];
+    const int k = f.nchild[tb + p];
+    const int first = f.first[tb + p];
+    leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
+    if (!leaf && k > RMAX * kWave) {
+      atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
+      leaf = true;
     }
-    // the leaves: group log, path entry, the arrival's virtual loss, end of the path
-    const uint64_t lm = __ballot(leaf);
-    if (lm == 0) continue;
+    keep = !leaf;
+  }
+  // the leaves: group log, path entry, the arrival's virtual loss, end of the path
+  const uint64_t lm = __ballot(leaf);
+  if (lm != 0) {
     const int nl = __popcll(lm);
     int gbase = 0;
     if (lane == 0) {
@@ -909,18 +899,16 @@ __device__ inline void leaf_pass(const SelArgs& f, const SelCfg& c, int t, int d
     }
   }
   __syncthreads();
-#pragma unroll
-  for (int e = 0; e < kLeafPer; ++e) {
-    const uint64_t km = __ballot(keep[e]);
-    if (km == 0) continue;
+  const uint64_t km = __ballot(keep);
+  if (km != 0) {
     int gbase = 0;
     if (lane == 0) gbase = atomicAdd(s_nbig, __popcll(km));
     gbase = readlane_i(gbase, 0);
-    if (keep[e]) {
+    if (keep) {
       const int g = gbase + (int)__builtin_amdgcn_mbcnt_hi(
                                 (uint32_t)(km >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)km, 0u));
-      gnode[cur * W + g] = kp[e];
-      gsl[cur * W + g] = ksl[e];
+      gnode[cur * W + g] = (uint32_t)p;
+      gsl[cur * W + g] = sl;
     }
   }
 }
@@ -930,10 +918,11 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   // small groups one per lane; kept out of the widest kernels, whose chains need every
   // register
   constexpr bool kLanePass = RMAX <= 3;
-  // single-member groups through the leaf pass: the kernel of 4 slots per lane (the wider
-  // kernels keep every group a chain: the pass's registers would add spills to their chains)
-  constexpr bool kLeafPass = RMAX == 4;
-  constexpr bool kSingles = kLanePass || kLeafPass;  // single-member groups kept apart
+  // single-member groups through the leaf pass in the kernels of 4 and 6 slots per lane, for
+  // waves of at most kSelThreads simulations (the 8-slot kernel keeps every group a chain: the
+  // pass's registers would add spills to its chains)
+  constexpr bool kLeafPass = RMAX == 4 || RMAX == 6;
+  const bool singles = kLanePass || (kLeafPass && c.W <= kSelThreads);  // kept apart
   SelArgs& w = f;
   extern __shared__ __align__(16) unsigned char smem[];
   const int W = c.W;
@@ -973,7 +962,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   if (tid < OMQ_NSTATS) s_st[tid] = 0;
   if (tid == 0) {
     // the root group is a chain unless the lane pass takes it
-    const bool root_big = !kSingles || W > kSmallGroup;
+    const bool root_big = !singles || W > kSmallGroup;
     const int g0 = root_big ? 0 : W - 1;
     gnode[g0] = 0;
     gsl[g0] = 0u | ((uint32_t)W << 16);
@@ -993,7 +982,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
     if (ng == 0) break;
     if (kLeafPass) {
       // single-member groups: leaves finished by all threads at once, the rest become chains
-      if (s_nsmall[cur] > 0) {
+      if (singles && s_nsmall[cur] > 0) {
         leaf_pass<RMAX>(f, c, t, d, W, tb, gmax, gnode, gsl, buf, lfs, lflag, &s_glog, s_st,
                         &s_nbig[cur], s_nsmall[cur]);
         __syncthreads();
@@ -1080,7 +1069,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         sum += v;
-        const bool big = !kSingles || v > kSmallGroup;
+        const bool big = !singles || v > kSmallGroup;
         nbg += v > 0 && big;
         nsm += v > 0 && !big;
       }
@@ -1096,7 +1085,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         if (v > 0) {
-          const bool big = !kSingles || v > kSmallGroup;
+          const bool big = !singles || v > kSmallGroup;
           const int g = big ? bbase + pbg++ : W - 1 - (sbase + psm++);
           gnode[nxt * W + g] = (uint32_t)(first + 1 + i);
           gsl[nxt * W + g] = (uint32_t)(seg + run) | ((uint32_t)v << 16);
