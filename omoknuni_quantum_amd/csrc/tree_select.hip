@@ -716,16 +716,21 @@ template <int RMAX>
 __device__ inline void small_groups(
     const SelArgs& f, const SelCfg& c, int t, int d, int ng, int W, int64_t tb, int64_t gmax,
     uint32_t* gnode, uint32_t* gsl, uint16_t* buf, uint16_t* lfs, int32_t* lflag,
-    int* s_glog, unsigned long long* s_st, int* s_nbig, int* s_nsmall) {
+    int* s_glog, unsigned long long* s_st, int* s_nbig, int* s_nsmall, int* s_snext) {
   const SelArgs& w = f;
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
   const int cur = d & 1, nxt = cur ^ 1;
   const int MW = w.max_wave, MD = w.max_depth_buf;
   int32_t* N = f.N;
-  // the small groups of the level sit at the top of the group arrays: [W - ns, W)
+  // the small groups of the level sit at the top of the group arrays: [W - ns, W); chunks of 64
+  // are dealt from an LDS counter, so that waves done with their chains take them first.  Every
+  // fetch advances the counter, so the loop ends after at most ns/64 + 1 fetches.
   const int ns = s_nsmall[cur];
-  for (int g0 = wave * kWave; g0 < ns; g0 += kSelThreads) {
+  for (int it = 0; it <= ns / kWave; ++it) {
+    int g0 = 0;
+    if (lane == 0) g0 = atomicAdd(s_snext, kWave);
+    g0 = readlane_i(g0, 0);
+    if (g0 >= ns) break;
     const int gi = W - 1 - (g0 + lane);
     const uint32_t sl = g0 + lane < ns ? gsl[cur * W + gi] : 0u;
     const int m = (int)(sl >> 16);
@@ -913,6 +918,44 @@ __device__ inline void leaf_pass(const SelArgs& f, const SelCfg& c, int t, int d
   }
 }
 
+// Size class of a chain group of m members: 0 for the largest (m >= 2^15), 15 for m = 1.
+__device__ inline int size_class(int m) { return 15 - min(15, 31 - __clz(m)); }
+
+// Chain groups [0, nb) of a level reordered by size class, largest first, so that the dynamic
+// deal hands out the longest chains first and a level does not end on a long chain taken late.
+// The order within a class is arbitrary (groups of one level are independent).  tn/ts is
+// scratch of nb entries (the group arrays of the next level, empty at this point).  Called by
+// every thread of the workgroup.  Kept out of line: inlined, it changes the register
+// allocation of the 6-slot kernel's chains (16 spilled registers become 53).
+__device__ __noinline__ void order_groups(uint32_t* gn, uint32_t* gs, uint32_t* tn, uint32_t* ts,
+                                    int nb, int* s_hist) {
+  const int tid = threadIdx.x;
+  if (tid < 16) s_hist[tid] = 0;
+  __syncthreads();
+  for (int i = tid; i < nb; i += kSelThreads)
+    atomicAdd(&s_hist[size_class((int)(gs[i] >> 16))], 1);
+  __syncthreads();
+  if (tid < kWave) {  // class counts -> class cursors (exclusive scan)
+    const int v = tid < 16 ? s_hist[tid] : 0;
+    int tot;
+    const int ex = wave_excl_scan(v, &tot);
+    if (tid < 16) s_hist[tid] = ex;
+  }
+  __syncthreads();
+  for (int i = tid; i < nb; i += kSelThreads) {
+    const uint32_t sl = gs[i];
+    const int pos = atomicAdd(&s_hist[size_class((int)(sl >> 16))], 1);
+    tn[pos] = gn[i];
+    ts[pos] = sl;
+  }
+  __syncthreads();
+  for (int i = tid; i < nb; i += kSelThreads) {
+    gn[i] = tn[i];
+    gs[i] = ts[i];
+  }
+  __syncthreads();
+}
+
 template <int RMAX>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c) {
   // small groups one per lane; kept out of the widest kernels, whose chains need every
@@ -940,6 +983,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   __shared__ int s_nbig[2];
   __shared__ int s_nsmall[2];
   __shared__ int s_next[2];  // next chain group to take at the level (dynamic deal)
+  __shared__ int s_snext;    // next chunk of the lane pass's groups
+  __shared__ int s_hist[16];
   __shared__ int s_glog;
   __shared__ int s_wtot[kSelWaves];
   __shared__ unsigned long long s_st[OMQ_NSTATS];
@@ -972,6 +1017,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
     s_nsmall[1] = 0;
     s_next[0] = 0;
     s_next[1] = 0;
+    s_snext = 0;
     s_glog = 0;
   }
   __syncthreads();
@@ -989,6 +1035,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       }
     }
     const int nb = s_nbig[cur];
+    // more chain groups than waves: the longest first
+    if (nb > kSelWaves)
+      order_groups(gnode + cur * W, gsl + cur * W, gnode + nxt * W, gsl + nxt * W, nb, s_hist);
     // The chain groups are dealt dynamically: each wave takes the next index from an LDS
     // counter, so a wave that finishes a short chain takes the next group at once.  The next
     // index is requested when a group starts, so that the answer is back by its end.  Every
@@ -1119,12 +1168,13 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
     }
     if (kLanePass)
       small_groups<RMAX>(f, c, t, d, ng, W, tb, gmax, gnode, gsl, buf, lfs, lflag, &s_glog, s_st,
-                         s_nbig, s_nsmall);
+                         s_nbig, s_nsmall, &s_snext);
     __syncthreads();
     if (tid == 0) {
       s_nbig[cur] = 0;
       s_nsmall[cur] = 0;
       s_next[cur] = 0;
+      s_snext = 0;
     }
     __syncthreads();
   }
