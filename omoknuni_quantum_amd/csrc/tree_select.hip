@@ -450,17 +450,40 @@ __device__ inline int wide_step(WideRow<R>& x, float s, float fvl, float vlf, fl
 // Wave max of a float as order-preserving keys (made uniform).
 __device__ inline float wave_max_key(float x) { return funkey(wave_max_u32(fkey(x))); }
 
-// Smallest key threshold t with at most 64 of the row's keys >= t (bisection on the keys).
+// A key threshold t with at most 64 of the row's k keys >= t, and at least kTopMin of them
+// where the search meets such a t: bisection on the keys between the row's smallest and
+// largest key, stopped at the first threshold whose count lies in [kTopMin, 64].  Any
+// threshold with at most 64 keys above it makes a valid contender set; the early stop only
+// trades a few contenders for fewer bisection steps.  Needs k > 64.
+constexpr int kTopMin = 56;
+
 template <int R>
-__device__ inline uint32_t top64_threshold(const uint32_t* key) {
-  uint64_t lo = 0, hi = 1ull << 32;  // count(>= lo) > 64 >= count(>= hi)
-  for (int it = 0; it < 32; ++it) {
+__device__ inline uint32_t top64_threshold(const uint32_t* key, int k) {
+  const int lane = lane_id();
+  uint32_t kmax = 0u, kmin = 0xFFFFFFFFu;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    if (j * kWave + lane < k) {
+      kmax = max(kmax, key[j]);
+      kmin = min(kmin, key[j]);
+    }
+  }
+  kmax = wave_max_u32(kmax);
+  kmin = ~wave_max_u32(~kmin);
+  // count(>= lo) = k > 64 >= count(>= hi) = 0
+  uint64_t lo = kmin, hi = (uint64_t)kmax + 1;
+  while (hi - lo > 1) {
     const uint64_t mid = (lo + hi) >> 1;
     const uint32_t mt = (uint32_t)mid;
     int cnt = 0;
 #pragma unroll
-    for (int j = 0; j < R; ++j) cnt += __popcll(__ballot(key[j] >= mt));
-    if (cnt <= kWave) hi = mid; else lo = mid;
+    for (int j = 0; j < R; ++j) cnt += __popcll(__ballot(j * kWave + lane < k && key[j] >= mt));
+    if (cnt <= kWave) {
+      hi = mid;
+      if (cnt >= kTopMin) break;
+    } else {
+      lo = mid;
+    }
   }
   return (uint32_t)hi;
 }
@@ -562,7 +585,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
           uint32_t key[R];
 #pragma unroll
           for (int j = 0; j < R; ++j) key[j] = fkey(__builtin_fmaf(s0, x.ar[j], x.q[j]));
-          const uint32_t tau = top64_threshold<R>(key);
+          const uint32_t tau = top64_threshold<R>(key, k);
           uint64_t cmask[R];
           int base = 0;
           float ub = -__builtin_inff();
