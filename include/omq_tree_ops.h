@@ -154,6 +154,8 @@ typedef struct omq_wave {
 /* device status bits */
 #define OMQ_STATUS_NOCHILD 1    /* best-child returned -1 at an expanded node */
 #define OMQ_STATUS_ROWLIMIT 2   /* a row longer than OMQ_MAX_ROW was met or refused */
+#define OMQ_STATUS_STALL 4      /* a bounded wait inside omq_select ran out (internal error: the
+                                   wave's selection is incomplete) */
 
 /* ---- library ---------------------------------------------------------------------- */
 int omq_abi_version(void);

@@ -27,7 +27,7 @@ STAT_NAMES = [
     "internal", "rowsum", "pathnodes", "pathentries", "uleaves", "expanded", "newchild",
     "sims", "steps", "capfail",
 ]
-OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT = 1, 2
+OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT, OMQ_STATUS_STALL = 1, 2, 4
 OMQ_RULE_FREESTYLE, OMQ_RULE_RENJU = 0, 1
 OMQ_TERM_NONE, OMQ_TERM_WIN1, OMQ_TERM_WIN2, OMQ_TERM_DRAW = 0, 1, 2, 3
 OMQ_SHIFT_WORKSPACE_PER_NODE = 8

@@ -342,6 +342,8 @@ class WaveEngine:
     # ---- results ----------------------------------------------------------------------
     def check_status(self) -> None:
         st = int(self.status[0].item())
+        if st & _lib.OMQ_STATUS_STALL:
+            raise _lib.OmqError("omq_select: a bounded wait ran out; the selection is incomplete")
         if st & _lib.OMQ_STATUS_ROWLIMIT:
             raise _lib.OmqError(f"a node has more than {_lib.OMQ_MAX_ROW} legal actions; "
                                 "its expansion was refused by the library")

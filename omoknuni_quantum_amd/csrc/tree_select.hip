@@ -488,9 +488,12 @@ __device__ inline uint32_t top64_threshold(const uint32_t* key, int k) {
   return (uint32_t)hi;
 }
 
+// With `progress` set, the chain publishes its progress after every block of 64 ranks: the
+// block's picks are in ch first (workgroup-scope release), then *progress = ranks done.
 template <int R>
 __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
-                         const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr) {
+                         const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
+                         int* progress) {
   const int lane = lane_id();
   const float vlf = c.vlf;
   const float fvl = (float)c.vli;
@@ -673,6 +676,11 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
       }
     }
     if (lane < rend) ch[r0 + lane] = rec != kNoChild ? ((rec << 16) | rnk) : kNoChild;
+    if (progress != nullptr) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0)
+        __hip_atomic_store(progress, r0 + rend, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
   }
   // the chain's pick counts per child (R == 1 keeps them in the lanes until here)
   if (R == 1 && lane < k) cnt_s[lane] = (uint16_t)y.cn[0];
@@ -686,15 +694,21 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
 template <int RMAX>
 __device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0,
                                      int m, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s,
-                                     float4* cscr) {
+                                     float4* cscr, int* progress) {
   const int r = (k + kWave - 1) / kWave;  // 1 <= r <= RMAX (checked by the caller)
-  if (RMAX <= 1 || r <= 1) return run_chain<1>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
-  if (RMAX >= 2 && r == 2) return run_chain<(RMAX >= 2 ? 2 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
-  if (RMAX >= 3 && r == 3) return run_chain<(RMAX >= 3 ? 3 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
-  if (RMAX >= 4 && r == 4) return run_chain<(RMAX >= 4 ? 4 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
-  if (RMAX >= 5 && r == 5) return run_chain<(RMAX >= 5 ? 5 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
-  if (RMAX >= 6 && r == 6) return run_chain<(RMAX >= 6 ? 6 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
-  return run_chain<(RMAX >= 8 ? 8 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
+  if (RMAX <= 1 || r <= 1)
+    return run_chain<1>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+  if (RMAX >= 2 && r == 2)
+    return run_chain<(RMAX >= 2 ? 2 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+  if (RMAX >= 3 && r == 3)
+    return run_chain<(RMAX >= 3 ? 3 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+  if (RMAX >= 4 && r == 4)
+    return run_chain<(RMAX >= 4 ? 4 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+  if (RMAX >= 5 && r == 5)
+    return run_chain<(RMAX >= 5 ? 5 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+  if (RMAX >= 6 && r == 6)
+    return run_chain<(RMAX >= 6 ? 6 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+  return run_chain<(RMAX >= 8 ? 8 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
 }
 
 // Block-wide exclusive scan of a[0..n) in place (n <= 4 * kSelThreads); returns the total.
@@ -739,7 +753,8 @@ template <int RMAX>
 __device__ inline void small_groups(
     const SelArgs& f, const SelCfg& c, int t, int d, int ng, int W, int64_t tb, int64_t gmax,
     uint32_t* gnode, uint32_t* gsl, uint16_t* buf, uint16_t* lfs, int32_t* lflag,
-    int* s_glog, unsigned long long* s_st, int* s_nbig, int* s_nsmall, int* s_snext) {
+    int* s_glog, unsigned long long* s_st, int* s_nbig, int* s_nsmall, int* s_snext,
+    bool vl_done) {
   const SelArgs& w = f;
   const int lane = lane_id();
   const int cur = d & 1, nxt = cur ^ 1;
@@ -772,10 +787,12 @@ __device__ inline void small_groups(
         w.gmembers[((int64_t)t * MD + d) * MW + seg + r] = (uint16_t)mem[r];
       }
     }
-    const int Np0 = N[tb + p];
+    int Np0 = N[tb + p];
     const int k = f.nchild[tb + p];
     const int first = f.first[tb + p];
-    if (c.vl_atomic)
+    if (vl_done)
+      Np0 -= c.vli * m;  // the members' virtual loss is in N already
+    else if (c.vl_atomic)
       atomicAdd(&N[tb + p], c.vli * m);
     else
       N[tb + p] = Np0 + c.vli * m;
@@ -873,7 +890,7 @@ template <int RMAX>
 __device__ inline void leaf_pass(const SelArgs& f, const SelCfg& c, int t, int d, int W,
                                  int64_t tb, int64_t gmax, uint32_t* gnode, uint32_t* gsl,
                                  const uint16_t* buf, uint16_t* lfs, int32_t* lflag, int* s_glog,
-                                 unsigned long long* s_st, int* s_nbig, int ns) {
+                                 unsigned long long* s_st, int* s_nbig, int ns, bool vl_done) {
   const SelArgs& w = f;
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -916,10 +933,13 @@ __device__ inline void leaf_pass(const SelArgs& f, const SelCfg& c, int t, int d
       *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, 1);
       w.paths[((int64_t)t * MW + s) * MD + d] = p;
       w.gmembers[((int64_t)t * MD + d) * MW + seg] = (uint16_t)s;
-      if (c.vl_atomic)
+      if (vl_done) {
+        // the arrival's virtual loss is in N already
+      } else if (c.vl_atomic) {
         atomicAdd(&N[tb + p], c.vli);
-      else
+      } else {
         N[tb + p] = Np0 + c.vli;
+      }
       w.path_len[(int64_t)t * MW + s] = d + 1;
       w.leaves[(int64_t)t * MW + s] = p;
       lfs[s] = (uint16_t)s;
@@ -979,6 +999,132 @@ __device__ __noinline__ void order_groups(uint32_t* gn, uint32_t* gs, uint32_t* 
   __syncthreads();
 }
 
+// ---- Level overlap -------------------------------------------------------------------
+// The root chain is one step per simulation, and during it the workgroup's other waves have
+// nothing to do in the level-by-level schedule.  With the overlap, wave 0 runs the root chain
+// and publishes every block of 64 picks; the other waves (followers) run the level-1 chains of
+// each published block: the block's members of a root child c, in simulation order, continue
+// c's chain where the previous blocks left it.  That is the same chain: the chain of c reads
+// only N of c and of c's children, and the followers keep both current in memory (N[c] grows by
+// VL per member of the block, and each picked child by VL per pick), so the block's r-th member
+// of c sees N[c] + VL*r with every earlier member's virtual loss already counted.  One follower
+// owns c (c mod the number of followers), so c's blocks run in order on one wave, and no two
+// waves touch the same node.  A follower waits only for the root chain, which waits for no one.
+// After the level, the level-1 groups are formed from the whole root chain as usual; their
+// chains are not run again: each member's pick is replayed from the followers' record (pick2),
+// and the virtual loss of levels 1 and 2 is not applied again.
+constexpr int kPipeMaxW = 2048;              // waves with LDS for the overlap buffers
+constexpr int kFollowers = kSelWaves - 1;
+constexpr int kSpinLimit = 1 << 22;          // bound of a follower's wait for a root block
+constexpr uint16_t kPickNone = 0xFFFFu;
+
+__host__ __device__ inline size_t select_base_bytes(int W) {
+  return (size_t)kSelWaves * kWave * 16 + (size_t)W * (4 + 4 + 8 + 8) + (size_t)W * (4 + 2) +
+         (size_t)kSelWaves * OMQ_MAX_ROW * 2;
+}
+__host__ __device__ inline size_t pipe_offset(int W) { return (select_base_bytes(W) + 15) & ~(size_t)15; }
+
+// Waits until the root chain has published `need` ranks (bounded: false when the bound runs
+// out, which the caller reports as OMQ_STATUS_STALL).
+__device__ inline bool wait_progress(const int* prog, int need) {
+  for (int it = 0; it < kSpinLimit; ++it) {
+    const int v = __hip_atomic_load(prog, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (readlane_i(v, 0) >= need) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      return true;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return false;
+}
+
+// Level-1 chains of the followers (wave index fw among them), block by block as the root chain
+// publishes its picks in root_ch.  Records each member's pick in pick2 (child index, or
+// kPickNone when its node has no child to give).
+template <int RMAX>
+__device__ inline void level1_followers(const SelArgs& f, const SelCfg& c, int64_t tb, int W,
+                                        int root_first, const uint32_t* root_ch, uint16_t* pick2,
+                                        uint32_t* chs, uint16_t* cnt_s, float4* cscr,
+                                        const int* progress, int fw) {
+  const int lane = lane_id();
+  int32_t* N = f.N;
+  for (int b0 = 0; b0 < W; b0 += kWave) {
+    if (!wait_progress(progress, min(W, b0 + kWave))) {
+      if (lane == 0) atomicOr(&f.status[0], OMQ_STATUS_STALL);
+      return;
+    }
+    const int s = b0 + lane;
+    const uint32_t cv = s < W ? root_ch[s] : kNoChild;
+    const int key = cv == kNoChild ? -1 : (int)(cv >> 16);
+    const bool mine = key >= 0 && key % kFollowers == fw;
+    uint64_t rest = __ballot(mine);
+    // one root child per iteration; each takes at least one lane out of rest
+    for (int it = 0; it < kWave && rest != 0; ++it) {
+      const int ck = readlane_i(key, lowest_lane(rest));
+      const uint64_t mm = __ballot(mine && key == ck);
+      rest &= ~mm;
+      const int m = __popcll(mm);
+      const int p = root_first + 1 + ck;
+      const int Np0 = N[tb + p];
+      const int k = f.nchild[tb + p];
+      const int first = f.first[tb + p];
+      if (lane == 0) N[tb + p] = Np0 + c.vli * m;
+      const bool leaf = (k <= 0) || (first < 0) || (c.max_depth <= 2) || (k > RMAX * kWave);
+      if (!leaf) {
+        dispatch_chain<RMAX>(f, tb, first, k, Np0, m, c, chs, cnt_s, cscr, nullptr);
+        if ((mm >> lane) & 1ull) {
+          const int r = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
+          const uint32_t v = chs[r];
+          pick2[s] = v == kNoChild ? kPickNone : (uint16_t)(v >> 16);
+        }
+        for (int i = lane; i < k; i += kWave) {
+          const int cn = cnt_s[i];
+          if (cn > 0) N[tb + first + 1 + i] += c.vli * cn;
+        }
+      }
+      // the next chain of this wave reads the counts written here
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    }
+  }
+}
+
+// Replays the picks of a level-1 group's members (simulation order) from pick2 into ch, as
+// the chain would write them: (child << 16) | rank among the members that picked the same
+// child, kNoChild for none.  Leaves the child counts in cnt_s[0..k); returns the first member
+// without a child, or -1.
+__device__ inline int replay_picks(const uint16_t* mem, int m, int k, const uint16_t* pick2,
+                                   uint32_t* ch, uint16_t* cnt_s) {
+  const int lane = lane_id();
+  for (int i = lane; i < k; i += kWave) cnt_s[i] = 0;
+  wave_sync();
+  int fe = -1;
+  for (int r0 = 0; r0 < m; r0 += kWave) {
+    const int r = r0 + lane;
+    const bool v = r < m;
+    const int key = v ? (int)pick2[mem[r]] : (int)kPickNone;
+    const bool has = v && key != (int)kPickNone;
+    const uint64_t none = __ballot(v && !has);
+    if (fe < 0 && none != 0) fe = r0 + lowest_lane(none);
+    const int base = has ? (int)cnt_s[key] : 0;
+    int rk = 0;
+    uint64_t rest = __ballot(has);
+    for (int it = 0; it < kWave && rest != 0; ++it) {
+      const int leader = lowest_lane(rest);
+      const int kk = readlane_i(key, leader);
+      const uint64_t mm = __ballot(has && key == kk);
+      rest &= ~mm;
+      if (has && key == kk)
+        rk = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
+      if (lane == leader) cnt_s[kk] = (uint16_t)(base + __popcll(mm));
+    }
+    if (v) ch[r] = has ? (((uint32_t)key << 16) | (uint32_t)rk) : kNoChild;
+    wave_sync();
+  }
+  return fe;
+}
+
 template <int RMAX>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c) {
   // small groups one per lane; kept out of the widest kernels, whose chains need every
@@ -988,6 +1134,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   // waves of at most kSelThreads simulations (the 8-slot kernel keeps every group a chain: the
   // pass's registers would add spills to its chains)
   constexpr bool kLeafPass = RMAX == 4 || RMAX == 6;
+  // the level overlap in the kernels whose chains keep their registers with a second copy of
+  // the chain code (the followers')
+  constexpr bool kPipe = RMAX <= 3;
   const bool singles = kLanePass || (kLeafPass && c.W <= kSelThreads);  // kept apart
   SelArgs& w = f;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -1000,6 +1149,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   uint16_t* buf = reinterpret_cast<uint16_t*>(gsl + 2 * W);   // [2W] members by position
   uint16_t* lfs = buf + 2 * W;                                // [W] first sim of own leaf group
   uint16_t* cnt_all = lfs + W;                                // [kSelWaves * OMQ_MAX_ROW]
+  // level-overlap buffers (waves of at most kPipeMaxW simulations)
+  uint32_t* pipe_ch = reinterpret_cast<uint32_t*>(smem + pipe_offset(W));  // [kSelWaves * 64]
+  uint16_t* pick2 = reinterpret_cast<uint16_t*>(pipe_ch + kSelWaves * kWave);  // [W]
 
   // Groups of a level: those a wave runs as a chain at [0, nbig), those the lane pass takes
   // (kernels with a lane pass) at [W - nsmall, W) of the level's group arrays.
@@ -1011,6 +1163,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   __shared__ int s_glog;
   __shared__ int s_wtot[kSelWaves];
   __shared__ unsigned long long s_st[OMQ_NSTATS];
+  __shared__ int s_progress;  // ranks of the root chain published to the followers
 
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
@@ -1022,6 +1175,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   int32_t* N = f.N;
   uint16_t* cnt_s = cnt_all + wave * OMQ_MAX_ROW;
   float4* cscr = cscr_all + wave * kWave;  // contender window scratch of this wave
+  // the level overlap needs an internal root, an integer virtual loss and the ordered mode
+  const int root_k = f.nchild[tb], root_first = f.first[tb];
+  const bool pipe = kPipe && W > kWave && W <= kPipeMaxW && !c.vl_atomic && c.vli > 0 &&
+                    c.max_depth >= 2 && root_k > 0 && root_first >= 0 && root_k <= RMAX * kWave;
 
   for (int s = tid; s < W; s += kSelThreads) {
     buf[s] = (uint16_t)s;
@@ -1042,6 +1199,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
     s_next[1] = 0;
     s_snext = 0;
     s_glog = 0;
+    s_progress = 0;
   }
   __syncthreads();
 
@@ -1049,11 +1207,14 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
     const int cur = d & 1, nxt = cur ^ 1;
     const int ng = s_nbig[cur] + s_nsmall[cur];
     if (ng == 0) break;
+    const bool replay = pipe && d == 1;   // level-1 picks recorded by the followers
+    const bool vl_done = pipe && d <= 2;  // virtual loss of levels 1, 2 applied by the overlap
+    const bool sg = singles && !(pipe && d == 0);  // level-1 groups of the overlap stay chains
     if (kLeafPass) {
       // single-member groups: leaves finished by all threads at once, the rest become chains
       if (singles && s_nsmall[cur] > 0) {
         leaf_pass<RMAX>(f, c, t, d, W, tb, gmax, gnode, gsl, buf, lfs, lflag, &s_glog, s_st,
-                        &s_nbig[cur], s_nsmall[cur]);
+                        &s_nbig[cur], s_nsmall[cur], vl_done && d == 2);
         __syncthreads();
       }
     }
@@ -1067,9 +1228,15 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
     // fetch advances the counter, so a wave sees an index >= nb after at most nb + 1
     // fetches; the loop bound states this (it never ends the loop early).  No barrier is
     // inside the loop.
+    if (pipe && d == 0 && wave != 0) {
+      level1_followers<RMAX>(f, c, tb, W, root_first, choice, pick2, pipe_ch + wave * kWave,
+                             cnt_s, cscr, &s_progress, wave - 1);
+    }
+    // (at level 0 of the overlap only wave 0 takes the root)
+    const bool deal = !(pipe && d == 0 && wave != 0);
     int gnext = 0;
-    if (lane == 0) gnext = atomicAdd(&s_next[cur], 1);
-    for (int it = 0; it <= nb; ++it) {
+    if (deal && lane == 0) gnext = atomicAdd(&s_next[cur], 1);
+    for (int it = 0; it <= nb && deal; ++it) {
       const int gi = readlane_i(gnext, 0);
       if (gi >= nb) break;
       if (lane == 0) gnext = atomicAdd(&s_next[cur], 1);
@@ -1093,10 +1260,12 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
         w.gmembers[((int64_t)t * MD + d) * MW + seg + r] = (uint16_t)s;
       }
 
-      const int Np0 = N[tb + p];
+      int Np0 = N[tb + p];
       const int k = f.nchild[tb + p];
       const int first = f.first[tb + p];
-      if (c.vl_atomic) {
+      if (vl_done && d > 0) {
+        Np0 -= c.vli * m;  // the members' virtual loss is in N already
+      } else if (c.vl_atomic) {
         for (int r = lane; r < m; r += kWave) atomicAdd(&N[tb + p], c.vli);
       } else if (lane == 0) {
         N[tb + p] = Np0 + c.vli * m;
@@ -1124,7 +1293,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       }
 
       uint32_t* ch = choice + seg;
-      const int fe = dispatch_chain<RMAX>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr);
+      const int fe = replay ? replay_picks(mem, m, k, pick2, ch, cnt_s)
+                            : dispatch_chain<RMAX>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr,
+                                                   pipe && d == 0 ? &s_progress : nullptr);
       if (lane == 0) {
         atomicAdd(&s_st[OMQ_ST_INTERNAL], 1ull);
         atomicAdd(&s_st[OMQ_ST_ROWSUM], (unsigned long long)k);
@@ -1141,7 +1312,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         sum += v;
-        const bool big = !singles || v > kSmallGroup;
+        const bool big = !sg || v > kSmallGroup;
         nbg += v > 0 && big;
         nsm += v > 0 && !big;
       }
@@ -1157,7 +1328,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         if (v > 0) {
-          const bool big = !singles || v > kSmallGroup;
+          const bool big = !sg || v > kSmallGroup;
           const int g = big ? bbase + pbg++ : W - 1 - (sbase + psm++);
           gnode[nxt * W + g] = (uint32_t)(first + 1 + i);
           gsl[nxt * W + g] = (uint32_t)(seg + run) | ((uint32_t)v << 16);
@@ -1191,7 +1362,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
     }
     if (kLanePass)
       small_groups<RMAX>(f, c, t, d, ng, W, tb, gmax, gnode, gsl, buf, lfs, lflag, &s_glog, s_st,
-                         s_nbig, s_nsmall, &s_snext);
+                         s_nbig, s_nsmall, &s_snext, vl_done && d == 2);
     __syncthreads();
     if (tid == 0) {
       s_nbig[cur] = 0;
@@ -1231,8 +1402,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
 namespace omq {
 
 size_t select_lds_bytes(int W) {
-  return (size_t)kSelWaves * kWave * 16 + (size_t)W * (4 + 4 + 8 + 8) + (size_t)W * (4 + 2) +
-         (size_t)kSelWaves * OMQ_MAX_ROW * 2;
+  if (W > kPipeMaxW) return select_base_bytes(W);
+  return pipe_offset(W) + (size_t)kSelWaves * kWave * 4 + (size_t)W * 2;
 }
 
 hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_puct,
