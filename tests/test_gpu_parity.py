@@ -2,6 +2,7 @@
 visit counts, CSR rows, priors and ordered-mode W)."""
 import pytest
 
+from omoknuni_quantum_amd.synthetic import games
 from omoknuni_quantum_amd.synthetic.workloads import get
 from oracle.parity import run_parity
 
@@ -18,6 +19,14 @@ CASES = {
                            "capacity": 60_000}),
     "C4-small": ("C4", {"num_trees": 2, "num_simulations": 4096, "wave_size": 2048,
                         "capacity": 200_000}),
+    # the root chain overlapped with the level-1 chains (kernels of rows up to 192 children):
+    # a last block of 8 picks, level-1 leaves forced by the depth limit, and a small board
+    "overlap-ragged": ("C4", {"num_trees": 3, "num_simulations": 600, "wave_size": 200,
+                              "capacity": 100_000}),
+    "overlap-depth2": ("C4", {"num_trees": 2, "num_simulations": 900, "wave_size": 300,
+                              "capacity": 100_000, "max_depth": 2}),
+    "overlap-board7": ("C2", {"model": games.gomoku(7), "max_stones": 10, "num_trees": 3,
+                              "num_simulations": 768, "wave_size": 384, "capacity": 100_000}),
 }
 
 
