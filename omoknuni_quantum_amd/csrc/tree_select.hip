@@ -15,9 +15,11 @@
 // are independent of each other.  A workgroup per tree takes the groups level by level, one
 // wavefront per group; the chain keeps the row's selection state in registers, slot j of lane
 // l holding child j*64 + l.  In the kernels for rows of at most 192 children, groups of one
-// member are taken one per lane instead (small_groups).  The members of a group are kept in
+// member are taken one per lane instead (small_groups); in those for 256 and 384, their leaves
+// are finished by all threads at once (leaf_pass).  The members of a group are kept in
 // simulation order in LDS and partitioned among the chosen children by a counting scatter,
-// which yields the groups of the next level.
+// which yields the groups of the next level.  In the kernels for rows of at most 192 children,
+// the level-1 chains run during the root chain, block by block (the level overlap below).
 //
 // Virtual loss is materialised once per group (N[p] += VL*m, p is owned by one group per
 // wave), or with one atomic per path entry when vl_atomic is set.
