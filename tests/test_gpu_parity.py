@@ -27,6 +27,10 @@ CASES = {
                               "capacity": 100_000, "max_depth": 2}),
     "overlap-board7": ("C2", {"model": games.gomoku(7), "max_stones": 10, "num_trees": 3,
                               "num_simulations": 768, "wave_size": 384, "capacity": 100_000}),
+    "overlap-knobs": ("C4", {"num_trees": 2, "num_simulations": 1536, "wave_size": 512,
+                             "capacity": 100_000, "virtual_loss": 2.5, "c_puct": 0.5,
+                             "expand_policy": "reference_pw", "dirichlet_alpha": 0.3,
+                             "dirichlet_epsilon": 0.25}),
 }
 
 
