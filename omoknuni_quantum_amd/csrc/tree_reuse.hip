@@ -49,7 +49,11 @@ __device__ inline int shift_block_scan(int v, int* s_wtot, int* total) {
 // is -1 for a tree to move and -2 for a tree left unchanged (no shift, or an inconsistent row:
 // a row that leaves [0, num_nodes), or more kept nodes than num_nodes, as from a cycle).
 // A level is taken in chunks of kShiftPer consecutive nodes per thread, so that the row loads
-// of a chunk are in flight together.
+// of a chunk are in flight together.  The chunk's children are written in tiles of 64
+// consecutive new ids, one tile per wave at a time: the chunk's nodes with children are
+// compacted (their first child's offset strictly increasing), the tile's first node is found
+// by a two-level search over that list (64 samples, then 64 entries: two LDS reads per lane),
+// and each lane walks forward from it to the node of its own id.
 constexpr int kShiftPer = 4;
 constexpr int kShiftChunk = kShiftThreads * kShiftPer;
 
@@ -57,10 +61,13 @@ __global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f
                                                                     const int32_t* new_roots,
                                                                     int32_t* ws) {
   __shared__ int s_wtot[kShiftWaves];
-  __shared__ int s_ex[kShiftChunk];
-  __shared__ int s_of[kShiftChunk];
+  __shared__ int s_cex[kShiftChunk];  // compacted nodes with children: first child's offset
+  __shared__ int s_cof[kShiftChunk];  //   their old row offset
+  __shared__ int s_cid[kShiftChunk];  //   their position in the chunk
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
   const int cap = f.capacity;
   const int64_t tb = (int64_t)t * cap;
   int32_t* old_of_new = ws + (int64_t)t * cap * 8;
@@ -83,7 +90,7 @@ __global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f
       const int i0 = c0 + tid * kShiftPer;  // this thread's nodes: i0 .. i0+kShiftPer-1
       int k[kShiftPer], of[kShiftPer];
       bool row_bad = false;
-      int mine = 0;
+      int mine = 0, nzm = 0;
 #pragma unroll
       for (int e = 0; e < kShiftPer; ++e) {
         k[e] = 0;
@@ -98,9 +105,11 @@ __global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f
           }
         }
         mine += k[e];
+        nzm += k[e] > 0 ? 1 : 0;
       }
-      int tot;
+      int tot, nz;
       int ex = shift_block_scan(mine, s_wtot, &tot);
+      int zx = shift_block_scan(nzm, s_wtot, &nz);
       if (__syncthreads_or(row_bad) || next + tot > n_old) {
         bad = true;
         break;
@@ -112,23 +121,32 @@ __global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f
           nnch[i] = k[e];
           nfirst[i] = k[e] > 0 ? next + ex - 1 : -1;
         }
-        // non-decreasing over the chunk; a childless node repeats its successor's offset
-        s_ex[tid * kShiftPer + e] = ex;
-        s_of[tid * kShiftPer + e] = of[e];
+        if (k[e] > 0) {
+          s_cex[zx] = ex;
+          s_cof[zx] = of[e];
+          s_cid[zx] = tid * kShiftPer + e;
+          ++zx;
+        }
         ex += k[e];
       }
       __syncthreads();
-      // the chunk's children, written by all threads: output q belongs to the last node j of
-      // the chunk with s_ex[j] <= q (binary search), as its child q - s_ex[j]
-      for (int q = tid; q < tot; q += kShiftThreads) {
-        int a = 0, b = kShiftChunk - 1;
-        while (a < b) {
-          const int mid = (a + b + 1) >> 1;
-          if (s_ex[mid] <= q) a = mid;
-          else b = mid - 1;
+      // the chunk's children, tile by tile: output q belongs to the last listed node j with
+      // s_cex[j] <= q, as its child q - s_cex[j]
+      for (int q0 = wave * kWave; q0 < tot; q0 += kShiftThreads) {
+        // the tile's first node: a sample every 64 entries, then the entries after the sample
+        const int si = lane * kWave;
+        const uint64_t b1 = __ballot(si < nz && s_cex[si] <= q0);  // lane 0 always qualifies
+        const int L = kWave - 1 - __clzll(b1);
+        const int sj = L * kWave + lane;
+        const uint64_t b2 = __ballot(sj < nz && s_cex[sj] <= q0);
+        int j = L * kWave + (kWave - 1 - __clzll(b2));
+        const int q = q0 + lane;
+        if (q < tot) {
+          // forward to the last node starting at or before q (at most nz - 1 - j steps)
+          while (j + 1 < nz && s_cex[j + 1] <= q) ++j;
+          old_of_new[next + q] = s_cof[j] + 1 + (q - s_cex[j]);  // child of edge of+x is node of+x+1
+          npar[next + q] = c0 + s_cid[j];
         }
-        old_of_new[next + q] = s_of[a] + 1 + (q - s_ex[a]);  // child of edge of+j is node of+j+1
-        npar[next + q] = c0 + a;
       }
       next += tot;
       __syncthreads();

@@ -127,3 +127,24 @@ def test_update_root_falls_back_to_reset(device):
     m.search(board)
     m.update_root(7 * 15 + 7)  # occupied cell: no such child
     assert m.stats["tree_reuse_count"] == 0 and int(m.engine.num_nodes[0].item()) == 1
+
+
+def test_shift_large_subtree_matches_oracle(device):
+    # a kept subtree whose levels span several chunks of 4096 nodes (C3 rows of ~300 children)
+    wl = get("C3").scaled(num_trees=1, num_simulations=4096, wave_size=1024, capacity=1_500_000)
+    eng, orc, ev = make_pair(wl, device=device)
+    eng.reset()
+    orc.reset_tree(0)
+    for w in [1] + [1024] * 4:
+        eng.run_wave(w, ev)
+        orc.wave(0, w)
+    torch.cuda.synchronize()
+    tr = orc.tree(0)
+    f, k = tr["first"][0], tr["nchild"][0]
+    kids = np.arange(f + 1, f + 1 + k)
+    pick = int(kids[np.argmax(tr["N"][kids])])
+    eng.shift_roots([pick])
+    kept = orc.shift_root(0, pick)
+    torch.cuda.synchronize()
+    assert kept > 3 * 4096
+    _assert_trees(eng, orc, "after a large shift")
