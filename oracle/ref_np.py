@@ -354,3 +354,75 @@ def grouped_select(tree: NpTree, W: int, max_depth: int):
         for x in path:
             tree.N[x] += tree.vli
     return paths
+
+
+def overlap_select(tree: NpTree, W: int, max_depth: int, block: int = 64):
+    """The level overlap of the device schedule, restated.  The root's chain runs over all W
+    members without touching the children's N.  Its members are then taken in blocks of
+    `block` simulations: for each block, each root child c continues its chain with the
+    block's members of c, N[c] growing by VL per member and each picked child's N by VL per
+    pick, in place, so that the next block of c sees them.  Deeper levels run as in
+    grouped_select, the level-2 nodes already holding their members' virtual loss.  Returns
+    the paths; must equal W sequential select_paths."""
+    vli = tree.vli
+    if (not tree.expanded[0]) or tree.nchild[0] == 0 or max_depth <= 1:
+        return grouped_select(tree, W, max_depth)
+    paths = [[0] for _ in range(W)]
+
+    def chain(p, np0, m, persist):
+        """picks of p's m members in order; the children's N keep the picks' VL if persist"""
+        f, k = int(tree.first[p]), int(tree.nchild[p])
+        saved = {int(tree.children[f + i]): int(tree.N[int(tree.children[f + i])])
+                 for i in range(k)}
+        extra, picks = {}, []
+        for r in range(1, m + 1):
+            for c, n in saved.items():
+                tree.N[c] = n + vli * extra.get(c, 0)
+            c = tree.best_child(p, np0 + vli * r)
+            picks.append(c)
+            if c >= 0:
+                extra[c] = extra.get(c, 0) + 1
+        for c, n in saved.items():
+            tree.N[c] = n + (vli * extra.get(c, 0) if persist else 0)
+        return picks
+
+    n_root = int(tree.N[0])
+    root_pick = chain(0, n_root, W, persist=False)
+    tree.N[0] = n_root + vli * W
+    pick1 = [-1] * W
+    for b0 in range(0, W, block):
+        members_of = {}
+        for s in range(b0, min(W, b0 + block)):
+            if root_pick[s] >= 0:
+                members_of.setdefault(root_pick[s], []).append(s)
+        for c, mem in members_of.items():
+            np0 = int(tree.N[c])
+            tree.N[c] = np0 + vli * len(mem)
+            if (not tree.expanded[c]) or tree.nchild[c] == 0 or max_depth <= 2:
+                continue
+            for s, x in zip(mem, chain(c, np0, len(mem), persist=True)):
+                pick1[s] = x
+    groups = {}
+    for s in range(W):
+        if root_pick[s] >= 0:
+            paths[s].append(root_pick[s])
+            if pick1[s] >= 0:
+                paths[s].append(pick1[s])
+                groups.setdefault(pick1[s], []).append(s)
+    depth = 2
+    while groups:
+        nxt = {}
+        for p, members in groups.items():
+            if (not tree.expanded[p]) or tree.nchild[p] == 0 or depth == max_depth - 1:
+                continue
+            np0 = int(tree.N[p]) - (vli * len(members) if depth == 2 else 0)
+            for s, c in zip(members, chain(p, np0, len(members), persist=False)):
+                if c >= 0:
+                    paths[s].append(c)
+                    nxt.setdefault(c, []).append(s)
+        groups = nxt
+        depth += 1
+    for path in paths:
+        for x in path[3:]:
+            tree.N[x] += vli
+    return paths

@@ -181,6 +181,35 @@ def test_grouped_selection_equals_sequential(seed):
         ref_np.np_wave(t, w, 100, legal_of, pol, val)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_overlap_selection_equals_sequential(seed):
+    """The level overlap (root chain, then each root child's chain continued block by block
+    with the virtual loss kept in N) reproduces sequential select_path exactly."""
+    import copy
+    rng = np.random.default_rng(300 + seed)
+    bs = 4
+    A = bs * bs
+    root_empty = list(range(A))
+    legal_of = lambda pacts: ref_np.board_legal(root_empty, pacts)
+    vl = [3.0, 1.0, 2.0][seed % 3]
+    t = ref_np.NpTree(4000, 1.4, vl)
+    for it in range(14):
+        w = 1 if it == 0 else int(rng.integers(2, 9))
+        pol = rng.random((w, A)).astype(np.float32)
+        if seed % 2:
+            pol[:] = 1.0  # equal priors: many exact ties
+        val = np.round(rng.random(w) * 4 - 2).astype(np.float32) / 4
+        W = int(rng.integers(2, 14))
+        for block in (1, 2, 3, 5):
+            for max_depth in (100, 2, 3):
+                a, b = copy.deepcopy(t), copy.deepcopy(t)
+                seq = [a.select_path(max_depth) for _ in range(W)]
+                ovl = ref_np.overlap_select(b, W, max_depth, block)
+                assert seq == ovl, (it, block, max_depth)
+                assert np.array_equal(a.N, b.N), (it, block, max_depth)
+        ref_np.np_wave(t, w, 100, legal_of, pol, val)
+
+
 def test_search_invariants_all_workload_models():
     from omoknuni_quantum_amd.synthetic.workloads import get
     for name, kw in [("C1", {"num_simulations": 256}), ("C3", {"num_trees": 1, "num_simulations": 2048}),
