@@ -24,6 +24,8 @@
 // Virtual loss is materialised once per group (N[p] += VL*m, p is owned by one group per
 // wave), or with one atomic per path entry when vl_atomic is set.
 
+#include <atomic>
+
 #include "omq_common.h"
 
 namespace omq {
@@ -1433,12 +1435,18 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
     case 6: kern = (const void*)select_kernel<6>; break;
     default: kern = (const void*)select_kernel<8>; break;
   }
-  static bool attr_set[9] = {};
-  if (!attr_set[rmax]) {
-    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)select_lds_bytes(OMQ_MAX_WAVE));
+  // the LDS limit is raised once per device and kernel width (the attribute is idempotent, so
+  // two threads racing here both set it)
+  constexpr int kMaxDevices = 64;
+  static std::atomic<bool> attr_set[kMaxDevices][9];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices || !attr_set[dev][rmax].load(std::memory_order_acquire)) {
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)select_lds_bytes(OMQ_MAX_WAVE));
     if (e != hipSuccess) return e;
-    attr_set[rmax] = true;
+    if (dev >= 0 && dev < kMaxDevices) attr_set[dev][rmax].store(true, std::memory_order_release);
   }
   SelArgs a;
   a.N = f.visit_counts;
@@ -1462,7 +1470,7 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   a.max_wave = w.max_wave;
   a.max_depth_buf = w.max_depth;
   void* args[] = {&a, &c};
-  hipError_t e = hipLaunchKernel(kern, dim3(f.num_trees), dim3(kSelThreads), args, lds, stream);
+  e = hipLaunchKernel(kern, dim3(f.num_trees), dim3(kSelThreads), args, lds, stream);
   if (e != hipSuccess) return e;
   return hipGetLastError();
 }
