@@ -329,6 +329,22 @@ int omq_paths_backup(const omq_forest* f, const int32_t* paths, const int32_t* p
 int omq_virtual_loss(const omq_forest* f, const int32_t* nodes, const int32_t* tree_of,
                      int32_t count, int32_t delta, void* stream);
 
+/* Reference fused UCB selection over explicit CSR edges.  For b < batch, parent
+ * p = node_indices[b] with row [children_start[p], children_end[p]) of children[] / priors[]:
+ *     ucb_i = (visit_counts[c_i] > 0 ? q_values[c_i] : 0)
+ *             + c_puct * priors_i * sqrtf((float)visit_counts[p]) / (1 + visit_counts[c_i])
+ * in float32 (left to right), and selected[b] = the row position of the first maximum above
+ * -1e10 (strict '>'), or -1 for an empty row.  Unvisited children get q = 0 and no priority
+ * (this is not omq_select's rule).  The index arrays are trusted: every index must lie in its
+ * array (as in the reference).
+ * Replaces mcts::fused_ucb_selection (python/mcts/gpu/torch_custom_ops.py:108-193) and its
+ * kernel fused_ucb_selection_adapter_kernel (python/mcts/gpu/mcts_kernels.cu:1466-1512). */
+int omq_fused_ucb_selection(const int32_t* node_indices, int32_t batch,
+                            const int32_t* children_start, const int32_t* children_end,
+                            const int32_t* children, const float* q_values,
+                            const int32_t* visit_counts, const float* priors, float c_puct,
+                            int32_t* selected, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,8 @@ SIGNATURES = {
     "omq_gomoku_terminal": (ctypes.c_int, [_FP, _WP, _p, _p, _i32, _p, _p]),
     "omq_shift_root": (ctypes.c_int, [_FP, _p, _p, ctypes.c_int64, _p]),
     "omq_leaf_features": (ctypes.c_int, [_FP, _WP, _p, _p, _p, _i32, _i32, _i32, _p, _p]),
+    "omq_fused_ucb_selection": (ctypes.c_int, [_p, _i32, _p, _p, _p, _p, _p, _p, ctypes.c_float,
+                                               _p, _p]),
     "omq_root_policy": (ctypes.c_int, [_FP, _p, _p]),
     "omq_sample_actions": (ctypes.c_int, [_FP, _p, ctypes.c_double, ctypes.c_uint64,
                                           ctypes.c_uint64, _p, _p]),

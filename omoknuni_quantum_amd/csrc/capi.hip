@@ -39,6 +39,10 @@ hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const 
 hipError_t launch_leaf_features(const omq_forest& f, const omq_wave& w, const int8_t* boards,
                                 const int32_t* root_player, const int32_t* root_moves, int bs,
                                 int planes, int dtype, int nhwc, void* out, hipStream_t st);
+hipError_t launch_fused_ucb(const int32_t* node_indices, int batch, const int32_t* starts,
+                            const int32_t* ends, const int32_t* children, const float* q,
+                            const int32_t* visits, const float* priors, float c_puct,
+                            int32_t* selected, hipStream_t st);
 size_t leaf_lds_per_wave_host(const omq_forest& f);
 }  // namespace omq
 
@@ -331,6 +335,22 @@ int omq_virtual_loss(const omq_forest* f, const int32_t* nodes, const int32_t* t
   return hip_status(omq::launch_virtual_loss(*f, nodes, tree_of, count, delta,
                                              (hipStream_t)stream),
                     "omq_virtual_loss");
+}
+
+int omq_fused_ucb_selection(const int32_t* node_indices, int32_t batch,
+                            const int32_t* children_start, const int32_t* children_end,
+                            const int32_t* children, const float* q_values,
+                            const int32_t* visit_counts, const float* priors, float c_puct,
+                            int32_t* selected, void* stream) {
+  if (batch < 0) return fail(OMQ_E_ARG, "batch %d < 0", batch);
+  if (batch == 0) return OMQ_OK;
+  if (!node_indices || !children_start || !children_end || !children || !q_values ||
+      !visit_counts || !priors || !selected)
+    return fail(OMQ_E_ARG, "omq_fused_ucb_selection: a null array");
+  return hip_status(omq::launch_fused_ucb(node_indices, batch, children_start, children_end,
+                                          children, q_values, visit_counts, priors, c_puct,
+                                          selected, (hipStream_t)stream),
+                    "omq_fused_ucb_selection");
 }
 
 }  // extern "C"

@@ -7,14 +7,21 @@ operations are registered here in the ``omq`` namespace, mutating their tensor a
 place on the caller's current HIP stream:
 
     torch.ops.omq.vectorized_backup(paths, path_lengths, values, visit_counts, value_sums)
+    torch.ops.omq.warp_vectorized_backup(paths, path_lengths, values, visit_counts, value_sums)
     torch.ops.omq.batch_apply_virtual_loss(node_indices, virtual_loss_counts)
     torch.ops.omq.batch_remove_virtual_loss(node_indices, virtual_loss_counts)
+    torch.ops.omq.fused_ucb_selection(node_indices, children_start, children_end, children,
+                                      q_values, visit_counts, priors, c_puct) -> int32 [batch]
 
 ``vectorized_backup`` follows the reference kernel (mcts_kernels.cu:121-158): for every path b
 and d < min(path_lengths[b], max_depth), node x = paths[b, d] in [0, num_nodes) gets
 visit_counts[x] += 1 and value_sums[x] += v * (-1)^(path_lengths[b]-1-d) (sign by distance
-from the leaf); other entries are skipped.  The virtual-loss operators add +1 / -1 per listed
-node (duplicates accumulate; indices outside the array are skipped).
+from the leaf); other entries are skipped.  ``warp_vectorized_backup`` is the same operation: the
+reference's warp variant (mcts_kernels.cu:164-230) never leaves out a lane, so it adds the same
+terms.  The virtual-loss operators add +1 / -1 per listed node (duplicates accumulate; indices
+outside the array are skipped).  ``fused_ucb_selection`` follows the reference's operator
+(torch_custom_ops.py:108-193, kernel mcts_kernels.cu:1466-1512): per parent, the row position
+of the first maximum of q + c*P*sqrt(N_parent)/(1+n), with q = 0 for an unvisited child.
 
 There is no CPU implementation: tensors must be on a HIP device, and a missing library raises.
 """
@@ -116,3 +123,46 @@ def batch_remove_virtual_loss(node_indices: torch.Tensor,
 @batch_remove_virtual_loss.register_fake
 def _(node_indices, virtual_loss_counts) -> None:
     return None
+
+
+@torch.library.custom_op("omq::warp_vectorized_backup",
+                         mutates_args=("visit_counts", "value_sums"))
+def warp_vectorized_backup(paths: torch.Tensor, path_lengths: torch.Tensor, values: torch.Tensor,
+                           visit_counts: torch.Tensor, value_sums: torch.Tensor) -> None:
+    vectorized_backup(paths, path_lengths, values, visit_counts, value_sums)
+
+
+@warp_vectorized_backup.register_fake
+def _(paths, path_lengths, values, visit_counts, value_sums) -> None:
+    return None
+
+
+@torch.library.custom_op("omq::fused_ucb_selection", mutates_args=())
+def fused_ucb_selection(node_indices: torch.Tensor, children_start: torch.Tensor,
+                        children_end: torch.Tensor, children: torch.Tensor,
+                        q_values: torch.Tensor, visit_counts: torch.Tensor,
+                        priors: torch.Tensor, c_puct: float) -> torch.Tensor:
+    dev = _check_device("fused_ucb_selection", node_indices, children_start, children_end,
+                        children, q_values, visit_counts, priors)
+    for name, t, dt in (("node_indices", node_indices, torch.int32),
+                        ("children_start", children_start, torch.int32),
+                        ("children_end", children_end, torch.int32),
+                        ("children", children, torch.int32),
+                        ("q_values", q_values, torch.float32),
+                        ("visit_counts", visit_counts, torch.int32),
+                        ("priors", priors, torch.float32)):
+        if t.dtype != dt:
+            raise RuntimeError(f"omq::fused_ucb_selection: {name} must be {dt}, not {t.dtype}")
+    selected = torch.empty(node_indices.numel(), dtype=torch.int32, device=dev)
+    _lib.check(_lib.load().omq_fused_ucb_selection(
+        node_indices.data_ptr(), node_indices.numel(), children_start.data_ptr(),
+        children_end.data_ptr(), children.data_ptr(), q_values.data_ptr(),
+        visit_counts.data_ptr(), priors.data_ptr(), float(c_puct), selected.data_ptr(),
+        _stream(dev)), "omq_fused_ucb_selection")
+    return selected
+
+
+@fused_ucb_selection.register_fake
+def _(node_indices, children_start, children_end, children, q_values, visit_counts, priors,
+      c_puct):
+    return torch.empty_like(node_indices, dtype=torch.int32)

@@ -426,3 +426,29 @@ def overlap_select(tree: NpTree, W: int, max_depth: int, block: int = 64):
         for x in path[3:]:
             tree.N[x] += vli
     return paths
+
+
+def fused_ucb_selection(node_indices, children_start, children_end, children, q_values,
+                        visit_counts, priors, c_puct):
+    """mcts::fused_ucb_selection as its CUDA kernel computes it
+    (python/mcts/gpu/mcts_kernels.cu:1466-1512), in float32: for parent p and row
+    [start, end), ucb_i = (n_i > 0 ? q[c_i] : 0) + ((c * P_i) * sqrtf(N_p)) / (1 + n_i), and the
+    row position of the first ucb above -1e10 (strict '>'), or -1 for an empty row."""
+    F = np.float32
+    c = F(c_puct)
+    out = np.full(len(node_indices), -1, np.int32)
+    for b, p in enumerate(node_indices):
+        start, end = int(children_start[p]), int(children_end[p])
+        if start >= end:
+            continue
+        sp = np.sqrt(F(visit_counts[p]))
+        best, arg = F(-1e10), -1
+        for i in range(start, end):
+            ch = int(children[i])
+            n = int(visit_counts[ch])
+            q = F(q_values[ch]) if n > 0 else F(0.0)
+            ucb = F(q + F(F(F(c * F(priors[i])) * sp) / F(F(1.0) + F(n))))
+            if ucb > best:
+                best, arg = ucb, i - start
+        out[b] = arg
+    return out
