@@ -219,174 +219,153 @@ struct Row {
   int cn[R];            // picks of the child in this chain so far
 };
 
-// Computes the pending next state of the previous pick now (leaves no pick pending).
-template <int R>
-__device__ inline void settle_pending(Row<R>& x, float fvl, float vlf) {
-  float dw = x.den[0], ww = x.wv[0], cw = x.cp[0];
-#pragma unroll
-  for (int j = 1; j < R; ++j) {
-    dw = x.pb[j] ? x.den[j] : dw;
-    ww = x.pb[j] ? x.wv[j] : ww;
-    cw = x.pb[j] ? x.cp[j] : cw;
-  }
-  const float d2 = dw + fvl;
-  const float qx = ww * refined_rcp((d2 - 1.0f) + vlf);
-  const float ax = cw * refined_rcp(d2);
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    x.qn[j] = x.pb[j] ? qx : x.qn[j];
-    x.arn[j] = x.pb[j] ? ax : x.arn[j];
-    x.pb[j] = false;
-  }
+// The lane of y whose next state is pending (pb set), or -1.
+__device__ inline int lane_pending(const Row<1>& y) {
+  const uint64_t m = __ballot(y.pb[0]);
+  return m ? lowest_lane(m) : -1;
 }
 
-// One step over the row held in x.  Returns the pick as j*64 + lane, -1 when no child can be
-// picked, or -2 (window mode only) when the step must be taken over the whole row: the
-// threshold does not exceed `ubnc` or there is no candidate.  Nothing is changed on -2.
-// `idx` is the row index of the child in slot 0 (for the unvisited marker).
-template <int R>
-__device__ inline int select_step(Row<R>& x, float s, float fvl, float vlf, float qbt_eff,
-                                  bool exact_only, int k, int idx0, bool window, float ubnc) {
+// Wave max of a float as order-preserving keys (made uniform).
+__device__ inline float wave_max_key(float x) { return funkey(wave_max_u32(fkey(x))); }
+
+// Steps of a chain whose children are held one per lane (rows of at most 64 children, or a
+// contender window), from rank rr up to rank rend.  A step ranks the lanes by
+// ap = fma(s, a, qa), takes the wave max A and the threshold T, and picks the single candidate
+// (ap >= T) when there is one; otherwise the candidates (all children when there is none, or
+// in exact-only mode) are compared exactly by exact_pick.  A pick advances the picked lane to
+// its next state (a register select); that lane's state after its following pick is computed
+// during the next step's wave max.  The steps with a single candidate run in a loop of their
+// own; a step with several candidates (or none) leaves that loop for the exact comparison and
+// comes back.  Keeping the rare step out
+// of the loop body leaves the common step without the register copies that joining the two
+// paths inside it costs.  Lane r of rec / rnk receives the pick at rank r (the lane, or -1 for
+// none) and its rank among the chain's earlier picks of that child.
+//   WINDOW: contender window.  The steps end before the first rank whose threshold does not
+//           exceed ubnc (the bound of the non-contenders); that rank is returned.  Every step
+//           of a window picks.
+//   else:   every step up to rend is taken; a rank without a child records -1, and the first
+//           such rank goes to first_end (when it is still negative).
+// Returns the first rank not taken.
+template <bool WINDOW>
+__device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float fvl, float vlf,
+                                 float qbt_eff, bool exact_only, int k, float ubnc, int r0,
+                                 int* first_end, uint32_t* rec, uint32_t* rnk) {
   const int lane = lane_id();
-  float ap[R];
-#pragma unroll
-  for (int j = 0; j < R; ++j) ap[j] = __builtin_fmaf(s, x.ar[j], x.q[j]);
-  float lm;
-  if (R == 1) {
-    lm = ap[0];
-  } else {
-    float t[R];
-#pragma unroll
-    for (int j = 0; j < R; ++j) t[j] = ap[j];
-#pragma unroll
-    for (int w = 1; w < R; w <<= 1)
-#pragma unroll
-      for (int j = 0; j + w < R; j += 2 * w) t[j] = fmaxf(t[j], t[j + w]);
-    lm = t[0];
-  }
-  // The wave max of the keys (6 dependent DPP steps) is interleaved with the state after
-  // the next pick of the previous step's child, which is independent of it (each
-  // independent instruction takes the place of a DPP hazard wait).
-  int v = (int)fkey(lm);
-  float dw = x.den[0], ww = x.wv[0], cw = x.cp[0];
-#pragma unroll
-  for (int j = 1; j < R; ++j) {
-    dw = x.pb[j] ? x.den[j] : dw;
-    ww = x.pb[j] ? x.wv[j] : ww;
-    cw = x.pb[j] ? x.cp[j] : cw;
-  }
-  float d2 = dw + fvl;
-  float e2 = (d2 - 1.0f) + vlf;
-  OMQ_PIN(d2);
-  OMQ_PIN(e2);
-  OMQ_SCHED_FENCE();
-  OMQ_DPP_MAX(v, 0x111, 0xF);  // row_shr:1
-  float r1 = __builtin_amdgcn_rcpf(e2);
-  float r2 = __builtin_amdgcn_rcpf(d2);
-  OMQ_PIN(r1);
-  OMQ_PIN(r2);
-  OMQ_SCHED_FENCE();
-  OMQ_DPP_MAX(v, 0x112, 0xF);  // row_shr:2
-  float t1 = __builtin_fmaf(-e2, r1, 1.0f);
-  float t2 = __builtin_fmaf(-d2, r2, 1.0f);
-  OMQ_PIN(t1);
-  OMQ_PIN(t2);
-  OMQ_SCHED_FENCE();
-  OMQ_DPP_MAX(v, 0x114, 0xF);  // row_shr:4
-  r1 = __builtin_fmaf(r1, t1, r1);
-  r2 = __builtin_fmaf(r2, t2, r2);
-  OMQ_PIN(r1);
-  OMQ_PIN(r2);
-  OMQ_SCHED_FENCE();
-  OMQ_DPP_MAX(v, 0x118, 0xF);  // row_shr:8
-  // a picked child is visited afterwards (virtual loss >= 1 here)
-  float qx = ww * r1;
-  float ax = cw * r2;
-  OMQ_PIN(qx);
-  OMQ_PIN(ax);
-  OMQ_SCHED_FENCE();
-  OMQ_DPP_MAX(v, 0x142, 0xA);  // row_bcast:15
-  float qnv[R], arnv[R];
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    qnv[j] = x.pb[j] ? qx : x.qn[j];
-    arnv[j] = x.pb[j] ? ax : x.arn[j];
-    OMQ_PIN(qnv[j]);
-    OMQ_PIN(arnv[j]);
-  }
-  OMQ_SCHED_FENCE();
-  OMQ_DPP_MAX(v, 0x143, 0xC);  // row_bcast:31
-  const uint32_t Ak = (uint32_t)__builtin_amdgcn_readlane(v, 63);
-  const float A = funkey(Ak);
-  // T = A - (|A| + QB) * 2^-19
-  const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt_eff;
-  bool b[R];
-  uint64_t cm = 0;
-  int tot = 0;
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    b[j] = ap[j] >= T;
-    const uint64_t mj = __ballot(b[j]);
-    cm |= mj;
-    tot += __popcll(mj);
-  }
-  if (window && (tot == 0 || !(T > ubnc))) return -2;
-  // the pending state is final now
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    x.qn[j] = qnv[j];
-    x.arn[j] = arnv[j];
-  }
-  // The candidates' next states are taken as if the single candidate were the pick; the
-  // exact comparison below undoes this when there is not exactly one candidate.
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    x.q[j] = b[j] ? x.qn[j] : x.q[j];
-    x.ar[j] = b[j] ? x.arn[j] : x.ar[j];
-    x.den[j] = b[j] ? x.den[j] + fvl : x.den[j];
-    x.cn[j] = b[j] ? x.cn[j] + 1 : x.cn[j];
-    x.pb[j] = b[j];
-  }
-  int win;
-  if (__builtin_expect(tot == 1, 1)) {
-    const int l = lowest_lane(cm);
-    if (R == 1) {
-      win = l;
-    } else {
-      int jv = 0;
-#pragma unroll
-      for (int j = 1; j < R; ++j) jv = b[j] ? j : jv;
-      win = readlane_i(jv, l) * kWave + l;
+  // the lane whose state after its next pick is pending (the previous step's pick), or -1
+  int pl = __builtin_amdgcn_readfirstlane(lane_pending(y));
+  while (rr < rend) {
+    // ---- steps with a single candidate: one exit, at the bottom; a step that is not taken
+    // here changes nothing but the pending state, and nothing of it is kept past the loop.
+    // The flags are scalar (from the ballot), so the loop keeps no lane masks across steps.
+    for (;;) {
+      const float s = readlane_f(svec, rr);
+      const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
+      // The wave max of the keys is interleaved with the pending state after the next pick
+      // of the previous step's child (independent of it).
+      int v = (int)fkey(ap);
+      float d2 = y.den[0] + fvl;
+      float e2 = (d2 - 1.0f) + vlf;
+      OMQ_PIN(d2);
+      OMQ_PIN(e2);
+      OMQ_SCHED_FENCE();
+      OMQ_DPP_MAX(v, 0x111, 0xF);  // row_shr:1
+      float r1 = __builtin_amdgcn_rcpf(e2);
+      float r2 = __builtin_amdgcn_rcpf(d2);
+      OMQ_PIN(r1);
+      OMQ_PIN(r2);
+      OMQ_SCHED_FENCE();
+      OMQ_DPP_MAX(v, 0x112, 0xF);  // row_shr:2
+      float t1 = __builtin_fmaf(-e2, r1, 1.0f);
+      float t2 = __builtin_fmaf(-d2, r2, 1.0f);
+      OMQ_PIN(t1);
+      OMQ_PIN(t2);
+      OMQ_SCHED_FENCE();
+      OMQ_DPP_MAX(v, 0x114, 0xF);  // row_shr:4
+      r1 = __builtin_fmaf(r1, t1, r1);
+      r2 = __builtin_fmaf(r2, t2, r2);
+      OMQ_PIN(r1);
+      OMQ_PIN(r2);
+      OMQ_SCHED_FENCE();
+      OMQ_DPP_MAX(v, 0x118, 0xF);  // row_shr:8
+      // a picked child is visited afterwards (virtual loss >= 1 here)
+      float qx = y.wv[0] * r1;
+      float ax = y.cp[0] * r2;
+      OMQ_PIN(qx);
+      OMQ_PIN(ax);
+      OMQ_SCHED_FENCE();
+      OMQ_DPP_MAX(v, 0x142, 0xA);  // row_bcast:15
+      const bool pb = lane == pl;
+      y.qn[0] = pb ? qx : y.qn[0];
+      y.arn[0] = pb ? ax : y.arn[0];
+      OMQ_PIN(y.qn[0]);
+      OMQ_PIN(y.arn[0]);
+      OMQ_SCHED_FENCE();
+      OMQ_DPP_MAX(v, 0x143, 0xC);  // row_bcast:31
+      const float A = funkey((uint32_t)__builtin_amdgcn_readlane(v, 63));
+      // T = A - (|A| + QB) * 2^-19
+      const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt_eff;
+      // The candidates, none when a window ends here (threshold NaN): a window ends where the
+      // threshold does not exceed the non-contenders' bound.  (A step without a candidate has a NaN threshold:
+      // the lane holding the maximum A has ap = A >= T whenever A is finite, since T <= A;
+      // A = +inf gives T = NaN.  It is not taken here either.)
+      const float Tw = WINDOW ? (T > ubnc ? T : __builtin_nanf("")) : T;
+      const uint64_t cm = __ballot(ap >= Tw);
+      // The step is taken when it has a single candidate l.  (s_ff1 of an empty mask gives -1:
+      // then any lane will do for the writes below, which the step that takes rank rr later
+      // repeats.)  inc = taken ? 1 : 0 and lt = taken ? l : -1 are formed in scalar registers
+      // (as plain C the compiler routes them through vector registers).
+      const int pc = __popcll(cm);
+      int l, inc, lt;
+      asm("s_ff1_i32_b64 %0, %1" : "=s"(l) : "s"(cm));
+      asm("s_cmp_eq_u32 %2, 1\n\ts_cselect_b32 %0, 1, 0\n\ts_cselect_b32 %1, %3, -1"
+          : "=s"(inc), "=s"(lt)
+          : "s"(pc), "s"(l)
+          : "scc");
+      // the step's pick, if taken; the pending state is final now
+      const bool hit = lane == lt;
+      y.q[0] = hit ? y.qn[0] : y.q[0];
+      y.ar[0] = hit ? y.arn[0] : y.ar[0];
+      y.den[0] = hit ? y.den[0] + fvl : y.den[0];
+      y.cn[0] = hit ? y.cn[0] + 1 : y.cn[0];
+      pl = lt;
+      // lane rr := pick / its rank.  The lane select goes through m0, which the "{m0}"
+      // operand hands to the compiler (v_writelane may read only one SGPR besides m0).
+      const int rk = readlane_i(y.cn[0], l) - 1;
+      asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rec) : "s"(l), "{m0}"(rr));
+      asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rnk) : "s"(rk), "{m0}"(rr));
+      rr += inc;
+      if (inc == 0 || rr >= rend) break;
     }
-  } else {
-    uint32_t bits = 0;
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-      bits |= b[j] ? (1u << j) : 0u;
-      // restore the candidates' states (the step's candidates were advanced above)
-      const float dr = b[j] ? x.den[j] - fvl : x.den[j];
-      float qr, ar0;
-      child_state(dr, x.wv[j], x.cp[j], idx0 + j * kWave, vlf, &qr, &ar0);
-      x.q[j] = b[j] ? qr : x.q[j];
-      x.ar[j] = b[j] ? ar0 : x.ar[j];
-      x.den[j] = dr;
-      x.cn[j] = b[j] ? x.cn[j] - 1 : x.cn[j];
-    }
-    win = exact_pick<R>(x.den, x.wv, x.cp, bits, exact_only || tot == 0, k, s, vlf);
-    win = __builtin_amdgcn_readfirstlane(win);
-    const bool mine = win >= 0 && lane == (win & (kWave - 1));
-    const int jj = win >> 6;
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-      const bool hit = mine && j == jj;
-      x.q[j] = hit ? x.qn[j] : x.q[j];
-      x.ar[j] = hit ? x.arn[j] : x.ar[j];
-      x.den[j] = hit ? x.den[j] + fvl : x.den[j];
-      x.cn[j] = hit ? x.cn[j] + 1 : x.cn[j];
-      x.pb[j] = hit;
-    }
+    y.pb[0] = lane == pl;
+    if (rr >= rend) return rr;
+    // ---- the step at rr was not taken above (its state is as it was, nothing pending):
+    // its threshold again, then the window's end or the exact comparison ----
+    const float s = readlane_f(svec, rr);
+    const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
+    const float A = wave_max_key(ap);
+    const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt_eff;
+    const bool b = ap >= T;
+    const uint64_t cb = __ballot(b);
+    if (WINDOW && !(T > ubnc)) return rr;
+    const bool all = !WINDOW && (exact_only || cb == 0);
+    const int win = __builtin_amdgcn_readfirstlane(
+        exact_pick<1>(y.den, y.wv, y.cp, b ? 1u : 0u, all, k, s, vlf));
+    if (WINDOW && win < 0) return rr;  // (no child scores above -1e9: not a window step)
+    if (!WINDOW && win < 0 && *first_end < 0) *first_end = r0 + rr;
+    const bool hit = win >= 0 && lane == win;
+    y.q[0] = hit ? y.qn[0] : y.q[0];
+    y.ar[0] = hit ? y.arn[0] : y.ar[0];
+    y.den[0] = hit ? y.den[0] + fvl : y.den[0];
+    y.cn[0] = hit ? y.cn[0] + 1 : y.cn[0];
+    y.pb[0] = hit;
+    pl = win >= 0 ? win : -1;
+    const int rk = readlane_i(y.cn[0], win & (kWave - 1)) - 1;
+    asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rec) : "s"(win), "{m0}"(rr));
+    asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rnk) : "s"(rk), "{m0}"(rr));
+    ++rr;
   }
-  return win;
+  y.pb[0] = lane == pl;
+  return rr;
 }
 
 // State of a row of more than 64 children held R slots per lane, for steps over the whole row
@@ -397,7 +376,7 @@ struct WideRow {
   float q[R], ar[R], den[R], wv[R], cp[R];
 };
 
-// One step over the whole row (see select_step); returns j*64 + lane of the pick or -1.
+// One step over the whole row (as in lane_steps); returns j*64 + lane of the pick or -1.
 template <int R>
 __device__ inline int wide_step(WideRow<R>& x, float s, float fvl, float vlf, float qbt_eff,
                                 bool exact_only, int k) {
@@ -451,8 +430,6 @@ __device__ inline int wide_step(WideRow<R>& x, float s, float fvl, float vlf, fl
   return win;
 }
 
-// Wave max of a float as order-preserving keys (made uniform).
-__device__ inline float wave_max_key(float x) { return funkey(wave_max_u32(fkey(x))); }
 
 // A key threshold t with at most 64 of the row's k keys >= t, and at least kTopMin of them
 // where the search meets such a t: bisection on the keys between the row's smallest and
@@ -570,17 +547,8 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     uint32_t rec = kNoChild;
     uint32_t rnk = 0;
     if (R == 1) {
-#pragma unroll 2
-      for (int rr = 0; rr < rend; ++rr) {
-        const float s = readlane_f(svec, rr);
-        const int win = select_step<1>(y, s, fvl, vlf, qbt_eff, exact_only, k, lane, false, 0.0f);
-        if (win < 0 && first_end < 0) first_end = r0 + rr;
-        const int rk = readlane_i(y.cn[0], win & (kWave - 1)) - 1;
-        // lane rr := win / rk; the lane select goes through m0, which the "{m0}" operand hands
-        // to the compiler (v_writelane may read only one SGPR besides m0)
-        asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(rec) : "s"(win), "{m0}"(rr));
-        asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(rnk) : "s"(rk), "{m0}"(rr));
-      }
+      lane_steps<false>(y, svec, 0, rend, fvl, vlf, qbt_eff, exact_only, k, 0.0f, r0, &first_end,
+                        &rec, &rnk);
     } else {
       int rr = 0;
       bool try_window = !exact_only;
@@ -628,14 +596,8 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
           const int rr0 = rr;
           // window steps record the picked lane; the lanes become child indices below.  A
           // window step always picks (no candidate or an unsafe threshold aborts it first).
-          for (; rr < rend; ++rr) {
-            const float s = readlane_f(svec, rr);
-            const int wl = select_step<1>(y, s, fvl, vlf, qbt_eff, false, ncon, cidx, true, ubnc);
-            if (wl < 0) break;
-            const int rk = readlane_i(y.cn[0], wl) - 1;
-            asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(rec) : "s"(wl), "{m0}"(rr));
-            asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(rnk) : "s"(rk), "{m0}"(rr));
-          }
+          rr = lane_steps<true>(y, svec, rr, rend, fvl, vlf, qbt_eff, false, ncon, ubnc, r0,
+                                &first_end, &rec, &rnk);
           {
             const int ci = __shfl(cidx, (int)(rec & 63u), 64);
             if (lane >= rr0 && lane < rr) rec = (uint32_t)ci;
