@@ -228,29 +228,56 @@ __device__ inline int lane_pending(const Row<1>& y) {
 // Wave max of a float as order-preserving keys (made uniform).
 __device__ inline float wave_max_key(float x) { return funkey(wave_max_u32(fkey(x))); }
 
+// Key of the raised value hi = ap + (|ap| + QB) * 2^-19 of a child (qb19 = QB * 2^-19).
+__device__ inline uint32_t raised_key(float ap, float qb19) {
+  return fkey(__builtin_fmaf(__builtin_fabsf(ap), 1.0f / 524288.0f, ap) + qb19);
+}
+
+// Smallest key at which lane_steps takes a step: that of -1e9 (below it no child can be picked
+// without the exact comparison).
+constexpr uint32_t kKeyFloor = 0x319194D7u;  // fkey(-1e9f)
+constexpr uint32_t kKeyInf = 0xFF800000u;    // fkey(+inf)
+static_assert(kKeyFloor == ~__builtin_bit_cast(uint32_t, -1e9f), "fkey of a negative float");
+static_assert(kKeyInf == (__builtin_bit_cast(uint32_t, __builtin_inff()) ^ 0x80000000u),
+              "fkey of a positive float");
+
 // Steps of a chain whose children are held one per lane (rows of at most 64 children, or a
-// contender window), from rank rr up to rank rend.  A step ranks the lanes by
-// ap = fma(s, a, qa), takes the wave max A and the threshold T, and picks the single candidate
-// (ap >= T) when there is one; otherwise the candidates (all children when there is none, or
-// in exact-only mode) are compared exactly by exact_pick.  A pick advances the picked lane to
-// its next state (a register select); that lane's state after its following pick is computed
-// during the next step's wave max.  The steps with a single candidate run in a loop of their
-// own; a step with several candidates (or none) leaves that loop for the exact comparison and
-// comes back.  Keeping the rare step out
-// of the loop body leaves the common step without the register copies that joining the two
-// paths inside it costs.  Lane r of rec / rnk receives the pick at rank r (the lane, or -1 for
-// none) and its rank among the chain's earlier picks of that child.
-//   WINDOW: contender window.  The steps end before the first rank whose threshold does not
-//           exceed ubnc (the bound of the non-contenders); that rank is returned.  Every step
-//           of a window picks.
+// contender window), from rank rr up to rank rend.
+//
+// A step ranks the lanes by ap = fma(s, a, qa) and takes the wave max A (as the key Ak).  The
+// candidates are the lanes whose raised key fkey(hi), hi = ap + (|ap| + QB) * 2^-19 (rounded as
+// in raised_key), is at least Ak.  The exact argmax is among them: with E = (|A| + QB)*2^-20.5
+// it has ap >= A - 2E (see the argument above run_chain's helpers), so its hi, rounded twice,
+// is at least A - 2E + 2^1.5 E - 0.2 E > A.  The lane holding A is a candidate (hi >= ap), so a
+// step has at least one.  A single candidate is the pick.  A step is taken here only when A
+// lies strictly between klo and khi (keys): klo is at least the key of -1e9, and khi at most
+// that of +inf (0 in exact-only mode, which takes no step here).  A NaN ap can only add
+// candidates (a NaN hi), which sends the step to the exact comparison.  Padding lanes hold
+// qa = -FLT_MAX, a = 0: their hi stays finite and below any A above -1e9.
+//
+// A pick advances the picked lane to its next state (a register select); that lane's state
+// after its following pick is computed during the next step's wave max.  The steps with a
+// single candidate run in a loop of their own; any other step leaves that loop for the exact
+// comparison among its candidates (all children when A is out of range) and comes back.
+// Keeping the rare step out of the loop body leaves the common step without the register
+// copies that joining the two paths inside it costs.  Lane r of rec / rnk receives the pick at
+// rank r (the lane, or -1 for none) and its rank among the chain's earlier picks of that child.
+//   WINDOW: contender window; klo is also at least the largest raised key of the
+//           non-contenders at the block's last rank, which bounds their raised keys over the
+//           whole window (ap and hi only grow with s).  With A above it, no non-contender is a
+//           candidate and A is the maximum over the whole row.  The steps end before the first
+//           rank whose A is not in range; that rank is returned.  Every step of a window picks.
 //   else:   every step up to rend is taken; a rank without a child records -1, and the first
 //           such rank goes to first_end (when it is still negative).
 // Returns the first rank not taken.
 template <bool WINDOW>
 __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float fvl, float vlf,
-                                 float qbt_eff, bool exact_only, int k, float ubnc, int r0,
+                                 float qb19, uint32_t klo, uint32_t khi, int k, int r0,
                                  int* first_end, uint32_t* rec, uint32_t* rnk) {
   const int lane = lane_id();
+  // A in range: (Ak - kbase) < kspan as unsigned
+  const uint32_t kbase = klo + 1u;
+  const uint32_t kspan = khi > kbase ? khi - kbase : 0u;
   // the lane whose state after its next pick is pending (the previous step's pick), or -1
   int pl = __builtin_amdgcn_readfirstlane(lane_pending(y));
   while (rr < rend) {
@@ -260,8 +287,8 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     for (;;) {
       const float s = readlane_f(svec, rr);
       const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
-      // The wave max of the keys is interleaved with the pending state after the next pick
-      // of the previous step's child (independent of it).
+      // The wave max of the keys is interleaved with the raised key and with the pending state
+      // after the next pick of the previous step's child (both independent of it).
       int v = (int)fkey(ap);
       float d2 = y.den[0] + fvl;
       float e2 = (d2 - 1.0f) + vlf;
@@ -283,8 +310,10 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       OMQ_DPP_MAX(v, 0x114, 0xF);  // row_shr:4
       r1 = __builtin_fmaf(r1, t1, r1);
       r2 = __builtin_fmaf(r2, t2, r2);
+      uint32_t hk = raised_key(ap, qb19);
       OMQ_PIN(r1);
       OMQ_PIN(r2);
+      OMQ_PIN(hk);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x118, 0xF);  // row_shr:8
       // a picked child is visited afterwards (virtual loss >= 1 here)
@@ -301,25 +330,23 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       OMQ_PIN(y.arn[0]);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x143, 0xC);  // row_bcast:31
-      const float A = funkey((uint32_t)__builtin_amdgcn_readlane(v, 63));
-      // T = A - (|A| + QB) * 2^-19
-      const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt_eff;
-      // The candidates, none when a window ends here (threshold NaN): a window ends where the
-      // threshold does not exceed the non-contenders' bound.  (A step without a candidate has a NaN threshold:
-      // the lane holding the maximum A has ap = A >= T whenever A is finite, since T <= A;
-      // A = +inf gives T = NaN.  It is not taken here either.)
-      const float Tw = WINDOW ? (T > ubnc ? T : __builtin_nanf("")) : T;
-      const uint64_t cm = __ballot(ap >= Tw);
-      // The step is taken when it has a single candidate l.  (s_ff1 of an empty mask gives -1:
-      // then any lane will do for the writes below, which the step that takes rank rr later
-      // repeats.)  inc = taken ? 1 : 0 and lt = taken ? l : -1 are formed in scalar registers
-      // (as plain C the compiler routes them through vector registers).
+      const uint32_t Ak = (uint32_t)__builtin_amdgcn_readlane(v, 63);
+      const uint64_t cm = __ballot(hk >= Ak);
+      // The step is taken when A is in range and it has a single candidate l.  (s_ff1 of an
+      // empty mask gives -1: then any lane will do for the writes below, which the step that
+      // takes rank rr later repeats.)  inc = taken ? 1 : 0 and lt = taken ? l : -1 are formed
+      // in scalar registers (as plain C the compiler routes them through vector registers).
       const int pc = __popcll(cm);
       int l, inc, lt;
       asm("s_ff1_i32_b64 %0, %1" : "=s"(l) : "s"(cm));
-      asm("s_cmp_eq_u32 %2, 1\n\ts_cselect_b32 %0, 1, 0\n\ts_cselect_b32 %1, %3, -1"
-          : "=s"(inc), "=s"(lt)
-          : "s"(pc), "s"(l)
+      asm("s_sub_u32 %0, %2, %3\n\t"
+          "s_cmp_lt_u32 %0, %4\n\t"
+          "s_cselect_b32 %0, %5, 0\n\t"
+          "s_cmp_eq_u32 %0, 1\n\t"
+          "s_cselect_b32 %0, 1, 0\n\t"
+          "s_cselect_b32 %1, %6, -1"
+          : "=&s"(inc), "=&s"(lt)
+          : "s"(Ak), "s"(kbase), "s"(kspan), "s"(pc), "s"(l)
           : "scc");
       // the step's pick, if taken; the pending state is final now
       const bool hit = lane == lt;
@@ -338,18 +365,16 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     }
     y.pb[0] = lane == pl;
     if (rr >= rend) return rr;
-    // ---- the step at rr was not taken above (its state is as it was, nothing pending):
-    // its threshold again, then the window's end or the exact comparison ----
+    // ---- the step at rr was not taken above (its state is as it was, nothing pending): its
+    // candidates again, then the window's end or the exact comparison ----
     const float s = readlane_f(svec, rr);
     const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
-    const float A = wave_max_key(ap);
-    const float T = __builtin_fmaf(__builtin_fabsf(A), -1.0f / 524288.0f, A) + qbt_eff;
-    const bool b = ap >= T;
-    const uint64_t cb = __ballot(b);
-    if (WINDOW && !(T > ubnc)) return rr;
-    const bool all = !WINDOW && (exact_only || cb == 0);
+    const uint32_t Ak = wave_max_u32(fkey(ap));
+    const bool cand = raised_key(ap, qb19) >= Ak;
+    const bool in_range = Ak - kbase < kspan;
+    if (WINDOW && !in_range) return rr;
     const int win = __builtin_amdgcn_readfirstlane(
-        exact_pick<1>(y.den, y.wv, y.cp, b ? 1u : 0u, all, k, s, vlf));
+        exact_pick<1>(y.den, y.wv, y.cp, cand ? 1u : 0u, !in_range, k, s, vlf));
     if (WINDOW && win < 0) return rr;  // (no child scores above -1e9: not a window step)
     if (!WINDOW && win < 0 && *first_end < 0) *first_end = r0 + rr;
     const bool hit = win >= 0 && lane == win;
@@ -505,6 +530,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
   }
   const uint32_t QBb = wave_max_rows(__float_as_uint(qbl));  // bits of QB (non-negative)
   const float qbt = __uint_as_float(QBb) * (-1.0f / 524288.0f);
+  const float qb19 = -qbt;  // QB * 2^-19
   const bool exact_only = __ballot(negcp) != 0 || !(__uint_as_float(QBb) < 1e8f);
   if (c.vli == 0) {
     // Without an integer virtual loss a pick changes no visit count: every rank sees the same
@@ -524,14 +550,14 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     y.den[0] = x.den[0];
     y.wv[0] = x.wv[0];
     y.cp[0] = x.cp[0];
-    y.q[0] = x.q[0];
+    y.q[0] = lane < k ? x.q[0] : -__FLT_MAX__;  // (padding lanes: see lane_steps)
     y.ar[0] = x.ar[0];
     y.pb[0] = false;
     y.cn[0] = 0;
     if (lane < k) {
       child_state(y.den[0] + fvl, y.wv[0], y.cp[0], lane, vlf, &y.qn[0], &y.arn[0]);
     } else {
-      y.qn[0] = -__builtin_inff();
+      y.qn[0] = -__FLT_MAX__;
       y.arn[0] = 0.0f;
     }
   }
@@ -547,8 +573,8 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     uint32_t rec = kNoChild;
     uint32_t rnk = 0;
     if (R == 1) {
-      lane_steps<false>(y, svec, 0, rend, fvl, vlf, qbt_eff, exact_only, k, 0.0f, r0, &first_end,
-                        &rec, &rnk);
+      lane_steps<false>(y, svec, 0, rend, fvl, vlf, qb19, kKeyFloor, exact_only ? 0u : kKeyInf,
+                        k, r0, &first_end, &rec, &rnk);
     } else {
       int rr = 0;
       bool try_window = !exact_only;
@@ -563,7 +589,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
           const uint32_t tau = top64_threshold<R>(key, k);
           uint64_t cmask[R];
           int base = 0;
-          float ub = -__builtin_inff();
+          uint32_t ubk = kKeyFloor;
 #pragma unroll
           for (int j = 0; j < R; ++j) {
             const int i = j * kWave + lane;
@@ -573,10 +599,13 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
                                         (uint32_t)(cmask[j] >> 32),
                                         __builtin_amdgcn_mbcnt_lo((uint32_t)cmask[j], 0u));
             if (con) cscr[dest] = make_float4(x.den[j], x.wv[j], x.cp[j], __int_as_float(i));
-            if (i < k && !con) ub = fmaxf(ub, __builtin_fmaf(s_end, x.ar[j], x.q[j]));
+            // (a NaN ap is never a pick, and not a candidate of the window's steps)
+            const float a = __builtin_fmaf(s_end, x.ar[j], x.q[j]);
+            const uint32_t ha = raised_key(a, qb19);
+            ubk = (i < k && !con && a == a) ? max(ubk, ha) : ubk;
             base += __popcll(cmask[j]);
           }
-          const float ubnc = wave_max_key(ub);
+          ubk = wave_max_u32(ubk);
           const int ncon = base;
           wave_sync();
           const float4 e = lane < ncon ? cscr[lane] : make_float4(2.0f, 0.0f, 0.0f, 0.0f);
@@ -590,13 +619,13 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
             child_state(y.den[0], y.wv[0], y.cp[0], cidx, vlf, &y.q[0], &y.ar[0]);
             child_state(y.den[0] + fvl, y.wv[0], y.cp[0], cidx, vlf, &y.qn[0], &y.arn[0]);
           } else {
-            y.q[0] = y.qn[0] = -__builtin_inff();
+            y.q[0] = y.qn[0] = -__FLT_MAX__;
             y.ar[0] = y.arn[0] = 0.0f;
           }
           const int rr0 = rr;
           // window steps record the picked lane; the lanes become child indices below.  A
           // window step always picks (no candidate or an unsafe threshold aborts it first).
-          rr = lane_steps<true>(y, svec, rr, rend, fvl, vlf, qbt_eff, false, ncon, ubnc, r0,
+          rr = lane_steps<true>(y, svec, rr, rend, fvl, vlf, qb19, ubk, kKeyInf, ncon, r0,
                                 &first_end, &rec, &rnk);
           {
             const int ci = __shfl(cidx, (int)(rec & 63u), 64);

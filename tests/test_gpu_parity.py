@@ -31,6 +31,15 @@ CASES = {
                              "capacity": 100_000, "virtual_loss": 2.5, "c_puct": 0.5,
                              "expand_policy": "reference_pw", "dirichlet_alpha": 0.3,
                              "dirichlet_epsilon": 0.25}),
+    # uniform priors (logit scale 0): close and equal scores, so that many steps have several
+    # candidates and go to the exact comparison, in the 4-slot and the 1-slot kernels
+    "uniform-priors-C2": ("C2", {"num_trees": 3, "num_simulations": 768, "wave_size": 256,
+                                 "capacity": 100_000, "logit_scale": 0.0}),
+    "uniform-priors-C4": ("C4", {"num_trees": 2, "num_simulations": 2048, "wave_size": 1024,
+                                 "capacity": 100_000, "logit_scale": 0.0}),
+    # a negative c_puct: every step is compared exactly (no fast path)
+    "negative-cpuct": ("C2", {"num_trees": 2, "num_simulations": 512, "wave_size": 256,
+                              "capacity": 100_000, "c_puct": -0.5}),
 }
 
 
