@@ -496,7 +496,7 @@ __device__ inline uint32_t top64_threshold(const uint32_t* key, int k) {
 
 // With `progress` set, the chain publishes its progress after every block of 64 ranks: the
 // block's picks are in ch first (workgroup-scope release), then *progress = ranks done.
-template <int R>
+template <int R, bool PERSIST>
 __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
                          const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
                          int* progress) {
@@ -564,6 +564,51 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
   int first_end = -1;
   // a NaN threshold sends every step to the exact comparison
   const float qbt_eff = exact_only ? __builtin_nanf("") : qbt;
+  // A contender window stays open across blocks of ranks while its bound holds: its contenders
+  // in y (row index cidx, ncon of them) and, per lane, the slots of x that are contenders (bit
+  // j: slot j).  The contenders' slots of x are stale while it is open.
+  bool wopen = false;
+  int ncon = 0, cidx = 0;
+  uint32_t conbits = 0u;
+  // Bound of the non-contenders' raised keys at rank s_end (a NaN ap is never a pick, and not
+  // a candidate of the window's steps).
+  auto noncon_bound = [&](float s_end) {
+    uint32_t ubk = kKeyFloor;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int i = j * kWave + lane;
+      const bool con = ((conbits >> j) & 1u) != 0;
+      const float a = __builtin_fmaf(s_end, x.ar[j], x.q[j]);
+      const uint32_t ha = raised_key(a, qb19);
+      ubk = (i < k && !con && a == a) ? max(ubk, ha) : ubk;
+    }
+    return wave_max_u32(ubk);
+  };
+  // Closes the window: the contenders' counts go back to cnt_s and their states to x (every
+  // state follows from its count).
+  auto close_window = [&]() {
+    wave_sync();
+    if (lane < ncon) {
+      cscr[lane].x = y.den[0];
+      cnt_s[cidx] = (uint16_t)y.cn[0];
+    }
+    wave_sync();
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int i = j * kWave + lane;
+      const bool con = ((conbits >> j) & 1u) != 0;
+      const uint64_t cm = __ballot(con);
+      const int dest = base + (int)__builtin_amdgcn_mbcnt_hi(
+                                  (uint32_t)(cm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)cm, 0u));
+      if (con) x.den[j] = cscr[dest].x;
+      if (i < k) child_state(x.den[j], x.wv[j], x.cp[j], i, vlf, &x.q[j], &x.ar[j]);
+      base += __popcll(cm);
+    }
+    wave_sync();
+    conbits = 0u;
+    wopen = false;
+  };
   for (int r0 = 0; r0 < m; r0 += kWave) {
     const int Npl = Np0 + c.vli * (r0 + lane + 1);
     const float svec = sqrtf((float)Npl);
@@ -578,38 +623,41 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     } else {
       int rr = 0;
       bool try_window = !exact_only;
+      if (PERSIST && wopen) {
+        // ---- the open window continues, with its bound for this block's last rank ----
+        const uint32_t ubk = noncon_bound(readlane_f(svec, rend - 1));
+        rr = lane_steps<true>(y, svec, 0, rend, fvl, vlf, qb19, ubk, kKeyInf, ncon, r0,
+                              &first_end, &rec, &rnk);
+        const int ci = __shfl(cidx, (int)(rec & 63u), 64);
+        if (lane < rr) rec = (uint32_t)ci;
+        if (rr < rend) close_window();  // (a fresh window may follow in this block)
+      }
       while (rr < rend) {
         if (try_window && rend - rr >= 8) {
           // ---- contender window: the top 64 children by ap at its first rank ----
           const float s0 = readlane_f(svec, rr);
-          const float s_end = readlane_f(svec, rend - 1);
           uint32_t key[R];
 #pragma unroll
           for (int j = 0; j < R; ++j) key[j] = fkey(__builtin_fmaf(s0, x.ar[j], x.q[j]));
           const uint32_t tau = top64_threshold<R>(key, k);
-          uint64_t cmask[R];
           int base = 0;
-          uint32_t ubk = kKeyFloor;
 #pragma unroll
           for (int j = 0; j < R; ++j) {
             const int i = j * kWave + lane;
             const bool con = i < k && key[j] >= tau;
-            cmask[j] = __ballot(con);
+            const uint64_t cm = __ballot(con);
             const int dest = base + (int)__builtin_amdgcn_mbcnt_hi(
-                                        (uint32_t)(cmask[j] >> 32),
-                                        __builtin_amdgcn_mbcnt_lo((uint32_t)cmask[j], 0u));
+                                        (uint32_t)(cm >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)cm, 0u));
             if (con) cscr[dest] = make_float4(x.den[j], x.wv[j], x.cp[j], __int_as_float(i));
-            // (a NaN ap is never a pick, and not a candidate of the window's steps)
-            const float a = __builtin_fmaf(s_end, x.ar[j], x.q[j]);
-            const uint32_t ha = raised_key(a, qb19);
-            ubk = (i < k && !con && a == a) ? max(ubk, ha) : ubk;
-            base += __popcll(cmask[j]);
+            conbits |= con ? (1u << j) : 0u;
+            base += __popcll(cm);
           }
-          ubk = wave_max_u32(ubk);
-          const int ncon = base;
+          const uint32_t ubk = noncon_bound(readlane_f(svec, rend - 1));
+          ncon = base;
           wave_sync();
           const float4 e = lane < ncon ? cscr[lane] : make_float4(2.0f, 0.0f, 0.0f, 0.0f);
-          const int cidx = __float_as_int(e.w);
+          cidx = __float_as_int(e.w);
           y.den[0] = e.x;
           y.wv[0] = e.y;
           y.cp[0] = e.z;
@@ -622,6 +670,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
             y.q[0] = y.qn[0] = -__FLT_MAX__;
             y.ar[0] = y.arn[0] = 0.0f;
           }
+          wopen = true;
           const int rr0 = rr;
           // window steps record the picked lane; the lanes become child indices below.  A
           // window step always picks (no candidate or an unsafe threshold aborts it first).
@@ -631,27 +680,10 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
             const int ci = __shfl(cidx, (int)(rec & 63u), 64);
             if (lane >= rr0 && lane < rr) rec = (uint32_t)ci;
           }
-          // write back the contenders' counts; every state follows from its count
-          wave_sync();
-          if (lane < ncon) {
-            cscr[lane].x = y.den[0];
-            cnt_s[cidx] = (uint16_t)y.cn[0];
+          if (rr < rend || !PERSIST) {  // (else the window stays open into the next block)
+            close_window();
+            if (rr - rr0 < 8) try_window = false;  // no more windows in this block
           }
-          wave_sync();
-          base = 0;
-#pragma unroll
-          for (int j = 0; j < R; ++j) {
-            const int i = j * kWave + lane;
-            const bool con = ((cmask[j] >> lane) & 1ull) != 0;
-            const int dest = base + (int)__builtin_amdgcn_mbcnt_hi(
-                                        (uint32_t)(cmask[j] >> 32),
-                                        __builtin_amdgcn_mbcnt_lo((uint32_t)cmask[j], 0u));
-            if (con) x.den[j] = cscr[dest].x;
-            if (i < k) child_state(x.den[j], x.wv[j], x.cp[j], i, vlf, &x.q[j], &x.ar[j]);
-            base += __popcll(cmask[j]);
-          }
-          wave_sync();
-          if (rr - rr0 < 8) try_window = false;  // no more windows in this block
           continue;
         }
         // ---- one step over the whole row ----
@@ -677,6 +709,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
         __hip_atomic_store(progress, r0 + rend, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
+  if (R > 1 && PERSIST && wopen) close_window();
   // the chain's pick counts per child (R == 1 keeps them in the lanes until here)
   if (R == 1 && lane < k) cnt_s[lane] = (uint16_t)y.cn[0];
   wave_sync();
@@ -691,19 +724,22 @@ __device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, in
                                      int m, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s,
                                      float4* cscr, int* progress) {
   const int r = (k + kWave - 1) / kWave;  // 1 <= r <= RMAX (checked by the caller)
+  // contender windows kept open across blocks in the kernels of up to 4 slots per lane (the
+  // wider kernels' chains have no registers left for it)
+  constexpr bool kPersist = RMAX <= 4;
   if (RMAX <= 1 || r <= 1)
-    return run_chain<1>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<1, kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 2 && r == 2)
-    return run_chain<(RMAX >= 2 ? 2 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 2 ? 2 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 3 && r == 3)
-    return run_chain<(RMAX >= 3 ? 3 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 3 ? 3 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 4 && r == 4)
-    return run_chain<(RMAX >= 4 ? 4 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 4 ? 4 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 5 && r == 5)
-    return run_chain<(RMAX >= 5 ? 5 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 5 ? 5 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 6 && r == 6)
-    return run_chain<(RMAX >= 6 ? 6 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
-  return run_chain<(RMAX >= 8 ? 8 : 1)>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 6 ? 6 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+  return run_chain<(RMAX >= 8 ? 8 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
 }
 
 // Block-wide exclusive scan of a[0..n) in place (n <= 4 * kSelThreads); returns the total.
