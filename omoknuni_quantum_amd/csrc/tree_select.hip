@@ -464,7 +464,39 @@ __device__ inline int wide_step(WideRow<R>& x, float s, float fvl, float vlf, fl
 constexpr int kTopMin = 56;
 
 template <int R>
-__device__ inline uint32_t top64_threshold(const uint32_t* key, int k) {
+struct RowKeys {
+  uint32_t v[R];
+};
+
+// number of the row's keys >= t (uniform)
+template <int R>
+__device__ inline int keys_at_least(const uint32_t* key, int k, uint32_t t) {
+  const int lane = lane_id();
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < R; ++j) cnt += __popcll(__ballot(j * kWave + lane < k && key[j] >= t));
+  return cnt;
+}
+
+// the bisection of [lo, hi), where count(>= lo) > 64 >= count(>= hi)
+template <int R>
+__device__ inline uint32_t top64_bisect(const uint32_t* key, int k, uint64_t lo, uint64_t hi) {
+  while (hi - lo > 1) {
+    const uint64_t mid = (lo + hi) >> 1;
+    const int cnt = keys_at_least<R>(key, k, (uint32_t)mid);
+    if (cnt <= kWave) {
+      hi = mid;
+      if (cnt >= kTopMin) break;
+    } else {
+      lo = mid;
+    }
+  }
+  return (uint32_t)hi;
+}
+
+// [smallest, largest + 1) of the row's keys: count(>= lo) = k > 64 >= count(>= hi) = 0
+template <int R>
+__device__ inline void key_range(const uint32_t* key, int k, uint64_t* lo, uint64_t* hi) {
   const int lane = lane_id();
   uint32_t kmax = 0u, kmin = 0xFFFFFFFFu;
 #pragma unroll
@@ -474,24 +506,58 @@ __device__ inline uint32_t top64_threshold(const uint32_t* key, int k) {
       kmin = min(kmin, key[j]);
     }
   }
-  kmax = wave_max_u32(kmax);
-  kmin = ~wave_max_u32(~kmin);
-  // count(>= lo) = k > 64 >= count(>= hi) = 0
-  uint64_t lo = kmin, hi = (uint64_t)kmax + 1;
-  while (hi - lo > 1) {
-    const uint64_t mid = (lo + hi) >> 1;
-    const uint32_t mt = (uint32_t)mid;
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < R; ++j) cnt += __popcll(__ballot(j * kWave + lane < k && key[j] >= mt));
-    if (cnt <= kWave) {
-      hi = mid;
-      if (cnt >= kTopMin) break;
+  *lo = ~wave_max_u32(~kmin);
+  *hi = (uint64_t)wave_max_u32(kmax) + 1;
+}
+
+template <int R>
+__device__ inline uint32_t top64_threshold(const uint32_t* key, int k) {
+  uint64_t lo, hi;
+  key_range<R>(key, k, &lo, &hi);
+  return top64_bisect<R>(key, k, lo, hi);
+}
+
+// The same search warm-started from hint, the previous window's threshold in the same chain
+// (for the kernels that form a window in every block of ranks).  Consecutive windows have
+// nearby thresholds, so the answer is first bracketed around the hint, with steps that double
+// from 2^16 keys; the bisection then runs in that bracket.  (Not inlined: its working registers
+// are not held across the chain; it runs once per window.)
+template <int R>
+__device__ __noinline__ uint32_t top64_threshold_near(RowKeys<R> keys, int k, uint32_t hint) {
+  const uint32_t* key = keys.v;
+  uint64_t lo, hi;
+  key_range<R>(key, k, &lo, &hi);
+  if (hint > lo && hint < hi) {
+    const int ch = keys_at_least<R>(key, k, hint);
+    if (ch <= kWave && ch >= kTopMin) return hint;
+    uint64_t d = 1u << 16;
+    if (ch > kWave) {
+      lo = hint;  // upwards: hint + d, + 2d, ... until the count is at most 64
+      while (lo + d < hi) {
+        const int c2 = keys_at_least<R>(key, k, (uint32_t)(lo + d));
+        if (c2 <= kWave) {
+          if (c2 >= kTopMin) return (uint32_t)(lo + d);
+          hi = lo + d;
+          break;
+        }
+        lo += d;
+        d <<= 1;
+      }
     } else {
-      lo = mid;
+      hi = hint;  // downwards: hint - d, - 2d, ... until the count exceeds 64
+      while (hi > lo + d) {
+        const int c2 = keys_at_least<R>(key, k, (uint32_t)(hi - d));
+        if (c2 > kWave) {
+          lo = hi - d;
+          break;
+        }
+        hi -= d;
+        if (c2 >= kTopMin) return (uint32_t)hi;
+        d <<= 1;
+      }
     }
   }
-  return (uint32_t)hi;
+  return top64_bisect<R>(key, k, lo, hi);
 }
 
 // With `progress` set, the chain publishes its progress after every block of 64 ranks: the
@@ -569,6 +635,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
   // j: slot j).  The contenders' slots of x are stale while it is open.
   bool wopen = false;
   int ncon = 0, cidx = 0;
+  uint32_t tau_hint = 0u;  // the last window's contender threshold (0: none yet)
   uint32_t conbits = 0u;
   // Bound of the non-contenders' raised keys at rank s_end (a NaN ap is never a pick, and not
   // a candidate of the window's steps).
@@ -636,10 +703,14 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
         if (try_window && rend - rr >= 8) {
           // ---- contender window: the top 64 children by ap at its first rank ----
           const float s0 = readlane_f(svec, rr);
-          uint32_t key[R];
+          RowKeys<R> keys;
+          uint32_t* key = keys.v;
 #pragma unroll
           for (int j = 0; j < R; ++j) key[j] = fkey(__builtin_fmaf(s0, x.ar[j], x.q[j]));
-          const uint32_t tau = top64_threshold<R>(key, k);
+          // (kernels whose windows stay open form few windows: the plain search there)
+          const uint32_t tau = PERSIST ? top64_threshold<R>(key, k)
+                                       : top64_threshold_near<R>(keys, k, tau_hint);
+          tau_hint = tau;
           int base = 0;
 #pragma unroll
           for (int j = 0; j < R; ++j) {
