@@ -36,8 +36,16 @@ __global__ void sim_value_kernel(omq_forest f, omq_wave w, int W, int sign_mode)
 // member values have been fetched (the loads of a lane are issued together); a big group is
 // folded by its wave: 64 member values at a time, one per lane, are read into scalar
 // registers and added in order (the loads of the next 256 are in flight meanwhile).
+//
+// FUSED: the signed leaf value of a member is formed here from its unique leaf's value and its
+// path length (as sim_value_kernel forms it), which saves that kernel's launch; used for waves
+// of at most kFuseMaxWave simulations.  Larger waves have more groups per lane, and there the
+// extra dependent load costs more than the launch (C3 and C4 backups were 6 % and 15 % slower).
+constexpr int kFuseMaxWave = 512;
+
+template <bool FUSED>
 __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_forest f, omq_wave w,
-                                                                       int vli) {
+                                                                       int vli, int sign_mode) {
   const int t = blockIdx.y;
   const int lane = lane_id();
   const int wib = threadIdx.x / kWave;
@@ -48,7 +56,17 @@ __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_fores
   const int G = w.gcount[t];
   const int waves_total = gridDim.x * (kBackupThreads / kWave);
   const int wave_global = blockIdx.x * (kBackupThreads / kWave) + wib;
-  const float* sv = w.sim_value + wb;
+  const int32_t* uid = w.sim_uid + wb;
+  const int32_t* plen = w.path_len + wb;
+  const float* uval = w.values + wb;
+  const float* svals = w.sim_value + wb;
+  const bool leaf_pos = sign_mode == OMQ_SIGN_LEAF_POSITIVE;
+  // signed leaf value of simulation s (sim_value_kernel's value)
+  auto sv = [&](int s) {
+    if (!FUSED) return svals[s];
+    const float v = uval[uid[s]];
+    return (leaf_pos && ((plen[s] - 1) & 1)) ? -v : v;
+  };
   for (int i0 = 0; wave_global + i0 * waves_total < G; i0 += kWave) {
     const int g = wave_global + (i0 + lane) * waves_total;
     int p = 0, d = 0, seg = 0, m = 0;
@@ -63,7 +81,7 @@ __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_fores
       const uint16_t* mem = w.gmembers + ((int64_t)t * MD + d) * MW + seg;
       float vals[kBigGroup];
 #pragma unroll
-      for (int i = 0; i < kBigGroup; ++i) vals[i] = i < m ? sv[mem[i]] : 0.0f;
+      for (int i = 0; i < kBigGroup; ++i) vals[i] = i < m ? sv(mem[i]) : 0.0f;
       float acc = f.value_sums[tb + p];
       const bool odd = d & 1;
 #pragma unroll
@@ -88,14 +106,14 @@ __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_fores
 #pragma unroll
       for (int u = 0; u < kBigChunk; ++u) {
         const int c = u * kWave + lane;
-        xa[u] = c < bm ? sv[bmem[c]] : 0.0f;
+        xa[u] = c < bm ? sv(bmem[c]) : 0.0f;
       }
       for (int c0 = 0; c0 < bm; c0 += kBigChunk * kWave) {
         const int cn = c0 + kBigChunk * kWave;
 #pragma unroll
         for (int u = 0; u < kBigChunk; ++u) {
           const int c = cn + u * kWave + lane;
-          xb[u] = c < bm ? sv[bmem[c]] : 0.0f;
+          xb[u] = c < bm ? sv(bmem[c]) : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < kBigChunk; ++u) {
@@ -188,9 +206,12 @@ hipError_t launch_backup(const omq_forest& f, const omq_wave& w, int W, float vi
                          int sign_mode, int w_mode, hipStream_t st) {
   const int vli = (int)virtual_loss;
   dim3 g1((W + 255) / 256, f.num_trees);
-  hipLaunchKernelGGL(sim_value_kernel, g1, dim3(256), 0, st, f, w, W, sign_mode);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  const bool fused = w_mode != OMQ_WACC_ATOMIC && W <= kFuseMaxWave;
+  if (!fused) {
+    hipLaunchKernelGGL(sim_value_kernel, g1, dim3(256), 0, st, f, w, W, sign_mode);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   if (w_mode == OMQ_WACC_ATOMIC) {
     hipLaunchKernelGGL(backup_atomic_kernel, g1, dim3(256), 0, st, f, w, W, vli);
     return hipGetLastError();
@@ -201,8 +222,12 @@ hipError_t launch_backup(const omq_forest& f, const omq_wave& w, int W, float vi
   int blocks = (est_groups + kBackupThreads - 1) / kBackupThreads;
   if (blocks < 1) blocks = 1;
   if (blocks > 1024) blocks = 1024;
-  hipLaunchKernelGGL(backup_groups_kernel, dim3(blocks, f.num_trees), dim3(kBackupThreads), 0, st,
-                     f, w, vli);
+  if (fused)
+    hipLaunchKernelGGL(backup_groups_kernel<true>, dim3(blocks, f.num_trees),
+                       dim3(kBackupThreads), 0, st, f, w, vli, sign_mode);
+  else
+    hipLaunchKernelGGL(backup_groups_kernel<false>, dim3(blocks, f.num_trees),
+                       dim3(kBackupThreads), 0, st, f, w, vli, sign_mode);
   return hipGetLastError();
 }
 
