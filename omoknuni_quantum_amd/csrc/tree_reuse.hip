@@ -25,6 +25,14 @@ namespace omq {
 constexpr int kShiftThreads = 1024;
 constexpr int kShiftWaves = kShiftThreads / kWave;
 
+// Workgroup barrier that orders LDS only: global loads in flight stay in flight across it
+// (__syncthreads also waits for them).
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // exclusive scan of one value per thread over the workgroup; total through *total
 __device__ inline int shift_block_scan(int v, int* s_wtot, int* total) {
   const int tid = threadIdx.x;
@@ -32,14 +40,14 @@ __device__ inline int shift_block_scan(int v, int* s_wtot, int* total) {
   int wt;
   const int wex = wave_excl_scan(v, &wt);
   if (lane_id() == 0) s_wtot[wave] = wt;
-  __syncthreads();
+  lds_barrier();
   int base = 0, tot = 0;
   for (int i = 0; i < kShiftWaves; ++i) {
     const int x = s_wtot[i];
     if (i < wave) base += x;
     tot += x;
   }
-  __syncthreads();  // s_wtot is reused by the next scan
+  lds_barrier();  // s_wtot is reused by the next scan
   *total = tot;
   return base + wex;
 }
@@ -64,6 +72,7 @@ __global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f
   __shared__ int s_cex[kShiftChunk];  // compacted nodes with children: first child's offset
   __shared__ int s_cof[kShiftChunk];  //   their old row offset
   __shared__ int s_cid[kShiftChunk];  //   their position in the chunk
+  __shared__ int s_bad;               // a row of the chunk is inconsistent
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -80,37 +89,59 @@ __global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f
     if (tid == 0) npar[0] = -2;
     return;
   }
-  if (tid == 0) old_of_new[0] = r;
+  if (tid == 0) {
+    old_of_new[0] = r;
+    s_bad = 0;
+  }
   __syncthreads();
   // level [lo, hi) of new ids; its children get [hi, next)
   int lo = 0, hi = 1, next = 1;
   bool bad = false;
+  // The rows of a level's next chunk are loaded while the current chunk is processed: a
+  // level's new-to-old ids were all written before the level began, and the barriers inside a
+  // chunk order LDS only, so the loads stay in flight until the chunk's end.
+  int pk[kShiftPer], pof[kShiftPer];
+  auto load_rows = [&](int c0) {
+    const int i0 = c0 + tid * kShiftPer;
+#pragma unroll
+    for (int e = 0; e < kShiftPer; ++e) {
+      pk[e] = 0;
+      pof[e] = 0;
+      if (i0 + e < hi) {
+        const int old = old_of_new[i0 + e];
+        pk[e] = f.num_children[tb + old];
+        pof[e] = f.first_child[tb + old];
+      }
+    }
+  };
   while (lo < hi && !bad) {
+    load_rows(lo);
     for (int c0 = lo; c0 < hi; c0 += kShiftChunk) {
       const int i0 = c0 + tid * kShiftPer;  // this thread's nodes: i0 .. i0+kShiftPer-1
       int k[kShiftPer], of[kShiftPer];
+#pragma unroll
+      for (int e = 0; e < kShiftPer; ++e) {
+        k[e] = pk[e];
+        of[e] = pof[e];
+      }
+      if (c0 + kShiftChunk < hi) load_rows(c0 + kShiftChunk);
       bool row_bad = false;
       int mine = 0, nzm = 0;
 #pragma unroll
       for (int e = 0; e < kShiftPer; ++e) {
-        k[e] = 0;
-        of[e] = 0;
-        if (i0 + e < hi) {
-          const int old = old_of_new[i0 + e];
-          k[e] = f.num_children[tb + old];
-          of[e] = f.first_child[tb + old];
-          if (k[e] < 0 || (k[e] > 0 && (of[e] < 0 || (int64_t)of[e] + k[e] >= n_old))) {
-            row_bad = true;
-            k[e] = 0;
-          }
+        if (i0 + e < hi && (k[e] < 0 || (k[e] > 0 && (of[e] < 0 || (int64_t)of[e] + k[e] >= n_old)))) {
+          row_bad = true;
+          k[e] = 0;
         }
         mine += k[e];
         nzm += k[e] > 0 ? 1 : 0;
       }
+      if (row_bad) s_bad = 1;  // (read after the first scan's barriers)
       int tot, nz;
       int ex = shift_block_scan(mine, s_wtot, &tot);
-      int zx = shift_block_scan(nzm, s_wtot, &nz);
-      if (__syncthreads_or(row_bad) || next + tot > n_old) {
+      const bool any_bad = s_bad != 0;
+      int zx = shift_block_scan(nzm, s_wtot, &nz);  // (its barriers order the read above)
+      if (any_bad || next + tot > n_old) {
         bad = true;
         break;
       }
@@ -129,7 +160,7 @@ __global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f
         }
         ex += k[e];
       }
-      __syncthreads();
+      lds_barrier();
       // the chunk's children, tile by tile: output q belongs to the last listed node j with
       // s_cex[j] <= q, as its child q - s_cex[j]
       for (int q0 = wave * kWave; q0 < tot; q0 += kShiftThreads) {
