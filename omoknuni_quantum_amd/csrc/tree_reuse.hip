@@ -33,23 +33,35 @@ __device__ inline void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// exclusive scan of one value per thread over the workgroup; total through *total
-__device__ inline int shift_block_scan(int v, int* s_wtot, int* total) {
+// Exclusive scans of two values per thread over the workgroup, together (one pair of
+// barriers); totals through *ta, *tb.  s_wtot holds 2 * kShiftWaves ints.
+__device__ inline void shift_block_scan2(int a, int b, int* s_wtot, int* ea, int* eb, int* ta,
+                                         int* tb) {
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
-  int wt;
-  const int wex = wave_excl_scan(v, &wt);
-  if (lane_id() == 0) s_wtot[wave] = wt;
+  int wa, wb;
+  const int xa = wave_excl_scan(a, &wa);
+  const int xb = wave_excl_scan(b, &wb);
+  if (lane_id() == 0) {
+    s_wtot[wave] = wa;
+    s_wtot[kShiftWaves + wave] = wb;
+  }
   lds_barrier();
-  int base = 0, tot = 0;
+  int ba = 0, bb = 0, sa = 0, sb = 0;
   for (int i = 0; i < kShiftWaves; ++i) {
-    const int x = s_wtot[i];
-    if (i < wave) base += x;
-    tot += x;
+    const int x = s_wtot[i], y = s_wtot[kShiftWaves + i];
+    if (i < wave) {
+      ba += x;
+      bb += y;
+    }
+    sa += x;
+    sb += y;
   }
   lds_barrier();  // s_wtot is reused by the next scan
-  *total = tot;
-  return base + wex;
+  *ea = ba + xa;
+  *eb = bb + xb;
+  *ta = sa;
+  *tb = sb;
 }
 
 // Breadth-first numbering of tree t's kept nodes (one workgroup per tree).  Writes, for new
@@ -68,7 +80,7 @@ constexpr int kShiftChunk = kShiftThreads * kShiftPer;
 __global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f,
                                                                     const int32_t* new_roots,
                                                                     int32_t* ws) {
-  __shared__ int s_wtot[kShiftWaves];
+  __shared__ int s_wtot[2 * kShiftWaves];
   __shared__ int s_cex[kShiftChunk];  // compacted nodes with children: first child's offset
   __shared__ int s_cof[kShiftChunk];  //   their old row offset
   __shared__ int s_cid[kShiftChunk];  //   their position in the chunk
@@ -136,11 +148,10 @@ __global__ __launch_bounds__(kShiftThreads) void shift_order_kernel(omq_forest f
         mine += k[e];
         nzm += k[e] > 0 ? 1 : 0;
       }
-      if (row_bad) s_bad = 1;  // (read after the first scan's barriers)
-      int tot, nz;
-      int ex = shift_block_scan(mine, s_wtot, &tot);
+      if (row_bad) s_bad = 1;  // (read after the scan's barriers)
+      int tot, nz, ex, zx;
+      shift_block_scan2(mine, nzm, s_wtot, &ex, &zx, &tot, &nz);
       const bool any_bad = s_bad != 0;
-      int zx = shift_block_scan(nzm, s_wtot, &nz);  // (its barriers order the read above)
       if (any_bad || next + tot > n_old) {
         bad = true;
         break;
