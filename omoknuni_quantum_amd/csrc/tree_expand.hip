@@ -35,9 +35,22 @@ __host__ __device__ inline size_t leaf_lds_per_wave(const omq_forest& f) {
   return b + lc * 8;
 }
 
-__device__ inline LeafLds carve(const omq_forest& f, unsigned char* base, int wave) {
+// Board games with at most kStageMaxA actions: the expansion stages the leaf's policy row in
+// LDS (loaded coalesced at the kernel's start), behind the wave's LeafLds region.
+constexpr int kStageMaxA = 6 * kWave;
+
+__host__ __device__ inline bool stage_policy(const omq_forest& f) {
+  return f.game != OMQ_GAME_SPARSE && f.num_actions <= kStageMaxA;
+}
+
+__host__ __device__ inline size_t expand_lds_per_wave(const omq_forest& f) {
+  return leaf_lds_per_wave(f) + (stage_policy(f) ? (size_t)f.num_actions * 4 : 0);
+}
+
+__device__ inline LeafLds carve(const omq_forest& f, unsigned char* base, int wave,
+                                size_t stride) {
   const size_t lc = (size_t)list_cap(f);
-  unsigned char* p = base + leaf_lds_per_wave(f) * wave;
+  unsigned char* p = base + stride * wave;
   LeafLds l;
   l.mask = reinterpret_cast<uint32_t*>(p);
   l.bits = l.mask + f.legal_words;
@@ -57,7 +70,7 @@ __global__ void leaf_info_kernel(omq_forest f, omq_wave w) {
   const int lane = lane_id();
   const int64_t wb = (int64_t)t * w.max_wave;
   if (u >= w.ucount[t]) return;
-  LeafLds l = carve(f, smem, wave);
+  LeafLds l = carve(f, smem, wave, leaf_lds_per_wave(f));
   const int s0 = w.ufirst[wb + u];
   int a_lo, a_hi;
   const int L = load_path_actions(f, w, t, s0, &a_lo, &a_hi);
@@ -90,7 +103,7 @@ __global__ void synth_eval_kernel(omq_forest f, omq_wave w, float scale) {
   const int lane = lane_id();
   const int64_t wb = (int64_t)t * w.max_wave;
   if (u >= w.ucount[t]) return;
-  LeafLds l = carve(f, smem, wave);
+  LeafLds l = carve(f, smem, wave, leaf_lds_per_wave(f));
   const uint64_t key = w.ukey[wb + u];
   const int n = leaf_legal_list(f, w, t, u, l.mask, l.list);
   float* row = w.policy + (wb + u) * (int64_t)f.num_actions;
@@ -242,14 +255,44 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
   const int lane = lane_id();
   const int64_t tb = (int64_t)t * f.capacity;
   const int64_t wb = (int64_t)t * w.max_wave;
-  if (u >= w.ucount[t]) return;
+  if (u >= c.W) return;
+  // The leaf's records, and (staged boards) its policy row, are loaded together before the
+  // checks below, so that their latencies overlap.  (For a slot past the wave's unique leaves
+  // they are stale and unused.)
+  const int ucnt = w.ucount[t];
   const int k = w.unew[wb + u];
-  if (k <= 0) return;
-  LeafLds l = carve(f, smem, wave);
   const int leaf = w.uleaf[wb + u];
   const int cbase = w.uedge[wb + u] + 1;  // node id of the first child
-  const int n = leaf_legal_list(f, w, t, u, l.mask, l.list);
+  const int s0 = w.ufirst[wb + u];
   const float* pol = w.policy + (wb + u) * (int64_t)f.num_actions;
+  const bool staged = stage_policy(f);
+  float prow[kStageMaxA / kWave];
+#pragma unroll
+  for (int j = 0; j < kStageMaxA / kWave; ++j) {
+    const int a = j * kWave + lane;
+    prow[j] = (staged && a < f.num_actions) ? pol[a] : 0.0f;
+  }
+  if (u >= ucnt || k <= 0) return;
+  LeafLds l = carve(f, smem, wave, expand_lds_per_wave(f));
+  float* spol = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(l.mask) +
+                                         leaf_lds_per_wave(f));
+  if (staged) {
+#pragma unroll
+    for (int j = 0; j < kStageMaxA / kWave; ++j) {
+      const int a = j * kWave + lane;
+      if (a < f.num_actions) spol[a] = prow[j];
+    }
+  }
+  int n;
+  if (f.game == OMQ_GAME_SPARSE) {
+    n = sparse_legal_list(f, w.ukey[wb + u], l.list);
+  } else {
+    int a_lo, a_hi;
+    const int L = load_path_actions(f, w, t, s0, &a_lo, &a_hi);
+    board_legal_mask(f, t, L, a_lo, a_hi, l.mask);  // (its barriers also order spol)
+    n = board_legal_list(f, l.mask, l.list);
+  }
+  if (staged) pol = spol;
 
   // legal priors renormalised by their sum (optimized_wave_search.py:384-385)
   float part = 0.0f;
@@ -382,10 +425,11 @@ hipError_t launch_expand(const omq_forest& f, const omq_wave& w, int W, float vi
                      (size_t)W * sizeof(int), st, f, w, c);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int wpb = leaf_waves_per_block(f);
-  const size_t lds = leaf_lds_per_wave_host(f) * wpb;
+  const size_t per = expand_lds_per_wave(f);
+  int wpb = 4;
+  while (wpb > 1 && per * wpb > 64 * 1024) wpb >>= 1;
   dim3 grid((W + wpb - 1) / wpb, f.num_trees);
-  hipLaunchKernelGGL(expand_write_kernel, grid, dim3(wpb * kWave), lds, st, f, w, c);
+  hipLaunchKernelGGL(expand_write_kernel, grid, dim3(wpb * kWave), per * wpb, st, f, w, c);
   return hipGetLastError();
 }
 
