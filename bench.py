@@ -29,7 +29,7 @@ TREE_PHASES = ("select", "leaf_info", "expand", "backup")
 
 def algorithmic_bytes(st: dict, sims: int) -> dict:
     """Compulsory HBM bytes of each tree-operation kernel family over the timed region,
-    from the device counters (definitions in DESIGN.md):
+    from the device counters (the stats slots OMQ_ST_* of omq_tree_ops.h):
       select    16 B per visited node (row header N, first, nchild + N write of the virtual
                 loss) + 12 B per child of each row scanned (N, W, P) + 4 B per path entry
                 (path output) + 8 B per simulation (leaf and path length)
