@@ -128,6 +128,16 @@ def crafted_row_cases(seed: int = 2024) -> list[dict]:
     add("narrow_in_wide", 30, 200, model="gomoku:15")
     add("narrow_in_go", 64, 300, model="go:19")
     add("small_in_8", 100, 130, model="gomoku:21")
+    # NaN values of either sign (a NaN score is never a pick: every comparison with it is
+    # false), in rows held one per lane, in windows and in wide rows
+    nan_pos = np.array([0x7FC00000], np.uint32).view(F32)[0]
+    nan_neg = np.array([0xFFC00000], np.uint32).view(F32)[0]
+    for k, m, nan in ((40, 100, nan_pos), (63, 100, nan_neg), (225, 256, nan_pos),
+                      (362, 300, nan_neg)):
+        Nc = rng.integers(1, 20, k)
+        Wc = (Nc * rng.uniform(-1, 1, k)).astype(F32)
+        Wc[rng.choice(k, 3, replace=False)] = nan
+        add("nanW", k, m, Nc=Nc, Wc=Wc)
     return cases
 
 

@@ -73,7 +73,7 @@ def test_select_rows_closed_forms():
                 best = order[0]
                 if len(sc) > 1 and sc[order[0]] - sc[order[1]] > 1e-5 * abs(sc[order[0]]):
                     assert picks[0] == best
-    assert {"ties", "all_unvisited", "late_unvisited", "vl0", "single", "bigQ", "negP"} <= seen
+    assert {"ties", "all_unvisited", "late_unvisited", "vl0", "single", "bigQ", "negP", "nanW"} <= seen
 
 
 @pytest.mark.parametrize("case", golden.SEARCH_CASES, ids=lambda c: c["name"])
