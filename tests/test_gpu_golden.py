@@ -27,8 +27,8 @@ def _put(t: torch.Tensor, values, dtype) -> None:
 
 def test_select_rows(device):
     """Every simulation's pick and the visit counts after one wave at a crafted root equal the
-    fixture: ties, one-ulp differences, late unvisited children, exact-only rows, NaN values, VL 0/1/2.5,
-    and every chain width (1..8 slots per lane) under the kernel of its game model."""
+    fixture: ties, one-ulp differences, late unvisited children, exact-only rows, NaN values,
+    VL 0/1/2.5, and every chain width (1..8 slots per lane) under the kernel of its game model."""
     fails = []
     for i, c in enumerate(_rows()):
         k, m = c["k"], c["m"]
