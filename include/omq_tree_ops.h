@@ -133,7 +133,8 @@ typedef struct omq_wave {
   int32_t* unew;            /* [T*max_wave] number of children created */
   float* policy;            /* [T*max_wave*num_actions] evaluator policy rows of the unique leaves */
   float* values;            /* [T*max_wave] evaluator values of the unique leaves */
-  float* sim_value;         /* [T*max_wave] backup scratch: signed leaf value of every simulation */
+  float* sim_value;         /* [T*max_wave] backup scratch: signed leaf value of every simulation
+                               (written in atomic mode and for waves of more than 512) */
   int64_t* stats;           /* [T*OMQ_NSTATS] accumulated operation counters */
   int32_t* status;          /* [4] device-side error flags (bit set, never cleared by the library) */
 } omq_wave;
