@@ -166,8 +166,14 @@ class WaveEngine:
 
     # ---- operations -------------------------------------------------------------------
     def reset(self) -> None:
+        """Every tree back to a lone root; the device status flags are cleared too."""
         self._check(self.lib.omq_forest_reset(self.forest_ref, self.stream_handle()),
                     "omq_forest_reset")
+        self.clear_status()
+
+    def clear_status(self) -> None:
+        """Zero the device status flags (the library sets bits and never clears them)."""
+        self.status.zero_()
 
     def select(self, wave_size: int) -> None:
         p = self.params

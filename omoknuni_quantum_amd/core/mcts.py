@@ -131,25 +131,97 @@ class MCTS:
         }
         self.stats_internal = defaultdict(float)
 
-    def _states_array(self, states) -> Optional[np.ndarray]:
-        if not self.model.is_board:
-            return None
+    @staticmethod
+    def _is_state_object(state) -> bool:
+        return hasattr(state, "get_basic_tensor_representation")
+
+    def _state_to_numpy(self, state, representation_type: Optional[str] = None) -> np.ndarray:
+        """GameInterface.state_to_numpy (python/mcts/core/game_interface.py:276-306): the game
+        interface's when it has one, else the state's own representation methods, which is
+        what the reference's interface calls ('basic' by default, 'minimal' for the
+        3-channel form)."""
+        gi = self.game_interface
+        if gi is not None and hasattr(gi, "state_to_numpy"):
+            if representation_type is None:
+                return np.asarray(gi.state_to_numpy(state))
+            return np.asarray(gi.state_to_numpy(state, representation_type=representation_type))
+        if representation_type == "minimal":
+            return np.asarray(state.get_tensor_representation())
+        return np.asarray(state.get_basic_tensor_representation())
+
+    def _board_of_state(self, state):
+        """Board, player to move and move count of a game-state object, as
+        MCTS._initialize_root reads them (python/mcts/core/mcts.py:1520-1600): a 3-channel
+        observation holds player 1's and player 2's stones in channels 0 and 1; otherwise the
+        3-channel 'minimal' form holds the mover's and the opponent's stones, mapped to
+        colours by state.get_current_player().  The move count is the length of the state's
+        move history."""
+        bs = self.config.board_size
+        obs = self._state_to_numpy(state)
+        board = np.zeros((bs, bs), np.int8)
+        player = int(state.get_current_player())
+        if obs.shape[0] == 3:
+            board[np.asarray(obs[0])[:bs, :bs] > 0.5] = 1
+            board[np.asarray(obs[1])[:bs, :bs] > 0.5] = 2
+        else:
+            obs3 = self._state_to_numpy(state, "minimal")
+            if obs3.shape[0] < 2:
+                raise ValueError(f"state representation with {obs3.shape[0]} channels")
+            board[np.asarray(obs3[0])[:bs, :bs] > 0.5] = player
+            board[np.asarray(obs3[1])[:bs, :bs] > 0.5] = 3 - player
+        if obs.shape[-2:] != (bs, bs):
+            raise ValueError(f"Invalid state shape: {obs.shape}, expected board {(bs, bs)}")
+        hist = state.get_move_history() if hasattr(state, "get_move_history") else None
+        moves = int(np.count_nonzero(board)) if hist is None else len(hist)
+        return board, player, moves
+
+    def _root_states(self, states):
+        """Root positions of the trees: (boards int8 [T, bs, bs], players, move counts), where
+        players and move counts are None for ndarray boards (then player 1 moves when the
+        stone count is even, and the move count is the stone count, as mcts.py:1503-1508).
+        states: one [bs, bs] board per tree as an array, or game-state objects (one, or a
+        sequence of one per tree) as the reference's callers pass them."""
+        if states is None or not self.model.is_board:
+            return None, None, None
+        objs = None
+        if self._is_state_object(states):
+            objs = [states]
+        elif isinstance(states, (list, tuple)) and states and all(
+                self._is_state_object(s) for s in states):
+            objs = list(states)
+        if objs is not None:
+            conv = [self._board_of_state(s) for s in objs]
+            boards = np.stack([c[0] for c in conv]).astype(np.int8)
+            return (boards, np.array([c[1] for c in conv], np.int32),
+                    np.array([c[2] for c in conv], np.int32))
         bs = self.config.board_size
         arr = np.asarray(states)
         if arr.shape[-2:] != (bs, bs):
             raise ValueError(f"Invalid state shape: {arr.shape}, expected {(bs, bs)}")
-        return arr.reshape(-1, bs, bs).astype(np.int8)
+        return arr.reshape(-1, bs, bs).astype(np.int8), None, None
 
-    def _set_roots(self, boards: Optional[np.ndarray]) -> None:
+    def _states_array(self, states) -> Optional[np.ndarray]:
+        return self._root_states(states)[0]
+
+    @staticmethod
+    def _roots_key_of(boards, players=None, moves=None) -> bytes:
+        if boards is None:
+            return b""
+        key = np.ascontiguousarray(boards, np.int8).tobytes()
+        for extra in (players, moves):
+            key += b"|" + (b"" if extra is None else np.asarray(extra, np.int32).tobytes())
+        return key
+
+    def _set_roots(self, boards: Optional[np.ndarray], players=None, moves=None) -> None:
         T = self.engine.T
         if boards is not None and boards.shape[0] != T:
             raise ValueError(f"{boards.shape[0]} states given for {T} trees")
-        key = b"" if boards is None else boards.tobytes()
+        key = self._roots_key_of(boards, players, moves)
         if key == self._roots_key and self._eval is not None:
             return
         keys = games.root_keys(self.config.seed, T)
         legal = games.legal_masks(self.model, boards, T)
-        self._install_roots(keys, legal, boards)
+        self._install_roots(keys, legal, boards, players, moves)
         self.engine.reset()
 
     def _root_noise(self, keys: np.ndarray, legal: np.ndarray) -> Optional[np.ndarray]:
@@ -163,13 +235,16 @@ class MCTS:
                                      self.config.seed + 7919 * (self._search_count + 1))
 
     def _install_roots(self, keys: np.ndarray, legal: np.ndarray,
-                       boards: Optional[np.ndarray]) -> None:
-        """Root inputs of every tree on the device (keys, legal masks, noise, Gomoku boards)
-        and the evaluator built on them; the tree arrays are left as they are."""
+                       boards: Optional[np.ndarray], players=None, moves=None) -> None:
+        """Root inputs of every tree on the device (keys, legal masks, noise, Gomoku boards,
+        the player to move and move count of game-state roots) and the evaluator built on
+        them; the tree arrays are left as they are."""
         T = self.engine.T
         self._root_keys_host = np.asarray(keys, dtype=np.uint64).copy()
         self._root_legal_host = np.asarray(legal, dtype=np.uint32).copy()
         self._root_boards_host = None if boards is None else np.asarray(boards, np.int8).copy()
+        self._root_players_host = None if players is None else np.asarray(players, np.int32).copy()
+        self._root_moves_host = None if moves is None else np.asarray(moves, np.int32).copy()
         self.engine.set_roots(keys, legal, self._root_noise(keys, legal))
         if self.config.dirichlet_epsilon > 0 and self.config.root_noise_source == "device":
             self.engine.device_root_noise(float(self.config.dirichlet_alpha), self.config.seed,
@@ -178,8 +253,8 @@ class MCTS:
         if rule is not None:
             b = boards if boards is not None else np.zeros(
                 (T, self.config.board_size, self.config.board_size), np.int8)
-            self.engine.set_gomoku_rules(b, rule)
-        self._roots_key = b"" if boards is None else np.ascontiguousarray(boards, np.int8).tobytes()
+            self.engine.set_gomoku_rules(b, rule, root_player=players)
+        self._roots_key = self._roots_key_of(boards, players, moves)
         self._boards = None if boards is None else torch.from_numpy(
             np.ascontiguousarray(boards, np.int8)).to(self.device)
         self._eval = self._make_evaluator()
@@ -202,35 +277,52 @@ class MCTS:
             raise NotImplementedError("feature-plane evaluators need a board game model")
         from .features import LeafFeatureBuilder
         planes = _input_planes(self.evaluator)
-        return _BatchEvaluatorAdapter(self.evaluator,
-                                      LeafFeatureBuilder(self.engine, self._boards, planes))
+        boards = self._boards
+        if boards is None:
+            boards = torch.zeros((self.engine.T, self.config.board_size, self.config.board_size),
+                                 dtype=torch.int8, device=self.device)
+        return _BatchEvaluatorAdapter(self.evaluator, LeafFeatureBuilder(
+            self.engine, boards, planes, root_player=self._root_players_host,
+            root_moves=self._root_moves_host))
 
     # ---- search --------------------------------------------------------------------------
     def search(self, state: Any, num_simulations: Optional[int] = None) -> np.ndarray:
         """Run the search from `state`; returns the root visit distribution [action_size]."""
         if self.engine.T != 1:
             raise ValueError("search() drives one tree; use search_batch() with num_trees > 1")
-        return self.search_batch(None if state is None else np.asarray(state)[None],
-                                 num_simulations)[0]
+        if state is None or self._is_state_object(state):
+            return self.search_batch(state, num_simulations)[0]
+        arr = np.asarray(state)
+        bs = self.config.board_size
+        if self.model.is_board and arr.shape != (bs, bs):  # mcts.py:935-938
+            raise ValueError(f"Invalid state shape: {arr.shape}, expected {(bs, bs)}")
+        return self.search_batch(arr[None], num_simulations)[0]
 
     def search_batch(self, states: Any, num_simulations: Optional[int] = None) -> np.ndarray:
-        """Search num_trees independent trees together; returns [num_trees, action_size]."""
-        boards = None if states is None else self._states_array(states)
-        num_sims = self.config.num_simulations if num_simulations is None else int(num_simulations)
+        """Search num_trees independent trees together; returns [num_trees, action_size].
+        states: [num_trees, bs, bs] boards, or game-state objects (one per tree)."""
+        boards, players, moves = self._root_states(states)
+        # mcts.py:940: 0 or None runs the configured count
+        num_sims = int(num_simulations or self.config.num_simulations)
         start = time.perf_counter()
         if not self.config.enable_subtree_reuse:
             self._roots_key = None
-        self._set_roots(boards)
-        if num_sims == 0:  # mcts.py:1022-1030
+        self._set_roots(boards, players, moves)
+        self.engine.clear_status()
+        if num_sims == 0:  # mcts.py:1022-1030 (a configured count of 0)
             return np.full((self.engine.T, self.action_size), 1.0 / self.action_size)
         eng = self.engine
         if int(eng.nchild[0].item()) == 0 and int(eng.num_nodes[0].item()) == 1:
             eng.run_wave(1, self._eval)  # root expansion with its own backup
         done = 0
+        first = True
         while done < num_sims:
             w = min(self.wave, num_sims - done)
             eng.run_wave(w, self._eval)
             done += w
+            if first:
+                eng.check_status()  # (a device error stops the search after its first wave)
+                first = False
         eng.check_status()
         policy = eng.root_policies()
         elapsed = time.perf_counter() - start
@@ -283,7 +375,9 @@ class MCTS:
         root."""
         if self.engine.T != 1:
             raise ValueError("update_root() drives one tree; use update_roots() with num_trees > 1")
-        self.update_roots([action], None if new_state is None else np.asarray(new_state)[None])
+        if new_state is not None and not self._is_state_object(new_state):
+            new_state = np.asarray(new_state)[None]
+        self.update_roots([action], new_state)
 
     def update_roots(self, actions, new_states: Any = None) -> bool:
         """update_root for every tree at once (actions[t] played in tree t).  Returns whether
@@ -294,9 +388,9 @@ class MCTS:
         for a in actions:
             if a < 0 or a >= self.action_size:
                 raise ValueError(f"Invalid action {a}. Must be in range [0, {self.action_size})")
-        boards = None if new_states is None else self._states_array(new_states)
+        boards, players, moves = self._root_states(new_states)
         if self.config.enable_subtree_reuse and self._roots_key is not None:
-            kept = self._reuse_subtrees(actions, boards)
+            kept = self._reuse_subtrees(actions, boards, players, moves)
             if kept is not None:
                 self.stats["tree_reuse_count"] += 1
                 self.stats["tree_reuse_nodes"] += kept
@@ -304,10 +398,11 @@ class MCTS:
         self._roots_key = None
         self.engine.reset()
         if boards is not None:
-            self._set_roots(boards)
+            self._set_roots(boards, players, moves)
         return False
 
-    def _reuse_subtrees(self, actions, boards: Optional[np.ndarray]) -> Optional[int]:
+    def _reuse_subtrees(self, actions, boards: Optional[np.ndarray], players=None,
+                        moves=None) -> Optional[int]:
         """Shift every tree's root to its child for actions[t] (CSRTree.shift_root on the
         device).  None, with nothing changed, when some tree lacks that child or the child has
         fewer than subtree_reuse_min_visits visits."""
@@ -345,11 +440,17 @@ class MCTS:
                     bs = self.config.board_size
                     prev = np.zeros((T, bs, bs), np.int8)
                 boards = prev.copy()
+                pp, pm = self._root_players_host, self._root_moves_host
                 for t, a in enumerate(actions):
                     flat = boards[t].reshape(-1)
+                    mover = (int(pp[t]) if pp is not None
+                             else (1 if int((boards[t] != 0).sum()) % 2 == 0 else 2))
                     if a < flat.size:  # Go's pass occupies no cell
-                        flat[a] = 1 if int((boards[t] != 0).sum()) % 2 == 0 else 2
-        self._install_roots(keys, legal, boards)
+                        flat[a] = mover
+                # a game-state root keeps its own player and move count: the opponent moves next
+                players = None if pp is None else (3 - pp).astype(np.int32)
+                moves = None if pm is None else (pm + 1).astype(np.int32)
+        self._install_roots(keys, legal, boards, players, moves)
         return int(eng.num_nodes.sum().item())
 
     def update_with_move(self, move: int) -> None:

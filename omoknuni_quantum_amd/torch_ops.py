@@ -4,7 +4,10 @@ The reference registers ``mcts::vectorized_backup`` (python/mcts/gpu/torch_custo
 and reaches ``batch_apply_virtual_loss`` / ``batch_remove_virtual_loss``
 (python/mcts/gpu/mcts_kernels.cu:845-860,934-953) through its pybind11 module.  The same
 operations are registered here in the ``omq`` namespace, mutating their tensor arguments in
-place on the caller's current HIP stream:
+place on the caller's current HIP stream; the three the reference registers itself are also
+registered under its own names, ``mcts::vectorized_backup``, ``mcts::warp_vectorized_backup``
+and ``mcts::fused_ucb_selection`` (torch_custom_ops.py:26,71,108), which is where
+AsyncWaveSearch probes for them (python/mcts/core/async_wave_search.py:255-260):
 
     torch.ops.omq.vectorized_backup(paths, path_lengths, values, visit_counts, value_sums)
     torch.ops.omq.warp_vectorized_backup(paths, path_lengths, values, visit_counts, value_sums)
@@ -60,7 +63,6 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
-@torch.library.custom_op("omq::vectorized_backup", mutates_args=("visit_counts", "value_sums"))
 def vectorized_backup(paths: torch.Tensor, path_lengths: torch.Tensor, values: torch.Tensor,
                       visit_counts: torch.Tensor, value_sums: torch.Tensor) -> None:
     dev = _check_device("vectorized_backup", paths, path_lengths, values, visit_counts,
@@ -85,11 +87,6 @@ def vectorized_backup(paths: torch.Tensor, path_lengths: torch.Tensor, values: t
                "omq_paths_backup")
 
 
-@vectorized_backup.register_fake
-def _(paths, path_lengths, values, visit_counts, value_sums) -> None:
-    return None
-
-
 def _virtual_loss(name: str, node_indices: torch.Tensor, counts: torch.Tensor, delta: int):
     dev = _check_device(name, node_indices, counts)
     if node_indices.dtype != torch.int32 or counts.dtype != torch.int32:
@@ -103,41 +100,21 @@ def _virtual_loss(name: str, node_indices: torch.Tensor, counts: torch.Tensor, d
                                     _stream(dev)), "omq_virtual_loss")
 
 
-@torch.library.custom_op("omq::batch_apply_virtual_loss", mutates_args=("virtual_loss_counts",))
 def batch_apply_virtual_loss(node_indices: torch.Tensor,
                              virtual_loss_counts: torch.Tensor) -> None:
     _virtual_loss("batch_apply_virtual_loss", node_indices, virtual_loss_counts, 1)
 
 
-@batch_apply_virtual_loss.register_fake
-def _(node_indices, virtual_loss_counts) -> None:
-    return None
-
-
-@torch.library.custom_op("omq::batch_remove_virtual_loss", mutates_args=("virtual_loss_counts",))
 def batch_remove_virtual_loss(node_indices: torch.Tensor,
                               virtual_loss_counts: torch.Tensor) -> None:
     _virtual_loss("batch_remove_virtual_loss", node_indices, virtual_loss_counts, -1)
 
 
-@batch_remove_virtual_loss.register_fake
-def _(node_indices, virtual_loss_counts) -> None:
-    return None
-
-
-@torch.library.custom_op("omq::warp_vectorized_backup",
-                         mutates_args=("visit_counts", "value_sums"))
 def warp_vectorized_backup(paths: torch.Tensor, path_lengths: torch.Tensor, values: torch.Tensor,
                            visit_counts: torch.Tensor, value_sums: torch.Tensor) -> None:
     vectorized_backup(paths, path_lengths, values, visit_counts, value_sums)
 
 
-@warp_vectorized_backup.register_fake
-def _(paths, path_lengths, values, visit_counts, value_sums) -> None:
-    return None
-
-
-@torch.library.custom_op("omq::fused_ucb_selection", mutates_args=())
 def fused_ucb_selection(node_indices: torch.Tensor, children_start: torch.Tensor,
                         children_end: torch.Tensor, children: torch.Tensor,
                         q_values: torch.Tensor, visit_counts: torch.Tensor,
@@ -162,7 +139,42 @@ def fused_ucb_selection(node_indices: torch.Tensor, children_start: torch.Tensor
     return selected
 
 
-@fused_ucb_selection.register_fake
-def _(node_indices, children_start, children_end, children, q_values, visit_counts, priors,
-      c_puct):
+def _fused_ucb_fake(node_indices, children_start, children_end, children, q_values, visit_counts,
+                    priors, c_puct):
     return torch.empty_like(node_indices, dtype=torch.int32)
+
+
+def _no_output(*args) -> None:
+    return None
+
+
+# (name, implementation, mutated arguments, fake, namespaces)
+_OPS = (
+    ("vectorized_backup", vectorized_backup, ("visit_counts", "value_sums"), _no_output,
+     ("omq", "mcts")),
+    ("warp_vectorized_backup", warp_vectorized_backup, ("visit_counts", "value_sums"),
+     _no_output, ("omq", "mcts")),
+    ("fused_ucb_selection", fused_ucb_selection, (), _fused_ucb_fake, ("omq", "mcts")),
+    ("batch_apply_virtual_loss", batch_apply_virtual_loss, ("virtual_loss_counts",), _no_output,
+     ("omq",)),
+    ("batch_remove_virtual_loss", batch_remove_virtual_loss, ("virtual_loss_counts",),
+     _no_output, ("omq",)),
+)
+
+REGISTERED: dict = {}
+
+
+def _register() -> None:
+    """Registers every operator under its namespaces.  A name already taken in the ``mcts``
+    namespace (the reference's own module imported first) is left to its owner."""
+    for name, fn, mutates, fake, namespaces in _OPS:
+        for ns in namespaces:
+            qual = f"{ns}::{name}"
+            if ns == "mcts" and hasattr(torch.ops, "mcts") and hasattr(torch.ops.mcts, name):
+                continue
+            op = torch.library.custom_op(qual, fn, mutates_args=mutates)
+            op.register_fake(fake)
+            REGISTERED[qual] = op
+
+
+_register()

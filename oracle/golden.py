@@ -138,13 +138,87 @@ def crafted_row_cases(seed: int = 2024) -> list[dict]:
         Wc = (Nc * rng.uniform(-1, 1, k)).astype(F32)
         Wc[rng.choice(k, 3, replace=False)] = nan
         add("nanW", k, m, Nc=Nc, Wc=Wc)
+    for c in pinned_row_cases():
+        c = dict(c)
+        c.update(N=np.asarray(c["N"], np.int32), W=np.asarray(c["W"], F32),
+                 P=np.asarray(c["P"], F32))
+        cases.append(c)
     return cases
 
 
-def crafted_expected_np(case: dict) -> tuple[np.ndarray, np.ndarray]:
-    """Picks (child index or -1 per simulation) and N after the wave, from the numpy restatement."""
+# ---- pinned rows --------------------------------------------------------------------------
+# Rows built by hand so that one plausible misreading of select_best_child_nogil /
+# select_path (cython_tree_optimized.pyx:177-202,436-461) picks another child than the rule
+# does.  The rule: Np = N0 + VL (the arriving simulation's virtual loss is added first); the
+# first child with N == 0 wins; otherwise the strict argmax of
+#     W / ((float)N + VL) + ((c * P) * sqrt((float)Np)) / (float)(1 + N)
+# in float32, source order, lowest index on ties; children carry the virtual loss of earlier
+# simulations of the wave.  "expect" holds the rule's picks, worked out by hand (in float64,
+# with the margins stated); "pins" names the misreadings of ref_np.SELECT_VARIANTS the row is
+# built against.  All rows: VL = 3, model sparse (one row per lane).
+
+def _pin(kind, pins, expect, N0, N, W, P, c=1.0, m=1):
+    k = len(N)
+    return {"kind": kind, "model": "sparse", "k": k, "m": m, "c": float(F32(c)), "vl": 3.0,
+            "N0": int(N0), "N": list(N), "W": [float(F32(x)) for x in W],
+            "P": [float(F32(x)) for x in P], "expect": list(expect), "pins": list(pins)}
+
+
+# The operand-order row: with c = 1.4f, Np = 5 and P = 0.000731f, (c*P)*s and c*(P*s) round to
+# neighbouring floats.  Child 1 has N = 1, W = 0 (its score is exactly u / 2); child 0 has P = 0
+# and W set so that its score W / 4 equals the smaller of the two roundings (halved): the rule
+# then picks child 1 strictly, the misreading ties and takes child 0.
+_PIN_OP_P = 0.000731
+_PIN_OP_NP = 5
+
+
+def _op_order_row():
+    c, P = F32(1.4), F32(_PIN_OP_P)
+    s = F32(np.sqrt(F32(_PIN_OP_NP)))
+    u_rule = F32(F32(c * P) * s)
+    u_alt = F32(c * F32(P * s))
+    lo = min(u_rule, u_alt)
+    w0 = F32(lo * F32(2.0))  # W/(1+3) = lo/2 exactly
+    expect = [1] if u_rule > u_alt else [0]
+    return _pin("pin_op_order", ["c_times_ps"], expect, _PIN_OP_NP - 3, [1, 1], [w0, 0.0],
+                [0.0, _PIN_OP_P], c=1.4)
+
+
+def pinned_row_cases() -> list[dict]:
+    """Hand-built rows, each against named misreadings (see the block comment above)."""
+    return [
+        # Q over N + VL: child 0 Q = 0.9/4 = 0.225, child 1 Q = 5/13 = 0.385 (P = 0) -> 1.
+        # With Q = W/N: 0.9 against 0.5 -> 0 (margins 0.16 and 0.4).
+        _pin("pin_q_vl", ["q_no_vl"], [1], 10, [1, 10], [0.9, 5.0], [0.0, 0.0]),
+        # sqrt(Np), Np = 1 + 3 = 4, s = 2: child 0 U = 0.42*2/2 = 0.42, child 1 Q = 1.78/4 =
+        # 0.445 -> 1 (margin 0.025).  With sqrt(Np + 1) = 2.236: U = 0.4696 -> 0 (margin 0.025).
+        _pin("pin_sqrt", ["sqrt_np_plus1"], [1], 1, [1, 1], [0.0, 1.78], [0.42, 0.0]),
+        # the arriving VL in Np: s = sqrt(1 + 3) = 2, child 0 U = 0.42 against child 1 Q =
+        # 1.2/4 = 0.3 -> 0 (margin 0.12).  With Np = 1 (VL added after the pick): U = 0.21 -> 1.
+        _pin("pin_np_arrival", ["np_without_arrival"], [0], 1, [1, 1], [0.0, 1.2], [0.42, 0.0]),
+        # exploration over 1 + N: child 0 U = 0.5*2/2 = 0.5, child 1 Q = 4.2/7 = 0.6 -> 1
+        # (margin 0.1).  Over N: U = 1.0 -> 0 (margin 0.4).
+        _pin("pin_denominator", ["denominator_n"], [1], 1, [1, 4], [0.0, 4.2], [0.5, 0.0]),
+        # first unvisited child: child 1 has N = 0 -> 1.  Scored with Q = 0 instead:
+        # child 0 = 4/8 + 0.1*sqrt(23)/6 = 0.580 against 0.01*sqrt(23) = 0.048 -> 0.
+        _pin("pin_unvisited", ["no_unvisited_rule"], [1], 20, [5, 0], [4.0, 0.0], [0.1, 0.01]),
+        # exact ties: three identical children -> 0 (lowest index); >= takes 2.
+        _pin("pin_ties", ["ties_highest"], [0], 9, [5, 5, 5], [1.25] * 3, [0.25] * 3),
+        # the children's in-flight VL: two identical children, two simulations.  The first
+        # takes 0 (tie, Np = 12); then Np = 15 and child 0 has N = 8: Q + U = 1.25/11 +
+        # 0.5*sqrt(15)/9 = 0.329 against child 1's 1.25/8 + 0.5*sqrt(15)/6 = 0.479 -> 1.
+        # Without child 0's VL the tie repeats -> 0.
+        _pin("pin_children_vl", ["children_no_vl"], [0, 1], 9, [5, 5], [1.25] * 2, [0.5] * 2,
+             m=2),
+        _op_order_row(),
+    ]
+
+
+def crafted_expected_np(case: dict, variant: str | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """Picks (child index or -1 per simulation) and N after the wave, from the numpy
+    restatement (with a planted misreading of ref_np.SELECT_VARIANTS when variant is set)."""
     k = case["k"]
-    t = ref_np.NpTree(k + 1, case["c"], case["vl"])
+    t = ref_np.NpTree(k + 1, case["c"], case["vl"], variant=variant)
     t.expand(0, list(range(k)), [F32(x) for x in case["P"]])
     t.N[0] = case["N0"]
     t.N[1:k + 1] = case["N"]
@@ -182,9 +256,12 @@ def crafted_expected_oracle(case: dict) -> tuple[np.ndarray, np.ndarray]:
     return picks, orc.array("N", k + 1)
 
 
+META_KEYS = ("kind", "model", "k", "m", "c", "vl", "N0", "expect", "pins")
+
+
 def pack_crafted(cases: list[dict], picks: list[np.ndarray], n_after: list[np.ndarray]) -> dict:
     """Flatten the cases into arrays for an npz file (no object arrays)."""
-    meta = [{key: c[key] for key in ("kind", "model", "k", "m", "c", "vl", "N0")} for c in cases]
+    meta = [{key: c[key] for key in META_KEYS if key in c} for c in cases]
     koff = np.concatenate([[0], np.cumsum([c["k"] for c in cases])]).astype(np.int64)
     moff = np.concatenate([[0], np.cumsum([c["m"] for c in cases])]).astype(np.int64)
     noff = np.concatenate([[0], np.cumsum([c["k"] + 1 for c in cases])]).astype(np.int64)
@@ -300,3 +377,78 @@ def search_expected(case: dict) -> dict:
     out["path_len"] = np.array(plens, np.int32)
     out["paths"] = np.array(pflat, np.int32)
     return out
+
+
+# ---- progressive widening of the reference driver ----------------------------------------
+# optimized_wave_search.py:394-415 and MAX_CHILDREN = 8 (cython_tree_optimized.pyx:31,239).
+# The closed form below is written with integer square roots: floor(10 * sqrt(N0)) =
+# isqrt(100 * N0) exactly (10 * sqrt(N0) is an integer only for square N0, where both are exact,
+# and is at least 1 / (20 sqrt(N0) + 1) away from an integer otherwise).
+PW_MODEL = "gomoku:5"
+PW_GRID_N0 = (0, 1, 2, 3, 4, 9, 10, 16, 17, 20, 30, 100, 1000)
+PW_GRID_L = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 14, 15, 16, 20, 25)
+
+
+def pw_root_count(N0: int, L: int) -> tuple[int, int]:
+    """(size of the chosen set, row length) of a root with N0 visits and L legal actions:
+    mc = max(5, min(L, floor(10 sqrt(N0)) + 1, 15)); chosen = the top-mc priors when L > mc,
+    else all L; the row is the first min(8, chosen) of them."""
+    import math
+
+    mc = max(5, min(L, math.isqrt(100 * N0) + 1, 15))
+    chosen = mc if L > mc else L
+    return chosen, min(8, chosen)
+
+
+def pw_inputs(L: int, seed: int):
+    """A 5x5 Gomoku root with exactly L empty cells (stones elsewhere), its legal mask and a
+    policy row of distinct values over the 25 cells (so that the order by prior has no ties).
+    Returns (model, board int8[1,5,5], legal uint32[1,words], legal action list, policy
+    float32[25])."""
+    model = model_from_name(PW_MODEL)
+    A = model.num_actions
+    rng = np.random.default_rng(seed)
+    board = np.zeros(A, np.int8)
+    filled = rng.permutation(A)[:A - L]
+    board[filled] = np.where(np.arange(A - L) % 2 == 0, 1, 2)
+    board = board.reshape(1, model.board_size, model.board_size)
+    legal = games.legal_masks(model, board, 1)
+    acts = [a for a in range(A) if board.reshape(-1)[a] == 0]
+    pol = ((rng.permutation(A) + 1) / (A * (A + 1) / 2)).astype(F32)
+    return model, board, legal, acts, pol
+
+
+def pw_expected(legal_actions, pol, N0: int | None):
+    """Children actions (ascending) of a leaf under the rule: the root (N0 given) by
+    pw_root_count, a non-root leaf (N0 None) the top min(3, L) priors.  The order by prior is
+    taken on the raw policy row (renormalising over the legal set keeps the order of distinct
+    values)."""
+    L = len(legal_actions)
+    by_prior = sorted(legal_actions, key=lambda a: (-float(pol[a]), a))
+    if N0 is None:
+        return sorted(by_prior[:min(3, L)])
+    chosen, k = pw_root_count(N0, L)
+    return sorted(by_prior[:chosen])[:k]
+
+
+def pw_oracle_root(N0: int, L: int, seed: int, vl: float = 3.0):
+    """The C oracle's root row after one simulation at a root with N0 visits and L legal
+    actions (reference_pw), and the row of the root's first child after a second simulation."""
+    model, board, legal, acts, pol = pw_inputs(L, seed)
+    orc = Oracle(model, 1, 128, 1, 100)
+    orc.set_params(1.4, vl, 1, 0, 1.0, 0.0)
+    orc.set_roots(games.root_keys(seed, 1), legal)
+    orc.reset_tree(0)
+    orc.write("N", np.array([N0], np.int32))
+    rows = np.stack([pol])
+    orc.wave(0, 1, replay_policy=rows, replay_values=np.zeros(1, F32))
+    tr = orc.tree(0)
+    root = [int(a) for a in tr["action"][tr["first"][0] + 1:tr["first"][0] + 1 + tr["nchild"][0]]]
+    child = None
+    if tr["nchild"][0] > 0:
+        orc.wave(0, 1, replay_policy=rows, replay_values=np.zeros(1, F32))
+        tr = orc.tree(0)
+        c0 = tr["first"][0] + 1
+        f, k = tr["first"][c0], tr["nchild"][c0]
+        child = [int(a) for a in tr["action"][f + 1:f + 1 + k]] if k > 0 else []
+    return root, child

@@ -49,8 +49,26 @@ def sum64d(x) -> float:
     return part[0]
 
 
+# Planted misreadings of the selection rule (cython_tree_optimized.pyx:177-202,421-464), used
+# only by the tests that show the pinning checks fail on each of them.  None is the rule.
+SELECT_VARIANTS = (
+    "q_no_vl",             # Q = W / N instead of W / (N + VL)
+    "sqrt_np_plus1",       # sqrt(Np + 1) instead of sqrt(Np)
+    "np_without_arrival",  # the arriving simulation's VL added to the parent after the pick
+    "denominator_n",       # exploration over N instead of 1 + N
+    "c_times_ps",          # c * (P * s) instead of (c * P) * s
+    "no_unvisited_rule",   # unvisited children scored (Q = 0) instead of taken first
+    "ties_highest",        # >= instead of > (ties to the highest index)
+    "children_no_vl",      # children scored without the in-flight VL of earlier simulations
+)
+
+
 class NpTree:
-    def __init__(self, cap: int, c_puct: float, vl: float):
+    def __init__(self, cap: int, c_puct: float, vl: float, variant: str | None = None):
+        if variant is not None and variant not in SELECT_VARIANTS:
+            raise ValueError(f"unknown selection variant {variant!r}")
+        self.variant = variant
+        self.inflight = np.zeros(cap, np.int32)  # simulations of the current wave per node
         self.cap = cap
         self.c = F(c_puct)
         self.vlf = F(vl)
@@ -75,28 +93,47 @@ class NpTree:
         f, k = int(self.first[p]), int(self.nchild[p])
         if k == 0 or f < 0 or Np == 0:
             return -1
-        s = F(math.sqrt(float(F(Np))))
+        var = self.variant
+        s = F(math.sqrt(float(F(Np + 1 if var == "sqrt_np_plus1" else Np))))
         best, arg = F(-1e9), -1
         for i in range(k):
             ch = int(self.children[f + i])
             n = int(self.N[ch])
-            if n == 0:
+            if var == "children_no_vl":
+                n -= self.vli * int(self.inflight[ch])
+            if n == 0 and var != "no_unvisited_rule":
                 return ch
-            q = F(self.W[ch] / F(F(n) + self.vlf))
-            u = F(F(F(self.c * self.P[ch]) * s) / F(1 + n))
+            if var == "q_no_vl":
+                q = F(self.W[ch] / F(n)) if n > 0 else F(0.0)
+            elif var == "no_unvisited_rule" and n == 0:
+                q = F(0.0)
+            else:
+                q = F(self.W[ch] / F(F(n) + self.vlf))
+            if var == "c_times_ps":
+                num = F(self.c * F(self.P[ch] * s))
+            else:
+                num = F(F(self.c * self.P[ch]) * s)
+            u = F(num / F(n if (var == "denominator_n" and n > 0) else 1 + n))
             sc = F(q + u)
-            if sc > best:
+            if sc > best or (var == "ties_highest" and sc == best):
                 best, arg = sc, ch
         return arg
 
     def select_path(self, max_depth: int):
         path, cur = [], 0
+        late = self.variant == "np_without_arrival"
         while True:
             path.append(cur)
-            self.N[cur] += self.vli
+            self.inflight[cur] += 1
+            if not late:
+                self.N[cur] += self.vli
             if not self.expanded[cur] or self.nchild[cur] == 0 or len(path) == max_depth:
+                if late:
+                    self.N[cur] += self.vli
                 return path
             c = self.best_child(cur)
+            if late:
+                self.N[cur] += self.vli
             if c < 0:
                 return path
             cur = c
@@ -165,14 +202,32 @@ class NpTree:
         v = F(v)
         for d, x in enumerate(path):
             e = d if root_positive else L - 1 - d
+            self.inflight[x] -= 1
             self.N[x] = self.N[x] - self.vli + 1
             self.W[x] = F(self.W[x] + (-v if e & 1 else v))
 
 
-def choose_children(legal, pol_row, is_root, policy, root_visits, noise=None, eps=0.0):
+# Planted misreadings of the reference's progressive widening (optimized_wave_search.py:394-415
+# and MAX_CHILDREN = 8 of cython_tree_optimized.pyx:31,239), used only by the tests that show
+# the widening checks fail on each of them.  None is the rule.
+PW_VARIANTS = (
+    "no_plus1",      # int(10 * sqrt(N0)) without the + 1
+    "no_floor5",     # without max(5, .)
+    "no_cap15",      # without min(., 15)
+    "no_cap8",       # the root row not cut to MAX_CHILDREN = 8
+    "top8_by_prior", # the root's children: the 8 best priors instead of the 8 lowest actions
+    "nonroot_top5",  # non-root rows of 5 instead of 3
+)
+
+
+def choose_children(legal, pol_row, is_root, policy, root_visits, noise=None, eps=0.0,
+                    pw_variant=None):
     """Expansion of one leaf (optimized_wave_search.py:377-415): legal priors renormalised by
     their canonical sum, Dirichlet at the root, 'full' or progressive widening; returns
-    (actions, priors) in ascending action order."""
+    (actions, priors) in ascending action order.  pw_variant plants a misreading of
+    PW_VARIANTS."""
+    if pw_variant is not None and pw_variant not in PW_VARIANTS:
+        raise ValueError(f"unknown widening variant {pw_variant!r}")
     legal = list(legal)
     n = len(legal)
     pf = [F(pol_row[a]) for a in legal]
@@ -185,10 +240,12 @@ def choose_children(legal, pol_row, is_root, policy, root_visits, noise=None, ep
     k = n
     if policy == "reference_pw":
         if is_root:
-            m1 = min(n, int(10.0 * math.sqrt(float(root_visits))) + 1)
-            sel = max(5, min(m1, 15))
+            plus = 0 if pw_variant == "no_plus1" else 1
+            m1 = min(n, int(10.0 * math.sqrt(float(root_visits))) + plus)
+            sel = m1 if pw_variant == "no_cap15" else min(m1, 15)
+            sel = sel if pw_variant == "no_floor5" else max(5, sel)
         else:
-            sel = 3
+            sel = 5 if pw_variant == "nonroot_top5" else 3
         if n > sel:
             order = sorted(range(n), key=lambda i: (-pd[i], i))[:sel]
             chosen = sorted(order)
@@ -200,7 +257,9 @@ def choose_children(legal, pol_row, is_root, policy, root_visits, noise=None, ep
                 Sf = sum64([F(pd[i]) for i in chosen])
                 for i in chosen:
                     pd[i] = float(F(F(pd[i]) / Sf))
-        k = min(len(chosen), 8) if is_root else len(chosen)
+        k = min(len(chosen), 8) if is_root and pw_variant != "no_cap8" else len(chosen)
+        if is_root and pw_variant == "top8_by_prior":
+            chosen = sorted(sorted(chosen, key=lambda i: (-pd[i], i))[:k])
     chosen = chosen[:k]
     return [legal[i] for i in chosen], [F(pd[i]) for i in chosen]
 

@@ -74,9 +74,17 @@ def test_second_search_continues_tree(device):
 
 
 def test_zero_simulations_and_shape_check(device):
-    m = MCTS(_config(), SyntheticEvaluator())
-    pol = m.search(_board(), num_simulations=0)
-    assert np.allclose(pol, 1.0 / 225)
+    # num_simulations=0 runs the configured count (mcts.py:940 `num_simulations or
+    # config.num_simulations`); a configured count of 0 gives the uniform policy
+    board = _board()
+    m = MCTS(_config(num_simulations=64), SyntheticEvaluator())
+    pol = m.search(board, num_simulations=0)
+    assert int(m.engine.N[0].item()) == 2 + 64
+    orc = _oracle_for(_config(num_simulations=64), board[None])
+    orc.search(64, 32)
+    assert np.array_equal(pol, orc.root_policy(0))
+    m0 = MCTS(_config(num_simulations=0), SyntheticEvaluator())
+    assert np.allclose(m0.search(board), 1.0 / 225)
     with pytest.raises(ValueError):
         m.search(np.zeros((9, 9), np.int8))
 
@@ -185,3 +193,72 @@ def test_feature_evaluator_replay_parity(device):
         orc.wave(0, W, replay_policy=p[:32], replay_values=v[:32])
     assert np.array_equal(pol, orc.root_policy(0))
     _assert_tree_equal(m, orc)
+
+
+class _StubState:
+    """A game-state object with the reference's interface (the C++ game state's Python
+    surface): get_basic_tensor_representation (18 planes), get_tensor_representation (3
+    planes: the mover's stones, the opponent's, the colour to play), get_current_player,
+    get_move_history."""
+
+    def __init__(self, board, player, history):
+        self.board, self.player, self.history = np.asarray(board, np.int8), player, history
+
+    def get_tensor_representation(self):
+        b = self.board
+        return np.stack([(b == self.player), (b == 3 - self.player),
+                         np.full(b.shape, self.player == 1)]).astype(np.float32)
+
+    def get_basic_tensor_representation(self):
+        t = np.zeros((18,) + self.board.shape, np.float32)
+        t[0] = self.board != 0
+        t[1] = self.player == 1
+        return t
+
+    def get_current_player(self):
+        return self.player
+
+    def get_move_history(self):
+        return list(self.history)
+
+
+def test_state_object_roots_match_oracle(device):
+    """search() takes the reference's game-state objects (mcts.py:1520-1600): the board comes
+    from the 3-channel form mapped by the player to move, who plays the first path move."""
+    cfg = _config(num_simulations=512)
+    board = _board(stones=21)  # odd stone count: parity would give player 2 ...
+    state = _StubState(board, 1, history=list(range(21)))  # ... the state says player 1
+    m = MCTS(cfg, SyntheticEvaluator())
+    pol = m.search(state)
+    orc = _oracle_for(cfg, board[None])
+    orc.set_gomoku_rules(board[None], 0, root_player=np.array([1], np.int32))
+    orc.search(512, 32)
+    assert np.array_equal(pol, orc.root_policy(0))
+    _assert_tree_equal(m, orc)
+    # a game interface's state_to_numpy is used when there is one
+    class _Iface:
+        calls = 0
+
+        def state_to_numpy(self, s, representation_type=None):
+            _Iface.calls += 1
+            if representation_type == "minimal":
+                return s.get_tensor_representation()
+            return s.get_basic_tensor_representation()
+
+    m2 = MCTS(cfg, SyntheticEvaluator(), game_interface=_Iface())
+    pol2 = m2.search(state)
+    assert _Iface.calls == 2 and np.array_equal(pol2, pol)
+    # the same root twice continues the tree; update_root with a state object keeps the
+    # played child's subtree, and the state's player moves next
+    m.search(state)
+    assert int(m.engine.N[0].item()) == 2 + 1024
+    nb = board.copy()
+    a = int(np.argmax(pol))
+    nb.reshape(-1)[a] = 1
+    tr = m.engine.host_tree(0)
+    kids = np.arange(tr["first"][0] + 1, tr["first"][0] + 1 + tr["nchild"][0])
+    n_child = int(tr["N"][kids[tr["action"][kids] == a][0]])
+    m.update_root(a, _StubState(nb, 2, history=list(range(22))))
+    assert m.stats["tree_reuse_count"] == 1
+    assert int(m.engine.N[0].item()) == n_child
+    assert list(m._root_players_host) == [2] and list(m._root_moves_host) == [22]

@@ -8,6 +8,7 @@ import torch
 
 from omoknuni_quantum_amd import _lib
 from omoknuni_quantum_amd.core.engine import SearchParams, WaveEngine
+from omoknuni_quantum_amd.synthetic import games
 from oracle import golden
 
 pytestmark = pytest.mark.gpu
@@ -106,3 +107,39 @@ def test_search_trees(device, case):
             assert np.array_equal(tr[key], g(key)), key
         for key in ("W", "P"):
             assert np.array_equal(tr[key].view(np.int32), g(key).view(np.int32)), key
+
+
+def test_reference_pw_rule(device):
+    """The device expansion follows the closed form of the reference's progressive widening
+    over the grid of root visit counts and legal-set sizes (oracle/golden.py pw_root_count),
+    for the root row and for the row of the root's first child."""
+    fails = []
+    for n0 in golden.PW_GRID_N0:
+        for L in golden.PW_GRID_L:
+            seed = 1000 + L
+            model, board, legal, acts, pol = golden.pw_inputs(L, seed)
+            eng = WaveEngine(model, 1, 128, 1, 100, device,
+                             SearchParams(c_puct=1.4, virtual_loss=3.0,
+                                          expand_policy=_lib.OMQ_EXPAND_REFERENCE_PW))
+            eng.set_roots(games.root_keys(seed, 1), legal)
+            eng.reset()
+            _put(eng.N, [n0], np.int32)
+            ev = _Replay(np.stack([pol[None], pol[None]]), np.zeros((2, 1), np.float32))
+            eng.run_wave(1, ev)
+            tr = eng.host_tree(0)
+            f0, k0 = int(tr["first"][0]), int(tr["nchild"][0])
+            root = [int(a) for a in tr["action"][f0 + 1:f0 + 1 + k0]]
+            want = golden.pw_expected(acts, pol, n0)
+            if root != want:
+                fails.append(f"N0={n0} L={L}: root row {root}, rule {want}")
+                continue
+            eng.run_wave(1, ev)
+            tr = eng.host_tree(0)
+            c0 = f0 + 1
+            f, k = int(tr["first"][c0]), int(tr["nchild"][c0])
+            child = [int(a) for a in tr["action"][f + 1:f + 1 + k]] if k > 0 else []
+            rest = [a for a in acts if a != root[0]]
+            want_c = golden.pw_expected(rest, pol, None) if rest else []
+            if child != want_c:
+                fails.append(f"N0={n0} L={L}: first child's row {child}, rule {want_c}")
+    assert not fails, "\n".join(fails[:10])

@@ -38,6 +38,11 @@ def test_fused_ucb_matches_restatement(device, seed):
                                             t(visits), t(priors), 1.4)
     torch.cuda.synchronize()
     assert np.array_equal(got.cpu().numpy(), exp)
+    # the reference's own operator name (torch_custom_ops.py:108), where AsyncWaveSearch looks
+    got2 = torch.ops.mcts.fused_ucb_selection(t(nodes), t(starts), t(ends), t(children), t(q),
+                                              t(visits), t(priors), 1.4)
+    torch.cuda.synchronize()
+    assert np.array_equal(got2.cpu().numpy(), exp)
 
 
 def test_warp_vectorized_backup_equals_vectorized_backup(device):
@@ -51,5 +56,11 @@ def test_warp_vectorized_backup_equals_vectorized_backup(device):
     n2, w2 = n1.clone(), w1.clone()
     torch.ops.omq.vectorized_backup(t(paths), t(plen), t(vals), n1, w1)
     torch.ops.omq.warp_vectorized_backup(t(paths), t(plen), t(vals), n2, w2)
+    n3, w3 = torch.zeros_like(n1), torch.zeros_like(w1)
+    n4, w4 = torch.zeros_like(n1), torch.zeros_like(w1)
+    torch.ops.mcts.vectorized_backup(t(paths), t(plen), t(vals), n3, w3)
+    torch.ops.mcts.warp_vectorized_backup(t(paths), t(plen), t(vals), n4, w4)
     torch.cuda.synchronize()
     assert torch.equal(n1, n2) and torch.equal(w1, w2)
+    assert torch.equal(n1, n3) and torch.equal(w1, w3)
+    assert torch.equal(n1, n4) and torch.equal(w1, w4)

@@ -161,3 +161,17 @@ def test_primitives_need_only_counts():
     assert lib.omq_virtual_loss(ctypes.byref(f), None, None, 0, 1, None) == _lib.OMQ_OK
     assert lib.omq_paths_backup(ctypes.byref(f), None, None, None, None, 1, 4, 0, None) == _lib.OMQ_E_ARG
     assert "null" in lib.omq_last_error().decode()
+
+
+def test_reference_operator_names_registered():
+    """torch.ops.mcts carries the reference's three operators (torch_custom_ops.py:26,71,108),
+    as AsyncWaveSearch probes for them (async_wave_search.py:255-260), beside torch.ops.omq."""
+    import torch
+
+    from omoknuni_quantum_amd import torch_ops
+
+    for name in ("vectorized_backup", "warp_vectorized_backup", "fused_ucb_selection"):
+        assert hasattr(torch.ops.mcts, name), name
+        assert hasattr(torch.ops.omq, name), name
+    assert {"omq::batch_apply_virtual_loss", "omq::batch_remove_virtual_loss"} <= set(
+        torch_ops.REGISTERED)
