@@ -50,8 +50,10 @@ def _input_planes(evaluator) -> int:
 
 
 class _BatchEvaluatorAdapter:
-    """Runs a reference-protocol evaluator on the device-built features of the unique leaves
-    and writes its outputs into the engine's policy/value rows."""
+    """Runs a reference-protocol evaluator on the device-built features of the wave's unique
+    leaves and writes its outputs into the engine's policy/value rows.  As in the reference
+    driver (optimized_wave_search.py:312-365), the evaluator sees one row per leaf to evaluate:
+    the unique leaves of tree 0, then of tree 1, and so on (no padding slots)."""
 
     def __init__(self, evaluator, builder):
         self.evaluator = evaluator
@@ -59,11 +61,30 @@ class _BatchEvaluatorAdapter:
 
     def evaluate_wave(self, engine) -> None:
         feats = self.builder.build()
+        counts = engine.ucount.cpu()  # the leaf counts decide the batch (one small copy)
+        MW = engine.MW
+        if engine.T == 1:
+            idx = None
+            feats = feats[:int(counts[0])]
+        else:
+            idx = torch.cat([torch.arange(int(c), dtype=torch.int64) + t * MW
+                             for t, c in enumerate(counts.tolist())]).to(engine.device)
+            feats = feats.index_select(0, idx)
+        if feats.shape[0] == 0:
+            return
         pol, val = self.evaluator.evaluate_batch(feats)
-        pol = torch.as_tensor(pol, device=engine.device, dtype=torch.float32)
+        pol = torch.as_tensor(pol, device=engine.device, dtype=torch.float32).reshape(-1, engine.A)
         val = torch.as_tensor(val, device=engine.device, dtype=torch.float32).reshape(-1)
-        engine.policy.view(-1, engine.A).copy_(pol.view(-1, engine.A))
-        engine.values.copy_(val)
+        if pol.shape[0] != feats.shape[0] or val.shape[0] != feats.shape[0]:
+            raise ValueError(f"evaluate_batch returned {pol.shape[0]} policies and "
+                             f"{val.shape[0]} values for {feats.shape[0]} positions")
+        rows = engine.policy.view(-1, engine.A)
+        if idx is None:
+            rows[:pol.shape[0]].copy_(pol)
+            engine.values[:val.shape[0]].copy_(val)
+        else:
+            rows.index_copy_(0, idx, pol)
+            engine.values.index_copy_(0, idx, val)
 
 
 class MCTS:

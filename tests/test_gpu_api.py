@@ -181,16 +181,21 @@ def test_feature_evaluator_replay_parity(device):
     m = MCTS(cfg, ev)
     pol = m.search(board)
     assert len(ev.calls) == 1 + 160 // 32
-    # reference 'basic' planes; the root wave's one leaf is the root position itself
-    assert ev.feats[0].shape[1:] == (19, 15, 15)
+    # reference 'basic' planes; the root wave's one leaf is the root position itself, and
+    # every call holds exactly the wave's unique leaves
+    assert ev.feats[0].shape == (1, 19, 15, 15)
     b, player, count = leaf_position(board, [])
     assert np.array_equal(ev.feats[0][0], nn_features(b, player, count, 19))
-    assert not ev.feats[0][1:].any()
+    assert all(1 <= f.shape[0] <= 32 for f in ev.feats[1:])
     orc = _oracle_for(cfg, board[None])
     orc.reset_tree(0)
     sizes = [1] + [32] * 5
     for (p, v), W in zip(ev.calls, sizes):
-        orc.wave(0, W, replay_policy=p[:32], replay_values=v[:32])
+        assert p.shape[0] == v.shape[0] <= W
+        rp = np.zeros((W, 225), np.float32)
+        rv = np.zeros(W, np.float32)
+        rp[:p.shape[0]], rv[:v.shape[0]] = p, v
+        orc.wave(0, W, replay_policy=rp, replay_values=rv)
     assert np.array_equal(pol, orc.root_policy(0))
     _assert_tree_equal(m, orc)
 
@@ -262,3 +267,31 @@ def test_state_object_roots_match_oracle(device):
     assert m.stats["tree_reuse_count"] == 1
     assert int(m.engine.N[0].item()) == n_child
     assert list(m._root_players_host) == [2] and list(m._root_moves_host) == [22]
+
+
+def test_feature_evaluator_batch_replay_parity(device):
+    """search_batch with a reference-protocol evaluator: each call holds the unique leaves of
+    tree 0, then tree 1, ...; replayed into the oracle tree by tree, the trees are bit-equal."""
+    cfg = _config(num_trees=3, num_simulations=96, max_wave_size=32)
+    boards = games.random_boards(3, 15, 30, seed=4)
+    ev = _RecordingEvaluator(seed=3)
+    m = MCTS(cfg, ev)
+    pol = m.search_batch(boards)
+    orc = _oracle_for(cfg, boards)
+    sizes = [1] + [32] * 3
+    assert len(ev.calls) == len(sizes)
+    for t in range(3):
+        orc.reset_tree(t)
+    for (p, v), W in zip(ev.calls, sizes):
+        off = 0
+        for t in range(3):
+            rp = np.zeros((W, 225), np.float32)
+            rv = np.zeros(W, np.float32)
+            n = min(W, p.shape[0] - off)
+            rp[:n], rv[:n] = p[off:off + n], v[off:off + n]
+            orc.wave(t, W, replay_policy=rp, replay_values=rv)
+            off += int(orc.last_wave(t, W)["ucount"])
+        assert off == p.shape[0]
+    for t in range(3):
+        assert np.array_equal(pol[t], orc.root_policy(t))
+        _assert_tree_equal(m, orc, t)
