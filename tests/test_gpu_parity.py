@@ -40,7 +40,14 @@ CASES = {
     # a negative c_puct: every step is compared exactly (no fast path)
     "negative-cpuct": ("C2", {"num_trees": 2, "num_simulations": 512, "wave_size": 256,
                               "capacity": 100_000, "c_puct": -0.5}),
+    # full simulation counts and capacities of C3 and C4 on two trees: contender windows deep
+    # into a search, the 6-slot kernel on a deep tree, C3's capacity-full rule (tens of
+    # thousands of refused expansions per tree) and C4's 2048-simulation waves
+    "C3-fullcount": ("C3", {"num_trees": 2}),
+    "C4-fullcount": ("C4", {"num_trees": 2}),
 }
+# compared after every wave, except the full-count cases (every third wave and the last)
+CHECK_EVERY = {"C3-fullcount": 3, "C4-fullcount": 3}
 
 
 @pytest.mark.gpu
@@ -50,5 +57,5 @@ def test_wave_parity(case, device):
     wl = get(name).scaled(name=case, **kw)
     print(f"[parity] {case}: T={wl.num_trees} sims={wl.num_simulations} W={wl.wave_size}",
           flush=True)
-    n = run_parity(wl, check_every=1, device=device)
+    n = run_parity(wl, check_every=CHECK_EVERY.get(case, 1), device=device)
     assert n >= 2
