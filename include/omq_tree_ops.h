@@ -79,6 +79,9 @@ extern "C" {
 
 /* workspace of omq_shift_root: int32 entries per node of capacity, per tree */
 #define OMQ_SHIFT_WORKSPACE_PER_NODE 8
+/* the library's own workspace of omq_shift_root_noalloc: int32 entries (32 MiB per GPU), so
+   num_trees * capacity * OMQ_SHIFT_WORKSPACE_PER_NODE may be at most this */
+#define OMQ_NOALLOC_SHIFT_INTS (8 * 1024 * 1024)
 
 /* output of omq_leaf_features */
 #define OMQ_DTYPE_F32 0   /* float32 planes */
@@ -277,6 +280,20 @@ int omq_leaf_features(const omq_forest* f, const omq_wave* w, const int8_t* root
  * reuse kernels of mcts_kernels.cu:2095-2337. */
 int omq_shift_root(const omq_forest* f, const int32_t* new_roots, int32_t* workspace,
                    int64_t workspace_ints, void* stream);
+
+/* omq_shift_root without a caller workspace, and without any allocation: the workspace is a
+ * device array of the library (OMQ_NOALLOC_SHIFT_INTS int32, 32 MiB, one per GPU the library
+ * runs on, held until the process ends).  Same semantics and results as omq_shift_root.
+ * - Limit.  num_trees * capacity * OMQ_SHIFT_WORKSPACE_PER_NODE must not exceed
+ *   OMQ_NOALLOC_SHIFT_INTS (num_trees * capacity <= 1,048,576 nodes); larger forests get
+ *   OMQ_E_LIMIT and nothing is launched.
+ * - No allocation.  The entry point calls no hipMalloc, hipFree or allocating library routine;
+ *   its first call on a device looks the array's address up (hipGetSymbolAddress).
+ * - Sharing.  Every call on one GPU uses that GPU's array: calls that overlap on one GPU (two
+ *   streams, two threads) race, and must be ordered by the caller.
+ * No counterpart in the reference: this entry point is for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid allocation). */
+int omq_shift_root_noalloc(const omq_forest* f, const int32_t* new_roots, void* stream);
 
 /* Root visit-count policy of every tree into policy[t*num_actions + a] (double):
  * N(child_a) / (sum of the root's children's N). When the root has no children, the policy

@@ -31,6 +31,7 @@ OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT, OMQ_STATUS_STALL = 1, 2, 4
 OMQ_RULE_FREESTYLE, OMQ_RULE_RENJU = 0, 1
 OMQ_TERM_NONE, OMQ_TERM_WIN1, OMQ_TERM_WIN2, OMQ_TERM_DRAW = 0, 1, 2, 3
 OMQ_SHIFT_WORKSPACE_PER_NODE = 8
+OMQ_NOALLOC_SHIFT_INTS = 8 * 1024 * 1024
 OMQ_DTYPE_F32, OMQ_DTYPE_BF16 = 0, 1
 OMQ_LAYOUT_NCHW, OMQ_LAYOUT_NHWC = 0, 1
 
@@ -74,6 +75,7 @@ SIGNATURES = {
     "omq_virtual_loss": (ctypes.c_int, [_FP, _p, _p, _i32, _i32, _p]),
     "omq_gomoku_terminal": (ctypes.c_int, [_FP, _WP, _p, _p, _i32, _p, _p]),
     "omq_shift_root": (ctypes.c_int, [_FP, _p, _p, ctypes.c_int64, _p]),
+    "omq_shift_root_noalloc": (ctypes.c_int, [_FP, _p, _p]),
     "omq_leaf_features": (ctypes.c_int, [_FP, _WP, _p, _p, _p, _i32, _i32, _i32, _p, _p]),
     "omq_fused_ucb_selection": (ctypes.c_int, [_p, _i32, _p, _p, _p, _p, _p, _p, ctypes.c_float,
                                                _p, _p]),

@@ -27,6 +27,7 @@ hipError_t launch_virtual_loss(const omq_forest& f, const int32_t* nodes, const 
 hipError_t launch_reset(const omq_forest& f, hipStream_t st);
 hipError_t launch_shift_root(const omq_forest& f, const int32_t* new_roots, int32_t* ws,
                              hipStream_t st);
+hipError_t shift_scratch(int32_t** out);
 hipError_t launch_root_policy(const omq_forest& f, double* pol, hipStream_t st);
 hipError_t launch_sample_actions(const omq_forest& f, const double* pol, double temperature,
                                  uint64_t seed, uint64_t counter, int32_t* actions,
@@ -232,6 +233,23 @@ int omq_shift_root(const omq_forest* f, const int32_t* new_roots, int32_t* works
                 (long long)workspace_ints, (long long)need);
   return hip_status(omq::launch_shift_root(*f, new_roots, workspace, (hipStream_t)stream),
                     "omq_shift_root");
+}
+
+int omq_shift_root_noalloc(const omq_forest* f, const int32_t* new_roots, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  if (!new_roots) return fail(OMQ_E_ARG, "new_roots is required");
+  const int64_t need = (int64_t)OMQ_SHIFT_WORKSPACE_PER_NODE * f->num_trees * f->capacity;
+  if (need > (int64_t)OMQ_NOALLOC_SHIFT_INTS)
+    return fail(OMQ_E_LIMIT,
+                "omq_shift_root_noalloc: %d trees x capacity %d needs %lld workspace int32, the "
+                "library's own workspace holds %d (use omq_shift_root with a workspace)",
+                f->num_trees, f->capacity, (long long)need, OMQ_NOALLOC_SHIFT_INTS);
+  int32_t* ws = nullptr;
+  rc = hip_status(omq::shift_scratch(&ws), "omq_shift_root_noalloc (workspace lookup)");
+  if (rc) return rc;
+  return hip_status(omq::launch_shift_root(*f, new_roots, ws, (hipStream_t)stream),
+                    "omq_shift_root_noalloc");
 }
 
 int omq_root_policy(const omq_forest* f, double* policy, void* stream) {

@@ -18,6 +18,8 @@
 // kernels follow: one gathers the kept nodes' fields into a workspace, the other writes them
 // over the front of the tree. The workspace holds eight int32 arrays of `capacity` entries
 // per tree.
+#include <mutex>
+
 #include "omq_common.h"
 
 namespace omq {
@@ -249,6 +251,38 @@ __global__ void shift_write_kernel(omq_forest f, const int32_t* ws) {
     f.num_children[d] = nnch[i];
     f.actions[d] = nA[i];
   }
+}
+
+// ---- the workspace of omq_shift_root_noalloc ----------------------------------------------
+// A file-scope device array, one copy per GPU the library runs on, held until the process
+// ends.  Its address on a device is looked up once per device, with that device current
+// (hipGetSymbolAddress); host code never passes the array's name to a kernel.  Every entry the
+// shift kernels read is written earlier in the same call, so nothing has to start at zero.
+// Calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) int32_t scratch[OMQ_NOALLOC_SHIFT_INTS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// The address of this device's scratch (looked up on the first call on the device).
+hipError_t shift_scratch(int32_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
 }
 
 hipError_t launch_shift_root(const omq_forest& f, const int32_t* new_roots, int32_t* ws,

@@ -175,3 +175,16 @@ def test_reference_operator_names_registered():
         assert hasattr(torch.ops.omq, name), name
     assert {"omq::batch_apply_virtual_loss", "omq::batch_remove_virtual_loss"} <= set(
         torch_ops.REGISTERED)
+
+
+def test_noalloc_shift_root_limit():
+    """omq_shift_root_noalloc refuses forests beyond its own workspace, and a missing
+    new_roots, before anything reaches the device."""
+    lib = _lib.load()
+    cap = _lib.OMQ_NOALLOC_SHIFT_INTS // _lib.OMQ_SHIFT_WORKSPACE_PER_NODE // 2 + 1
+    f = _forest(num_trees=2, capacity=cap)
+    assert lib.omq_shift_root_noalloc(ctypes.byref(f), 8, None) == _lib.OMQ_E_LIMIT
+    msg = lib.omq_last_error().decode()
+    assert "omq_shift_root_noalloc" in msg and str(_lib.OMQ_NOALLOC_SHIFT_INTS) in msg
+    g = _forest(num_trees=2, capacity=cap - 1)
+    assert lib.omq_shift_root_noalloc(ctypes.byref(g), None, None) == _lib.OMQ_E_ARG
