@@ -50,6 +50,8 @@ def algorithmic_bytes(st: dict, sims: int) -> dict:
     }
 
 
+SCHEDULES = {"auto": 0, "whole": 1, "split": 2}
+
 KERNEL_OF_PHASE = {"select": "select_kernel", "leaf_info": "leaf_info_kernel",
                    "expand": "expand_write_kernel", "backup": "backup_groups_kernel"}
 
@@ -83,6 +85,8 @@ def run(args) -> dict:
     if args.trees:
         wl = wl.scaled(num_trees=args.trees)
     dev = torch.device("cuda:0")
+    _lib.check(_lib.load().omq_select_options(SCHEDULES[args.select_schedule],
+                                              _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
     params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth,
                           expand_policy=_lib.OMQ_EXPAND_FULL,
                           w_mode=_lib.OMQ_WACC_ATOMIC if args.w_mode == "atomic" else _lib.OMQ_WACC_ORDERED,
@@ -421,6 +425,9 @@ def main():
     ap.add_argument("--config", default="C2")
     ap.add_argument("--trees", type=int, default=0, help="override the workload's tree count")
     ap.add_argument("--w-mode", choices=("ordered", "atomic"), default="ordered")
+    ap.add_argument("--select-schedule", choices=tuple(SCHEDULES), default="auto",
+                    help="omq_select schedule: by size (auto), one workgroup per tree (whole), "
+                         "or root chains and subtree tasks (split)")
     ap.add_argument("--vl-atomic", action="store_true")
     ap.add_argument("--cpu-baseline", choices=("auto", "skip"), default="auto")
     ap.add_argument("--cpu-trees", type=int, default=0,

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define OMQ_ABI_VERSION 1
+#define OMQ_ABI_VERSION 2
 
 /* error codes */
 #define OMQ_OK 0
@@ -140,7 +140,13 @@ typedef struct omq_wave {
                                (written in atomic mode and for waves of more than 512) */
   int64_t* stats;           /* [T*OMQ_NSTATS] accumulated operation counters */
   int32_t* status;          /* [4] device-side error flags (bit set, never cleared by the library) */
+  int32_t* sel_scratch;     /* [OMQ_SEL_SCRATCH_INTS(T, max_wave)] omq_select's scratch: per-
+                               simulation leaf records and the subtree tasks of its split
+                               schedule (no contents to keep between calls) */
 } omq_wave;
+
+/* int32 entries of omq_wave::sel_scratch for T trees of max_wave simulations */
+#define OMQ_SEL_SCRATCH_INTS(T, MW) (4 * (int64_t)(T) * (MW) + 10 * (int64_t)(T) + 16)
 
 /* stats counters (per tree, accumulated over waves) */
 #define OMQ_ST_INTERNAL 0     /* groups that selected a child (distinct internal nodes per wave) */
@@ -181,6 +187,17 @@ int omq_forest_reset(const omq_forest* f, void* stream);
  * batch_apply_virtual_loss (python/mcts/gpu/mcts_kernels.cu:451-643,845-860,962-1053). */
 int omq_select(const omq_forest* f, const omq_wave* w, int32_t wave_size, float c_puct,
                float virtual_loss, int32_t max_depth, int32_t vl_atomic, void* stream);
+
+/* Process-wide options of omq_select, for tests and tuning; no counterpart in the reference.
+ * - split_mode.  0 (default) and 1 run each tree's whole wave in one workgroup.  2 takes the
+ *   split schedule (forests of at most 128 trees): the root chains in one workgroup per tree,
+ *   then the subtrees below them as tasks spread over the whole chip, then the unique-leaf
+ *   pass.  Both schedules give the same results; the split one measured slower.
+ * - spin_limit.  Bound of the polls of a wait inside omq_select (default 2^22, at least 0).
+ *   Running out sets OMQ_STATUS_STALL, and the simulations it held up end their paths early;
+ *   the trees must then be reset.
+ * Returns OMQ_E_ARG for an unknown mode or a negative limit. */
+int omq_select_options(int32_t split_mode, int32_t spin_limit);
 
 /* Compute the hash key and the number of legal actions of every unique leaf of the wave.
  * (Game-model step between selection and evaluation; no reference counterpart in the

@@ -13,7 +13,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libomq_tree_ops.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # constants of include/omq_tree_ops.h
 OMQ_OK, OMQ_E_ARG, OMQ_E_LAUNCH, OMQ_E_LIMIT = 0, -1, -2, -3
@@ -55,8 +55,16 @@ class OmqWave(ctypes.Structure):
         ("paths", _p), ("path_len", _p), ("leaves", _p), ("sim_uid", _p), ("uleaf", _p),
         ("ufirst", _p), ("ucount", _p), ("glog", _p), ("gcount", _p), ("gmembers", _p),
         ("ukey", _p), ("ulegal", _p), ("uedge", _p), ("unew", _p), ("policy", _p),
-        ("values", _p), ("sim_value", _p), ("stats", _p), ("status", _p),
+        ("values", _p), ("sim_value", _p), ("stats", _p), ("status", _p), ("sel_scratch", _p),
     ]
+
+
+def sel_scratch_ints(T: int, MW: int) -> int:
+    """OMQ_SEL_SCRATCH_INTS of include/omq_tree_ops.h."""
+    return 4 * T * MW + 10 * T + 16
+
+
+OMQ_SPIN_LIMIT_DEFAULT = 1 << 22
 
 
 # exported symbols and their signatures (name -> (restype, argtypes))
@@ -68,6 +76,7 @@ SIGNATURES = {
     "omq_forest_reset": (ctypes.c_int, [_FP, _p]),
     "omq_select": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, ctypes.c_float, _i32, _i32, _p]),
     "omq_leaf_info": (ctypes.c_int, [_FP, _WP, _p]),
+    "omq_select_options": (ctypes.c_int, [_i32, _i32]),
     "omq_synthetic_evaluate": (ctypes.c_int, [_FP, _WP, ctypes.c_float, _p]),
     "omq_expand": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _p, ctypes.c_double, _p]),
     "omq_backup": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _i32, _p]),

@@ -93,6 +93,7 @@ class WaveEngine:
         self.sim_value = z(T * MW, f32)
         self.stats = z(T * _lib.OMQ_NSTATS, i64)
         self.status = z(4, i32)
+        self.sel_scratch = z(_lib.sel_scratch_ints(T, MW), i32)
         self.noise = z(T * A, torch.float64)
         self.has_noise = False
         # Gomoku rules (terminal leaves are not expanded), off until set_gomoku_rules
@@ -117,7 +118,7 @@ class WaveEngine:
         w.max_wave, w.max_depth = MW, MD
         for name in ("paths", "path_len", "leaves", "sim_uid", "uleaf", "ufirst", "ucount",
                      "glog", "gcount", "gmembers", "ukey", "ulegal", "uedge", "unew", "policy",
-                     "values", "sim_value", "stats", "status"):
+                     "values", "sim_value", "stats", "status", "sel_scratch"):
             setattr(w, name, getattr(self, name).data_ptr())
         self.forest = f
         self.wave = w

@@ -12,6 +12,7 @@ namespace omq {
 size_t select_lds_bytes(int W);
 hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_puct,
                          float virtual_loss, int max_depth, int vl_atomic, hipStream_t stream);
+void select_set_options(int split_mode, int spin_limit);
 hipError_t launch_leaf_info(const omq_forest& f, const omq_wave& w, int W, hipStream_t st);
 hipError_t launch_synth_eval(const omq_forest& f, const omq_wave& w, int W, float scale,
                              hipStream_t st);
@@ -119,7 +120,7 @@ int check_wave(const omq_forest* f, const omq_wave* w, int wave_size) {
   if (!w->paths || !w->path_len || !w->leaves || !w->sim_uid || !w->uleaf || !w->ufirst ||
       !w->ucount || !w->glog || !w->gcount || !w->gmembers || !w->ukey || !w->ulegal ||
       !w->uedge || !w->unew || !w->policy || !w->values || !w->sim_value || !w->stats ||
-      !w->status)
+      !w->status || !w->sel_scratch)
     return fail(OMQ_E_ARG, "wave buffers have a null array");
   (void)f;
   return OMQ_OK;
@@ -160,6 +161,15 @@ int omq_select(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
   return hip_status(omq::launch_select(*f, *w, wave_size, c_puct, virtual_loss, max_depth,
                                        vl_atomic ? 1 : 0, (hipStream_t)stream),
                     "omq_select");
+}
+
+int omq_select_options(int32_t split_mode, int32_t spin_limit) {
+  if (split_mode < 0 || split_mode > 2)
+    return fail(OMQ_E_ARG, "split_mode %d is not 0 (automatic), 1 (whole) or 2 (split)",
+                split_mode);
+  if (spin_limit < 0) return fail(OMQ_E_ARG, "spin_limit %d < 0", spin_limit);
+  omq::select_set_options(split_mode, spin_limit);
+  return OMQ_OK;
 }
 
 int omq_leaf_info(const omq_forest* f, const omq_wave* w, void* stream) {

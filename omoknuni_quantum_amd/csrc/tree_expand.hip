@@ -213,28 +213,60 @@ __global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f,
       run += k;
     }
     if (tid == 0) s_total = total;
-  } else if (tid == 0) {
-    // capacity boundary: sequential first-fit in leaf order (expand_node refuses a leaf whose
-    // children do not fit; later, smaller leaves may still fit)
-    int cur = base;
-    for (int i = 0; i < U; ++i) {
-      const int k = want[i];
-      if (k > 0 && (int64_t)cur + k <= (int64_t)f.capacity) {
-        w.uedge[wb + i] = cur - 1;
-        w.unew[wb + i] = k;
-        const int leaf = w.uleaf[wb + i];
-        f.first_child[tb + leaf] = cur - 1;
-        f.num_children[tb + leaf] = k;
-        s_exp += 1;
-        s_new += (unsigned long long)k;
-        cur += k;
-      } else {
-        w.uedge[wb + i] = -1;
-        w.unew[wb + i] = 0;
-        if (k > 0) s_fail += 1;
+  } else if (tid < kWave) {
+    // Capacity boundary: first-fit in leaf order (expand_node refuses a leaf whose children do
+    // not fit; later, smaller leaves may still fit), decided by one wave, 64 leaves at a time.
+    // Leaf i fits when cur_i + k_i <= capacity, cur_i = base + the children of the leaves
+    // before it that fit.  Within a chunk each round first drops the leaves that cannot fit
+    // even now (cur only grows, so they never will), then lets every remaining leaf fit up to
+    // the first one whose running sum overflows; that one is dropped by the next round.  Each
+    // round settles at least one leaf.
+    const int lane = tid;
+    const int64_t cap = f.capacity;
+    int64_t cur = base;
+    unsigned long long n_exp = 0, n_new = 0, n_fail = 0;
+    for (int c0 = 0; c0 < U; c0 += kWave) {
+      const int i = c0 + lane;
+      const int k = i < U ? want[i] : 0;
+      bool pend = k > 0;
+      bool fits = false;
+      int64_t at = -1;  // node id of the first child, when the leaf fits
+      for (int round = 0; round <= kWave && __ballot(pend) != 0; ++round) {
+        pend = pend && !(cur + k > cap);
+        int tot;
+        const int ex = wave_excl_scan(pend ? k : 0, &tot);
+        const uint64_t over = __ballot(pend && cur + ex + k > cap);
+        const int f0 = over != 0 ? lowest_lane(over) : kWave;
+        if (pend && lane < f0) {
+          fits = true;
+          at = cur + ex;
+          pend = false;
+        }
+        // the children of the leaves that fit this round: those before f0 (all when f0 = 64)
+        cur += f0 < kWave ? readlane_i(ex, f0) : tot;
       }
+      if (i < U) {
+        if (fits) {
+          w.uedge[wb + i] = (int)at - 1;
+          w.unew[wb + i] = k;
+          const int leaf = w.uleaf[wb + i];
+          f.first_child[tb + leaf] = (int)at - 1;
+          f.num_children[tb + leaf] = k;
+        } else {
+          w.uedge[wb + i] = -1;
+          w.unew[wb + i] = 0;
+        }
+      }
+      n_exp += __popcll(__ballot(fits));
+      n_new += (unsigned long long)wave_sum_i(fits ? k : 0);
+      n_fail += __popcll(__ballot(k > 0 && !fits));
     }
-    s_total = cur - base;
+    if (lane == 0) {
+      s_exp = n_exp;
+      s_new = n_new;
+      s_fail = n_fail;
+      s_total = (int)(cur - base);
+    }
   }
   __syncthreads();
   if (tid == 0) {

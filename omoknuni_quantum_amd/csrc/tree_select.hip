@@ -30,20 +30,16 @@
 
 namespace omq {
 
-#ifndef OMQ_SEL_THREADS
-#define OMQ_SEL_THREADS 1024
-#endif
-constexpr int kSelThreads = OMQ_SEL_THREADS;
-constexpr int kSelWaves = kSelThreads / kWave;
 constexpr uint32_t kNoChild = 0xFFFFFFFFu;
 
 struct SelCfg {
-  int W;          // simulations per tree in this wave
+  int W;           // simulations per tree in this wave
   float c_puct;
-  float vlf;      // virtual loss as float
-  int vli;        // (int)virtual loss
-  int max_depth;  // forced leaf at depth max_depth-1
+  float vlf;       // virtual loss as float
+  int vli;         // (int)virtual loss
+  int max_depth;   // forced leaf at depth max_depth-1
   int vl_atomic;
+  int spin_limit;  // polls of a follower's bounded wait for the root chain
 };
 
 // The arrays the selection touches (a compact kernel argument block: passing both full
@@ -69,6 +65,15 @@ struct SelArgs {
   int capacity;
   int max_wave;
   int max_depth_buf;
+  int num_trees;
+  // selection scratch (omq_wave::sel_scratch)
+  int32_t* lflag;  // [T*max_wave] 1 for the first simulation of a leaf group
+  int32_t* lfs;    // [T*max_wave] first simulation of a simulation's leaf group
+  int32_t* tasks;  // [T*max_wave*2] subtree tasks: node, seg | members << 16
+  int32_t* ntask;  // [T] subtree tasks of a tree
+  int32_t* tinfo;  // [T] level of a tree's tasks, + 256 when its virtual loss is applied
+  int32_t* tcls;   // [T*8] tasks per size class
+  int32_t* ctl;    // [16] the subtree kernel's task counter
 };
 
 // Max of a uint32 over the 64 lanes, made uniform: DPP row shifts 1,2,4,8 (each a single
@@ -813,10 +818,13 @@ __device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, in
   return run_chain<(RMAX >= 8 ? 8 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
 }
 
-// Block-wide exclusive scan of a[0..n) in place (n <= 4 * kSelThreads); returns the total.
+// Block-wide exclusive scan of a[0..n) in place (n <= 4 * NT); returns the total.  a may be
+// LDS or global memory (each thread touches its own chunk only).
+template <int NT>
 __device__ int block_excl_scan(int32_t* a, int n, int* s_wtot) {
+  constexpr int NW = NT / kWave;
   const int tid = threadIdx.x;
-  const int per = (n + kSelThreads - 1) / kSelThreads;
+  const int per = (n + NT - 1) / NT;
   const int lo = tid * per;
   const int hi = min(lo + per, n);
   int sum = 0;
@@ -827,7 +835,7 @@ __device__ int block_excl_scan(int32_t* a, int n, int* s_wtot) {
   if (lane_id() == 0) s_wtot[wave] = wtotal;
   __syncthreads();
   int wbase = 0, total = 0;
-  for (int i = 0; i < kSelWaves; ++i) {
+  for (int i = 0; i < NW; ++i) {
     const int v = s_wtot[i];
     if (i < wave) wbase += v;
     total += v;
@@ -842,6 +850,80 @@ __device__ int block_excl_scan(int32_t* a, int n, int* s_wtot) {
   return total;
 }
 
+// ---- State of the level loop -----------------------------------------------------------
+// Dynamic LDS (sized for W, the simulations of the wave; a group's members occupy a segment
+// [seg, seg + m) of [0, W) at every level, so the arrays are indexed by absolute positions):
+//   cscr_all [NW * 64] float4   contender window scratch, per wave
+//   choice   [W]       uint32   chain output per member position
+//   gnode    [2W]      uint32   group node, per level parity
+//   gsl      [2W]      uint32   group seg | len << 16, per level parity
+//   buf      [2W]      uint16   members by position, per level parity
+//   cnt_all  [NW * OMQ_MAX_ROW] uint16   child pick counts of each wave's chain
+//   pipe_ch  [NW * 64] uint32   (level overlap) the followers' chain output
+//   pick2    [W]       uint16   (level overlap) level-1 picks recorded by the followers
+struct LevelLds {
+  float4* cscr_all;
+  uint32_t* choice;
+  uint32_t* gnode;
+  uint32_t* gsl;
+  uint16_t* buf;
+  uint16_t* cnt_all;
+  uint32_t* pipe_ch;
+  uint16_t* pick2;
+};
+
+template <int NT>
+__host__ __device__ inline size_t level_base_bytes(int W) {
+  // cscr_all, then 24 B per simulation (choice 4, gnode 8, gsl 8, buf 4), then cnt_all
+  return (size_t)(NT / kWave) * kWave * 16 + (size_t)W * 24 +
+         (size_t)(NT / kWave) * OMQ_MAX_ROW * 2;
+}
+template <int NT>
+__host__ __device__ inline size_t level_pipe_offset(int W) {
+  return (level_base_bytes<NT>(W) + 15) & ~(size_t)15;
+}
+constexpr int kPipeMaxW = 2048;  // waves with LDS for the overlap buffers
+template <int NT>
+__host__ __device__ inline size_t level_lds_bytes(int W, bool with_pipe) {
+  if (!with_pipe || W > kPipeMaxW) return level_base_bytes<NT>(W);
+  return level_pipe_offset<NT>(W) + (size_t)(NT / kWave) * kWave * 4 + (size_t)W * 2;
+}
+
+template <int NT>
+__device__ inline LevelLds carve_level_lds(unsigned char* smem, int W, bool with_pipe) {
+  constexpr int NW = NT / kWave;
+  LevelLds L;
+  L.cscr_all = reinterpret_cast<float4*>(smem);
+  L.choice = reinterpret_cast<uint32_t*>(L.cscr_all + NW * kWave);
+  L.gnode = L.choice + W;
+  L.gsl = L.gnode + 2 * W;
+  L.buf = reinterpret_cast<uint16_t*>(L.gsl + 2 * W);
+  L.cnt_all = L.buf + 2 * W;
+  L.pipe_ch = nullptr;
+  L.pick2 = nullptr;
+  if (with_pipe && W <= kPipeMaxW) {
+    L.pipe_ch = reinterpret_cast<uint32_t*>(smem + level_pipe_offset<NT>(W));
+    L.pick2 = reinterpret_cast<uint16_t*>(L.pipe_ch + NW * kWave);
+  }
+  return L;
+}
+
+// Static LDS of the level loop.
+template <int NT>
+struct LevelShared {
+  int nbig[2];    // groups of a level a wave runs as a chain: [0, nbig)
+  int nsmall[2];  // (kernels that keep single-member groups apart) those at [W - nsmall, W)
+  int next[2];    // next chain group to take at the level (dynamic deal)
+  int snext;      // next chunk of the lane pass's groups
+  int kept;       // single-member groups of the leaf pass that become chains
+  int progress;   // ranks of the root chain published to the followers
+  int gbase;      // the level's first group-log entry (allocated once per level)
+  int gnext;      // next group-log entry of the level, from gbase
+  int hist[16];
+  int wtot[NT / kWave];
+  unsigned long long st[OMQ_NSTATS];
+};
+
 // Groups of at most kSmallGroup members at level d, one group per lane.  Each member in turn
 // takes the reference's best child (first unvisited child, else the strict argmax of the
 // exact score) at the parent count N + VL*(rank+1), the children picked by earlier members
@@ -851,24 +933,41 @@ __device__ int block_excl_scan(int32_t* a, int n, int* s_wtot) {
 // order.
 constexpr int kSmallGroup = 1;
 
+// Single-member groups are kept apart from the chain groups in the kernels with a lane pass
+// (rows of at most 192 children) or a leaf pass (256 and 384); the 8-slot kernel keeps every
+// group a chain (the passes' registers would add spills to its chains).
 template <int RMAX>
-__device__ inline void small_groups(
-    const SelArgs& f, const SelCfg& c, int t, int d, int ng, int W, int64_t tb, int64_t gmax,
-    uint32_t* gnode, uint32_t* gsl, uint16_t* buf, uint16_t* lfs, int32_t* lflag,
-    int* s_glog, unsigned long long* s_st, int* s_nbig, int* s_nsmall, int* s_snext,
-    bool vl_done) {
+struct SelTraits {
+  static constexpr bool kLanePass = RMAX <= 3;
+  static constexpr bool kLeafPass = RMAX == 4 || RMAX == 6;
+  static constexpr bool kSingles = kLanePass || kLeafPass;
+  // single-member groups at internal nodes that the leaf pass keeps go through the lane pass
+  // (instead of becoming chains) in the 4-slot kernels; the 6- and 8-slot kernels' chains have
+  // no registers left for it.  (Measured: no change on C2, whose such groups are leaves.)
+  static constexpr bool kWideLanePass = RMAX == 4;
+};
+
+
+template <int RMAX, int NT>
+__device__ inline void small_groups_body(const SelArgs& f, const SelCfg& c, int t, int d, int W,
+                                         int64_t tb, int64_t gmax, const LevelLds& L,
+                                         LevelShared<NT>& sh, int32_t* lfs, int32_t* lflag,
+                                         bool vl_done) {
   const SelArgs& w = f;
-  const int lane = lane_id();
   const int cur = d & 1, nxt = cur ^ 1;
   const int MW = w.max_wave, MD = w.max_depth_buf;
   int32_t* N = f.N;
+  uint32_t* gnode = L.gnode;
+  uint32_t* gsl = L.gsl;
+  uint16_t* buf = L.buf;
   // the small groups of the level sit at the top of the group arrays: [W - ns, W); chunks of 64
   // are dealt from an LDS counter, so that waves done with their chains take them first.  Every
   // fetch advances the counter, so the loop ends after at most ns/64 + 1 fetches.
-  const int ns = s_nsmall[cur];
+  const int lane = lane_id();
+  const int ns = sh.nsmall[cur];
   for (int it = 0; it <= ns / kWave; ++it) {
     int g0 = 0;
-    if (lane == 0) g0 = atomicAdd(s_snext, kWave);
+    if (lane == 0) g0 = atomicAdd(&sh.snext, kWave);
     g0 = readlane_i(g0, 0);
     if (g0 >= ns) break;
     const int gi = W - 1 - (g0 + lane);
@@ -880,7 +979,7 @@ __device__ inline void small_groups(
     int mem[kSmallGroup];
 #pragma unroll
     for (int r = 0; r < kSmallGroup; ++r) mem[r] = r < m ? (int)buf[cur * W + seg + r] : 0;
-    const int gid = atomicAdd(s_glog, 1);
+    const int gid = sh.gbase + atomicAdd(&sh.gnext, 1);
     *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, m);
 #pragma unroll
     for (int r = 0; r < kSmallGroup; ++r) {
@@ -898,7 +997,7 @@ __device__ inline void small_groups(
       atomicAdd(&N[tb + p], c.vli * m);
     else
       N[tb + p] = Np0 + c.vli * m;
-    atomicAdd(&s_st[OMQ_ST_PATHNODES], 1ull);
+    atomicAdd(&sh.st[OMQ_ST_PATHNODES], 1ull);
     bool leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
     if (!leaf && k > RMAX * kWave) {
       atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
@@ -908,9 +1007,9 @@ __device__ inline void small_groups(
 #pragma unroll
     for (int r = 0; r < kSmallGroup; ++r) pick[r] = -1;
     if (!leaf) {
-      atomicAdd(&s_st[OMQ_ST_INTERNAL], 1ull);
-      atomicAdd(&s_st[OMQ_ST_ROWSUM], (unsigned long long)k);
-      atomicAdd(&s_st[OMQ_ST_STEPS], (unsigned long long)m);
+      atomicAdd(&sh.st[OMQ_ST_INTERNAL], 1ull);
+      atomicAdd(&sh.st[OMQ_ST_ROWSUM], (unsigned long long)k);
+      atomicAdd(&sh.st[OMQ_ST_STEPS], (unsigned long long)m);
 #pragma unroll
       for (int r = 0; r < kSmallGroup; ++r) {
         if (r >= m) break;
@@ -919,23 +1018,38 @@ __device__ inline void small_groups(
         const float sp = sqrtf((float)Np);
         float best = -1e9f;
         int bi = -1, unv = -1;
-        for (int i = 0; i < k; ++i) {
-          const int64_t node = tb + first + 1 + i;
-          int n = N[node];
+        // the row in order, four children's loads in flight at a time; the first unvisited
+        // child ends the scan (it is the reference's pick)
+        const int64_t row = tb + first + 1;
+        for (int i0 = 0; i0 < k && unv < 0; i0 += 4) {
+          int n4[4];
+          float w4[4], p4[4];
 #pragma unroll
-          for (int r2 = 0; r2 < kSmallGroup - 1; ++r2)
-            if (r2 < r && pick[r2] == i) n += c.vli;
-          const float wvv = f.W[node];
-          const float pv = f.P[node];
-          if (n == 0) {
-            unv = unv < 0 ? i : unv;
-          } else {
-            const float q = wvv / ((float)n + c.vlf);
-            const float u = ((c.c_puct * pv) * sp) / (float)(1 + n);
-            const float sc = q + u;
-            if (sc > best) {
-              best = sc;
-              bi = i;
+          for (int j = 0; j < 4; ++j) {
+            const bool in = i0 + j < k;
+            n4[j] = in ? N[row + i0 + j] : 1;
+            w4[j] = in ? f.W[row + i0 + j] : 0.0f;
+            p4[j] = in ? f.P[row + i0 + j] : 0.0f;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int i = i0 + j;
+            int n = n4[j];
+#pragma unroll
+            for (int r2 = 0; r2 < kSmallGroup - 1; ++r2)
+              if (r2 < r && pick[r2] == i) n += c.vli;
+            if (i < k && unv < 0) {
+              if (n == 0) {
+                unv = i;
+              } else {
+                const float q = w4[j] / ((float)n + c.vlf);
+                const float u = ((c.c_puct * p4[j]) * sp) / (float)(1 + n);
+                const float sc = q + u;
+                if (sc > best) {
+                  best = sc;
+                  bi = i;
+                }
+              }
             }
           }
         }
@@ -953,8 +1067,8 @@ __device__ inline void small_groups(
         if (s_end < 0) s_end = mem[r];
         w.path_len[(int64_t)t * MW + mem[r]] = d + 1;
         w.leaves[(int64_t)t * MW + mem[r]] = p;
-        lfs[mem[r]] = (uint16_t)s_end;
-        atomicAdd(&s_st[OMQ_ST_PATHENTRIES], (unsigned long long)(d + 1));
+        lfs[mem[r]] = s_end;
+        atomicAdd(&sh.st[OMQ_ST_PATHENTRIES], (unsigned long long)(d + 1));
         continue;
       }
       bool seen = false;
@@ -970,8 +1084,8 @@ __device__ inline void small_groups(
           ++cntc;
         }
       }
-      const int g = cntc > kSmallGroup ? atomicAdd(&s_nbig[nxt], 1)
-                                       : W - 1 - atomicAdd(&s_nsmall[nxt], 1);
+      const int g = cntc > kSmallGroup ? atomicAdd(&sh.nbig[nxt], 1)
+                                       : W - 1 - atomicAdd(&sh.nsmall[nxt], 1);
       gnode[nxt * W + g] = (uint32_t)(first + 1 + pick[r]);
       gsl[nxt * W + g] = (uint32_t)pos | ((uint32_t)cntc << 16);
       pos += cntc;
@@ -980,86 +1094,122 @@ __device__ inline void small_groups(
   }
 }
 
-// Single-member groups of level d in the kernels without a lane pass, for waves of at most
-// kSelThreads simulations.  Such a group's node is usually a leaf, which needs only the node's
-// header (visit count, row offset, row length): every thread takes one group, so the header
-// loads of the whole level are in flight together, and the leaves are finished here as the
-// chain groups finish theirs.  The groups that are not leaves join the level's chain groups.
-// Every single-member group's entry is read before the barrier, and the chain entries are
-// appended after it, so an appended entry may overwrite only entries already read.  Called by
-// every thread of the workgroup.
-template <int RMAX>
+// The lane pass: the narrow kernels take every single-member group through it, the 4-slot
+// kernels those the leaf pass finds at internal nodes.
+template <int RMAX, int NT>
+__device__ inline void small_groups(const SelArgs& f, const SelCfg& c, int t, int d, int W,
+                                    int64_t tb, int64_t gmax, const LevelLds& L,
+                                    LevelShared<NT>& sh, int32_t* lfs, int32_t* lflag,
+                                    bool vl_done) {
+  small_groups_body<RMAX, NT>(f, c, t, d, W, tb, gmax, L, sh, lfs, lflag, vl_done);
+}
+template <int RMAX, int NT>
+__device__ inline void small_groups_call(const SelArgs& f, const SelCfg& c, int t, int d,
+                                               int W, int64_t tb, int64_t gmax,
+                                               const LevelLds& L, LevelShared<NT>& sh,
+                                               int32_t* lfs, int32_t* lflag, bool vl_done) {
+  small_groups_body<RMAX, NT>(f, c, t, d, W, tb, gmax, L, sh, lfs, lflag, vl_done);
+}
+
+// Single-member groups of level d in the kernels without a lane pass.  Such a group's node is
+// usually a leaf, which needs only the node's header (visit count, row offset, row length):
+// every thread takes one group per chunk of NT, so the header loads of a chunk are in flight
+// together, and the leaves are finished here as the chain groups finish theirs.  The groups
+// that are not leaves are staged in the next level's group arrays (empty at this point) and,
+// once every single-member group has been read, appended to the level's chain groups (which
+// may overwrite the single-member entries, all read by then).  Called by every thread of the
+// workgroup.
+template <int RMAX, int NT>
 __device__ inline void leaf_pass(const SelArgs& f, const SelCfg& c, int t, int d, int W,
-                                 int64_t tb, int64_t gmax, uint32_t* gnode, uint32_t* gsl,
-                                 const uint16_t* buf, uint16_t* lfs, int32_t* lflag, int* s_glog,
-                                 unsigned long long* s_st, int* s_nbig, int ns, bool vl_done) {
+                                 int64_t tb, int64_t gmax, const LevelLds& L,
+                                 LevelShared<NT>& sh, int32_t* lfs, int32_t* lflag, int ns,
+                                 bool vl_done) {
   const SelArgs& w = f;
   const int tid = threadIdx.x;
   const int lane = lane_id();
-  const int cur = d & 1;
+  const int cur = d & 1, nxt = cur ^ 1;
   const int MW = w.max_wave, MD = w.max_depth_buf;
   int32_t* N = f.N;
-  bool keep = false, leaf = false;
-  uint32_t sl = 0;
-  int p = 0, seg = 0, s = 0, Np0 = 0;
-  if (tid < ns) {
-    const int gi = W - 1 - tid;
-    sl = gsl[cur * W + gi];
-    p = (int)gnode[cur * W + gi];
-    seg = (int)(sl & 0xFFFFu);
-    s = buf[cur * W + seg];
-    Np0 = N[tb + p];
-    const int k = f.nchild[tb + p];
-    const int first = f.first[tb + p];
-    leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
-    if (!leaf && k > RMAX * kWave) {
-      atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
-      leaf = true;
-    }
-    keep = !leaf;
-  }
-  // the leaves: group log, path entry, the arrival's virtual loss, end of the path
-  const uint64_t lm = __ballot(leaf);
-  if (lm != 0) {
-    const int nl = __popcll(lm);
-    int gbase = 0;
-    if (lane == 0) {
-      gbase = atomicAdd(s_glog, nl);
-      atomicAdd(&s_st[OMQ_ST_PATHNODES], (unsigned long long)nl);
-      atomicAdd(&s_st[OMQ_ST_PATHENTRIES], (unsigned long long)nl * (d + 1));
-    }
-    gbase = readlane_i(gbase, 0);
-    if (leaf) {
-      const int gid = gbase + (int)__builtin_amdgcn_mbcnt_hi(
-                                  (uint32_t)(lm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)lm, 0u));
-      *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, 1);
-      w.paths[((int64_t)t * MW + s) * MD + d] = p;
-      w.gmembers[((int64_t)t * MD + d) * MW + seg] = (uint16_t)s;
-      if (vl_done) {
-        // the arrival's virtual loss is in N already
-      } else if (c.vl_atomic) {
-        atomicAdd(&N[tb + p], c.vli);
-      } else {
-        N[tb + p] = Np0 + c.vli;
+  if (tid == 0) sh.kept = 0;
+  __syncthreads();
+  for (int c0 = 0; c0 < ns; c0 += NT) {
+    bool keep = false, leaf = false;
+    uint32_t sl = 0;
+    int p = 0, seg = 0, s = 0, Np0 = 0;
+    if (c0 + tid < ns) {
+      const int gi = W - 1 - (c0 + tid);
+      sl = L.gsl[cur * W + gi];
+      p = (int)L.gnode[cur * W + gi];
+      seg = (int)(sl & 0xFFFFu);
+      s = L.buf[cur * W + seg];
+      Np0 = N[tb + p];
+      const int k = f.nchild[tb + p];
+      const int first = f.first[tb + p];
+      leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
+      if (!leaf && k > RMAX * kWave) {
+        atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
+        leaf = true;
       }
-      w.path_len[(int64_t)t * MW + s] = d + 1;
-      w.leaves[(int64_t)t * MW + s] = p;
-      lfs[s] = (uint16_t)s;
-      lflag[s] = 1;
+      keep = !leaf;
+    }
+    // the leaves: group log, path entry, the arrival's virtual loss, end of the path
+    const uint64_t lm = __ballot(leaf);
+    if (lm != 0) {
+      const int nl = __popcll(lm);
+      int gbase = 0;
+      if (lane == 0) {
+        gbase = sh.gbase + atomicAdd(&sh.gnext, nl);
+        atomicAdd(&sh.st[OMQ_ST_PATHNODES], (unsigned long long)nl);
+        atomicAdd(&sh.st[OMQ_ST_PATHENTRIES], (unsigned long long)nl * (d + 1));
+      }
+      gbase = readlane_i(gbase, 0);
+      if (leaf) {
+        const int gid = gbase + (int)__builtin_amdgcn_mbcnt_hi(
+                                    (uint32_t)(lm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)lm, 0u));
+        *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, 1);
+        w.paths[((int64_t)t * MW + s) * MD + d] = p;
+        w.gmembers[((int64_t)t * MD + d) * MW + seg] = (uint16_t)s;
+        if (vl_done) {
+          // the arrival's virtual loss is in N already
+        } else if (c.vl_atomic) {
+          atomicAdd(&N[tb + p], c.vli);
+        } else {
+          N[tb + p] = Np0 + c.vli;
+        }
+        w.path_len[(int64_t)t * MW + s] = d + 1;
+        w.leaves[(int64_t)t * MW + s] = p;
+        lfs[s] = s;
+        lflag[s] = 1;
+      }
+    }
+    const uint64_t km = __ballot(keep);
+    if (km != 0) {
+      int gbase = 0;
+      if (lane == 0) gbase = atomicAdd(&sh.kept, __popcll(km));
+      gbase = readlane_i(gbase, 0);
+      if (keep) {
+        const int g = gbase + (int)__builtin_amdgcn_mbcnt_hi(
+                                  (uint32_t)(km >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)km, 0u));
+        L.gnode[nxt * W + g] = (uint32_t)p;
+        L.gsl[nxt * W + g] = sl;
+      }
     }
   }
   __syncthreads();
-  const uint64_t km = __ballot(keep);
-  if (km != 0) {
-    int gbase = 0;
-    if (lane == 0) gbase = atomicAdd(s_nbig, __popcll(km));
-    gbase = readlane_i(gbase, 0);
-    if (keep) {
-      const int g = gbase + (int)__builtin_amdgcn_mbcnt_hi(
-                                (uint32_t)(km >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)km, 0u));
-      gnode[cur * W + g] = (uint32_t)p;
-      gsl[cur * W + g] = sl;
-    }
+  const int kept = sh.kept;
+  const int nb = sh.nbig[cur];
+  // (kernels with the wide lane pass: back to the single-member section, for the lane pass)
+  const int dst = SelTraits<RMAX>::kWideLanePass ? W - kept : nb;
+  for (int i = tid; i < kept; i += NT) {
+    L.gnode[cur * W + dst + i] = L.gnode[nxt * W + i];
+    L.gsl[cur * W + dst + i] = L.gsl[nxt * W + i];
+  }
+  __syncthreads();
+  if (tid == 0) {
+    if (SelTraits<RMAX>::kWideLanePass)
+      sh.nsmall[cur] = kept;
+    else
+      sh.nbig[cur] = nb + kept;
   }
 }
 
@@ -1071,14 +1221,14 @@ __device__ inline int size_class(int m) { return 15 - min(15, 31 - __clz(m)); }
 // The order within a class is arbitrary (groups of one level are independent).  tn/ts is
 // scratch of nb entries (the group arrays of the next level, empty at this point).  Called by
 // every thread of the workgroup.  Kept out of line: inlined, it changes the register
-// allocation of the 6-slot kernel's chains (16 spilled registers become 53).
+// allocation of the 6-slot kernel's chains.
+template <int NT>
 __device__ __noinline__ void order_groups(uint32_t* gn, uint32_t* gs, uint32_t* tn, uint32_t* ts,
-                                    int nb, int* s_hist) {
+                                          int nb, int* s_hist) {
   const int tid = threadIdx.x;
   if (tid < 16) s_hist[tid] = 0;
   __syncthreads();
-  for (int i = tid; i < nb; i += kSelThreads)
-    atomicAdd(&s_hist[size_class((int)(gs[i] >> 16))], 1);
+  for (int i = tid; i < nb; i += NT) atomicAdd(&s_hist[size_class((int)(gs[i] >> 16))], 1);
   __syncthreads();
   if (tid < kWave) {  // class counts -> class cursors (exclusive scan)
     const int v = tid < 16 ? s_hist[tid] : 0;
@@ -1087,14 +1237,14 @@ __device__ __noinline__ void order_groups(uint32_t* gn, uint32_t* gs, uint32_t* 
     if (tid < 16) s_hist[tid] = ex;
   }
   __syncthreads();
-  for (int i = tid; i < nb; i += kSelThreads) {
+  for (int i = tid; i < nb; i += NT) {
     const uint32_t sl = gs[i];
     const int pos = atomicAdd(&s_hist[size_class((int)(sl >> 16))], 1);
     tn[pos] = gn[i];
     ts[pos] = sl;
   }
   __syncthreads();
-  for (int i = tid; i < nb; i += kSelThreads) {
+  for (int i = tid; i < nb; i += NT) {
     gn[i] = tn[i];
     gs[i] = ts[i];
   }
@@ -1114,22 +1264,15 @@ __device__ __noinline__ void order_groups(uint32_t* gn, uint32_t* gs, uint32_t* 
 // waves touch the same node.  A follower waits only for the root chain, which waits for no one.
 // After the level, the level-1 groups are formed from the whole root chain as usual; their
 // chains are not run again: each member's pick is replayed from the followers' record (pick2),
-// and the virtual loss of levels 1 and 2 is not applied again.
-constexpr int kPipeMaxW = 2048;              // waves with LDS for the overlap buffers
-constexpr int kFollowers = kSelWaves - 1;
-constexpr int kSpinLimit = 1 << 22;          // bound of a follower's wait for a root block
+// and the virtual loss of levels 1 and 2 is not applied again.  pick2 starts as kPickNone for
+// every simulation, so a member whose block a follower never ran (its bounded wait ran out,
+// OMQ_STATUS_STALL) ends its path at its level-1 node.
 constexpr uint16_t kPickNone = 0xFFFFu;
 
-__host__ __device__ inline size_t select_base_bytes(int W) {
-  return (size_t)kSelWaves * kWave * 16 + (size_t)W * (4 + 4 + 8 + 8) + (size_t)W * (4 + 2) +
-         (size_t)kSelWaves * OMQ_MAX_ROW * 2;
-}
-__host__ __device__ inline size_t pipe_offset(int W) { return (select_base_bytes(W) + 15) & ~(size_t)15; }
-
-// Waits until the root chain has published `need` ranks (bounded: false when the bound runs
-// out, which the caller reports as OMQ_STATUS_STALL).
-__device__ inline bool wait_progress(const int* prog, int need) {
-  for (int it = 0; it < kSpinLimit; ++it) {
+// Waits until the root chain has published `need` ranks (bounded by `limit` polls: false when
+// the bound runs out, which the caller reports as OMQ_STATUS_STALL).
+__device__ inline bool wait_progress(const int* prog, int need, int limit) {
+  for (int it = 0; it < limit; ++it) {
     const int v = __hip_atomic_load(prog, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (readlane_i(v, 0) >= need) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -1140,25 +1283,25 @@ __device__ inline bool wait_progress(const int* prog, int need) {
   return false;
 }
 
-// Level-1 chains of the followers (wave index fw among them), block by block as the root chain
+// Level-1 chains of the followers (wave index fw among nfol), block by block as the root chain
 // publishes its picks in root_ch.  Records each member's pick in pick2 (child index, or
 // kPickNone when its node has no child to give).
 template <int RMAX>
 __device__ inline void level1_followers(const SelArgs& f, const SelCfg& c, int64_t tb, int W,
                                         int root_first, const uint32_t* root_ch, uint16_t* pick2,
                                         uint32_t* chs, uint16_t* cnt_s, float4* cscr,
-                                        const int* progress, int fw) {
+                                        const int* progress, int fw, int nfol) {
   const int lane = lane_id();
   int32_t* N = f.N;
   for (int b0 = 0; b0 < W; b0 += kWave) {
-    if (!wait_progress(progress, min(W, b0 + kWave))) {
+    if (!wait_progress(progress, min(W, b0 + kWave), c.spin_limit)) {
       if (lane == 0) atomicOr(&f.status[0], OMQ_STATUS_STALL);
       return;
     }
     const int s = b0 + lane;
     const uint32_t cv = s < W ? root_ch[s] : kNoChild;
     const int key = cv == kNoChild ? -1 : (int)(cv >> 16);
-    const bool mine = key >= 0 && key % kFollowers == fw;
+    const bool mine = key >= 0 && key % nfol == fw;
     uint64_t rest = __ballot(mine);
     // one root child per iteration; each takes at least one lane out of rest
     for (int it = 0; it < kWave && rest != 0; ++it) {
@@ -1227,47 +1370,22 @@ __device__ inline int replay_picks(const uint16_t* mem, int m, int k, const uint
   return fe;
 }
 
-template <int RMAX>
-__global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c) {
-  // small groups one per lane; kept out of the widest kernels, whose chains need every
-  // register
-  constexpr bool kLanePass = RMAX <= 3;
-  // single-member groups through the leaf pass in the kernels of 4 and 6 slots per lane, for
-  // waves of at most kSelThreads simulations (the 8-slot kernel keeps every group a chain: the
-  // pass's registers would add spills to its chains)
-  constexpr bool kLeafPass = RMAX == 4 || RMAX == 6;
-  // the level overlap in the kernels whose chains keep their registers with a second copy of
-  // the chain code (the followers')
-  constexpr bool kPipe = RMAX <= 3;
-  const bool singles = kLanePass || (kLeafPass && c.W <= kSelThreads);  // kept apart
-  SelArgs& w = f;
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int W = c.W;
-  float4* cscr_all = reinterpret_cast<float4*>(smem);         // [kSelWaves * 64] (16-aligned)
-  uint32_t* choice = reinterpret_cast<uint32_t*>(cscr_all + kSelWaves * kWave);  // [W]
-  int32_t* lflag = reinterpret_cast<int32_t*>(choice + W);    // [W] leaf-first flags, then scan
-  uint32_t* gnode = reinterpret_cast<uint32_t*>(lflag + W);   // [2W] group node per level
-  uint32_t* gsl = gnode + 2 * W;                              // [2W] seg | len << 16
-  uint16_t* buf = reinterpret_cast<uint16_t*>(gsl + 2 * W);   // [2W] members by position
-  uint16_t* lfs = buf + 2 * W;                                // [W] first sim of own leaf group
-  uint16_t* cnt_all = lfs + W;                                // [kSelWaves * OMQ_MAX_ROW]
-  // level-overlap buffers (waves of at most kPipeMaxW simulations)
-  uint32_t* pipe_ch = reinterpret_cast<uint32_t*>(smem + pipe_offset(W));  // [kSelWaves * 64]
-  uint16_t* pick2 = reinterpret_cast<uint16_t*>(pipe_ch + kSelWaves * kWave);  // [W]
 
-  // Groups of a level: those a wave runs as a chain at [0, nbig), those the lane pass takes
-  // (kernels with a lane pass) at [W - nsmall, W) of the level's group arrays.
-  __shared__ int s_nbig[2];
-  __shared__ int s_nsmall[2];
-  __shared__ int s_next[2];  // next chain group to take at the level (dynamic deal)
-  __shared__ int s_snext;    // next chunk of the lane pass's groups
-  __shared__ int s_hist[16];
-  __shared__ int s_glog;
-  __shared__ int s_wtot[kSelWaves];
-  __shared__ unsigned long long s_st[OMQ_NSTATS];
-  __shared__ int s_progress;  // ranks of the root chain published to the followers
-
-  const int t = blockIdx.x;
+// The level-by-level selection of a set of groups, from level d0 until no group is left or
+// level dend is reached (its groups then stay in L at parity dend & 1, for the caller).  The
+// groups of level d0 are in L and sh at parity d0 & 1.  Returns the level at which it stopped.
+//   pipe:       the root chain is overlapped with the level-1 chains (root kernel, d0 = 0);
+//               level 1 then replays the followers' picks
+//   vl_done_to: levels 1..vl_done_to have their virtual loss in N already (the overlap)
+//   glog_ctr:   counter of the tree's group-log entries (LDS or global)
+//   lfs, lflag: the tree's per-simulation leaf records (global)
+template <int RMAX, int NT>
+__device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int dend, int W,
+                          const LevelLds& L, LevelShared<NT>& sh, int* glog_ctr, int32_t* lfs,
+                          int32_t* lflag, bool pipe, int root_first, int vl_done_to) {
+  constexpr int NW = NT / kWave;
+  using Tr = SelTraits<RMAX>;
+  const SelArgs& w = f;
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = lane_id();
@@ -1275,55 +1393,41 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   const int MW = w.max_wave, MD = w.max_depth_buf;
   const int64_t gmax = (int64_t)MW * MD;
   int32_t* N = f.N;
-  uint16_t* cnt_s = cnt_all + wave * OMQ_MAX_ROW;
-  float4* cscr = cscr_all + wave * kWave;  // contender window scratch of this wave
-  // the level overlap needs an internal root, an integer virtual loss and the ordered mode
-  const int root_k = f.nchild[tb], root_first = f.first[tb];
-  const bool pipe = kPipe && W > kWave && W <= kPipeMaxW && !c.vl_atomic && c.vli > 0 &&
-                    c.max_depth >= 2 && root_k > 0 && root_first >= 0 && root_k <= RMAX * kWave;
-
-  for (int s = tid; s < W; s += kSelThreads) {
-    buf[s] = (uint16_t)s;
-    lflag[s] = 0;
-  }
-  if (tid < OMQ_NSTATS) s_st[tid] = 0;
-  if (tid == 0) {
-    // the root group is a chain unless the lane pass takes it
-    const bool root_big = !singles || W > kSmallGroup;
-    const int g0 = root_big ? 0 : W - 1;
-    gnode[g0] = 0;
-    gsl[g0] = 0u | ((uint32_t)W << 16);
-    s_nbig[0] = root_big ? 1 : 0;
-    s_nsmall[0] = root_big ? 0 : 1;
-    s_nbig[1] = 0;
-    s_nsmall[1] = 0;
-    s_next[0] = 0;
-    s_next[1] = 0;
-    s_snext = 0;
-    s_glog = 0;
-    s_progress = 0;
-  }
-  __syncthreads();
-
-  for (int d = 0; d < c.max_depth; ++d) {
+  uint16_t* cnt_s = L.cnt_all + wave * OMQ_MAX_ROW;
+  float4* cscr = L.cscr_all + wave * kWave;  // contender window scratch of this wave
+  uint32_t* gnode = L.gnode;
+  uint32_t* gsl = L.gsl;
+  uint16_t* buf = L.buf;
+  int d = d0;
+  for (; d < c.max_depth && d < dend; ++d) {
     const int cur = d & 1, nxt = cur ^ 1;
-    const int ng = s_nbig[cur] + s_nsmall[cur];
+    const int ng = sh.nbig[cur] + sh.nsmall[cur];
     if (ng == 0) break;
-    const bool replay = pipe && d == 1;   // level-1 picks recorded by the followers
-    const bool vl_done = pipe && d <= 2;  // virtual loss of levels 1, 2 applied by the overlap
-    const bool sg = singles && !(pipe && d == 0);  // level-1 groups of the overlap stay chains
-    if (kLeafPass) {
+    // every group of the level logs one entry: the level's entries are taken at once (one
+    // atomic on the tree's counter), the groups then number themselves in LDS
+    if (tid == 0) {
+      sh.gbase = atomicAdd(glog_ctr, ng);
+      sh.gnext = 0;
+    }
+    __syncthreads();
+    const bool replay = pipe && d == 1;  // level-1 picks recorded by the followers
+    const bool vl_done = d > 0 && d <= vl_done_to;
+    const bool sg = Tr::kSingles && !(pipe && d == 0);  // level-1 groups of the overlap stay chains
+    if (Tr::kLeafPass) {
       // single-member groups: leaves finished by all threads at once, the rest become chains
-      if (singles && s_nsmall[cur] > 0) {
-        leaf_pass<RMAX>(f, c, t, d, W, tb, gmax, gnode, gsl, buf, lfs, lflag, &s_glog, s_st,
-                        &s_nbig[cur], s_nsmall[cur], vl_done && d == 2);
+      const int ns = sh.nsmall[cur];
+      if (ns > 0) {
+        leaf_pass<RMAX, NT>(f, c, t, d, W, tb, gmax, L, sh, lfs, lflag, ns,
+                            vl_done && d == vl_done_to);
+        if (!Tr::kWideLanePass && tid == 0) sh.nsmall[cur] = 0;
         __syncthreads();
       }
     }
-    const int nb = s_nbig[cur];
+    const int nb = sh.nbig[cur];
     // more chain groups than waves: the longest first
-    if (nb > kSelWaves)
-      order_groups(gnode + cur * W, gsl + cur * W, gnode + nxt * W, gsl + nxt * W, nb, s_hist);
+    if (nb > NW)
+      order_groups<NT>(gnode + cur * W, gsl + cur * W, gnode + nxt * W, gsl + nxt * W, nb,
+                       sh.hist);
     // The chain groups are dealt dynamically: each wave takes the next index from an LDS
     // counter, so a wave that finishes a short chain takes the next group at once.  The next
     // index is requested when a group starts, so that the answer is back by its end.  Every
@@ -1331,17 +1435,18 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
     // fetches; the loop bound states this (it never ends the loop early).  No barrier is
     // inside the loop.
     if (pipe && d == 0 && wave != 0) {
-      level1_followers<RMAX>(f, c, tb, W, root_first, choice, pick2, pipe_ch + wave * kWave,
-                             cnt_s, cscr, &s_progress, wave - 1);
+      level1_followers<RMAX>(f, c, tb, W, root_first, L.choice, L.pick2,
+                             L.pipe_ch + wave * kWave, cnt_s, cscr, &sh.progress, wave - 1,
+                             NW - 1);
     }
     // (at level 0 of the overlap only wave 0 takes the root)
     const bool deal = !(pipe && d == 0 && wave != 0);
     int gnext = 0;
-    if (deal && lane == 0) gnext = atomicAdd(&s_next[cur], 1);
+    if (deal && lane == 0) gnext = atomicAdd(&sh.next[cur], 1);
     for (int it = 0; it <= nb && deal; ++it) {
       const int gi = readlane_i(gnext, 0);
       if (gi >= nb) break;
-      if (lane == 0) gnext = atomicAdd(&s_next[cur], 1);
+      if (lane == 0) gnext = atomicAdd(&sh.next[cur], 1);
       const int p = (int)gnode[cur * W + gi];
       const uint32_t sl = gsl[cur * W + gi];
       const int seg = (int)(sl & 0xFFFFu);
@@ -1350,7 +1455,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
 
       // log the group and record the path entries
       int gid = 0;
-      if (lane == 0) gid = atomicAdd(&s_glog, 1);
+      if (lane == 0) gid = sh.gbase + atomicAdd(&sh.gnext, 1);
       gid = readlane_i(gid, 0);
       if (lane < 4) {
         const int v = lane == 0 ? p : lane == 1 ? d : lane == 2 ? seg : m;
@@ -1365,14 +1470,14 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       int Np0 = N[tb + p];
       const int k = f.nchild[tb + p];
       const int first = f.first[tb + p];
-      if (vl_done && d > 0) {
+      if (vl_done) {
         Np0 -= c.vli * m;  // the members' virtual loss is in N already
       } else if (c.vl_atomic) {
         for (int r = lane; r < m; r += kWave) atomicAdd(&N[tb + p], c.vli);
       } else if (lane == 0) {
         N[tb + p] = Np0 + c.vli * m;
       }
-      if (lane == 0) atomicAdd(&s_st[OMQ_ST_PATHNODES], 1ull);
+      if (lane == 0) atomicAdd(&sh.st[OMQ_ST_PATHNODES], 1ull);
 
       bool leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
       if (!leaf && k > RMAX * kWave) {
@@ -1385,31 +1490,31 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
           const int s = mem[r];
           w.path_len[(int64_t)t * MW + s] = d + 1;
           w.leaves[(int64_t)t * MW + s] = p;
-          lfs[s] = (uint16_t)s0;
+          lfs[s] = s0;
         }
         if (lane == 0) {
           lflag[s0] = 1;
-          atomicAdd(&s_st[OMQ_ST_PATHENTRIES], (unsigned long long)m * (d + 1));
+          atomicAdd(&sh.st[OMQ_ST_PATHENTRIES], (unsigned long long)m * (d + 1));
         }
         continue;
       }
 
-      uint32_t* ch = choice + seg;
-      const int fe = replay ? replay_picks(mem, m, k, pick2, ch, cnt_s)
+      uint32_t* ch = L.choice + seg;
+      const int fe = replay ? replay_picks(mem, m, k, L.pick2, ch, cnt_s)
                             : dispatch_chain<RMAX>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr,
-                                                   pipe && d == 0 ? &s_progress : nullptr);
+                                                   pipe && d == 0 ? &sh.progress : nullptr);
       if (lane == 0) {
-        atomicAdd(&s_st[OMQ_ST_INTERNAL], 1ull);
-        atomicAdd(&s_st[OMQ_ST_ROWSUM], (unsigned long long)k);
-        atomicAdd(&s_st[OMQ_ST_STEPS], (unsigned long long)m);
+        atomicAdd(&sh.st[OMQ_ST_INTERNAL], 1ull);
+        atomicAdd(&sh.st[OMQ_ST_ROWSUM], (unsigned long long)k);
+        atomicAdd(&sh.st[OMQ_ST_STEPS], (unsigned long long)m);
       }
 
       // exclusive scan of the child counts (blocks of B children per lane) -> offsets, and
       // the groups of the next level
       const int B = (k + kWave - 1) / kWave;
       const int lo = lane * B, hi = min(lo + B, k);
-      // (chain groups go to the bottom of the next level's group arrays, the lane pass's
-      // groups to the top)
+      // (chain groups go to the bottom of the next level's group arrays, single-member groups
+      // of the kernels that keep them apart to the top)
       int sum = 0, nbg = 0, nsm = 0;
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
@@ -1423,8 +1528,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       int pbg = wave_excl_scan(nbg, &tot_bg);
       int psm = wave_excl_scan(nsm, &tot_sm);
       int bbase = 0, sbase = 0;
-      if (lane == 0 && tot_bg > 0) bbase = atomicAdd(&s_nbig[nxt], tot_bg);
-      if (lane == 0 && tot_sm > 0) sbase = atomicAdd(&s_nsmall[nxt], tot_sm);
+      if (lane == 0 && tot_bg > 0) bbase = atomicAdd(&sh.nbig[nxt], tot_bg);
+      if (lane == 0 && tot_sm > 0) sbase = atomicAdd(&sh.nsmall[nxt], tot_sm);
       bbase = readlane_i(bbase, 0);
       sbase = readlane_i(sbase, 0);
       for (int i = lo; i < hi; ++i) {
@@ -1448,8 +1553,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
         if (cv == kNoChild) {
           w.path_len[(int64_t)t * MW + s] = d + 1;
           w.leaves[(int64_t)t * MW + s] = p;
-          lfs[s] = (uint16_t)s_end;
-          atomicAdd(&s_st[OMQ_ST_PATHENTRIES], (unsigned long long)(d + 1));
+          lfs[s] = s_end;
+          atomicAdd(&sh.st[OMQ_ST_PATHENTRIES], (unsigned long long)(d + 1));
         } else {
           const int i = (int)(cv >> 16);
           const int rk = (int)(cv & 0xFFFFu);
@@ -1462,22 +1567,61 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
       }
       wave_sync();
     }
-    if (kLanePass)
-      small_groups<RMAX>(f, c, t, d, ng, W, tb, gmax, gnode, gsl, buf, lfs, lflag, &s_glog, s_st,
-                         s_nbig, s_nsmall, &s_snext, vl_done && d == 2);
+    if (Tr::kLanePass)
+      small_groups<RMAX, NT>(f, c, t, d, W, tb, gmax, L, sh, lfs, lflag,
+                             vl_done && d == vl_done_to);
+    if (Tr::kWideLanePass && sh.nsmall[cur] > 0)
+      small_groups_call<RMAX, NT>(f, c, t, d, W, tb, gmax, L, sh, lfs, lflag,
+                                  vl_done && d == vl_done_to);
     __syncthreads();
     if (tid == 0) {
-      s_nbig[cur] = 0;
-      s_nsmall[cur] = 0;
-      s_next[cur] = 0;
-      s_snext = 0;
+      sh.nbig[cur] = 0;
+      sh.nsmall[cur] = 0;
+      sh.next[cur] = 0;
+      sh.snext = 0;
     }
     __syncthreads();
   }
+  return d;
+}
 
-  // unique leaves in order of first occurrence
-  const int nu = block_excl_scan(lflag, W, s_wtot);
-  for (int s = tid; s < W; s += kSelThreads) {
+// The level-d0 group set of (node p, segment [seg, seg + m)) put into L / sh (members read
+// from mem_src, or 0..m-1 when it is null).  Called by every thread; ends with a barrier.
+template <int RMAX, int NT>
+__device__ inline void start_group(const LevelLds& L, LevelShared<NT>& sh, int W, int d0, int p,
+                                   int seg, int m, const uint16_t* mem_src) {
+  const int tid = threadIdx.x;
+  const int cur = d0 & 1;
+  for (int r = tid; r < m; r += NT)
+    L.buf[cur * W + seg + r] = mem_src ? mem_src[r] : (uint16_t)(seg + r);
+  if (tid < OMQ_NSTATS) sh.st[tid] = 0;
+  if (tid == 0) {
+    // a single member goes to the single-member groups of the kernels that keep them apart
+    const bool big = !SelTraits<RMAX>::kSingles || m > kSmallGroup;
+    const int g0 = big ? 0 : W - 1;
+    L.gnode[cur * W + g0] = (uint32_t)p;
+    L.gsl[cur * W + g0] = (uint32_t)seg | ((uint32_t)m << 16);
+    sh.nbig[cur] = big ? 1 : 0;
+    sh.nsmall[cur] = big ? 0 : 1;
+    sh.nbig[cur ^ 1] = 0;
+    sh.nsmall[cur ^ 1] = 0;
+    sh.next[0] = 0;
+    sh.next[1] = 0;
+    sh.snext = 0;
+    sh.progress = 0;
+  }
+  __syncthreads();
+}
+
+// Unique leaves of tree t in order of first occurrence, from the per-simulation leaf records
+// lflag / lfs (global; lflag is scanned in place).  Called by every thread of the workgroup.
+template <int NT>
+__device__ inline void finish_tree(const SelArgs& w, int t, int W, int32_t* lfs, int32_t* lflag,
+                                   int* s_wtot) {
+  const int tid = threadIdx.x;
+  const int MW = w.max_wave;
+  const int nu = block_excl_scan<NT>(lflag, W, s_wtot);
+  for (int s = tid; s < W; s += NT) {
     const int s0 = lfs[s];
     const int uid = lflag[s0];
     w.sim_uid[(int64_t)t * MW + s] = uid;
@@ -1488,14 +1632,212 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
   }
   if (tid == 0) {
     w.ucount[t] = nu;
-    w.gcount[t] = s_glog;
-    s_st[OMQ_ST_ULEAVES] += (unsigned long long)nu;
-    s_st[OMQ_ST_SIMS] += (unsigned long long)W;
+    atomicAdd(reinterpret_cast<unsigned long long*>(&w.stats[(int64_t)t * OMQ_NSTATS +
+                                                             OMQ_ST_ULEAVES]),
+              (unsigned long long)nu);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&w.stats[(int64_t)t * OMQ_NSTATS +
+                                                             OMQ_ST_SIMS]),
+              (unsigned long long)W);
+  }
+}
+
+template <int NT>
+__device__ inline void flush_stats(const SelArgs& w, int t, LevelShared<NT>& sh) {
+  const int tid = threadIdx.x;
+  if (tid < OMQ_NSTATS && sh.st[tid] != 0)
+    atomicAdd(reinterpret_cast<unsigned long long*>(&w.stats[(int64_t)t * OMQ_NSTATS + tid]),
+              sh.st[tid]);
+}
+
+// ---- Subtree tasks ---------------------------------------------------------------------
+// The groups of one level below the root chain are independent: the members of a group only
+// ever meet the nodes of its node's subtree.  In the split schedule the root kernel stops at
+// that level and hands its groups over as subtree tasks; the subtree kernel's workgroups take
+// them from a global counter, largest size class first over all trees (the longest subtrees
+// start first), and each runs the level loop of its subtree in LDS.  No workgroup waits for
+// another; the kernel boundaries order the root kernel, the subtree kernel and the finish.
+constexpr int kTaskClasses = 8;
+constexpr int kSplitMaxTrees = 128;  // trees of a forest for the split schedule (LDS table)
+constexpr int kSubThreads = 256;
+
+// Size class of a subtree task of m members: 0 for m >= 128, ..., 7 for m = 1.
+__device__ inline int task_class(int m) { return 7 - min(7, 31 - __clz(m)); }
+
+// The groups of level d (in L / sh at parity d & 1) as subtree tasks of tree t: members copied
+// to gmembers level d (their place in the group log), tasks written in size-class order with
+// the per-class counts, and the tree's task level (d, plus 256 when the level's virtual loss is
+// in N already).  Called by every thread of the workgroup.
+template <int NT>
+__device__ inline void export_tasks(const SelArgs& f, int t, int d, bool vl_done, int W,
+                                    const LevelLds& L, LevelShared<NT>& sh) {
+  const int tid = threadIdx.x;
+  const int cur = d & 1;
+  const int MW = f.max_wave, MD = f.max_depth_buf;
+  const int nb = sh.nbig[cur];
+  const int ns = sh.nsmall[cur];
+  const int n = nb + ns;
+  if (n > 0)
+    for (int s = tid; s < W; s += NT)
+      f.gmembers[((int64_t)t * MD + d) * MW + s] = L.buf[cur * W + s];
+  if (tid < kTaskClasses) sh.hist[tid] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += NT) {
+    const int gi = i < nb ? i : W - 1 - (i - nb);
+    atomicAdd(&sh.hist[task_class((int)(L.gsl[cur * W + gi] >> 16))], 1);
   }
   __syncthreads();
-  if (tid < OMQ_NSTATS && s_st[tid] != 0)
-    atomicAdd(reinterpret_cast<unsigned long long*>(&w.stats[(int64_t)t * OMQ_NSTATS + tid]),
-              s_st[tid]);
+  if (tid == 0) {
+    int run = 0;
+    for (int k = 0; k < kTaskClasses; ++k) {
+      const int v = sh.hist[k];
+      f.tcls[t * kTaskClasses + k] = v;
+      sh.hist[kTaskClasses + k] = run;
+      run += v;
+    }
+    f.ntask[t] = n;
+    f.tinfo[t] = d | (vl_done ? 256 : 0);
+  }
+  __syncthreads();
+  int32_t* tasks = f.tasks + (int64_t)t * MW * 2;
+  for (int i = tid; i < n; i += NT) {
+    const int gi = i < nb ? i : W - 1 - (i - nb);
+    const uint32_t sl = L.gsl[cur * W + gi];
+    const int pos = atomicAdd(&sh.hist[kTaskClasses + task_class((int)(sl >> 16))], 1);
+    tasks[2 * pos] = (int)L.gnode[cur * W + gi];
+    tasks[2 * pos + 1] = (int)sl;
+  }
+}
+
+// ---- Kernels ---------------------------------------------------------------------------
+// The root kernel: one workgroup per tree.  SPLIT: levels below dend are left to the subtree
+// kernel as tasks; otherwise the whole selection runs here, with the unique-leaf pass.
+template <int RMAX, int NT, bool SPLIT>
+__global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c) {
+  // the level overlap in the kernels whose chains keep their registers with a second copy of
+  // the chain code (the followers'), with a full workgroup of followers
+  constexpr bool kPipe = RMAX <= 3 && NT == 1024;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ LevelShared<NT> sh;
+  __shared__ int s_glog;
+  const int W = c.W;
+  const LevelLds L = carve_level_lds<NT>(smem, W, kPipe);
+  const int t = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t tb = (int64_t)t * f.capacity;
+  const int MW = f.max_wave;
+  int32_t* lflag = f.lflag + (int64_t)t * MW;
+  int32_t* lfs = f.lfs + (int64_t)t * MW;
+  // the level overlap needs an internal root, an integer virtual loss and the ordered mode
+  const int root_k = f.nchild[tb], root_first = f.first[tb];
+  const bool pipe = kPipe && L.pick2 != nullptr && W > kWave && !c.vl_atomic && c.vli > 0 &&
+                    c.max_depth >= 2 && root_k > 0 && root_first >= 0 &&
+                    root_k <= RMAX * kWave;
+  for (int s = tid; s < W; s += NT) {
+    lflag[s] = 0;
+    if (L.pick2 != nullptr) L.pick2[s] = kPickNone;
+  }
+  if (tid == 0) s_glog = 0;
+  start_group<RMAX, NT>(L, sh, W, 0, 0, 0, W, nullptr);
+  const int dend = SPLIT ? (pipe ? 2 : 1) : c.max_depth;
+  const int d = level_loop<RMAX, NT>(f, c, t, 0, dend, W, L, sh, &s_glog, lfs, lflag, pipe,
+                                     root_first, pipe ? 2 : -1);
+  if (SPLIT) {
+    export_tasks<NT>(f, t, d, pipe && d == 2, W, L, sh);
+  } else {
+    __syncthreads();
+    finish_tree<NT>(f, t, W, lfs, lflag, sh.wtot);
+  }
+  __syncthreads();
+  if (tid == 0) f.gcount[t] = s_glog;  // (the subtree kernel adds its groups)
+  flush_stats<NT>(f, t, sh);
+}
+
+// The subtree kernel: persistent workgroups dealing the subtree tasks of every tree.
+template <int RMAX>
+__global__ __launch_bounds__(kSubThreads, 4) void select_subtree_kernel(SelArgs f, SelCfg c) {
+  constexpr int NT = kSubThreads;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ LevelShared<NT> sh;
+  __shared__ int s_off[kTaskClasses * kSplitMaxTrees];  // first global index of (class, tree)
+  __shared__ int s_base[kTaskClasses + 1];               // first global index of a class
+  __shared__ int s_job[3];                               // tree, node, seg | m << 16
+  const int W = c.W;
+  const LevelLds L = carve_level_lds<NT>(smem, W, false);
+  const int tid = threadIdx.x;
+  const int T = f.num_trees;
+  const int MW = f.max_wave, MD = f.max_depth_buf;
+  // global task order: size class, then tree, then the tree's order
+  for (int i = tid; i < kTaskClasses * T; i += NT) {
+    const int k = i / T, tt = i - k * T;
+    s_off[i] = f.tcls[tt * kTaskClasses + k];
+  }
+  __syncthreads();
+  if (tid < kTaskClasses) {  // per class: exclusive prefix over the trees, in place
+    int run = 0;
+    for (int tt = 0; tt < T; ++tt) {
+      const int v = s_off[tid * T + tt];
+      s_off[tid * T + tt] = run;
+      run += v;
+    }
+    s_base[tid + 1] = run;  // class total, for now
+  }
+  __syncthreads();
+  if (tid == 0) {
+    s_base[0] = 0;
+    for (int k = 0; k < kTaskClasses; ++k) s_base[k + 1] += s_base[k];
+  }
+  __syncthreads();
+  for (int i = tid; i < kTaskClasses * T; i += NT) s_off[i] += s_base[i / T];
+  __syncthreads();
+  const int ntot = s_base[kTaskClasses];
+  // Tasks are dealt round-robin in the global order (largest size class first): workgroup b
+  // takes tasks b, b + grid, ...  (A shared task counter would put every workgroup's fetch
+  // behind one contended device-scope atomic.)
+  for (int g = blockIdx.x; g < ntot; g += gridDim.x) {
+    if (tid == 0) {
+      {
+        int k = 0;
+        while (k + 1 < kTaskClasses && s_base[k + 1] <= g) ++k;
+        int lo = 0, hi = T - 1;  // the last tree whose class-k range starts at or before g
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (s_off[k * T + mid] <= g) lo = mid; else hi = mid - 1;
+        }
+        const int tt = lo;
+        int cstart = 0;
+        for (int k2 = 0; k2 < k; ++k2) cstart += f.tcls[tt * kTaskClasses + k2];
+        const int i = cstart + (g - s_off[k * T + tt]);
+        const int32_t* tasks = f.tasks + (int64_t)tt * MW * 2;
+        s_job[0] = tt;
+        s_job[1] = tasks[2 * i];
+        s_job[2] = tasks[2 * i + 1];
+      }
+    }
+    __syncthreads();
+    const int t = s_job[0], p = s_job[1];
+    const uint32_t sl = (uint32_t)s_job[2];
+    const int seg = (int)(sl & 0xFFFFu), m = (int)(sl >> 16);
+    const int info = f.tinfo[t];
+    const int d0 = info & 255;
+    const uint16_t* src = f.gmembers + ((int64_t)t * MD + d0) * MW + seg;
+    start_group<RMAX, NT>(L, sh, W, d0, p, seg, m, src);
+    level_loop<RMAX, NT>(f, c, t, d0, c.max_depth, W, L, sh, f.gcount + t,
+                         f.lfs + (int64_t)t * MW, f.lflag + (int64_t)t * MW, false, 0,
+                         (info & 256) ? d0 : -1);
+    __syncthreads();
+    flush_stats<NT>(f, t, sh);
+    __syncthreads();
+  }
+}
+
+// The unique-leaf pass of the split schedule: one workgroup per tree.
+constexpr int kFinishThreads = 1024;
+__global__ __launch_bounds__(kFinishThreads) void select_finish_kernel(SelArgs f, SelCfg c) {
+  __shared__ int s_wtot[kFinishThreads / kWave];
+  const int t = blockIdx.x;
+  const int MW = f.max_wave;
+  finish_tree<kFinishThreads>(f, t, c.W, f.lfs + (int64_t)t * MW, f.lflag + (int64_t)t * MW,
+                              s_wtot);
 }
 
 }  // namespace omq
@@ -1503,10 +1845,67 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs f, SelCfg c
 // ---- host launcher (C++ linkage; the C ABI wrappers live in capi.hip) ----
 namespace omq {
 
-size_t select_lds_bytes(int W) {
-  if (W > kPipeMaxW) return select_base_bytes(W);
-  return pipe_offset(W) + (size_t)kSelWaves * kWave * 4 + (size_t)W * 2;
+namespace {
+std::atomic<int> g_split_mode{0};          // 0 automatic, 1 whole, 2 split
+std::atomic<int> g_spin_limit{1 << 22};    // polls of a follower's bounded wait
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];  // 0: not known yet
+std::atomic<bool> g_attr_set[kMaxDevices][3][9];
+
+// Threads of the whole-wave kernel.  (512 threads for the 6-slot kernel, which lets its chains
+// keep 256 registers, made C3's level-1 chains slower than the spills they save: 8 waves for
+// its 40-130 level-1 groups.)
+template <int RMAX>
+constexpr int whole_threads() {
+  return 1024;
 }
+
+template <int RMAX>
+const void* root_kernel(bool split) {
+  if (!split) return (const void*)select_root_kernel<RMAX, whole_threads<RMAX>(), false>;
+  if (RMAX <= 3) return (const void*)select_root_kernel<RMAX, 1024, true>;
+  return (const void*)select_root_kernel<RMAX, 256, true>;
+}
+
+struct SelKernels {
+  const void* root;
+  const void* sub;
+  int root_threads;
+};
+
+SelKernels pick_kernels(int rmax, bool split) {
+  SelKernels k{};
+  switch (rmax) {
+#define OMQ_PICK(R)                                            \
+  case R:                                                      \
+    k.root = root_kernel<R>(split);                            \
+    k.sub = (const void*)select_subtree_kernel<R>;             \
+    k.root_threads = split ? (R > 3 ? 256 : 1024) : whole_threads<R>(); \
+    break;
+    OMQ_PICK(1)
+    OMQ_PICK(2)
+    OMQ_PICK(3)
+    OMQ_PICK(4)
+    OMQ_PICK(5)
+    OMQ_PICK(6)
+    default:
+    OMQ_PICK(8)
+#undef OMQ_PICK
+  }
+  return k;
+}
+}  // namespace
+
+void select_set_options(int split_mode, int spin_limit) {
+  g_split_mode.store(split_mode, std::memory_order_relaxed);
+  g_spin_limit.store(spin_limit, std::memory_order_relaxed);
+}
+
+bool select_split_fits(int num_trees, int W) {
+  return num_trees <= kSplitMaxTrees && W >= 1;
+}
+
+size_t select_lds_bytes(int W) { return level_lds_bytes<1024>(W, true); }
 
 hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_puct,
                          float virtual_loss, int max_depth, int vl_atomic, hipStream_t stream) {
@@ -1517,34 +1916,35 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   c.vli = (int)virtual_loss;
   c.max_depth = max_depth;
   c.vl_atomic = vl_atomic;
-  const size_t lds = select_lds_bytes(W);
+  c.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   // widest row the game model can produce: every legal action (board games) or max_legal
   const int max_row = f.game == OMQ_GAME_SPARSE ? f.max_legal : f.num_actions;
   int rmax = (max_row + kWave - 1) / kWave;
+  if (rmax < 1) rmax = 1;
   if (rmax > 6) rmax = 8;
-  const void* kern = nullptr;
-  switch (rmax) {
-    case 0:
-    case 1: kern = (const void*)select_kernel<1>; break;
-    case 2: kern = (const void*)select_kernel<2>; break;
-    case 3: kern = (const void*)select_kernel<3>; break;
-    case 4: kern = (const void*)select_kernel<4>; break;
-    case 5: kern = (const void*)select_kernel<5>; break;
-    case 6: kern = (const void*)select_kernel<6>; break;
-    default: kern = (const void*)select_kernel<8>; break;
-  }
-  // the LDS limit is raised once per device and kernel width (the attribute is idempotent, so
-  // two threads racing here both set it)
-  constexpr int kMaxDevices = 64;
-  static std::atomic<bool> attr_set[kMaxDevices][9];
+  // The schedule: one workgroup per tree unless the split schedule is asked for (it measured
+  // slower on every workload: a subtree task pays a few microseconds of barriers and dependent
+  // loads per level, and the largest subtree of a wave runs on one workgroup).
+  const int mode = g_split_mode.load(std::memory_order_relaxed);
+  const bool split = select_split_fits(f.num_trees, W) && mode == 2;
+  const SelKernels k = pick_kernels(rmax, split);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= kMaxDevices || !attr_set[dev][rmax].load(std::memory_order_acquire)) {
-    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)select_lds_bytes(OMQ_MAX_WAVE));
+  const bool cache = dev >= 0 && dev < kMaxDevices;
+  // the LDS limit is raised once per device and kernel (the attribute is idempotent, so two
+  // threads racing here both set it)
+  const int slot = split ? 1 : 0;
+  if (!cache || !g_attr_set[dev][slot][rmax].load(std::memory_order_acquire)) {
+    e = hipFuncSetAttribute(k.root, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)level_lds_bytes<1024>(OMQ_MAX_WAVE, true));
     if (e != hipSuccess) return e;
-    if (dev >= 0 && dev < kMaxDevices) attr_set[dev][rmax].store(true, std::memory_order_release);
+    if (split) {
+      e = hipFuncSetAttribute(k.sub, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)level_lds_bytes<kSubThreads>(OMQ_MAX_WAVE, false));
+      if (e != hipSuccess) return e;
+    }
+    if (cache) g_attr_set[dev][slot][rmax].store(true, std::memory_order_release);
   }
   SelArgs a;
   a.N = f.visit_counts;
@@ -1567,8 +1967,44 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   a.capacity = f.capacity;
   a.max_wave = w.max_wave;
   a.max_depth_buf = w.max_depth;
+  a.num_trees = f.num_trees;
+  const int64_t TM = (int64_t)f.num_trees * w.max_wave;
+  a.lflag = w.sel_scratch;
+  a.lfs = w.sel_scratch + TM;
+  a.tasks = w.sel_scratch + 2 * TM;
+  a.ntask = w.sel_scratch + 4 * TM;
+  a.tinfo = a.ntask + f.num_trees;
+  a.tcls = a.tinfo + f.num_trees;
+  a.ctl = a.tcls + (int64_t)f.num_trees * kTaskClasses;
   void* args[] = {&a, &c};
-  e = hipLaunchKernel(kern, dim3(f.num_trees), dim3(kSelThreads), args, lds, stream);
+  const size_t lds_root = k.root_threads == 1024  ? level_lds_bytes<1024>(W, true)
+                          : k.root_threads == 512 ? level_lds_bytes<512>(W, false)
+                                                  : level_lds_bytes<256>(W, false);
+  e = hipLaunchKernel(k.root, dim3(f.num_trees), dim3(k.root_threads), args, lds_root, stream);
+  if (e != hipSuccess) return e;
+  e = hipGetLastError();
+  if (e != hipSuccess || !split) return e;
+  // Subtree workgroups: as many as fit on the chip at once (at most 4 per CU: the chains'
+  // 128 registers per lane), and no more than the simulations could make tasks.
+  int cus = cache ? g_cu_count[dev].load(std::memory_order_relaxed) : 0;
+  if (cus <= 0) {
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    if (cache) g_cu_count[dev].store(cus, std::memory_order_relaxed);
+  }
+  const size_t lds_sub = level_lds_bytes<kSubThreads>(W, false) + 8 * 1024;
+  int per_cu = (int)((160 * 1024) / lds_sub);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 4 ? 4 : per_cu);
+  int64_t blocks = (int64_t)cus * per_cu;
+  if (blocks > TM) blocks = TM;
+  if (blocks < 1) blocks = 1;
+  e = hipLaunchKernel(k.sub, dim3((unsigned)blocks), dim3(kSubThreads), args,
+                      level_lds_bytes<kSubThreads>(W, false), stream);
+  if (e != hipSuccess) return e;
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = hipLaunchKernel((const void*)select_finish_kernel, dim3(f.num_trees), dim3(kFinishThreads),
+                      args, 0, stream);
   if (e != hipSuccess) return e;
   return hipGetLastError();
 }

@@ -59,3 +59,71 @@ def test_wave_parity(case, device):
           flush=True)
     n = run_parity(wl, check_every=CHECK_EVERY.get(case, 1), device=device)
     assert n >= 2
+
+
+# The split schedule of omq_select (root chains, then subtree tasks over the whole chip, then
+# the unique-leaf pass; omq_select_options split_mode 2) must give the same waves.
+SPLIT_CASES = ["C2-small", "C3-small", "C3-capacity", "C4-small", "overlap-ragged",
+               "overlap-depth2", "overlap-knobs", "uniform-priors-C2", "negative-cpuct"]
+
+
+@pytest.fixture
+def split_schedule():
+    from omoknuni_quantum_amd import _lib
+
+    lib = _lib.load()
+    _lib.check(lib.omq_select_options(2, _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
+    yield
+    _lib.check(lib.omq_select_options(0, _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_wave_parity_split_schedule(case, device, split_schedule):
+    name, kw = CASES[case]
+    wl = get(name).scaled(name=case + "-split", **kw)
+    print(f"[parity split] {case}: T={wl.num_trees} sims={wl.num_simulations} "
+          f"W={wl.wave_size}", flush=True)
+    assert run_parity(wl, check_every=1, device=device) >= 2
+
+
+@pytest.mark.gpu
+def test_follower_wait_running_out(device):
+    """A follower whose bounded wait runs out (spin limit 0, set from the host) sets
+    OMQ_STATUS_STALL; the kernel exits normally, every path stays inside its tree, and the
+    engine searches on after a reset."""
+    import numpy as np
+    import torch
+
+    from omoknuni_quantum_amd import _lib
+    from oracle.parity import make_pair
+
+    lib = _lib.load()
+    wl = get("C4").scaled(name="stall", num_trees=2, num_simulations=600, wave_size=200,
+                          capacity=100_000)
+    eng, orc, ev = make_pair(wl, device=device)
+    eng.reset()
+    eng.run_wave(1, ev)
+    eng.run_wave(wl.wave_size, ev)  # an expanded first level, so that the overlap runs
+    try:
+        _lib.check(lib.omq_select_options(0, 0), "omq_select_options")
+        eng.select(wl.wave_size)
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(lib.omq_select_options(0, _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
+    assert int(eng.status[0].item()) & _lib.OMQ_STATUS_STALL
+    with pytest.raises(_lib.OmqError):
+        eng.check_status()
+    T, MW = eng.T, eng.MW
+    plen = eng.path_len.view(T, MW)[:, :wl.wave_size].cpu().numpy()
+    leaves = eng.leaves.view(T, MW)[:, :wl.wave_size].cpu().numpy()
+    nn = eng.num_nodes.cpu().numpy()
+    assert np.all((plen >= 1) & (plen <= 2))  # the held-up members end at their level-1 node
+    assert np.all((leaves >= 0) & (leaves < nn[:, None]))
+    # a reset clears the status; the same engine then searches without error
+    eng.reset()
+    eng.check_status()
+    eng.search(wl.num_simulations, wl.wave_size, ev)
+    eng.check_status()
+    # and a fresh pair follows the oracle bit for bit
+    assert run_parity(wl, check_every=2, device=device) >= 2
