@@ -5,9 +5,12 @@ num_simulations simulations are run in waves (select -> synthetic evaluator -> e
 backup).  Inputs are resident in HBM before the timed region.  The metric is tree-operation
 simulations per second: simulations / time of the tree-operation kernels (select, leaf info,
 expand, backup), measured with HIP events on the launch stream; the synthetic evaluator is
-timed apart.  Prints one JSON line.
+timed apart.  Prints one JSON line: the headline workload (C3, the largest single-GPU config)
+at the top level, then every other workload of the benchmark under "configs", each with its
+roofline, CPU baseline and full-size parity check.
 
-    python bench.py [--steps K] [--warmup W] [--config C2] [--cpu-baseline auto|skip]
+    python bench.py [--steps K] [--warmup W] [--config C3] [--configs all|none|C1,C2,...]
+                    [--cpu-baseline auto|skip] [--select-schedule auto|whole|split]
 """
 from __future__ import annotations
 
@@ -52,8 +55,21 @@ def algorithmic_bytes(st: dict, sims: int) -> dict:
 
 SCHEDULES = {"auto": 0, "whole": 1, "split": 2}
 
-KERNEL_OF_PHASE = {"select": "select_kernel", "leaf_info": "leaf_info_kernel",
+KERNEL_OF_PHASE = {"select": "select_root_kernel", "leaf_info": "leaf_info_kernel",
                    "expand": "expand_write_kernel", "backup": "backup_groups_kernel"}
+ALL_CONFIGS = ("C1", "C2", "C3", "C4", "C5")
+
+
+def parse_configs(spec: str) -> list[str]:
+    if spec == "all":
+        return list(ALL_CONFIGS)
+    if spec in ("", "none"):
+        return []
+    out = [s.strip() for s in spec.split(",") if s.strip()]
+    for s in out:
+        if s not in ALL_CONFIGS:
+            raise SystemExit(f"unknown workload {s!r}: one of {', '.join(ALL_CONFIGS)}")
+    return out
 
 
 def measured_traffic(workload: str, phase: str, args):
@@ -72,21 +88,13 @@ def measured_traffic(workload: str, phase: str, args):
     return int(e["bytes_per_dispatch"]), e["source"]
 
 
-def run(args) -> dict:
+def _engine(wl, args, dev):
     import torch
 
     from omoknuni_quantum_amd import _lib
     from omoknuni_quantum_amd.core.engine import SearchParams, WaveEngine
-    from omoknuni_quantum_amd.core.timing import PhaseTimer
     from omoknuni_quantum_amd.synthetic.evaluator import SyntheticEvaluator
-    from omoknuni_quantum_amd.synthetic.workloads import get
 
-    wl = get(args.config)
-    if args.trees:
-        wl = wl.scaled(num_trees=args.trees)
-    dev = torch.device("cuda:0")
-    _lib.check(_lib.load().omq_select_options(SCHEDULES[args.select_schedule],
-                                              _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
     params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth,
                           expand_policy=_lib.OMQ_EXPAND_FULL,
                           w_mode=_lib.OMQ_WACC_ATOMIC if args.w_mode == "atomic" else _lib.OMQ_WACC_ORDERED,
@@ -100,8 +108,24 @@ def run(args) -> dict:
         ev = ResNetEvaluator(eng, boards)
     else:
         ev = SyntheticEvaluator(wl.logit_scale)
+    return eng, ev
 
-    if args.copy_probe_mib > 0:
+
+def measure(name: str, args, steps: int, warmup: int, extras: bool) -> dict:
+    """One workload: warm-up searches, then `steps` timed searches (tree operations timed by
+    HIP events on the launch stream), the roofline of the dominant kernel, and (unless
+    skipped) the CPU baseline with the full-size parity check against it."""
+    import torch
+
+    from omoknuni_quantum_amd.core.timing import PhaseTimer
+    from omoknuni_quantum_amd.synthetic.workloads import get
+
+    wl = get(name)
+    if args.trees:
+        wl = wl.scaled(num_trees=args.trees)
+    dev = torch.device("cuda:0")
+    eng, ev = _engine(wl, args, dev)
+    if args.copy_probe_mib > 0 and extras:
         # one plain device copy of known size, outside the timed region: the reference point
         # that scales the HBM counters (FETCH_SIZE / WRITE_SIZE) of a --pmc profile of this run
         n = args.copy_probe_mib * (1 << 20) // 4
@@ -110,21 +134,21 @@ def run(args) -> dict:
         dst.copy_(src)
         torch.cuda.synchronize(dev)
         del src, dst
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         eng.search(wl.num_simulations, wl.wave_size, ev)
     torch.cuda.synchronize(dev)
     eng.stats.zero_()
     timer = PhaseTimer(dev)
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         eng.search(wl.num_simulations, wl.wave_size, ev, timer)
     torch.cuda.synchronize(dev)
     t1 = time.perf_counter()
     eng.check_status()
     tot = timer.totals_ms()
     st = eng.host_stats()
-    sims = wl.num_trees * wl.num_simulations * args.steps
+    sims = wl.num_trees * wl.num_simulations * steps
     tree_ms = sum(tot.get(p, 0.0) for p in TREE_PHASES)
     eval_ms = tot.get("eval", 0.0)
     value = sims / (tree_ms / 1e3)
@@ -142,7 +166,7 @@ def run(args) -> dict:
     d_s = tot[dominant] / 1e3 / dn
     achieved = d_bytes / d_s / 1e9
     traffic, traffic_src = measured_traffic(wl.name, dominant, args)
-    roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 2),
+    roofline = {"bound": "hbm", "kernel": KERNEL_OF_PHASE[dominant], "achieved": round(achieved, 2),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
                 "traffic": traffic, "algorithmic_bytes_per_launch": int(d_bytes),
                 "us_per_launch": round(d_s * 1e6, 3)}
@@ -150,26 +174,17 @@ def run(args) -> dict:
         roofline["traffic_source"] = traffic_src
     whole_bytes = sum(ab.values())
     out = {
-        "metric": METRIC,
         "value": round(value, 1),
-        "unit": "simulations/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(1e3 * (t1 - t0) / args.steps, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp32",
-        "data": "synthetic",
+        "ms_per_step": round(1e3 * (t1 - t0) / steps, 3),
         "config": {"workload": wl.name, "trees": wl.num_trees,
                    "simulations_per_tree": wl.num_simulations, "wave": wl.wave_size,
                    "capacity": wl.capacity, "game": wl.model.kind,
                    "actions": wl.model.num_actions, "w_mode": args.w_mode,
-                   "vl_atomic": bool(args.vl_atomic), "parallelism": "none (1 GPU)"},
+                   "vl_atomic": bool(args.vl_atomic), "select_schedule": args.select_schedule,
+                   "parallelism": "none (1 GPU)"},
         "roofline": roofline,
-        "tree_op_ms_per_step": round(tree_ms / args.steps, 4),
-        "eval_ms_per_step": round(eval_ms / args.steps, 4),
+        "tree_op_ms_per_step": round(tree_ms / steps, 4),
+        "eval_ms_per_step": round(eval_ms / steps, 4),
         "end_to_end_sims_per_s": round(sims / (t1 - t0), 1),
         "tree_op_algorithmic_GBps": round(whole_bytes / (tree_ms / 1e3) / 1e9, 2),
         "phases": phases,
@@ -183,7 +198,7 @@ def run(args) -> dict:
                             f"{wl.num_trees * wl.wave_size} positions")
         out["tree_op_share"] = round(tree_ms / (tree_ms + eval_ms), 4)
         out["end_to_end_gpu_sims_per_s"] = round(sims / ((tree_ms + eval_ms) / 1e3), 1)
-    if args.graph and wl.evaluator == "synthetic":
+    if extras and args.graph and wl.evaluator == "synthetic":
         out["graph"] = graph_replay(wl, eng, ev, args)
     if args.cpu_baseline != "skip":
         replay = None
@@ -194,8 +209,42 @@ def run(args) -> dict:
             torch.cuda.synchronize(dev)
             replay = ev.calls
         out["cpu_baseline"], out["parity_full_size"] = cpu_baseline(wl, eng, args, replay)
-    if args.next_rows != "skip":
+    if extras and args.next_rows != "skip":
         out["next_rows"] = next_rows(wl, eng, ev)
+    del eng, ev
+    torch.cuda.empty_cache()
+    return out
+
+
+def run(args) -> dict:
+    from omoknuni_quantum_amd import _lib
+
+    _lib.check(_lib.load().omq_select_options(SCHEDULES[args.select_schedule],
+                                              _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
+    head = measure(args.config, args, args.steps, args.warmup, extras=True)
+    out = {
+        "metric": METRIC,
+        "value": head.pop("value"),
+        "unit": "simulations/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+    }
+    out.update(head)
+    others = [c for c in parse_configs(args.configs) if c != args.config]
+    if others:
+        table = {}
+        for name in others:
+            e = measure(name, args, args.steps, min(args.warmup, 2), extras=False)
+            e.pop("counters", None)
+            table[name] = e
+        out["configs"] = table
     return out
 
 
@@ -341,10 +390,22 @@ def next_rows(wl, eng, ev) -> dict:
     return out
 
 
+# Host threads of the CPU baseline: one tree per thread, at most the CPU share of one GPU on
+# the benchmark boxes (16 cores per GPU), whatever nproc reports there.
+CPU_SHARE = 16
+
+
+def _cpu_threads(T: int, args) -> tuple[int, int]:
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    want = args.cpu_threads or min(CPU_SHARE, avail)
+    return max(1, min(want, T)), avail
+
+
 def cpu_baseline(wl, eng, args, replay=None):
-    """The C oracle timed on the host on the same workload (one thread, then one tree per thread
-    on all threads), then its final
-    trees compared bit for bit with the GPU's (state after the last timed search)."""
+    """The C oracle (the CPU restatement of the reference tree path, gcc -O3) timed on the host
+    on the same workload: the median of 5 searches after one warm-up, one tree per thread; and
+    one thread on a bounded sample.  Its final trees are then compared bit for bit with the
+    GPU's (the state after the last timed search: both searched the same roots)."""
     from oracle.oracle import Oracle
     from oracle.parity import EXPAND_CODES
 
@@ -355,6 +416,7 @@ def cpu_baseline(wl, eng, args, replay=None):
                    wl.dirichlet_epsilon)
     orc.set_roots(keys[:T], None if legal is None else legal[:T],
                   None if noise is None else noise[:T])
+    reps = 5
     if replay is not None:
         # evaluator outputs recorded on the GPU, replayed wave by wave (one thread)
         sizes = [1]
@@ -363,38 +425,46 @@ def cpu_baseline(wl, eng, args, replay=None):
             sizes.append(min(wl.wave_size, wl.num_simulations - done))
             done += sizes[-1]
         assert len(sizes) == len(replay)
-        t0 = time.perf_counter()
-        for t in range(T):
-            orc.reset_tree(t)
-            for (pol, val), W in zip(replay, sizes):
-                orc.wave(t, W, replay_policy=pol[t], replay_values=val[t])
-        dt = time.perf_counter() - t0
+        times = []
+        for _ in range(1 + reps):
+            t0 = time.perf_counter()
+            for t in range(T):
+                orc.reset_tree(t)
+                for (pol, val), W in zip(replay, sizes):
+                    orc.wave(t, W, replay_policy=pol[t], replay_values=val[t])
+            times.append(time.perf_counter() - t0)
+        dt = float(np.median(times[1:]))
         cpu = {"value": round(T * wl.num_simulations / dt, 1), "unit": "simulations/s",
                "cores": 1, "kind": "port",
                "sample": f"{T} of {wl.num_trees} trees x {wl.num_simulations} simulations of "
                          f"{wl.name}, tree operations only with the GPU run's evaluator outputs "
-                         f"replayed ({dt:.2f} s, C oracle, gcc -O3, one thread)"}
+                         f"replayed; median of {reps} after 1 warm-up ({dt:.3f} s per search, "
+                         "C oracle, gcc -O3, one thread)"}
     else:
-        # single thread: the first tree(s), about 10 s of work at most
+        threads, avail = _cpu_threads(T, args)
+        times = []
+        for _ in range(1 + reps):
+            t0 = time.perf_counter()
+            orc.search(wl.num_simulations, wl.wave_size, wl.max_depth, nthreads=threads)
+            times.append(time.perf_counter() - t0)
+        dt = float(np.median(times[1:]))
+        # single thread: whole trees, about 2 s of work at most
         t0 = time.perf_counter()
         t1 = 0
-        while t1 < T and (t1 == 0 or time.perf_counter() - t0 < 10.0):
+        while t1 < T and (t1 == 0 or time.perf_counter() - t0 < 2.0):
             orc.lib.orc_search_tree(orc.f, t1, wl.num_simulations, wl.wave_size, wl.max_depth)
             t1 += 1
         dt1 = time.perf_counter() - t0
         single = t1 * wl.num_simulations / dt1
-        # all threads: every tree of the sample, one tree at a time per thread
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1, T)
-        t0 = time.perf_counter()
-        orc.search(wl.num_simulations, wl.wave_size, wl.max_depth, nthreads=threads)
-        dt = time.perf_counter() - t0
+        # (each search resets its trees: the last one leaves every tree as one full search)
         cpu = {"value": round(T * wl.num_simulations / dt, 1), "unit": "simulations/s",
                "cores": threads, "kind": "port",
                "sample": f"{T} of {wl.num_trees} trees x {wl.num_simulations} simulations of "
-                         f"{wl.name} on {threads} threads, one tree per thread ({dt:.2f} s, C "
-                         f"oracle, gcc -O3); single thread: {single:.1f} sims/s over {t1} "
-                         f"tree(s) ({dt1:.2f} s)",
-               "single_thread_value": round(single, 1)}
+                         f"{wl.name}, one tree per thread on {threads} threads (the CPU share of "
+                         f"one GPU on this box; {avail} cores visible), median of {reps} "
+                         f"searches after 1 warm-up ({dt:.3f} s per search; C oracle, gcc -O3); "
+                         f"single thread: {single:.1f} sims/s over {t1} tree(s) ({dt1:.2f} s)",
+               "single_thread_value": round(single, 1), "host_cores_visible": avail}
     ok = True
     mismatch = None
     w_exact = args.w_mode == "ordered"
@@ -422,7 +492,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="C2")
+    ap.add_argument("--config", default="C3",
+                    help="the headline workload (the largest single-GPU config, C3, by default)")
+    ap.add_argument("--configs", default="all",
+                    help="workloads measured after the headline, in the same run: all, none, or "
+                         "a comma-separated list of C1..C5")
     ap.add_argument("--trees", type=int, default=0, help="override the workload's tree count")
     ap.add_argument("--w-mode", choices=("ordered", "atomic"), default="ordered")
     ap.add_argument("--select-schedule", choices=tuple(SCHEDULES), default="auto",
@@ -433,7 +507,7 @@ def main():
     ap.add_argument("--cpu-trees", type=int, default=0,
                     help="trees of the CPU baseline sample (0 = all)")
     ap.add_argument("--cpu-threads", type=int, default=0,
-                    help="threads of the CPU baseline (0 = min(16, cores, trees))")
+                    help="threads of the CPU baseline (0 = min(16, visible cores, trees))")
     ap.add_argument("--graph", action="store_true",
                     help="also time the search replayed from one HIP graph")
     ap.add_argument("--next-rows", choices=("auto", "skip"), default="auto",

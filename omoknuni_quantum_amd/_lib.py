@@ -109,8 +109,13 @@ _lock = threading.Lock()
 
 
 def load(path: str | None = None) -> ctypes.CDLL:
-    """Load the HIP library once; raise LibraryNotBuilt when it is absent."""
+    """Load the HIP library once; raise LibraryNotBuilt when it is absent.  torch is imported
+    first: the library then binds the HIP runtime torch has loaded, so that both share one
+    runtime (loaded first, the library would bring the system's and torch its own, and the
+    second runtime finds no device)."""
     global _lib
+    import torch  # noqa: F401  (the HIP runtime the library shares)
+
     with _lock:
         if _lib is not None and path is None:
             return _lib
