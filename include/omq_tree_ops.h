@@ -76,6 +76,11 @@ extern "C" {
 #define OMQ_TERM_WIN1 1  /* player 1 has five */
 #define OMQ_TERM_WIN2 2  /* player 2 has five */
 #define OMQ_TERM_DRAW 3  /* full board without five */
+#define OMQ_TERM_END 4   /* Go: two consecutive passes, or no empty point (omq_go_rules) */
+
+/* flags of omq_go_rules */
+#define OMQ_GO_KO 1       /* the root's ko point (root_ko) is not a legal move in the tree */
+#define OMQ_GO_SUICIDE 2  /* a point without an empty orthogonal neighbour is not a legal move */
 
 /* workspace of omq_shift_root: int32 entries per node of capacity, per tree */
 #define OMQ_SHIFT_WORKSPACE_PER_NODE 8
@@ -143,6 +148,12 @@ typedef struct omq_wave {
   int32_t* sel_scratch;     /* [OMQ_SEL_SCRATCH_INTS(T, max_wave)] omq_select's scratch: per-
                                simulation leaf records and the subtree tasks of its split
                                schedule (no contents to keep between calls) */
+  uint32_t* umask;          /* NULL, or [T*max_wave*legal_words]: legal-action masks of the unique
+                               leaves, written by omq_go_rules.  When it is not NULL,
+                               omq_synthetic_evaluate and omq_expand take a board leaf's legal
+                               actions from it (the caller then runs omq_go_rules after
+                               omq_leaf_info in every wave) instead of the root mask minus the
+                               path's cells. */
 } omq_wave;
 
 /* int32 entries of omq_wave::sel_scratch for T trees of max_wave simulations */
@@ -255,6 +266,36 @@ int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
 int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
                         const int32_t* root_player, int32_t rule, int32_t* uterminal,
                         void* stream);
+
+/* Go rules of every unique leaf of the wave; call it after omq_leaf_info and before the
+ * evaluator and omq_expand.  Needs an OMQ_GAME_GO forest with num_actions = bs*bs + 1 (the pass
+ * is action bs*bs), w->umask set, and the root positions root_boards [T*bs*bs] (int8: 0 empty,
+ * 1 and 2 stones).
+ * - Position.  A leaf's position is its root board with the path's moves played in alternating
+ *   colours from root_player[t] (NULL: 1 when the root board holds an even number of stones,
+ *   else 2); a pass places no stone.  No stone is captured, as in the reference's GPU game
+ *   states (GPUGameStates.apply_moves, python/mcts/gpu/gpu_game_states.py:405-460).
+ * - Legal moves (umask).  The empty points, except: with OMQ_GO_KO, root_ko[t] (a point, or -1
+ *   for none) at every node of the tree (GPUGameStates.get_legal_moves_mask,
+ *   gpu_game_states.py:373-395, excludes a state's ko point; clone_states, :336-337, copies it
+ *   from parent to child and apply_moves never updates it, so the root's ko point holds in the
+ *   whole tree); with OMQ_GO_SUICIDE, the points without an empty orthogonal neighbour (the
+ *   simplified suicide rule of gpu_get_legal_moves, python/mcts/gpu/go_kernels.py:46-110).
+ *   The pass is always legal.
+ * - Terminal (gpu_check_terminal_states, go_kernels.py:17-44).  A leaf whose path ends in two
+ *   consecutive passes (the root's own trailing passes root_passes[t] counting when every path
+ *   move is a pass; NULL: 0), or whose position has no empty point (that function's legal
+ *   moves are the empty points: it passes no player), is terminal: uterminal OMQ_TERM_END and
+ *   ulegal 0, so omq_expand leaves it unexpanded.  The root (a path of length 1) is never
+ *   terminal.  (The reference's FastTerminalChecker.check_terminal_gpu,
+ *   python/mcts/utils/fast_terminal_check.py:87-93, hands that function zero pass counts;
+ *   here the passes are counted.)
+ * - Otherwise ulegal is the number of legal moves.  uterminal, when not NULL, is [T*max_wave].
+ * Replaces the Go legality and terminal checks of the reference's GPU game states
+ * (gpu_game_states.py:373-395, go_kernels.py:17-110), which its GPU search runs per leaf. */
+int omq_go_rules(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
+                 const int32_t* root_player, const int32_t* root_passes, const int32_t* root_ko,
+                 int32_t flags, int32_t* uterminal, void* stream);
 
 /* Neural-network feature planes of every wave slot of a Gomoku forest; call it after
  * omq_leaf_info.  Needs an OMQ_GAME_BOARD forest with num_actions = bs*bs.

@@ -29,7 +29,8 @@ STAT_NAMES = [
 ]
 OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT, OMQ_STATUS_STALL = 1, 2, 4
 OMQ_RULE_FREESTYLE, OMQ_RULE_RENJU = 0, 1
-OMQ_TERM_NONE, OMQ_TERM_WIN1, OMQ_TERM_WIN2, OMQ_TERM_DRAW = 0, 1, 2, 3
+OMQ_TERM_NONE, OMQ_TERM_WIN1, OMQ_TERM_WIN2, OMQ_TERM_DRAW, OMQ_TERM_END = 0, 1, 2, 3, 4
+OMQ_GO_KO, OMQ_GO_SUICIDE = 1, 2
 OMQ_SHIFT_WORKSPACE_PER_NODE = 8
 OMQ_NOALLOC_SHIFT_INTS = 8 * 1024 * 1024
 OMQ_DTYPE_F32, OMQ_DTYPE_BF16 = 0, 1
@@ -56,6 +57,7 @@ class OmqWave(ctypes.Structure):
         ("ufirst", _p), ("ucount", _p), ("glog", _p), ("gcount", _p), ("gmembers", _p),
         ("ukey", _p), ("ulegal", _p), ("uedge", _p), ("unew", _p), ("policy", _p),
         ("values", _p), ("sim_value", _p), ("stats", _p), ("status", _p), ("sel_scratch", _p),
+        ("umask", _p),
     ]
 
 
@@ -83,6 +85,7 @@ SIGNATURES = {
     "omq_paths_backup": (ctypes.c_int, [_FP, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "omq_virtual_loss": (ctypes.c_int, [_FP, _p, _p, _i32, _i32, _p]),
     "omq_gomoku_terminal": (ctypes.c_int, [_FP, _WP, _p, _p, _i32, _p, _p]),
+    "omq_go_rules": (ctypes.c_int, [_FP, _WP, _p, _p, _p, _p, _i32, _p, _p]),
     "omq_shift_root": (ctypes.c_int, [_FP, _p, _p, ctypes.c_int64, _p]),
     "omq_shift_root_noalloc": (ctypes.c_int, [_FP, _p, _p]),
     "omq_leaf_features": (ctypes.c_int, [_FP, _WP, _p, _p, _p, _i32, _i32, _i32, _p, _p]),

@@ -101,6 +101,11 @@ class WaveEngine:
         self.rule: int | None = None
         self.root_boards: torch.Tensor | None = None
         self.root_player: torch.Tensor | None = None
+        # Go rules (legal masks per unique leaf, terminal leaves), off until set_go_rules
+        self.go_flags: int | None = None
+        self.umask: torch.Tensor | None = None
+        self.root_passes: torch.Tensor | None = None
+        self.root_ko: torch.Tensor | None = None
         self._shift_ws: torch.Tensor | None = None  # subtree-reuse workspace, made on first use
         self._policy: torch.Tensor | None = None    # root policies [T, A] float64
 
@@ -162,6 +167,46 @@ class WaveEngine:
             self.root_player = rp.to(self.device)
         self.rule = int(rule)
 
+    def set_go_rules(self, boards, flags: int = _lib.OMQ_GO_KO, root_player=None,
+                     root_passes=None, root_ko=None) -> None:
+        """Turn on the Go rules of every wave's leaves (omq_go_rules): legal moves from the leaf
+        position (the root's ko point excluded in the whole tree with OMQ_GO_KO, points without
+        an empty neighbour with OMQ_GO_SUICIDE), leaves after two consecutive passes or without
+        an empty point terminal.  boards: int8 [T, bs, bs] root positions; root_player,
+        root_passes (the root's trailing passes) and root_ko (a point or -1): optional [T].
+        boards=None turns them off."""
+        if boards is None:
+            self.go_flags = None
+            self.root_passes = self.root_ko = None
+            self.wave.umask = None
+            if self.rule is None:
+                self.root_boards = self.root_player = None
+            return
+        if self.model.kind != "go":
+            raise ValueError("the Go rules need a go game model")
+        cells = self.A - 1
+        b = torch.as_tensor(np.ascontiguousarray(boards, dtype=np.int8)).reshape(-1)
+        if b.numel() != self.T * cells:
+            raise ValueError(f"boards hold {b.numel()} points, expected {self.T} x {cells}")
+
+        def per_tree(x, name):
+            if x is None:
+                return None
+            v = torch.as_tensor(np.ascontiguousarray(x, dtype=np.int32)).reshape(-1)
+            if v.numel() != self.T:
+                raise ValueError(f"one {name} per tree")
+            return v.to(self.device)
+
+        self.root_boards = b.to(self.device)
+        self.root_player = per_tree(root_player, "root player")
+        self.root_passes = per_tree(root_passes, "root pass count")
+        self.root_ko = per_tree(root_ko, "ko point")
+        if self.umask is None:
+            self.umask = torch.zeros(self.T * self.MW * self.model.legal_words,
+                                     dtype=torch.int32, device=self.device)
+        self.wave.umask = self.umask.data_ptr()
+        self.go_flags = int(flags)
+
     def _check(self, rc: int, what: str) -> None:
         _lib.check(rc, what)
 
@@ -189,6 +234,12 @@ class WaveEngine:
                     "omq_leaf_info")
         if self.rule is not None:
             self.leaf_info_terminal_only()
+        if self.go_flags is not None:
+            ptr = lambda x: None if x is None else x.data_ptr()  # noqa: E731
+            self._check(self.lib.omq_go_rules(
+                self.forest_ref, self.wave_ref, self.root_boards.data_ptr(), ptr(self.root_player),
+                ptr(self.root_passes), ptr(self.root_ko), self.go_flags, self.uterm.data_ptr(),
+                self.stream_handle()), "omq_go_rules")
 
     def leaf_info_terminal_only(self) -> None:
         """The Gomoku terminal check alone, over the unique leaves already looked up."""

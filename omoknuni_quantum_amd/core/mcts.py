@@ -210,9 +210,12 @@ class MCTS:
         elif isinstance(states, (list, tuple)) and states and all(
                 self._is_state_object(s) for s in states):
             objs = list(states)
+        self._root_go_host = None
         if objs is not None:
             conv = [self._board_of_state(s) for s in objs]
             boards = np.stack([c[0] for c in conv]).astype(np.int8)
+            if self.model.kind == "go":
+                self._root_go_host = self._go_state_info(objs)
             return (boards, np.array([c[1] for c in conv], np.int32),
                     np.array([c[2] for c in conv], np.int32))
         bs = self.config.board_size
@@ -220,6 +223,29 @@ class MCTS:
         if arr.shape[-2:] != (bs, bs):
             raise ValueError(f"Invalid state shape: {arr.shape}, expected {(bs, bs)}")
         return arr.reshape(-1, bs, bs).astype(np.int8), None, None
+
+    def _go_state_info(self, objs):
+        """(trailing passes, ko point) of Go state objects: the passes that end the state's
+        move history, and get_ko_point() where the state has it (GoState::getKoPoint,
+        include/games/go/go_state.h:192), else -1."""
+        pass_action = self.action_size - 1
+        passes, ko = [], []
+        for st in objs:
+            hist = list(st.get_move_history()) if hasattr(st, "get_move_history") else []
+            n = 0
+            while n < len(hist) and int(hist[-1 - n]) == pass_action:
+                n += 1
+            passes.append(n)
+            ko.append(int(st.get_ko_point()) if hasattr(st, "get_ko_point") else -1)
+        return np.array(passes, np.int32), np.array(ko, np.int32)
+
+    def _go_flags(self) -> Optional[int]:
+        if self.model.kind != "go" or self.config.go_rules == "off":
+            return None
+        flags = _lib.OMQ_GO_KO
+        if self.config.go_rules == "ko_suicide":
+            flags |= _lib.OMQ_GO_SUICIDE
+        return flags
 
     def _states_array(self, states) -> Optional[np.ndarray]:
         return self._root_states(states)[0]
@@ -233,11 +259,17 @@ class MCTS:
             key += b"|" + (b"" if extra is None else np.asarray(extra, np.int32).tobytes())
         return key
 
+    def _go_key(self) -> bytes:
+        info = getattr(self, "_root_go_host", None)
+        if info is None or self._go_flags() is None:
+            return b""
+        return b"|go" + info[0].tobytes() + info[1].tobytes()
+
     def _set_roots(self, boards: Optional[np.ndarray], players=None, moves=None) -> None:
         T = self.engine.T
         if boards is not None and boards.shape[0] != T:
             raise ValueError(f"{boards.shape[0]} states given for {T} trees")
-        key = self._roots_key_of(boards, players, moves)
+        key = self._roots_key_of(boards, players, moves) + self._go_key()
         if key == self._roots_key and self._eval is not None:
             return
         keys = games.root_keys(self.config.seed, T)
@@ -261,6 +293,14 @@ class MCTS:
         the player to move and move count of game-state roots) and the evaluator built on
         them; the tree arrays are left as they are."""
         T = self.engine.T
+        go_flags = self._go_flags()
+        if go_flags is not None:
+            if boards is None:
+                boards = np.zeros((T, self.config.board_size, self.config.board_size), np.int8)
+            info = getattr(self, "_root_go_host", None)
+            self._root_go_host = info if info is not None else (
+                np.zeros(T, np.int32), np.full(T, -1, np.int32))
+            legal = self._go_root_legal(boards, go_flags)
         self._root_keys_host = np.asarray(keys, dtype=np.uint64).copy()
         self._root_legal_host = np.asarray(legal, dtype=np.uint32).copy()
         self._root_boards_host = None if boards is None else np.asarray(boards, np.int8).copy()
@@ -275,10 +315,36 @@ class MCTS:
             b = boards if boards is not None else np.zeros(
                 (T, self.config.board_size, self.config.board_size), np.int8)
             self.engine.set_gomoku_rules(b, rule, root_player=players)
-        self._roots_key = self._roots_key_of(boards, players, moves)
+        if go_flags is not None:
+            passes, ko = self._root_go_host
+            self.engine.set_go_rules(boards, go_flags, root_player=players, root_passes=passes,
+                                     root_ko=ko)
+        self._roots_key = self._roots_key_of(boards, players, moves) + self._go_key()
         self._boards = None if boards is None else torch.from_numpy(
             np.ascontiguousarray(boards, np.int8)).to(self.device)
         self._eval = self._make_evaluator()
+
+    def _go_root_legal(self, boards: np.ndarray, flags: int) -> np.ndarray:
+        """Root legal masks under the Go rules: the empty points and the pass, without the
+        root's ko point (OMQ_GO_KO) and the points with no empty orthogonal neighbour
+        (OMQ_GO_SUICIDE), so that the root's Dirichlet noise has one entry per legal move."""
+        T = boards.shape[0]
+        legal = games.legal_masks(self.model, boards, T)
+        ko = self._root_go_host[1]
+        empty = boards == 0
+        closed = np.zeros_like(empty)
+        if flags & _lib.OMQ_GO_SUICIDE:
+            pad = np.zeros((T, boards.shape[1] + 2, boards.shape[2] + 2), bool)
+            pad[:, 1:-1, 1:-1] = empty
+            open_nb = pad[:, :-2, 1:-1] | pad[:, 2:, 1:-1] | pad[:, 1:-1, :-2] | pad[:, 1:-1, 2:]
+            closed = empty & ~open_nb
+        for t in range(T):
+            drop = np.flatnonzero(closed[t].reshape(-1)).tolist()
+            if flags & _lib.OMQ_GO_KO and 0 <= int(ko[t]) < empty[t].size:
+                drop.append(int(ko[t]))
+            for a in drop:
+                legal[t, a // 32] &= np.uint32(~(1 << (a % 32)) & 0xFFFFFFFF)
+        return legal
 
     def _gomoku_rule(self) -> Optional[int]:
         """Terminal rule of Gomoku leaves: the config's, renju when the game interface says
@@ -471,6 +537,15 @@ class MCTS:
                 # a game-state root keeps its own player and move count: the opponent moves next
                 players = None if pp is None else (3 - pp).astype(np.int32)
                 moves = None if pm is None else (pm + 1).astype(np.int32)
+                # Go: a pass adds to the root's trailing passes, a stone ends them; no capture
+                # is modelled, so no new ko point arises
+                info = getattr(self, "_root_go_host", None)
+                if self.model.kind == "go" and info is not None:
+                    pass_action = self.action_size - 1
+                    self._root_go_host = (
+                        np.array([int(info[0][t]) + 1 if a == pass_action else 0
+                                  for t, a in enumerate(actions)], np.int32),
+                        np.full(T, -1, np.int32))
         self._install_roots(keys, legal, boards, players, moves)
         return int(eng.num_nodes.sum().item())
 

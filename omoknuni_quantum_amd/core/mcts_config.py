@@ -25,6 +25,12 @@ New fields of this build:
                     reference's game states run it after every move
                     (python/mcts/utils/fast_terminal_check.py:132-232); terminal leaves are
                     not expanded
+  go_rules          'off' (a Go leaf's legal moves are the root's minus the path's points),
+                    'ko' or 'ko_suicide': the Go rules of the reference's GPU game states
+                    (python/mcts/gpu/go_kernels.py:17-110, gpu_game_states.py:373-395):
+                    legal moves from the leaf position without the root's ko point (and,
+                    with 'ko_suicide', without points lacking an empty neighbour); two
+                    consecutive passes or a board without an empty point end the game
   root_noise_source 'host' (numpy PCG64 Dirichlet, per tree seed + t) or 'device'
                     (omq_root_dirichlet: Marsaglia-Tsang gamma variates from a counter-based
                     SplitMix64 stream keyed by seed and search count)
@@ -80,6 +86,7 @@ _EXPANSION = ("full", "reference_pw")
 _SIGNS = ("leaf_positive", "root_positive")
 _WACC = ("ordered", "atomic")
 _RULES = ("freestyle", "renju", "off")
+_GO_RULES = ("off", "ko", "ko_suicide")
 
 
 @dataclass
@@ -125,6 +132,7 @@ class _ConfigFields:
     seed: int = 0
     sparse_legal: tuple = (20, 45)
     gomoku_rules: str = "freestyle"
+    go_rules: str = "off"
     root_noise_source: str = "host"
     extra: Dict[str, Any] = field(default_factory=dict)
 
@@ -163,6 +171,8 @@ class MCTSConfig(_ConfigFields):
             raise ValueError("num_trees must be >= 1")
         if self.gomoku_rules not in _RULES:
             raise ValueError(f"gomoku_rules must be one of {_RULES}")
+        if self.go_rules not in _GO_RULES:
+            raise ValueError(f"go_rules must be one of {_GO_RULES}")
         if self.root_noise_source not in ("host", "device"):
             raise ValueError("root_noise_source must be 'host' or 'device'")
 

@@ -119,6 +119,84 @@ __global__ void gomoku_terminal_kernel(omq_forest f, omq_wave w, const int8_t* r
   }
 }
 
+// Go rules of unique leaf u of tree t (one wavefront per leaf): the leaf's position is rebuilt
+// as for Gomoku (a pass, action cells, places no stone), then lane l takes the points l, l+64,
+// ... of the board.  A point is legal when it is empty, is not the root's ko point (OMQ_GO_KO:
+// the reference's clones inherit a state's ko point, so it holds at every depth), and, with
+// OMQ_GO_SUICIDE, has an empty orthogonal neighbour; the pass is always legal.  The 64 points of each chunk become two mask words by one ballot.  Trailing passes are
+// counted from the path's end (the root's own when every path move is a pass).
+__global__ void go_rules_kernel(omq_forest f, omq_wave w, const int8_t* root_boards,
+                                const int32_t* root_player, const int32_t* root_passes,
+                                const int32_t* root_ko, int flags, int bs, int32_t* uterm) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int cells = bs * bs;
+  const int stride = (cells + 15) & ~15;
+  const int t = blockIdx.y;
+  const int wave = threadIdx.x / kWave;
+  const int u = blockIdx.x * (blockDim.x / kWave) + wave;
+  const int lane = lane_id();
+  const int64_t wb = (int64_t)t * w.max_wave;
+  if (u >= w.ucount[t]) return;
+  int8_t* b = reinterpret_cast<int8_t*>(smem + (size_t)wave * stride);
+  int rp, stones;
+  const int L = rebuild_leaf_board(f, w, root_boards, root_player, t, u, cells, b, &rp, &stones);
+  // trailing passes of the path (moves 0..L-2; lane j holds move j, lane j holds move j+64 in
+  // the high word)
+  const int s0 = w.ufirst[wb + u];
+  int a_lo, a_hi;
+  load_path_actions(f, w, t, s0, &a_lo, &a_hi);
+  int trail = 0;
+  for (int j = L - 2; j >= 0; --j) {
+    const int a = j < kWave ? readlane_i(a_lo, j) : readlane_i(a_hi, j - kWave);
+    if (a != cells) break;
+    ++trail;
+  }
+  if (trail == L - 1 && root_passes != nullptr) trail += root_passes[t];
+  const int ko = ((flags & OMQ_GO_KO) && root_ko != nullptr) ? root_ko[t] : -1;
+  const bool suicide = (flags & OMQ_GO_SUICIDE) != 0;
+  uint32_t* mask = w.umask + (wb + u) * (int64_t)f.legal_words;
+  int legal = 0, empty = 0;
+  // points 0..cells-1, then the pass (action cells, always legal)
+  for (int c0 = 0; c0 <= cells; c0 += kWave) {
+    const int c = c0 + lane;
+    bool ok = c == cells;
+    if (c < cells && b[c] == 0) {
+      ++empty;
+      ok = c != ko;
+      if (ok && suicide) {
+        const int r = c / bs, col = c - r * bs;
+        const bool lib = (r > 0 && b[c - bs] == 0) || (r + 1 < bs && b[c + bs] == 0) ||
+                         (col > 0 && b[c - 1] == 0) || (col + 1 < bs && b[c + 1] == 0);
+        ok = lib;
+      }
+    }
+    const uint64_t m = __ballot(ok);
+    legal += ok ? 1 : 0;
+    // words c0/32 and c0/32 + 1 (legal_words = ceil((cells + 1) / 32) covers the pass)
+    if (lane == 0) mask[c0 >> 5] = (uint32_t)m;
+    if (lane == 1 && (c0 >> 5) + 1 < f.legal_words) mask[(c0 >> 5) + 1] = (uint32_t)(m >> 32);
+  }
+  legal = wave_sum_i(legal);
+  empty = wave_sum_i(empty);
+  if (lane == 0) {
+    const bool term = L > 1 && (trail >= 2 || empty == 0);
+    w.ulegal[wb + u] = term ? 0 : legal;
+    if (uterm != nullptr) uterm[wb + u] = term ? OMQ_TERM_END : OMQ_TERM_NONE;
+  }
+}
+
+hipError_t launch_go_rules(const omq_forest& f, const omq_wave& w, const int8_t* boards,
+                           const int32_t* root_player, const int32_t* root_passes,
+                           const int32_t* root_ko, int flags, int bs, int32_t* uterm,
+                           hipStream_t st) {
+  constexpr int wpb = 4;
+  const size_t lds = (size_t)(((bs * bs) + 15) & ~15) * wpb;
+  dim3 grid((w.max_wave + wpb - 1) / wpb, f.num_trees);
+  hipLaunchKernelGGL(go_rules_kernel, grid, dim3(wpb * kWave), lds, st, f, w, boards,
+                     root_player, root_passes, root_ko, flags, bs, uterm);
+  return hipGetLastError();
+}
+
 hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const int8_t* boards,
                                   const int32_t* root_player, int rule, int bs, int32_t* uterm,
                                   hipStream_t st) {

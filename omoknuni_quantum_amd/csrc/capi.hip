@@ -38,6 +38,10 @@ hipError_t launch_root_dirichlet(const omq_forest& f, double alpha, uint64_t see
 hipError_t launch_gomoku_terminal(const omq_forest& f, const omq_wave& w, const int8_t* boards,
                                   const int32_t* root_player, int rule, int bs, int32_t* uterm,
                                   hipStream_t st);
+hipError_t launch_go_rules(const omq_forest& f, const omq_wave& w, const int8_t* boards,
+                           const int32_t* root_player, const int32_t* root_passes,
+                           const int32_t* root_ko, int flags, int bs, int32_t* uterm,
+                           hipStream_t st);
 hipError_t launch_leaf_features(const omq_forest& f, const omq_wave& w, const int8_t* boards,
                                 const int32_t* root_player, const int32_t* root_moves, int bs,
                                 int planes, int dtype, int nhwc, void* out, hipStream_t st);
@@ -202,6 +206,27 @@ int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* ro
   return hip_status(omq::launch_gomoku_terminal(*f, *w, root_boards, root_player, rule, bs,
                                                 uterminal, (hipStream_t)stream),
                     "omq_gomoku_terminal");
+}
+
+int omq_go_rules(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,
+                 const int32_t* root_player, const int32_t* root_passes, const int32_t* root_ko,
+                 int32_t flags, int32_t* uterminal, void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  rc = check_wave(f, w, w ? w->max_wave : 1);
+  if (rc) return rc;
+  if (f->game != OMQ_GAME_GO)
+    return fail(OMQ_E_ARG, "omq_go_rules needs a Go forest (game %d)", f->game);
+  int bs = 0;
+  while ((bs + 1) * (bs + 1) <= f->num_actions - 1) ++bs;
+  if (bs * bs + 1 != f->num_actions)
+    return fail(OMQ_E_ARG, "num_actions %d is not a square board plus the pass", f->num_actions);
+  if (!root_boards) return fail(OMQ_E_ARG, "root_boards is required");
+  if (!w->umask) return fail(OMQ_E_ARG, "omq_go_rules writes the wave's umask: it is null");
+  if (flags & ~(OMQ_GO_KO | OMQ_GO_SUICIDE)) return fail(OMQ_E_ARG, "unknown Go flags %d", flags);
+  return hip_status(omq::launch_go_rules(*f, *w, root_boards, root_player, root_passes, root_ko,
+                                         flags, bs, uterminal, (hipStream_t)stream),
+                    "omq_go_rules");
 }
 
 int omq_leaf_features(const omq_forest* f, const omq_wave* w, const int8_t* root_boards,

@@ -260,6 +260,15 @@ __device__ inline void board_legal_mask(const omq_forest& f, int t, int L, int a
   wave_sync();
 }
 
+// Legal mask of unique leaf u of tree t from the wave's umask (the rule kernel's) into
+// wave-private LDS words.
+__device__ inline void leaf_umask(const omq_forest& f, const omq_wave& w, int t, int u,
+                                  uint32_t* mask) {
+  const uint32_t* src = w.umask + ((int64_t)t * w.max_wave + u) * f.legal_words;
+  for (int i = lane_id(); i < f.legal_words; i += kWave) mask[i] = src[i];
+  wave_sync();
+}
+
 // Sorted legal list from a board mask (ascending actions).  Returns the count.
 __device__ inline int board_legal_list(const omq_forest& f, const uint32_t* mask, int* list) {
   const int lane = lane_id();
@@ -286,6 +295,10 @@ __device__ inline int leaf_legal_list(const omq_forest& f, const omq_wave& w, in
                                       uint32_t* mask, int* list) {
   if (f.game == OMQ_GAME_SPARSE) {
     return sparse_legal_list(f, w.ukey[(int64_t)t * w.max_wave + u], list);
+  }
+  if (w.umask != nullptr) {
+    leaf_umask(f, w, t, u, mask);
+    return board_legal_list(f, mask, list);
   }
   const int s0 = w.ufirst[(int64_t)t * w.max_wave + u];
   int a_lo, a_hi;

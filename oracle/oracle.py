@@ -66,6 +66,8 @@ def load() -> ctypes.CDLL:
         "orc_sum64d": (d, [P, i]),
         "orc_set_gomoku_rules": (None, [P, i, i, P, P]),
         "orc_gomoku_terminal": (i, [P, i, i]),
+        "orc_set_go_rules": (None, [P, i, i, P, P, P, P]),
+        "orc_go_leaf_rules": (i, [P, i, P, i, P, P]),
         "orc_shift_root": (i, [P, i, i]),
         "orc_exp_d": (d, [d]),
         "orc_log_d": (d, [d]),
@@ -145,6 +147,29 @@ class Oracle:
         self._rp = None if root_player is None else np.ascontiguousarray(root_player, np.int32)
         self.lib.orc_set_gomoku_rules(self.f, 1, rule, self._boards.ctypes.data,
                                       None if self._rp is None else self._rp.ctypes.data)
+
+    def set_go_rules(self, boards, flags: int = 1, root_player=None, root_passes=None,
+                     root_ko=None) -> None:
+        """Go rules on the leaves (boards: int8 [T, bs, bs] root positions; flags 1 ko,
+        2 suicide; per-tree root player, trailing passes and ko point); boards=None switches
+        them off."""
+        if boards is None:
+            self.lib.orc_set_go_rules(self.f, 0, 0, None, None, None, None)
+            return
+        self._go = [np.ascontiguousarray(boards, dtype=np.int8).reshape(self.T, self.A - 1)]
+        for x in (root_player, root_passes, root_ko):
+            self._go.append(None if x is None else np.ascontiguousarray(x, np.int32).reshape(-1))
+        ptr = lambda x: None if x is None else x.ctypes.data  # noqa: E731
+        self.lib.orc_set_go_rules(self.f, 1, int(flags), *[ptr(x) for x in self._go])
+
+    def go_leaf_rules(self, t: int, moves):
+        """(legal list, terminal code) of tree t's position after the moves, Go rules on."""
+        acts = np.ascontiguousarray(moves, dtype=np.int32)
+        out = np.zeros(self.A + 1, np.int32)
+        term = ctypes.c_int(0)
+        n = self.lib.orc_go_leaf_rules(self.f, t, acts.ctypes.data if acts.size else None,
+                                       int(acts.size), out.ctypes.data, ctypes.byref(term))
+        return out[:n].tolist(), term.value
 
     def shift_root(self, t: int, node: int) -> int:
         """Subtree reuse on tree t (CSRTree.shift_root); returns the kept node count (0 when

@@ -20,10 +20,27 @@ class ParityError(AssertionError):
     pass
 
 
+def go_root_info(wl, seed=0):
+    """Go root inputs for the rules: the workload's boards (empty when it has none), a ko
+    point on an empty point for every other tree (-1 for the rest) and 0 or 1 root passes."""
+    boards = wl.boards()
+    bs = wl.model.board_size
+    if boards is None:
+        boards = np.zeros((wl.num_trees, bs, bs), np.int8)
+    rng = np.random.default_rng(1000 + seed)
+    ko = np.full(wl.num_trees, -1, np.int32)
+    for t in range(0, wl.num_trees, 2):
+        empty = np.flatnonzero(boards[t].reshape(-1) == 0)
+        ko[t] = int(rng.choice(empty))
+    passes = (np.arange(wl.num_trees) % 3 == 1).astype(np.int32)
+    return boards, passes, ko
+
+
 def make_pair(wl, max_wave=None, w_mode=0, vl_atomic=False, device="cuda", sign_mode=0,
-              rule=None):
+              rule=None, go_flags=None):
     """Engine and oracle for the workload; rule (0 freestyle, 1 renju) turns the Gomoku
-    terminal check on for both, from the workload's root boards."""
+    terminal check on for both, from the workload's root boards; go_flags (1 ko, 2 suicide)
+    the Go rules, from go_root_info."""
     from omoknuni_quantum_amd.core.engine import SearchParams, WaveEngine
     from omoknuni_quantum_amd.synthetic.evaluator import SyntheticEvaluator
 
@@ -45,6 +62,10 @@ def make_pair(wl, max_wave=None, w_mode=0, vl_atomic=False, device="cuda", sign_
             boards = np.zeros((wl.num_trees, wl.model.board_size, wl.model.board_size), np.int8)
         eng.set_gomoku_rules(boards, rule)
         orc.set_gomoku_rules(boards, rule)
+    if go_flags is not None:
+        boards, passes, ko = go_root_info(wl)
+        eng.set_go_rules(boards, go_flags, root_passes=passes, root_ko=ko)
+        orc.set_go_rules(boards, go_flags, root_passes=passes, root_ko=ko)
     return eng, orc, SyntheticEvaluator(wl.logit_scale)
 
 
@@ -83,7 +104,7 @@ def compare_wave(eng, orc, W, ctx, w_exact=True):
         if ucount[t] != lw["ucount"]:
             raise ParityError(f"{c}: unique leaves {ucount[t]} != oracle {lw['ucount']}")
         _cmp("uleaf", uleaf_all[t, :ucount[t]], lw["uleaf"], c)
-        if eng.rule is not None:
+        if eng.rule is not None or eng.go_flags is not None:
             _cmp("uterm", eng.uterm.view(T, MW)[t, :ucount[t]].cpu().numpy(), lw["uterm"], c)
             _cmp("ulegal", eng.ulegal.view(T, MW)[t, :ucount[t]].cpu().numpy(), lw["ulegal"], c)
         g = eng.host_tree(t)
@@ -106,14 +127,14 @@ def compare_wave(eng, orc, W, ctx, w_exact=True):
 
 
 def run_parity(wl, check_every=1, w_mode=0, vl_atomic=False, device="cuda", log=None,
-               sign_mode=0, rule=None, stats=None):
+               sign_mode=0, rule=None, stats=None, go_flags=None):
     """Run the whole search on both sides; compare after every check_every-th wave and at
-    the end.  Returns the number of waves compared.  With a Gomoku rule, stats (a dict)
-    receives the number of terminal unique leaves met."""
+    the end.  Returns the number of waves compared.  With a Gomoku rule or the Go rules,
+    stats (a dict) receives the number of terminal unique leaves met."""
     import torch
 
     eng, orc, ev = make_pair(wl, w_mode=w_mode, vl_atomic=vl_atomic, device=device,
-                             sign_mode=sign_mode, rule=rule)
+                             sign_mode=sign_mode, rule=rule, go_flags=go_flags)
     T = wl.num_trees
     eng.reset()
     for t in range(T):
@@ -129,7 +150,7 @@ def run_parity(wl, check_every=1, w_mode=0, vl_atomic=False, device="cuda", log=
         eng.run_wave(W, ev)
         for t in range(T):
             orc.wave(t, W)
-        if stats is not None and rule is not None:
+        if stats is not None and (rule is not None or go_flags is not None):
             for t in range(T):
                 stats["terminal"] = stats.get("terminal", 0) + int(
                     (orc.last_wave(t, W)["uterm"] != 0).sum())

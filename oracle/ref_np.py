@@ -340,6 +340,75 @@ def nn_features(board, player, move_count, planes: int = 19):
     return f[:planes]
 
 
+# Planted misreadings of the Go rules, used only by the tests that show the known answers fail
+# on each of them.  None is the rule.
+GO_VARIANTS = (
+    "ko_root_only",        # the ko point excluded at the root only (clones do inherit it)
+    "suicide_diagonal",    # diagonal empty points counted as liberties
+    "no_suicide_check",    # occupied neighbours counted as liberties too (no check at all)
+    "passes_no_root",      # the root's own trailing passes not counted
+    "passes_any_two",      # any two passes on the path, not two consecutive ones
+    "full_not_terminal",   # a board without an empty point not terminal
+    "pass_not_legal",      # the pass left out of the legal moves
+    "root_terminal",       # the root itself checked for two passes
+)
+
+
+def go_rules(root_board, path_actions, root_player=None, root_passes=0, ko=-1, flags=1,
+             variant=None):
+    """Go rules of the position after the path moves: (legal moves ascending, terminal).
+
+    * The position: the root board with the moves played alternately from the root's player
+      (1 for an even stone count when not given), a pass (action bs*bs) placing no stone and no
+      stone ever captured (GPUGameStates.apply_moves, python/mcts/gpu/gpu_game_states.py:
+      430-441).
+    * Legal: empty points; with flags & 1 not the root's ko point, which every descendant
+      inherits (get_legal_moves_mask :373-395, clone_states :336-337); with flags & 2 only the
+      points whose 4-neighbourhood holds an empty point (go_kernels.py:46-110, the liberty
+      count of a 0/1 empty map convolved with the plus-shaped kernel, zero padding); then the
+      pass.
+    * Terminal (go_kernels.py:17-44), for a path of at least one move: the last two moves are
+      passes (the root's trailing passes prepended), or no point is empty.
+
+    Written with array operations (a padded empty map and shifted sums), independently of the
+    C oracle's point loop."""
+    b = np.array(root_board, dtype=np.int8, copy=True)
+    bs = b.shape[0]
+    cells = bs * bs
+    stones = int(np.count_nonzero(b))
+    player = (1 if stones % 2 == 0 else 2) if root_player is None else int(root_player)
+    flat = b.reshape(-1)
+    for a in path_actions:
+        if a != cells:
+            flat[a] = player
+        player = 3 - player
+    empty = (b == 0)
+    legal = empty.copy()
+    if flags & 1 and ko >= 0 and not (variant == "ko_root_only" and len(path_actions) > 0):
+        legal.reshape(-1)[ko] = False
+    if flags & 2:
+        pad = np.zeros((bs + 2, bs + 2), np.int32)
+        pad[1:-1, 1:-1] = empty
+        libs = pad[:-2, 1:-1] + pad[2:, 1:-1] + pad[1:-1, :-2] + pad[1:-1, 2:]
+        if variant == "suicide_diagonal":
+            libs = libs + pad[:-2, :-2] + pad[:-2, 2:] + pad[2:, :-2] + pad[2:, 2:]
+        if variant == "no_suicide_check":
+            pad[1:-1, 1:-1] = 1
+            libs = pad[:-2, 1:-1] + pad[2:, 1:-1] + pad[1:-1, :-2] + pad[1:-1, 2:]
+        legal &= libs > 0
+    moves = np.flatnonzero(legal.reshape(-1)).tolist()
+    if variant != "pass_not_legal":
+        moves.append(cells)
+    seq = ([cells] * int(root_passes) if variant != "passes_no_root" else []) + list(path_actions)
+    if variant == "passes_any_two":
+        two = seq.count(cells) >= 2
+    else:
+        two = len(seq) >= 2 and seq[-1] == cells and seq[-2] == cells
+    full = not empty.any() and variant != "full_not_terminal"
+    checked = len(path_actions) >= 1 or variant == "root_terminal"
+    return moves, bool(checked and (two or full))
+
+
 def board_legal(root_empty, path_actions, pass_action=None):
     taken = {a for a in path_actions if a != pass_action}
     return [a for a in root_empty if a not in taken]

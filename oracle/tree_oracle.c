@@ -39,6 +39,9 @@
 #define ORC_RULE_RENJU 1
 #define ORC_TERM_NONE 0
 #define ORC_TERM_DRAW 3
+#define ORC_TERM_END 4
+#define ORC_GO_KO 1
+#define ORC_GO_SUICIDE 2
 
 typedef struct orc_forest {
   /* shape */
@@ -70,6 +73,12 @@ typedef struct orc_forest {
   int8_t *root_boards;    /* [T*A] 0 empty, 1/2 stones */
   int32_t *root_player;   /* [T] player of the first path move */
   int32_t *uterm;         /* [T*max_wave] ORC_TERM_* of each unique leaf */
+  /* Go rules (legal moves from the leaf position, terminal leaves); off unless
+     orc_set_go_rules */
+  int go_on, go_flags;
+  int8_t *go_boards;                      /* [T*(A-1)] root positions */
+  int32_t *go_player, *go_passes, *go_ko; /* [T]: player of the first path move, the root's
+                                             trailing passes, the root's ko point (-1: none) */
 } orc_forest;
 
 /* ---- synthetic workload (same specification as the device code) ---------------------- */
@@ -179,9 +188,12 @@ static int sparse_list(const orc_forest *f, uint64_t k, int *list) {
 }
 
 /* legal list of a node given its path actions (depth 1..L-1) and key */
+static int go_legal_list(const orc_forest *f, int t, const int *acts, int np, int *list);
+
 static int legal_list(const orc_forest *f, int t, const int *pacts, int npacts, uint64_t key,
                       int *list) {
   if (f->game == ORC_GAME_SPARSE) return sparse_list(f, key, list);
+  if (f->go_on) return go_legal_list(f, t, pacts, npacts, list);
   const int A = f->A;
   const int pass = f->game == ORC_GAME_GO ? A - 1 : -1;
   const uint32_t *root = f->root_legal + (size_t)t * f->legal_words;
@@ -258,7 +270,8 @@ void orc_destroy(orc_forest *f) {
                   f->children, f->child_actions, f->num_nodes, f->num_edges, f->root_keys,
                   f->root_legal, f->paths, f->path_len, f->leaves, f->sim_uid, f->uleaf,
                   f->ufirst, f->ucount, f->ukey, f->ulegal, f->uexpanded, f->policy, f->values,
-                  f->root_noise, f->seen, f->uterm, f->root_boards, f->root_player};
+                  f->root_noise, f->seen, f->uterm, f->root_boards, f->root_player,
+                  f->go_boards, f->go_player, f->go_passes, f->go_ko};
   for (size_t i = 0; i < sizeof ptrs / sizeof ptrs[0]; ++i) free(ptrs[i]);
   free(f);
 }
@@ -310,6 +323,104 @@ void orc_set_gomoku_rules(orc_forest *f, int enable, int rule, const int8_t *boa
     }
   }
   f->rules_on = 1;
+}
+
+/* Go rules for every wave's leaves: boards [T*(A-1)] (0 empty, 1/2 stones) are the root
+   positions, root_player[T] the player of the first path move (NULL: 1 for an even stone
+   count, else 2), root_passes[T] the root's trailing passes (NULL: 0), root_ko[T] the root's
+   ko point or -1 (NULL: none).  flags: ORC_GO_KO, ORC_GO_SUICIDE.  enable=0 switches them
+   off.  The rules are stated at go_legal_list and go_terminal below. */
+void orc_set_go_rules(orc_forest *f, int enable, int flags, const int8_t *boards,
+                      const int32_t *root_player, const int32_t *root_passes,
+                      const int32_t *root_ko) {
+  free(f->go_boards);
+  free(f->go_player);
+  free(f->go_passes);
+  free(f->go_ko);
+  f->go_boards = NULL;
+  f->go_player = f->go_passes = f->go_ko = NULL;
+  f->go_on = 0;
+  if (!enable) return;
+  const int cells = f->A - 1;
+  f->go_flags = flags;
+  f->go_boards = (int8_t *)malloc((size_t)f->T * cells);
+  memcpy(f->go_boards, boards, (size_t)f->T * cells);
+  f->go_player = (int32_t *)malloc(sizeof(int32_t) * (size_t)f->T);
+  f->go_passes = (int32_t *)malloc(sizeof(int32_t) * (size_t)f->T);
+  f->go_ko = (int32_t *)malloc(sizeof(int32_t) * (size_t)f->T);
+  for (int t = 0; t < f->T; ++t) {
+    int stones = 0;
+    for (int c = 0; c < cells; ++c) stones += boards[(size_t)t * cells + c] != 0;
+    f->go_player[t] = root_player ? root_player[t] : (stones % 2 == 0 ? 1 : 2);
+    f->go_passes[t] = root_passes ? root_passes[t] : 0;
+    f->go_ko[t] = root_ko ? root_ko[t] : -1;
+  }
+  f->go_on = 1;
+}
+
+/* the Go position after the path moves acts[0..np): the root board, move q played by the root's
+   player when q is even, else by the other; a pass (action A-1) places no stone and no stone
+   is ever captured (GPUGameStates.apply_moves, python/mcts/gpu/gpu_game_states.py:430-441) */
+static void go_board(const orc_forest *f, int t, const int *acts, int np, int8_t *board) {
+  const int cells = f->A - 1;
+  memcpy(board, f->go_boards + (size_t)t * cells, (size_t)cells);
+  const int rp = f->go_player[t];
+  for (int q = 0; q < np; ++q)
+    if (acts[q] >= 0 && acts[q] < cells) board[acts[q]] = (int8_t)(q % 2 == 0 ? rp : 3 - rp);
+}
+
+/* legal moves of the position after acts, ascending: every empty point that is not the root's
+   ko point (with ORC_GO_KO; get_legal_moves_mask, gpu_game_states.py:373-395, excludes the
+   state's ko point, and clone_states, :336-337, hands it on to every descendant unchanged)
+   and, with ORC_GO_SUICIDE, has an empty orthogonal neighbour (gpu_get_legal_moves,
+   python/mcts/gpu/go_kernels.py:46-110: a 4-neighbour count of empty points > 0); then the
+   pass, always legal */
+static int go_legal_list(const orc_forest *f, int t, const int *acts, int np, int *list) {
+  int8_t board[8192];
+  const int cells = f->A - 1;
+  int bs = 0;
+  while ((bs + 1) * (bs + 1) <= cells) ++bs;
+  go_board(f, t, acts, np, board);
+  const int ko = (f->go_flags & ORC_GO_KO) ? f->go_ko[t] : -1;
+  int n = 0;
+  for (int c = 0; c < cells; ++c) {
+    if (board[c] != 0 || c == ko) continue;
+    if (f->go_flags & ORC_GO_SUICIDE) {
+      const int r = c / bs, k = c % bs;
+      const int up = r > 0 && board[c - bs] == 0;
+      const int down = r < bs - 1 && board[c + bs] == 0;
+      const int left = k > 0 && board[c - 1] == 0;
+      const int right = k < bs - 1 && board[c + 1] == 0;
+      if (!(up || down || left || right)) continue;
+    }
+    list[n++] = c;
+  }
+  list[n++] = cells;
+  return n;
+}
+
+/* gpu_check_terminal_states (go_kernels.py:17-44): two consecutive passes (the trailing passes
+   of the path, plus the root's own when every path move is a pass) or no empty point.  The
+   root itself (np = 0) is never terminal. */
+static int go_terminal(const orc_forest *f, int t, const int *acts, int np) {
+  if (np < 1) return ORC_TERM_NONE;
+  const int cells = f->A - 1;
+  int trail = 0;
+  while (trail < np && acts[np - 1 - trail] == cells) ++trail;
+  if (trail == np) trail += f->go_passes[t];
+  int8_t board[8192];
+  go_board(f, t, acts, np, board);
+  int empty = 0;
+  for (int c = 0; c < cells; ++c) empty += board[c] == 0;
+  return (trail >= 2 || empty == 0) ? ORC_TERM_END : ORC_TERM_NONE;
+}
+
+/* the Go rules of one position, for the known-answer tests: legal list and terminal code */
+int orc_go_leaf_rules(const orc_forest *f, int t, const int *acts, int np, int *list,
+                      int *term) {
+  if (!f->go_on) return -1;
+  *term = go_terminal(f, t, acts, np);
+  return go_legal_list(f, t, acts, np, list);
 }
 
 /* FastTerminalChecker._check_gomoku_terminal_cpu without last_move
@@ -772,6 +883,10 @@ static void leaves_info(orc_forest *f, int t, int W) {
     f->uterm[wb + u] = ORC_TERM_NONE;
     if (f->rules_on && np >= 1) {  /* the root itself is never flagged */
       f->uterm[wb + u] = leaf_terminal(f, t, acts, np);
+      if (f->uterm[wb + u] != ORC_TERM_NONE) f->ulegal[wb + u] = 0;
+    }
+    if (f->go_on) {
+      f->uterm[wb + u] = go_terminal(f, t, acts, np);
       if (f->uterm[wb + u] != ORC_TERM_NONE) f->ulegal[wb + u] = 0;
     }
   }

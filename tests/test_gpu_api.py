@@ -295,3 +295,45 @@ def test_feature_evaluator_batch_replay_parity(device):
     for t in range(3):
         assert np.array_equal(pol[t], orc.root_policy(t))
         _assert_tree_equal(m, orc, t)
+
+
+class _GoStubState(_StubState):
+    """A Go state: also get_ko_point (GoState::getKoPoint)."""
+
+    def __init__(self, board, player, history, ko):
+        super().__init__(board, player, history)
+        self.ko = ko
+
+    def get_ko_point(self):
+        return self.ko
+
+
+@pytest.mark.parametrize("rules", ["ko", "ko_suicide"])
+def test_go_rules_via_api(device, rules):
+    """MCTSConfig(go_rules=...) on a Go game-state root whose history ends in a pass and that
+    has a ko point: the tree equals the oracle's with the same root passes and ko point; the
+    ko point is never a child, and a pass reply to the root's pass is a terminal leaf (visited,
+    never expanded)."""
+    bs = 9
+    cfg = _config(game_type=GameType.GO, board_size=bs, num_simulations=1024, max_wave_size=64,
+                  go_rules=rules)
+    board = games.random_boards(1, bs, 24, 5, min_stones=24)[0]
+    pass_action = bs * bs
+    ko = int(np.flatnonzero(board.reshape(-1) == 0)[3])
+    state = _GoStubState(board, 1, history=[0] * 23 + [pass_action], ko=ko)
+    m = MCTS(cfg, SyntheticEvaluator())
+    pol = m.search(state)
+    flags = 1 if rules == "ko" else 3
+    orc = _oracle_for(cfg, board[None])
+    orc.set_go_rules(board[None], flags, root_player=[1], root_passes=[1], root_ko=[ko])
+    # the root's legal set under the rules is what the host hands the oracle too
+    orc.set_roots(games.root_keys(cfg.seed, 1), m._root_legal_host, None)
+    orc.search(1024, 64)
+    assert np.array_equal(pol, orc.root_policy(0))
+    _assert_tree_equal(m, orc)
+    tr = m.engine.host_tree(0)
+    n = tr["num_nodes"]
+    assert ko not in tr["action"][1:n].tolist()
+    kids = np.arange(tr["first"][0] + 1, tr["first"][0] + 1 + tr["nchild"][0])
+    p = kids[tr["action"][kids] == pass_action]
+    assert p.size == 1 and tr["N"][p[0]] > 0 and tr["nchild"][p[0]] == 0

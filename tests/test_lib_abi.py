@@ -39,7 +39,7 @@ def test_struct_layout_matches_header():
     # two int32 per 8 bytes, then pointers: offsets the C compiler uses
     assert ctypes.sizeof(_lib.OmqForest) == 8 * 4 + 10 * 8
     assert _lib.OmqForest.visit_counts.offset == 32
-    assert ctypes.sizeof(_lib.OmqWave) == 8 + 20 * 8
+    assert ctypes.sizeof(_lib.OmqWave) == 8 + 21 * 8
     assert _lib.OmqWave.paths.offset == 8
 
 
