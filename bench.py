@@ -36,8 +36,9 @@ def algorithmic_bytes(st: dict, sims: int) -> dict:
       select    16 B per visited node (row header N, first, nchild + N write of the virtual
                 loss) + 12 B per child of each row scanned (N, W, P) + 4 B per path entry
                 (path output) + 8 B per simulation (leaf and path length)
-      leaf_info 4 B per path entry of the first simulation of a unique leaf (upper bound: all
-                path entries) is not counted; 12 B per unique leaf (key, legal count)
+      leaf_info 8 B per path entry below the root of each unique leaf's path (the entry and its
+                node's action) + 20 B per unique leaf (first simulation, path length, key,
+                legal count)
       expand    8 B per expanded leaf (row header) + 28 B per child written (N, W, P, parent,
                 action, row offset, row length) + 4 B per prior gathered (= per child in the
                 full policy)
@@ -47,7 +48,7 @@ def algorithmic_bytes(st: dict, sims: int) -> dict:
     G, K, PE = st["pathnodes"], st["rowsum"], st["pathentries"]
     return {
         "select": 16 * G + 12 * K + 4 * PE + 8 * sims,
-        "leaf_info": 12 * st["uleaves"],
+        "leaf_info": 8 * (st["uleafpath"] - st["uleaves"]) + 20 * st["uleaves"],
         "expand": 8 * st["expanded"] + 32 * st["newchild"],
         "backup": 16 * G + 4 * PE + 12 * sims,
     }

@@ -170,6 +170,7 @@ typedef struct omq_wave {
 #define OMQ_ST_SIMS 7         /* simulations selected */
 #define OMQ_ST_STEPS 8        /* argmax steps (simulation x level decisions) */
 #define OMQ_ST_CAPFAIL 9      /* expansions refused for lack of capacity */
+#define OMQ_ST_ULEAFPATH 10   /* sum over unique leaves of path length (omq_leaf_info) */
 #define OMQ_NSTATS 16
 
 /* device status bits */

@@ -25,7 +25,7 @@ OMQ_MAX_WAVE, OMQ_MAX_ROW, OMQ_MAX_DEPTH, OMQ_MAX_ACTIONS = 4096, 512, 128, 8192
 OMQ_NSTATS = 16
 STAT_NAMES = [
     "internal", "rowsum", "pathnodes", "pathentries", "uleaves", "expanded", "newchild",
-    "sims", "steps", "capfail",
+    "sims", "steps", "capfail", "uleafpath",
 ]
 OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT, OMQ_STATUS_STALL = 1, 2, 4
 OMQ_RULE_FREESTYLE, OMQ_RULE_RENJU = 0, 1

@@ -8,7 +8,7 @@
 // wave order (wave_sum_canonical) in place of numpy's pairwise order.
 //
 // Kernels per wave:
-//   leaf_info_kernel    wave per unique leaf: hash key (fold over path actions), legal count
+//   leaf_info_kernel    thread per unique leaf: hash key (fold over path actions), legal count
 //   synth_eval_kernel   wave per unique leaf: synthetic priors/value (evaluator stand-in)
 //   expand_plan_kernel  workgroup per tree: children counts, scan, capacity rule, row headers
 //   expand_write_kernel wave per expanded leaf: priors, children N/W/P/parent/action/row
@@ -62,35 +62,58 @@ __device__ inline LeafLds carve(const omq_forest& f, unsigned char* base, int wa
 }
 
 // ---------------------------------------------------------------------------------------
-__global__ void leaf_info_kernel(omq_forest f, omq_wave w) {
-  extern __shared__ __align__(16) unsigned char smem[];
+// One thread per unique leaf: its path is read once (the entries of its first simulation, then
+// the action of each path node), the key is folded over the actions, and the legal count of a
+// board leaf is the root's count less the path's moves (a pass stays legal).  Every legal list
+// excludes the moves on its path, so those moves are distinct and legal at the root: the count
+// equals that of the root mask with the path's cells cleared.  Consecutive threads write
+// consecutive keys and counts.  The block also adds its leaves' path entries to the tree's
+// OMQ_ST_ULEAFPATH counter (one atomic per block).
+constexpr int kLeafInfoThreads = 256;
+
+__global__ __launch_bounds__(kLeafInfoThreads) void leaf_info_kernel(omq_forest f, omq_wave w) {
+  __shared__ int s_part[kLeafInfoThreads / kWave];
   const int t = blockIdx.y;
-  const int wave = threadIdx.x / kWave;
-  const int u = blockIdx.x * (blockDim.x / kWave) + wave;
-  const int lane = lane_id();
+  const int u = blockIdx.x * kLeafInfoThreads + threadIdx.x;
   const int64_t wb = (int64_t)t * w.max_wave;
-  if (u >= w.ucount[t]) return;
-  LeafLds l = carve(f, smem, wave, leaf_lds_per_wave(f));
-  const int s0 = w.ufirst[wb + u];
-  int a_lo, a_hi;
-  const int L = load_path_actions(f, w, t, s0, &a_lo, &a_hi);
-  uint64_t key = f.root_keys[t];
-  for (int d = 1; d < L; ++d) {
-    const int a = (d <= 64) ? readlane_i(a_lo, d - 1) : readlane_i(a_hi, d - 65);
-    key = child_key(key, a);
-  }
-  int count;
-  if (f.game == OMQ_GAME_SPARSE) {
-    count = sparse_legal_count(f, key);
-  } else {
-    board_legal_mask(f, t, L, a_lo, a_hi, l.mask);
-    int c = 0;
-    for (int i = lane; i < f.legal_words; i += kWave) c += __popc(l.mask[i]);
-    count = wave_sum_i(c);
-  }
-  if (lane == 0) {
+  const int64_t tb = (int64_t)t * f.capacity;
+  const int nu = w.ucount[t];
+  int L = 0;
+  if (u < nu) {
+    const int s0 = w.ufirst[wb + u];
+    L = w.path_len[wb + s0];
+    const int32_t* path = w.paths + (wb + s0) * w.max_depth;
+    const bool board = f.game != OMQ_GAME_SPARSE;
+    const int pass = f.game == OMQ_GAME_GO ? f.num_actions - 1 : -1;
+    const uint32_t* root = f.root_legal + (int64_t)t * f.legal_words;
+    uint64_t key = f.root_keys[t];
+    int taken = 0;
+    for (int d = 1; d < L; ++d) {
+      const int a = f.actions[tb + path[d]];
+      key = child_key(key, a);
+      if (board && a != pass && a >= 0 && a < f.num_actions) taken += (root[a >> 5] >> (a & 31)) & 1u;
+    }
+    int count;
+    if (board) {
+      int c = 0;
+      for (int i = 0; i < f.legal_words; ++i) c += __popc(root[i]);
+      count = c - taken;
+    } else {
+      count = sparse_legal_count(f, key);
+    }
     w.ukey[wb + u] = key;
     w.ulegal[wb + u] = count;
+  }
+  const int part = wave_sum_i(L);
+  if (lane_id() == 0) s_part[threadIdx.x / kWave] = part;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int sum = 0;
+    for (int i = 0; i < kLeafInfoThreads / kWave; ++i) sum += s_part[i];
+    if (sum > 0)
+      atomicAdd(reinterpret_cast<unsigned long long*>(&w.stats[(int64_t)t * OMQ_NSTATS +
+                                                               OMQ_ST_ULEAFPATH]),
+                (unsigned long long)sum);
   }
 }
 
@@ -432,10 +455,8 @@ static int leaf_waves_per_block(const omq_forest& f) {
 }
 
 hipError_t launch_leaf_info(const omq_forest& f, const omq_wave& w, int W, hipStream_t st) {
-  const int wpb = leaf_waves_per_block(f);
-  const size_t lds = leaf_lds_per_wave_host(f) * wpb;
-  dim3 grid((W + wpb - 1) / wpb, f.num_trees);
-  hipLaunchKernelGGL(leaf_info_kernel, grid, dim3(wpb * kWave), lds, st, f, w);
+  dim3 grid((W + kLeafInfoThreads - 1) / kLeafInfoThreads, f.num_trees);
+  hipLaunchKernelGGL(leaf_info_kernel, grid, dim3(kLeafInfoThreads), 0, st, f, w);
   return hipGetLastError();
 }
 
