@@ -233,10 +233,27 @@ __device__ inline int lane_pending(const Row<1>& y) {
 // Wave max of a float as order-preserving keys (made uniform).
 __device__ inline float wave_max_key(float x) { return funkey(wave_max_u32(fkey(x))); }
 
-// Key of the raised value hi = ap + (|ap| + QB) * 2^-19 of a child (qb19 = QB * 2^-19).
-__device__ inline uint32_t raised_key(float ap, float qb19) {
-  return fkey(__builtin_fmaf(__builtin_fabsf(ap), 1.0f / 524288.0f, ap) + qb19);
+// Key of the raised value hi = ap + (2|ap| + |qa| + QW) * M of a lane in the steps over one lane
+// per child, M = 2^-20.5 rounded up.  QW bounds |qa| of every visited lane that can hold the
+// step's maximum (the chain's QB, or the window's contenders' bound).
+//
+// Why the exact argmax w is a candidate (hi_w >= A, A = max ap, held by lane m): each lane's
+// |ap - sc| <= e = 7u (|ap| + |Q|) (1 + 2^-20), u = 2^-24 (the argument above run_chain's
+// helpers, written per child: 4u U from the two U's, 3u |Q| from qa and Q, u |ap| + u |sc| from
+// the last roundings, and U <= |ap| + |Q|).  Then sc_w >= sc_m >= A - e_m and ap_w >= A - e_m
+// - e_w; with |A| <= |ap_w| + e_m + e_w and |Q_m| <= QW, e_m + e_w <= 7u X (1 + 8u) for
+// X = 2|ap_w| + |qa_w| + QW.  hi_w is the rounded ap_w + fl(fl(2|ap_w| + |qa_w|) + QW) M >=
+// ap_w + X (1 - 2u) M, and M > 1.6 * 7u covers it; rounding to nearest keeps a real value >= A
+// (a float) >= A.  The lane holding A has hi >= ap = A.
+constexpr float kMarg = 0x1.6a09e8p-21f;
+__device__ inline uint32_t raised_key(float ap, float qa, float qw) {
+  const float x = (2.0f * __builtin_fabsf(ap) + __builtin_fabsf(qa)) + qw;
+  return fkey(__builtin_fmaf(x, kMarg, ap));
 }
+
+// qa of a padding lane in the one-lane steps: its ap stays here and its raised value stays
+// finite, far below any maximum above -1e9
+constexpr float kPadQ = -1e30f;
 
 // Smallest key at which lane_steps takes a step: that of -1e9 (below it no child can be picked
 // without the exact comparison).
@@ -250,15 +267,13 @@ static_assert(kKeyInf == (__builtin_bit_cast(uint32_t, __builtin_inff()) ^ 0x800
 // contender window), from rank rr up to rank rend.
 //
 // A step ranks the lanes by ap = fma(s, a, qa) and takes the wave max A (as the key Ak).  The
-// candidates are the lanes whose raised key fkey(hi), hi = ap + (|ap| + QB) * 2^-19 (rounded as
-// in raised_key), is at least Ak.  The exact argmax is among them: with E = (|A| + QB)*2^-20.5
-// it has ap >= A - 2E (see the argument above run_chain's helpers), so its hi, rounded twice,
-// is at least A - 2E + 2^1.5 E - 0.2 E > A.  The lane holding A is a candidate (hi >= ap), so a
-// step has at least one.  A single candidate is the pick.  A step is taken here only when A
-// lies strictly between klo and khi (keys): klo is at least the key of -1e9, and khi at most
-// that of +inf (0 in exact-only mode, which takes no step here).  A NaN ap can only add
-// candidates (a NaN hi), which sends the step to the exact comparison.  Padding lanes hold
-// qa = -FLT_MAX, a = 0: their hi stays finite and below any A above -1e9.
+// candidates are the lanes whose raised key (raised_key: hi = ap + (2|ap| + |qa| + QW) * 2^-20.5)
+// is at least Ak; the exact argmax is among them (the argument at raised_key), and the lane
+// holding A is one, so a step has at least one.  A single candidate is the pick.  A step is
+// taken here only when A lies strictly between klo and khi (keys): klo is at least the key of
+// -1e9, and khi at most that of +inf (0 in exact-only mode, which takes no step here).  A NaN
+// ap can only add candidates (a NaN hi), which sends the step to the exact comparison.
+// Padding lanes hold qa = kPadQ, a = 0: their hi stays finite and below any A above -1e9.
 //
 // A pick advances the picked lane to its next state (a register select); that lane's state
 // after its following pick is computed during the next step's wave max.  The steps with a
@@ -277,7 +292,7 @@ static_assert(kKeyInf == (__builtin_bit_cast(uint32_t, __builtin_inff()) ^ 0x800
 // Returns the first rank not taken.
 template <bool WINDOW>
 __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float fvl, float vlf,
-                                 float qb19, uint32_t klo, uint32_t khi, int k, int r0,
+                                 float qw, uint32_t klo, uint32_t khi, int k, int r0,
                                  int* first_end, uint32_t* rec, uint32_t* rnk) {
   const int lane = lane_id();
   // A in range: (Ak - kbase) < kspan as unsigned
@@ -315,7 +330,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       OMQ_DPP_MAX(v, 0x114, 0xF);  // row_shr:4
       r1 = __builtin_fmaf(r1, t1, r1);
       r2 = __builtin_fmaf(r2, t2, r2);
-      uint32_t hk = raised_key(ap, qb19);
+      uint32_t hk = raised_key(ap, y.q[0], qw);
       OMQ_PIN(r1);
       OMQ_PIN(r2);
       OMQ_PIN(hk);
@@ -375,7 +390,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     const float s = readlane_f(svec, rr);
     const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
     const uint32_t Ak = wave_max_u32(fkey(ap));
-    const bool cand = raised_key(ap, qb19) >= Ak;
+    const bool cand = raised_key(ap, y.q[0], qw) >= Ak;
     const bool in_range = Ak - kbase < kspan;
     if (WINDOW && !in_range) return rr;
     const int win = __builtin_amdgcn_readfirstlane(
@@ -601,7 +616,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
   }
   const uint32_t QBb = wave_max_rows(__float_as_uint(qbl));  // bits of QB (non-negative)
   const float qbt = __uint_as_float(QBb) * (-1.0f / 524288.0f);
-  const float qb19 = -qbt;  // QB * 2^-19
+  const float qb = __uint_as_float(QBb);  // QB
   const bool exact_only = __ballot(negcp) != 0 || !(__uint_as_float(QBb) < 1e8f);
   if (c.vli == 0) {
     // Without an integer virtual loss a pick changes no visit count: every rank sees the same
@@ -621,14 +636,14 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     y.den[0] = x.den[0];
     y.wv[0] = x.wv[0];
     y.cp[0] = x.cp[0];
-    y.q[0] = lane < k ? x.q[0] : -__FLT_MAX__;  // (padding lanes: see lane_steps)
+    y.q[0] = lane < k ? x.q[0] : kPadQ;  // (padding lanes: see lane_steps)
     y.ar[0] = x.ar[0];
     y.pb[0] = false;
     y.cn[0] = 0;
     if (lane < k) {
       child_state(y.den[0] + fvl, y.wv[0], y.cp[0], lane, vlf, &y.qn[0], &y.arn[0]);
     } else {
-      y.qn[0] = -__FLT_MAX__;
+      y.qn[0] = kPadQ;
       y.arn[0] = 0.0f;
     }
   }
@@ -643,7 +658,8 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
   uint32_t tau_hint = 0u;  // the last window's contender threshold (0: none yet)
   uint32_t conbits = 0u;
   // Bound of the non-contenders' raised keys at rank s_end (a NaN ap is never a pick, and not
-  // a candidate of the window's steps).
+  // a candidate of the window's steps).  QB bounds |qa| of every visited child, the window's
+  // contenders (the lanes that can hold a window step's maximum) among them.
   auto noncon_bound = [&](float s_end) {
     uint32_t ubk = kKeyFloor;
 #pragma unroll
@@ -651,7 +667,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
       const int i = j * kWave + lane;
       const bool con = ((conbits >> j) & 1u) != 0;
       const float a = __builtin_fmaf(s_end, x.ar[j], x.q[j]);
-      const uint32_t ha = raised_key(a, qb19);
+      const uint32_t ha = raised_key(a, x.q[j], qb);
       ubk = (i < k && !con && a == a) ? max(ubk, ha) : ubk;
     }
     return wave_max_u32(ubk);
@@ -690,7 +706,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     uint32_t rec = kNoChild;
     uint32_t rnk = 0;
     if (R == 1) {
-      lane_steps<false>(y, svec, 0, rend, fvl, vlf, qb19, kKeyFloor, exact_only ? 0u : kKeyInf,
+      lane_steps<false>(y, svec, 0, rend, fvl, vlf, qb, kKeyFloor, exact_only ? 0u : kKeyInf,
                         k, r0, &first_end, &rec, &rnk);
     } else {
       int rr = 0;
@@ -698,7 +714,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
       if (PERSIST && wopen) {
         // ---- the open window continues, with its bound for this block's last rank ----
         const uint32_t ubk = noncon_bound(readlane_f(svec, rend - 1));
-        rr = lane_steps<true>(y, svec, 0, rend, fvl, vlf, qb19, ubk, kKeyInf, ncon, r0,
+        rr = lane_steps<true>(y, svec, 0, rend, fvl, vlf, qb, ubk, kKeyInf, ncon, r0,
                               &first_end, &rec, &rnk);
         const int ci = __shfl(cidx, (int)(rec & 63u), 64);
         if (lane < rr) rec = (uint32_t)ci;
@@ -743,14 +759,14 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
             child_state(y.den[0], y.wv[0], y.cp[0], cidx, vlf, &y.q[0], &y.ar[0]);
             child_state(y.den[0] + fvl, y.wv[0], y.cp[0], cidx, vlf, &y.qn[0], &y.arn[0]);
           } else {
-            y.q[0] = y.qn[0] = -__FLT_MAX__;
+            y.q[0] = y.qn[0] = kPadQ;
             y.ar[0] = y.arn[0] = 0.0f;
           }
           wopen = true;
           const int rr0 = rr;
           // window steps record the picked lane; the lanes become child indices below.  A
           // window step always picks (no candidate or an unsafe threshold aborts it first).
-          rr = lane_steps<true>(y, svec, rr, rend, fvl, vlf, qb19, ubk, kKeyInf, ncon, r0,
+          rr = lane_steps<true>(y, svec, rr, rend, fvl, vlf, qb, ubk, kKeyInf, ncon, r0,
                                 &first_end, &rec, &rnk);
           {
             const int ci = __shfl(cidx, (int)(rec & 63u), 64);
