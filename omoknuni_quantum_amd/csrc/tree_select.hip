@@ -940,14 +940,14 @@ struct LevelShared {
   unsigned long long st[OMQ_NSTATS];
 };
 
-// Groups of at most kSmallGroup members at level d, one group per lane.  Each member in turn
-// takes the reference's best child (first unvisited child, else the strict argmax of the
-// exact score) at the parent count N + VL*(rank+1), the children picked by earlier members
-// carrying their virtual loss; the lane scans the row in order, exactly as
+// Groups of at most SelTraits<RMAX>::kSmall members at level d, one group per lane.  Each
+// member in turn takes the reference's best child (first unvisited child, else the strict
+// argmax of the exact score) at the parent count N + VL*(rank+1), the children picked by
+// earlier members carrying their virtual loss; the lane scans the row in order, exactly as
 // CythonLockFreeTree.select_best_child_nogil does.  The members of each picked child are
 // placed in the parent's segment, children in order of their first pick, members in rank
 // order.
-constexpr int kSmallGroup = 1;
+constexpr int kLaneGroup = 2;
 
 // Single-member groups are kept apart from the chain groups in the kernels with a lane pass
 // (rows of at most 192 children) or a leaf pass (256 and 384); the 8-slot kernel keeps every
@@ -961,6 +961,11 @@ struct SelTraits {
   // (instead of becoming chains) in the 4-slot kernels; the 6- and 8-slot kernels' chains have
   // no registers left for it.  (Measured: no change on C2, whose such groups are leaves.)
   static constexpr bool kWideLanePass = RMAX == 4;
+  // members of the groups that the lane pass takes (one group per lane): up to kLaneGroup in
+  // the 1- and 2-slot kernels (C4 select 514 -> 506 us with 2 members, 510 with 4, 565 with 8;
+  // the 3-slot kernel spills with them), single members elsewhere (the leaf pass takes single
+  // members only)
+  static constexpr int kSmall = RMAX <= 2 ? kLaneGroup : 1;
 };
 
 
@@ -969,6 +974,7 @@ __device__ inline void small_groups_body(const SelArgs& f, const SelCfg& c, int 
                                          int64_t tb, int64_t gmax, const LevelLds& L,
                                          LevelShared<NT>& sh, int32_t* lfs, int32_t* lflag,
                                          bool vl_done) {
+  constexpr int kSmallGroup = SelTraits<RMAX>::kSmall;
   const SelArgs& w = f;
   const int cur = d & 1, nxt = cur ^ 1;
   const int MW = w.max_wave, MD = w.max_depth_buf;
@@ -1535,7 +1541,7 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         sum += v;
-        const bool big = !sg || v > kSmallGroup;
+        const bool big = !sg || v > Tr::kSmall;
         nbg += v > 0 && big;
         nsm += v > 0 && !big;
       }
@@ -1551,7 +1557,7 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
       for (int i = lo; i < hi; ++i) {
         const int v = cnt_s[i];
         if (v > 0) {
-          const bool big = !sg || v > kSmallGroup;
+          const bool big = !sg || v > Tr::kSmall;
           const int g = big ? bbase + pbg++ : W - 1 - (sbase + psm++);
           gnode[nxt * W + g] = (uint32_t)(first + 1 + i);
           gsl[nxt * W + g] = (uint32_t)(seg + run) | ((uint32_t)v << 16);
@@ -1613,7 +1619,7 @@ __device__ inline void start_group(const LevelLds& L, LevelShared<NT>& sh, int W
   if (tid < OMQ_NSTATS) sh.st[tid] = 0;
   if (tid == 0) {
     // a single member goes to the single-member groups of the kernels that keep them apart
-    const bool big = !SelTraits<RMAX>::kSingles || m > kSmallGroup;
+    const bool big = !SelTraits<RMAX>::kSingles || m > SelTraits<RMAX>::kSmall;
     const int g0 = big ? 0 : W - 1;
     L.gnode[cur * W + g0] = (uint32_t)p;
     L.gsl[cur * W + g0] = (uint32_t)seg | ((uint32_t)m << 16);
