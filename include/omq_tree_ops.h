@@ -422,6 +422,106 @@ int omq_fused_ucb_selection(const int32_t* node_indices, int32_t batch,
                             const int32_t* visit_counts, const float* priors, float c_puct,
                             int32_t* selected, void* stream);
 
+/* The reference accelerator's remaining operators (MCTSGPUAccelerator,
+ * python/mcts/gpu/mcts_gpu_accelerator.py:81-207, over the pybind module of
+ * python/mcts/gpu/mcts_kernels.cu:2342-2410).  Their trees are the reference's GPU variant: a
+ * dense children table children[num_nodes * max_children] (a row ends at its first negative
+ * entry) and explicit CSR edges.  Index arrays are trusted as in the reference, except where a
+ * check is stated. */
+
+/* Paths whose current node needs expansion: for s < wave_size with valid_mask[s] != 0 and
+ * 0 <= current_nodes[s] < num_nodes, the node when its table row holds no child and its visit
+ * count is 0.  The nodes are written to out_nodes in path order (a node reached by two paths is
+ * written twice, as in the reference) and their number to out_count[0] (device memory);
+ * out_nodes holds wave_size entries, all of which the call may write.
+ * Replaces find_expansion_nodes_cuda (mcts_kernels.cu:46-87,1329-1362), which writes them in
+ * the order its atomics land and bounds the node index by the number of paths. */
+int omq_find_expansion_nodes(const int32_t* current_nodes, const uint8_t* valid_mask,
+                             int32_t wave_size, const int32_t* children, int32_t max_children,
+                             const int32_t* visit_counts, int32_t num_nodes, int32_t* out_nodes,
+                             int32_t* out_count, void* stream);
+
+/* UCB selection over CSR rows: for row b < batch, edges [row_ptr[b], row_ptr[b+1]) of
+ * col_indices / priors, child c_i = col_indices[i]:
+ *     ucb_i = (visit_counts[c_i] > 0 ? q_values[c_i] : 0)
+ *             + c_puct * priors[i] * sqrtf((float)parent_visits[b] + 1) / (1 + visit_counts[c_i])
+ * in float32, left to right; an edge is skipped when c_i < 0, and also (the reference reads
+ * past its arrays there) when i >= num_children or c_i >= num_children.  selected[b] = the row
+ * position of the first maximum above -1e10 (strict '>'), 0 when no score is above it or when
+ * row_ptr[b] < 0 or row_ptr[b+1] < row_ptr[b], and -1 for an empty row; scores[b] (when not
+ * NULL) that maximum (-1e10 without one, 0 for the last three cases).
+ * Replaces batched_ucb_selection_cuda (mcts_kernels.cu:240-318,1412-1464). */
+int omq_batched_ucb_selection(const float* q_values, const int32_t* visit_counts,
+                              int32_t num_children, const int32_t* parent_visits,
+                              const float* priors, const int32_t* row_ptr,
+                              const int32_t* col_indices, int32_t batch, float c_puct,
+                              int32_t* selected, float* scores, void* stream);
+
+/* Selection down the dense children table, one path per root: from roots[w], while depth <
+ * max_depth - 1, an expanded node (is_expanded) scores its children (up to the first negative
+ * entry): an unvisited child +inf, else q_values[c] + c_puct * prior_probs[c] *
+ * sqrtf((float)visit_counts[node]) / (1 + visit_counts[c]) (float32, left to right); the first
+ * maximum (strict '>' from -inf) is next.  A node that is not expanded, has no child or no
+ * child above -inf ends the path: expand_nodes[w] = node, needs_expansion[w] = 1,
+ * path_lengths[w] = depth + 1.  A path that reaches depth max_depth - 1 leaves path_lengths[w],
+ * expand_nodes[w] and needs_expansion[w] at 0, as the reference's kernel does.
+ * paths[w * max_depth + i] holds the path's nodes and -1 after its last.  The children table
+ * has num_nodes rows: a child entry >= num_nodes ends its row as a negative one does, and a
+ * root outside [0, num_nodes) is a path of one node that needs expansion (the reference reads
+ * past its arrays in both cases).  max_depth >= 1.
+ * Replaces fused_select_expand_cuda (mcts_kernels.cu:451-544,2002-2045). */
+int omq_fused_select_expand(const int32_t* roots, int32_t num_paths, const int32_t* children,
+                            int32_t num_nodes, int32_t max_children,
+                            const int32_t* visit_counts, const float* q_values,
+                            const float* prior_probs, const uint8_t* is_expanded,
+                            int32_t max_depth, float c_puct, int32_t* paths,
+                            int32_t* path_lengths, int32_t* expand_nodes,
+                            uint8_t* needs_expansion, void* stream);
+
+/* The reference's second form of the same descent: from roots[w], while depth < max_depth - 1
+ * and depth < 32, a node with visit_counts[node] == 0 ends the path; otherwise its children (up
+ * to the first negative entry) score
+ *     q = n > 0 ? value_sums[c] * (1 / ((float)n + 1e-8f)) : 0,   n = visit_counts[c]
+ *     ucb = q + c_puct * priors[c] * sqrt_parent * (1 / (1 + (float)n))
+ * with correctly rounded float32 reciprocals and sqrt_parent = 1 / sqrt(r), r = 1 / (float)(N +
+ * 1) in float32, the square root and its reciprocal taken in float64 and rounded once to float32
+ * (the reference's rsqrtf is an approximation with no published rounding); the first maximum
+ * (strict '>' from -inf) is next, and a node with no such child ends the path.
+ * path_lengths[w] = depth + 1 always; paths as above; ucb_scores[w * max_children + i] = the
+ * root's score of child i (0 past the row's end, or when the root is not scored).  Bounds as
+ * above.  Replaces fused_select_expand_optimized_cuda (mcts_kernels.cu:546-640,2047-2083). */
+int omq_fused_select_expand_optimized(const int32_t* roots, int32_t num_paths,
+                                      const int32_t* children, int32_t num_nodes,
+                                      int32_t max_children, const int32_t* visit_counts,
+                                      const float* value_sums, const float* priors,
+                                      int32_t max_depth, float c_puct, float* ucb_scores,
+                                      int32_t* paths, int32_t* path_lengths, void* stream);
+
+/* Children appended for a batch of parents, in batch order.  Parent b with 0 <=
+ * parent_indices[b] < max_nodes and n = num_children[b] > 0 takes nodes [node_counter[0],
+ * + n) and edges [edge_counter[0], + n) (both counters advance by n); when either range passes
+ * max_nodes / max_edges nothing is written for it (the counters still advance, as the
+ * reference's atomic bump does).  For i < min(n, max_children), child c = first node + i and
+ * edge e = first edge + i: parent_indices_out[c] = p, parent_actions_out[c] = actions[b *
+ * max_children + i], node_priors_out[c] = priors[b * max_children + i], visit_counts_out[c] =
+ * 0, value_sums_out[c] = 0, children[p * max_children + i] = c (when that slot is below
+ * max_nodes * max_children), col_indices[e] = c, edge_actions[e] and edge_priors[e] as the
+ * child's.  child_indices[b * max_children + i] = c for every child written, -1 otherwise.
+ * Two items with the same parent write the same children-table slots, and which lands last is
+ * not specified (nor is it in the reference).  max_children >= 1.
+ * Replaces batched_add_children_cuda (mcts_kernels.cu:1122-1189,1679-1733), which allocates in
+ * the order its threads' atomics land (batch order is one of them) and returns the index
+ * tensor unfilled. */
+int omq_batched_add_children(const int32_t* parent_indices, int32_t batch,
+                             const int32_t* actions, const float* priors,
+                             const int32_t* num_children, int32_t* node_counter,
+                             int32_t* edge_counter, int32_t* children,
+                             int32_t* parent_indices_out, int32_t* parent_actions_out,
+                             float* node_priors_out, int32_t* visit_counts_out,
+                             float* value_sums_out, int32_t* col_indices, int32_t* edge_actions,
+                             float* edge_priors, int32_t max_nodes, int32_t max_children,
+                             int32_t max_edges, int32_t* child_indices, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -91,6 +91,15 @@ SIGNATURES = {
     "omq_leaf_features": (ctypes.c_int, [_FP, _WP, _p, _p, _p, _i32, _i32, _i32, _p, _p]),
     "omq_fused_ucb_selection": (ctypes.c_int, [_p, _i32, _p, _p, _p, _p, _p, _p, ctypes.c_float,
                                                _p, _p]),
+    "omq_find_expansion_nodes": (ctypes.c_int, [_p, _p, _i32, _p, _i32, _p, _i32, _p, _p, _p]),
+    "omq_batched_ucb_selection": (ctypes.c_int, [_p, _p, _i32, _p, _p, _p, _p, _i32,
+                                                 ctypes.c_float, _p, _p, _p]),
+    "omq_fused_select_expand": (ctypes.c_int, [_p, _i32, _p, _i32, _i32, _p, _p, _p, _p, _i32,
+                                               ctypes.c_float, _p, _p, _p, _p, _p]),
+    "omq_fused_select_expand_optimized": (ctypes.c_int, [_p, _i32, _p, _i32, _i32, _p, _p, _p,
+                                                         _i32, ctypes.c_float, _p, _p, _p, _p]),
+    "omq_batched_add_children": (ctypes.c_int, [_p, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                                                _p, _p, _p, _p, _p, _i32, _i32, _i32, _p, _p]),
     "omq_root_policy": (ctypes.c_int, [_FP, _p, _p]),
     "omq_sample_actions": (ctypes.c_int, [_FP, _p, ctypes.c_double, ctypes.c_uint64,
                                           ctypes.c_uint64, _p, _p]),

@@ -49,6 +49,36 @@ hipError_t launch_fused_ucb(const int32_t* node_indices, int batch, const int32_
                             const int32_t* ends, const int32_t* children, const float* q,
                             const int32_t* visits, const float* priors, float c_puct,
                             int32_t* selected, hipStream_t st);
+hipError_t launch_find_expansion_nodes(const int32_t* current_nodes, const uint8_t* valid_mask,
+                                       int wave_size, const int32_t* children, int max_children,
+                                       const int32_t* visit_counts, int num_nodes,
+                                       int32_t* out_nodes, int32_t* out_count, hipStream_t st);
+hipError_t launch_batched_ucb(const float* q_values, const int32_t* visit_counts,
+                              int num_children, const int32_t* parent_visits,
+                              const float* priors, const int32_t* row_ptr,
+                              const int32_t* col_indices, int batch, float c_puct,
+                              int32_t* selected, float* scores, hipStream_t st);
+hipError_t launch_fused_select_expand(const int32_t* roots, int num_paths,
+                                      const int32_t* children, int num_nodes, int max_children,
+                                      const int32_t* visit_counts, const float* q_values,
+                                      const float* prior_probs, const uint8_t* is_expanded,
+                                      int max_depth, float c_puct, int32_t* paths,
+                                      int32_t* path_lengths, int32_t* expand_nodes,
+                                      uint8_t* needs_expansion, hipStream_t st);
+hipError_t launch_fused_select_expand_opt(const int32_t* roots, int num_paths,
+                                          const int32_t* children, int num_nodes,
+                                          int max_children, const int32_t* visit_counts,
+                                          const float* value_sums, const float* priors,
+                                          int max_depth, float c_puct, float* ucb_scores,
+                                          int32_t* paths, int32_t* path_lengths,
+                                          hipStream_t st);
+hipError_t launch_batched_add_children(
+    const int32_t* parent_indices, int batch, const int32_t* actions, const float* priors,
+    const int32_t* num_children, int32_t* node_counter, int32_t* edge_counter,
+    int32_t* children, int32_t* parent_indices_out, int32_t* parent_actions_out,
+    float* node_priors_out, int32_t* visit_counts_out, float* value_sums_out,
+    int32_t* col_indices, int32_t* edge_actions, float* edge_priors, int max_nodes,
+    int max_children, int max_edges, int32_t* child_indices, hipStream_t st);
 size_t leaf_lds_per_wave_host(const omq_forest& f);
 }  // namespace omq
 
@@ -404,6 +434,118 @@ int omq_fused_ucb_selection(const int32_t* node_indices, int32_t batch,
                                           children, q_values, visit_counts, priors, c_puct,
                                           selected, (hipStream_t)stream),
                     "omq_fused_ucb_selection");
+}
+
+int omq_find_expansion_nodes(const int32_t* current_nodes, const uint8_t* valid_mask,
+                             int32_t wave_size, const int32_t* children, int32_t max_children,
+                             const int32_t* visit_counts, int32_t num_nodes, int32_t* out_nodes,
+                             int32_t* out_count, void* stream) {
+  if (wave_size < 0 || max_children < 0 || num_nodes < 0)
+    return fail(OMQ_E_ARG, "omq_find_expansion_nodes: wave_size %d, max_children %d, "
+                "num_nodes %d must not be negative", wave_size, max_children, num_nodes);
+  if (!out_count) return fail(OMQ_E_ARG, "omq_find_expansion_nodes: null count");
+  if (wave_size > 0 && (!current_nodes || !valid_mask || !out_nodes ||
+                        (num_nodes > 0 && (!visit_counts || (max_children > 0 && !children)))))
+    return fail(OMQ_E_ARG, "omq_find_expansion_nodes: a null array");
+  return hip_status(omq::launch_find_expansion_nodes(current_nodes, valid_mask, wave_size,
+                                                     children, max_children, visit_counts,
+                                                     num_nodes, out_nodes, out_count,
+                                                     (hipStream_t)stream),
+                    "omq_find_expansion_nodes");
+}
+
+int omq_batched_ucb_selection(const float* q_values, const int32_t* visit_counts,
+                              int32_t num_children, const int32_t* parent_visits,
+                              const float* priors, const int32_t* row_ptr,
+                              const int32_t* col_indices, int32_t batch, float c_puct,
+                              int32_t* selected, float* scores, void* stream) {
+  if (batch < 0 || num_children < 0)
+    return fail(OMQ_E_ARG, "omq_batched_ucb_selection: batch %d, num_children %d < 0", batch,
+                num_children);
+  if (batch == 0) return OMQ_OK;
+  if (!parent_visits || !row_ptr || !selected ||
+      (num_children > 0 && (!q_values || !visit_counts || !priors || !col_indices)))
+    return fail(OMQ_E_ARG, "omq_batched_ucb_selection: a null array");
+  return hip_status(omq::launch_batched_ucb(q_values, visit_counts, num_children, parent_visits,
+                                            priors, row_ptr, col_indices, batch, c_puct,
+                                            selected, scores, (hipStream_t)stream),
+                    "omq_batched_ucb_selection");
+}
+
+int omq_fused_select_expand(const int32_t* roots, int32_t num_paths, const int32_t* children,
+                            int32_t num_nodes, int32_t max_children,
+                            const int32_t* visit_counts, const float* q_values,
+                            const float* prior_probs, const uint8_t* is_expanded,
+                            int32_t max_depth, float c_puct, int32_t* paths,
+                            int32_t* path_lengths, int32_t* expand_nodes,
+                            uint8_t* needs_expansion, void* stream) {
+  if (num_paths < 0 || num_nodes < 0 || max_children < 0 || max_depth < 1)
+    return fail(OMQ_E_ARG, "omq_fused_select_expand: num_paths %d, num_nodes %d, "
+                "max_children %d must not be negative and max_depth %d >= 1", num_paths,
+                num_nodes, max_children, max_depth);
+  if (num_paths == 0) return OMQ_OK;
+  if (!roots || !paths || !path_lengths || !expand_nodes || !needs_expansion ||
+      (num_nodes > 0 && (!visit_counts || !q_values || !prior_probs || !is_expanded ||
+                         (max_children > 0 && !children))))
+    return fail(OMQ_E_ARG, "omq_fused_select_expand: a null array");
+  return hip_status(omq::launch_fused_select_expand(roots, num_paths, children, num_nodes,
+                                                    max_children, visit_counts, q_values,
+                                                    prior_probs, is_expanded, max_depth,
+                                                    c_puct, paths, path_lengths, expand_nodes,
+                                                    needs_expansion, (hipStream_t)stream),
+                    "omq_fused_select_expand");
+}
+
+int omq_fused_select_expand_optimized(const int32_t* roots, int32_t num_paths,
+                                      const int32_t* children, int32_t num_nodes,
+                                      int32_t max_children, const int32_t* visit_counts,
+                                      const float* value_sums, const float* priors,
+                                      int32_t max_depth, float c_puct, float* ucb_scores,
+                                      int32_t* paths, int32_t* path_lengths, void* stream) {
+  if (num_paths < 0 || num_nodes < 0 || max_children < 0 || max_depth < 1)
+    return fail(OMQ_E_ARG, "omq_fused_select_expand_optimized: num_paths %d, num_nodes %d, "
+                "max_children %d must not be negative and max_depth %d >= 1", num_paths,
+                num_nodes, max_children, max_depth);
+  if (num_paths == 0) return OMQ_OK;
+  if (!roots || !paths || !path_lengths || (max_children > 0 && !ucb_scores) ||
+      (num_nodes > 0 && (!visit_counts || !value_sums || !priors ||
+                         (max_children > 0 && !children))))
+    return fail(OMQ_E_ARG, "omq_fused_select_expand_optimized: a null array");
+  return hip_status(omq::launch_fused_select_expand_opt(roots, num_paths, children, num_nodes,
+                                                        max_children, visit_counts, value_sums,
+                                                        priors, max_depth, c_puct, ucb_scores,
+                                                        paths, path_lengths,
+                                                        (hipStream_t)stream),
+                    "omq_fused_select_expand_optimized");
+}
+
+int omq_batched_add_children(const int32_t* parent_indices, int32_t batch,
+                             const int32_t* actions, const float* priors,
+                             const int32_t* num_children, int32_t* node_counter,
+                             int32_t* edge_counter, int32_t* children,
+                             int32_t* parent_indices_out, int32_t* parent_actions_out,
+                             float* node_priors_out, int32_t* visit_counts_out,
+                             float* value_sums_out, int32_t* col_indices, int32_t* edge_actions,
+                             float* edge_priors, int32_t max_nodes, int32_t max_children,
+                             int32_t max_edges, int32_t* child_indices, void* stream) {
+  if (batch < 0 || max_nodes < 0 || max_edges < 0 || max_children < 1)
+    return fail(OMQ_E_ARG, "omq_batched_add_children: batch %d, max_nodes %d, max_edges %d "
+                "must not be negative and max_children %d >= 1", batch, max_nodes, max_edges,
+                max_children);
+  if (batch == 0) return OMQ_OK;
+  if (!parent_indices || !actions || !priors || !num_children || !node_counter ||
+      !edge_counter || !child_indices ||
+      (max_nodes > 0 && (!children || !parent_indices_out || !parent_actions_out ||
+                         !node_priors_out || !visit_counts_out || !value_sums_out)) ||
+      (max_edges > 0 && (!col_indices || !edge_actions || !edge_priors)))
+    return fail(OMQ_E_ARG, "omq_batched_add_children: a null array");
+  return hip_status(omq::launch_batched_add_children(
+                        parent_indices, batch, actions, priors, num_children, node_counter,
+                        edge_counter, children, parent_indices_out, parent_actions_out,
+                        node_priors_out, visit_counts_out, value_sums_out, col_indices,
+                        edge_actions, edge_priors, max_nodes, max_children, max_edges,
+                        child_indices, (hipStream_t)stream),
+                    "omq_batched_add_children");
 }
 
 }  // extern "C"

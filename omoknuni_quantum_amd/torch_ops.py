@@ -26,6 +26,13 @@ outside the array are skipped).  ``fused_ucb_selection`` follows the reference's
 (torch_custom_ops.py:108-193, kernel mcts_kernels.cu:1466-1512): per parent, the row position
 of the first maximum of q + c*P*sqrt(N_parent)/(1+n), with q = 0 for an unvisited child.
 
+The reference accelerator's other operators (MCTSGPUAccelerator,
+python/mcts/gpu/mcts_gpu_accelerator.py:81-207, over its pybind module
+mcts_kernels.cu:2342-2366) are plain functions here with the same signatures:
+``find_expansion_nodes``, ``batched_ucb_selection``, ``fused_select_expand``,
+``fused_select_expand_optimized`` and ``batched_add_children``; mcts_gpu_accelerator.py of this
+package wraps them in the reference's accelerator class.
+
 There is no CPU implementation: tensors must be on a HIP device, and a missing library raises.
 """
 from __future__ import annotations
@@ -137,6 +144,182 @@ def fused_ucb_selection(node_indices: torch.Tensor, children_start: torch.Tensor
         visit_counts.data_ptr(), priors.data_ptr(), float(c_puct), selected.data_ptr(),
         _stream(dev)), "omq_fused_ucb_selection")
     return selected
+
+
+def _need(name: str, **tensors) -> None:
+    """dtype checks: name=(tensor, dtype)."""
+    for arg, (t, dt) in tensors.items():
+        if t.dtype != dt:
+            raise RuntimeError(f"omq::{name}: {arg} must be {dt}, not {t.dtype}")
+
+
+# ---- the reference accelerator's operators -------------------------------------------------
+# Plain functions with the signatures of the reference's pybind module
+# (python/mcts/gpu/mcts_kernels.cu:2342-2366), as MCTSGPUAccelerator calls them.
+
+def find_expansion_nodes(current_nodes: torch.Tensor, children: torch.Tensor,
+                         visit_counts: torch.Tensor, valid_path_mask: torch.Tensor,
+                         wave_size: int, max_children: int) -> torch.Tensor:
+    """The nodes among current_nodes[:wave_size] (valid paths) whose children row holds no
+    child and whose visit count is 0, in path order (find_expansion_nodes_cuda,
+    mcts_kernels.cu:1329-1362).  Waits for the device to read the count, as the reference
+    does."""
+    dev = _check_device("find_expansion_nodes", current_nodes, children, visit_counts,
+                        valid_path_mask)
+    _need("find_expansion_nodes", current_nodes=(current_nodes, torch.int32),
+          children=(children, torch.int32), visit_counts=(visit_counts, torch.int32),
+          valid_path_mask=(valid_path_mask, torch.bool))
+    wave_size, max_children = int(wave_size), int(max_children)
+    if wave_size < 0 or max_children < 0:
+        raise RuntimeError("omq::find_expansion_nodes: negative wave_size or max_children")
+    if wave_size > current_nodes.numel() or wave_size > valid_path_mask.numel():
+        raise RuntimeError(f"omq::find_expansion_nodes: wave_size {wave_size} exceeds the "
+                           f"paths given ({current_nodes.numel()}, {valid_path_mask.numel()})")
+    rows = children.numel() // max_children if max_children else visit_counts.numel()
+    num_nodes = min(rows, visit_counts.numel())
+    out = torch.empty(max(wave_size, 1), dtype=torch.int32, device=dev)
+    count = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.check(_lib.load().omq_find_expansion_nodes(
+        current_nodes.data_ptr(), valid_path_mask.data_ptr(), wave_size, children.data_ptr(),
+        max_children, visit_counts.data_ptr(), num_nodes, out.data_ptr(), count.data_ptr(),
+        _stream(dev)), "omq_find_expansion_nodes")
+    return out[:int(count.item())]
+
+
+def batched_ucb_selection(q_values: torch.Tensor, visit_counts: torch.Tensor,
+                          parent_visits: torch.Tensor, priors: torch.Tensor,
+                          row_ptr: torch.Tensor, col_indices: torch.Tensor,
+                          c_puct: float) -> torch.Tensor:
+    """The row position of each CSR row's UCB maximum (batched_ucb_selection_cuda,
+    mcts_kernels.cu:1412-1464); all -1 for an empty batch, no children, or arrays whose sizes
+    disagree, as the reference returns."""
+    dev = _check_device("batched_ucb_selection", q_values, visit_counts, parent_visits, priors,
+                        row_ptr, col_indices)
+    _need("batched_ucb_selection", q_values=(q_values, torch.float32),
+          visit_counts=(visit_counts, torch.int32), parent_visits=(parent_visits, torch.int32),
+          priors=(priors, torch.float32), row_ptr=(row_ptr, torch.int32),
+          col_indices=(col_indices, torch.int32))
+    batch, nc = parent_visits.numel(), q_values.numel()
+    selected = torch.full((batch,), -1, dtype=torch.int32, device=dev)
+    if batch == 0 or nc == 0 or visit_counts.numel() != nc or priors.numel() != nc or \
+            col_indices.numel() != nc or row_ptr.numel() != batch + 1:
+        return selected
+    _lib.check(_lib.load().omq_batched_ucb_selection(
+        q_values.data_ptr(), visit_counts.data_ptr(), nc, parent_visits.data_ptr(),
+        priors.data_ptr(), row_ptr.data_ptr(), col_indices.data_ptr(), batch, float(c_puct),
+        selected.data_ptr(), None, _stream(dev)), "omq_batched_ucb_selection")
+    return selected
+
+
+def _table(name: str, children: torch.Tensor) -> tuple[int, int]:
+    if children.dim() != 2:
+        raise RuntimeError(f"omq::{name}: children must be [num_nodes, max_children]")
+    return int(children.shape[0]), int(children.shape[1])
+
+
+def fused_select_expand(roots: torch.Tensor, children: torch.Tensor, visit_counts: torch.Tensor,
+                        q_values: torch.Tensor, prior_probs: torch.Tensor,
+                        is_expanded: torch.Tensor, max_depth: int, c_puct: float):
+    """(paths [W, max_depth], path_lengths, expand_nodes, needs_expansion) of one descent per
+    root (fused_select_expand_cuda, mcts_kernels.cu:2002-2045)."""
+    name = "fused_select_expand"
+    dev = _check_device(name, roots, children, visit_counts, q_values, prior_probs, is_expanded)
+    _need(name, roots=(roots, torch.int32), children=(children, torch.int32),
+          visit_counts=(visit_counts, torch.int32), q_values=(q_values, torch.float32),
+          prior_probs=(prior_probs, torch.float32), is_expanded=(is_expanded, torch.bool))
+    rows, mc = _table(name, children)
+    num_nodes = min(rows, visit_counts.numel(), q_values.numel(), prior_probs.numel(),
+                    is_expanded.numel())
+    W, D = roots.numel(), int(max_depth)
+    if D < 1:
+        raise RuntimeError(f"omq::{name}: max_depth {D} < 1")
+    paths = torch.empty((W, D), dtype=torch.int32, device=dev)
+    plen = torch.empty(W, dtype=torch.int32, device=dev)
+    expand = torch.empty(W, dtype=torch.int32, device=dev)
+    needs = torch.empty(W, dtype=torch.bool, device=dev)
+    _lib.check(_lib.load().omq_fused_select_expand(
+        roots.data_ptr(), W, children.data_ptr(), num_nodes, mc, visit_counts.data_ptr(),
+        q_values.data_ptr(), prior_probs.data_ptr(), is_expanded.data_ptr(), D, float(c_puct),
+        paths.data_ptr(), plen.data_ptr(), expand.data_ptr(), needs.data_ptr(), _stream(dev)),
+        "omq_fused_select_expand")
+    return paths, plen, expand, needs
+
+
+def fused_select_expand_optimized(root_nodes: torch.Tensor, children: torch.Tensor,
+                                  visit_counts: torch.Tensor, value_sums: torch.Tensor,
+                                  priors: torch.Tensor, max_depth: int, c_puct: float):
+    """(paths [B, max_depth], path_lengths, ucb_scores [B, max_children]) of the reference's
+    second descent (fused_select_expand_optimized_cuda, mcts_kernels.cu:2047-2083)."""
+    name = "fused_select_expand_optimized"
+    dev = _check_device(name, root_nodes, children, visit_counts, value_sums, priors)
+    _need(name, root_nodes=(root_nodes, torch.int32), children=(children, torch.int32),
+          visit_counts=(visit_counts, torch.int32), value_sums=(value_sums, torch.float32),
+          priors=(priors, torch.float32))
+    rows, mc = _table(name, children)
+    num_nodes = min(rows, visit_counts.numel(), value_sums.numel(), priors.numel())
+    B, D = root_nodes.numel(), int(max_depth)
+    if D < 1:
+        raise RuntimeError(f"omq::{name}: max_depth {D} < 1")
+    paths = torch.empty((B, D), dtype=torch.int32, device=dev)
+    plen = torch.empty(B, dtype=torch.int32, device=dev)
+    ucb = torch.empty((B, mc), dtype=torch.float32, device=dev)
+    _lib.check(_lib.load().omq_fused_select_expand_optimized(
+        root_nodes.data_ptr(), B, children.data_ptr(), num_nodes, mc, visit_counts.data_ptr(),
+        value_sums.data_ptr(), priors.data_ptr(), D, float(c_puct), ucb.data_ptr(),
+        paths.data_ptr(), plen.data_ptr(), _stream(dev)), "omq_fused_select_expand_optimized")
+    return paths, plen, ucb
+
+
+def batched_add_children(parent_indices, actions, priors, num_children, node_counter,
+                         edge_counter, children, parent_indices_out, parent_actions_out,
+                         node_priors_out, visit_counts_out, value_sums_out, col_indices,
+                         edge_actions, edge_priors, max_nodes, max_children,
+                         max_edges) -> torch.Tensor:
+    """Children appended for a batch of parents in batch order, updating the tree tensors in
+    place (batched_add_children_cuda, mcts_kernels.cu:1679-1733); returns child_indices
+    [batch * max_children], -1 where no child is written.  Array sizes are checked against
+    max_nodes / max_children / max_edges (the reference writes past short arrays)."""
+    name = "batched_add_children"
+    ints = dict(parent_indices=parent_indices, actions=actions, num_children=num_children,
+                node_counter=node_counter, edge_counter=edge_counter, children=children,
+                parent_indices_out=parent_indices_out, parent_actions_out=parent_actions_out,
+                visit_counts_out=visit_counts_out, col_indices=col_indices,
+                edge_actions=edge_actions)
+    floats = dict(priors=priors, node_priors_out=node_priors_out,
+                  value_sums_out=value_sums_out, edge_priors=edge_priors)
+    dev = _check_device(name, *ints.values(), *floats.values())
+    _need(name, **{k: (v, torch.int32) for k, v in ints.items()},
+          **{k: (v, torch.float32) for k, v in floats.items()})
+    B, mn, mc, me = parent_indices.numel(), int(max_nodes), int(max_children), int(max_edges)
+    if mn < 0 or me < 0 or mc < 1:
+        raise RuntimeError(f"omq::{name}: max_nodes {mn}, max_edges {me} >= 0 and "
+                           f"max_children {mc} >= 1")
+    short = [k for k, t, n in (("actions", actions, B * mc), ("priors", priors, B * mc),
+                               ("num_children", num_children, B),
+                               ("node_counter", node_counter, 1),
+                               ("edge_counter", edge_counter, 1),
+                               ("children", children, mn * mc),
+                               ("parent_indices_out", parent_indices_out, mn),
+                               ("parent_actions_out", parent_actions_out, mn),
+                               ("node_priors_out", node_priors_out, mn),
+                               ("visit_counts_out", visit_counts_out, mn),
+                               ("value_sums_out", value_sums_out, mn),
+                               ("col_indices", col_indices, me),
+                               ("edge_actions", edge_actions, me),
+                               ("edge_priors", edge_priors, me)) if t.numel() < n]
+    if short:
+        raise RuntimeError(f"omq::{name}: arrays shorter than the sizes given: {short}")
+    child_indices = torch.empty(B * mc, dtype=torch.int32, device=dev)  # every entry written
+    if B == 0:
+        return child_indices
+    _lib.check(_lib.load().omq_batched_add_children(
+        parent_indices.data_ptr(), B, actions.data_ptr(), priors.data_ptr(),
+        num_children.data_ptr(), node_counter.data_ptr(), edge_counter.data_ptr(),
+        children.data_ptr(), parent_indices_out.data_ptr(), parent_actions_out.data_ptr(),
+        node_priors_out.data_ptr(), visit_counts_out.data_ptr(), value_sums_out.data_ptr(),
+        col_indices.data_ptr(), edge_actions.data_ptr(), edge_priors.data_ptr(), mn, mc, me,
+        child_indices.data_ptr(), _stream(dev)), "omq_batched_add_children")
+    return child_indices
 
 
 def _fused_ucb_fake(node_indices, children_start, children_end, children, q_values, visit_counts,

@@ -580,3 +580,198 @@ def fused_ucb_selection(node_indices, children_start, children_end, children, q_
                 best, arg = ucb, i - start
         out[b] = arg
     return out
+
+
+# ---- the reference accelerator's remaining operators (mcts_gpu_accelerator.py:81-207) ----------
+# Trees of the reference's GPU variant: a dense children table [num_nodes, max_children] whose
+# rows end at the first negative entry, per-node arrays, CSR edges.  Sequential float32 loops,
+# in the order the reference's kernels take their elements.
+
+def _row(children, node):
+    """The children of `node` up to the row's first negative entry (or the first entry past the
+    table's rows, which the HIP operators take as the row's end)."""
+    out = []
+    for c in children[node]:
+        c = int(c)
+        if c < 0 or c >= children.shape[0]:
+            break
+        out.append(c)
+    return out
+
+
+def find_expansion_nodes(current_nodes, valid_mask, wave_size, children, visit_counts):
+    """find_expansion_nodes_kernel (python/mcts/gpu/mcts_kernels.cu:46-87): for path s <
+    wave_size with valid_mask[s] and 0 <= node < num_nodes, the node when no entry of its table
+    row is >= 0 and its visit count is 0; listed here in path order."""
+    out = []
+    for s in range(wave_size):
+        node = int(current_nodes[s])
+        if not valid_mask[s] or node < 0 or node >= children.shape[0]:
+            continue
+        if not (children[node] >= 0).any() and int(visit_counts[node]) == 0:
+            out.append(node)
+    return np.array(out, np.int32)
+
+
+def batched_ucb_selection(q_values, visit_counts, parent_visits, priors, row_ptr, col_indices,
+                          c_puct):
+    """batched_ucb_selection_kernel (mcts_kernels.cu:240-318) for each row b: (selected, score).
+    sqrt_parent = sqrtf((float)parent_visits[b] + 1); ucb_i = (n_i > 0 ? q[c_i] : 0) +
+    ((c * P_i) * sqrt_parent) / (1 + n_i) over edges i with c_i >= 0 (and, as the HIP operator
+    bounds them, i and c_i below the number of children); the first maximum above -1e10
+    (position 0 / score -1e10 without one), -1 / 0 for an empty row, 0 / 0 for a negative start
+    or a decreasing row."""
+    nc = len(q_values)
+    c = F(c_puct)
+    B = len(parent_visits)
+    sel = np.zeros(B, np.int32)
+    sc = np.zeros(B, np.float32)
+    for b in range(B):
+        start, end = int(row_ptr[b]), int(row_ptr[b + 1])
+        if start < 0 or end < start:
+            continue
+        if start == end:
+            sel[b] = -1
+            continue
+        sp = np.sqrt(F(F(parent_visits[b]) + F(1.0)))
+        best, arg = F(-1e10), 0
+        for i in range(start, min(end, nc)):
+            ch = int(col_indices[i])
+            if ch < 0 or ch >= nc:
+                continue
+            n = F(visit_counts[ch])
+            q = F(q_values[ch]) if n > 0 else F(0.0)
+            ucb = F(q + F(F(F(c * F(priors[i])) * sp) / F(F(1.0) + n)))
+            if ucb > best:
+                best, arg = ucb, i - start
+        sel[b], sc[b] = arg, best
+    return sel, sc
+
+
+def fused_select_expand(roots, children, visit_counts, q_values, prior_probs, is_expanded,
+                        max_depth, c_puct):
+    """fused_select_expand_kernel (mcts_kernels.cu:451-544): (paths [W, max_depth],
+    path_lengths, expand_nodes, needs_expansion).  From the root, while depth < max_depth - 1:
+    an expanded node scores its children, +inf when unvisited, else q[c] + ((c_puct * P[c]) *
+    sqrtf((float)N[node])) / (1 + n); the first maximum above -inf is next.  A node that is not
+    expanded or has no such child ends the path (expansion at depth + 1); a path that reaches
+    the depth limit reports 0, 0, False."""
+    c = F(c_puct)
+    W, nn = len(roots), children.shape[0]
+    paths = np.full((W, max_depth), -1, np.int32)
+    plen = np.zeros(W, np.int32)
+    exp = np.zeros(W, np.int32)
+    need = np.zeros(W, np.bool_)
+    for w in range(W):
+        node = int(roots[w])
+        path = [node]
+        leaf = node < 0 or node >= nn
+        while not leaf and len(path) - 1 < max_depth - 1:
+            nxt = -1
+            if is_expanded[node]:
+                sp = np.sqrt(F(visit_counts[node]))
+                best = F(-np.inf)
+                for ch in _row(children, node):
+                    n = int(visit_counts[ch])
+                    if n == 0:
+                        u = F(np.inf)
+                    else:
+                        u = F(F(q_values[ch]) + F(F(F(c * F(prior_probs[ch])) * sp) /
+                                                  F(F(1.0) + F(n))))
+                    if u > best:
+                        best, nxt = u, ch
+            if nxt < 0:
+                leaf = True
+                break
+            node = nxt
+            path.append(node)
+        paths[w, :len(path)] = path
+        if leaf:
+            plen[w], exp[w], need[w] = len(path), node, True
+    return paths, plen, exp, need
+
+
+def _rsqrt_of_rcp(pv):
+    """1 / sqrt(r), r = 1 / (float)(pv + 1) in float32, the square root and its reciprocal in
+    float64, rounded once to float32."""
+    r = F(F(1.0) / F(pv + 1))
+    return F(1.0 / np.sqrt(np.float64(r)))
+
+
+def fused_select_expand_optimized(roots, children, visit_counts, value_sums, priors, max_depth,
+                                  c_puct):
+    """fused_select_expand_optimized_kernel (mcts_kernels.cu:546-640): (paths, path_lengths,
+    ucb_scores).  While depth < max_depth - 1 and depth < 32: a node without visits ends the
+    path; its children score q + ((c_puct * P[c]) * sqrt_parent) * (1 / (1 + n)), q = n > 0 ?
+    W[c] * (1 / (n + 1e-8)) : 0 (float32 reciprocals, sqrt_parent as _rsqrt_of_rcp); the first
+    maximum above -inf is next, and none ends the path.  path_lengths = depth + 1; ucb_scores
+    holds the root's row of scores (0 elsewhere)."""
+    c = F(c_puct)
+    W, nn = len(roots), children.shape[0]
+    mc = children.shape[1]
+    paths = np.full((W, max_depth), -1, np.int32)
+    plen = np.zeros(W, np.int32)
+    ucb = np.zeros((W, mc), np.float32)
+    for w in range(W):
+        node = int(roots[w])
+        path = [node]
+        if 0 <= node < nn:
+            while len(path) - 1 < max_depth - 1 and len(path) - 1 < 32:
+                pv = int(visit_counts[node])
+                if pv == 0:
+                    break
+                sp = _rsqrt_of_rcp(pv)
+                best, nxt = F(-np.inf), -1
+                for i, ch in enumerate(_row(children, node)):
+                    n = int(visit_counts[ch])
+                    q = F(F(value_sums[ch]) * F(F(1.0) / F(F(n) + F(1e-8)))) if n > 0 else F(0)
+                    u = F(q + F(F(F(c * F(priors[ch])) * sp) * F(F(1.0) / F(F(1.0) + F(n)))))
+                    if len(path) == 1:
+                        ucb[w, i] = u
+                    if u > best:
+                        best, nxt = u, ch
+                if nxt < 0:
+                    break
+                node = nxt
+                path.append(node)
+        paths[w, :len(path)] = path
+        plen[w] = len(path)
+    return paths, plen, ucb
+
+
+def _wrap32(x):
+    return np.int32((x + 2**31) % 2**32 - 2**31)
+
+
+def batched_add_children(parent_indices, actions, priors, num_children, tree, max_nodes,
+                         max_children, max_edges):
+    """batched_add_children_kernel (mcts_kernels.cu:1122-1189) with the items taken in batch
+    order.  tree: dict of numpy arrays node_counter [1], edge_counter [1], children [max_nodes *
+    max_children], parent_indices_out, parent_actions_out, node_priors_out, visit_counts_out,
+    value_sums_out [max_nodes], col_indices, edge_actions, edge_priors [max_edges], updated in
+    place.  Returns child_indices [batch * max_children] (-1 where nothing is written)."""
+    B = len(parent_indices)
+    out = np.full(B * max_children, -1, np.int32)
+    for b in range(B):
+        p, n = int(parent_indices[b]), int(num_children[b])
+        if p < 0 or p >= max_nodes or n <= 0:
+            continue
+        nd, ed = int(tree["node_counter"][0]), int(tree["edge_counter"][0])
+        tree["node_counter"][0] = _wrap32(nd + n)   # int32 atomics wrap
+        tree["edge_counter"][0] = _wrap32(ed + n)
+        if nd < 0 or ed < 0 or nd + n > max_nodes or ed + n > max_edges:
+            continue
+        for i in range(min(n, max_children)):
+            ch, e = nd + i, ed + i
+            a, pr = actions[b * max_children + i], priors[b * max_children + i]
+            tree["parent_indices_out"][ch] = p
+            tree["parent_actions_out"][ch] = a
+            tree["node_priors_out"][ch] = pr
+            tree["visit_counts_out"][ch] = 0
+            tree["value_sums_out"][ch] = 0.0
+            tree["children"][p * max_children + i] = ch
+            tree["col_indices"][e] = ch
+            tree["edge_actions"][e] = a
+            tree["edge_priors"][e] = pr
+            out[b * max_children + i] = ch
+    return out

@@ -1,0 +1,238 @@
+"""The reference accelerator's operators on the GPU (through torch_ops, the accelerator class
+and the C ABI) against the numpy restatements, bit for bit: random dense children tables with
+rows of 0 to 300 children, entries past a row's end, coarse values (exact ties), unvisited
+children, -inf and NaN values, and batches beyond one scan chunk (1024)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from omoknuni_quantum_amd import _lib, torch_ops
+from omoknuni_quantum_amd.mcts_gpu_accelerator import get_mcts_gpu_accelerator
+from oracle import ref_np
+
+pytestmark = pytest.mark.gpu
+F = np.float32
+
+
+def _t(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def _table(rng, nn, mc, frac_rows=0.6):
+    """A dense children table: row lengths 0..mc of random node ids, -1 padding, a few valid
+    ids behind a -1 and a few ids past the table (both end the row)."""
+    ch = np.full((nn, mc), -1, np.int32)
+    for x in range(nn):
+        if rng.random() < frac_rows:
+            k = int(rng.integers(1, mc + 1))
+            ch[x, :k] = rng.integers(0, nn, k)
+            if k < mc and rng.random() < 0.1:
+                ch[x, int(rng.integers(k + 1, mc + 1)) - 1] = int(rng.integers(0, nn))
+            if rng.random() < 0.05:
+                ch[x, int(rng.integers(0, k))] = nn + int(rng.integers(0, 5))
+    return ch
+
+
+def _node_values(rng, nn, special=True):
+    visits = rng.integers(0, 6, nn).astype(np.int32)
+    visits[rng.random(nn) < 0.3] = 0
+    q = (np.round(rng.random(nn) * 16 - 8) / 8).astype(F)
+    if special:
+        q[rng.random(nn) < 0.02] = -np.inf
+        q[rng.random(nn) < 0.02] = np.nan
+    prior = (np.round(rng.random(nn) * 8) / 8).astype(F)
+    return visits, q, prior
+
+
+def _same_f32(a, b):
+    return np.array_equal(np.asarray(a, F).view(np.int32), np.asarray(b, F).view(np.int32))
+
+
+@pytest.mark.parametrize("mc", [3, 64, 65, 300])
+def test_find_expansion_nodes(device, mc):
+    rng = np.random.default_rng(mc)
+    nn = 2000
+    ch = _table(rng, nn, mc, frac_rows=0.5)
+    visits, _, _ = _node_values(rng, nn)
+    W = 2500  # beyond one 1024-entry chunk of the compaction
+    cur = rng.integers(-3, nn + 3, W).astype(np.int32)
+    valid = rng.random(W) < 0.9
+    print(f"find_expansion_nodes mc={mc}", flush=True)
+    for ws in (W, 1, 0, 1024, 1025):
+        want = ref_np.find_expansion_nodes(cur, valid, ws, ch, visits)
+        got = torch_ops.find_expansion_nodes(_t(cur, device), _t(ch, device), _t(visits, device),
+                                             _t(valid, device), ws, mc)
+        assert np.array_equal(got.cpu().numpy(), want), ws
+    assert len(want) > 100
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_batched_ucb_selection(device, seed):
+    rng = np.random.default_rng(100 + seed)
+    B, nc = 700, 60_000
+    sizes = rng.integers(0, 301, B)
+    sizes[:6] = [0, 1, 63, 64, 65, 300]
+    row_ptr = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    row_ptr = np.minimum(row_ptr, nc + 10)       # the last rows run past the children
+    row_ptr[rng.integers(1, B, 5)] -= 3           # a few decreasing rows
+    row_ptr[rng.integers(0, B, 3)] = -2           # negative starts
+    col = rng.integers(-1, nc, nc).astype(np.int32)
+    col[rng.random(nc) < 0.01] = nc + 7           # past the children
+    visits, q, _ = _node_values(rng, nc)
+    priors = (np.round(rng.random(nc) * 8) / 8).astype(F)
+    pv = rng.integers(0, 50, B).astype(np.int32)
+    args = (q, visits, pv, priors, row_ptr, col)
+    sel_np, sc_np = ref_np.batched_ucb_selection(*args, 1.4)
+    dq, dv, dp, dpr, drp, dc = (_t(a, device) for a in args)
+    print(f"batched_ucb_selection seed={seed}", flush=True)
+    got = torch_ops.batched_ucb_selection(dq, dv, dp, dpr, drp, dc, 1.4)
+    assert np.array_equal(got.cpu().numpy(), sel_np)
+    # the scores, through the C ABI
+    sel = torch.empty(B, dtype=torch.int32, device=device)
+    sc = torch.empty(B, dtype=torch.float32, device=device)
+    _lib.check(_lib.load().omq_batched_ucb_selection(
+        dq.data_ptr(), dv.data_ptr(), nc, dp.data_ptr(), dpr.data_ptr(), drp.data_ptr(),
+        dc.data_ptr(), B, 1.4, sel.data_ptr(), sc.data_ptr(), None), "ucb")
+    torch.cuda.synchronize()
+    assert np.array_equal(sel.cpu().numpy(), sel_np)
+    assert _same_f32(sc.cpu().numpy(), sc_np)
+    # the reference's size checks: all -1
+    bad = torch_ops.batched_ucb_selection(dq, dv[:-1], dp, dpr, drp, dc, 1.4)
+    assert (bad.cpu() == -1).all()
+
+
+@pytest.mark.parametrize("mc", [4, 64, 150])
+def test_fused_select_expand(device, mc):
+    rng = np.random.default_rng(7 + mc)
+    nn = 3000
+    ch = _table(rng, nn, mc, frac_rows=0.8)
+    visits, q, prior = _node_values(rng, nn)
+    visits[rng.random(nn) < 0.5] += 3    # deeper descents
+    expanded = rng.random(nn) < 0.85
+    roots = rng.integers(0, nn, 600).astype(np.int32)
+    roots[:4] = [-1, nn, nn + 9, 0]
+    print(f"fused_select_expand mc={mc}", flush=True)
+    for D in (1, 2, 7, 20):
+        want = ref_np.fused_select_expand(roots, ch, visits, q, prior, expanded, D, 1.25)
+        got = torch_ops.fused_select_expand(*(_t(a, device) for a in
+                                              (roots, ch, visits, q, prior, expanded)), D, 1.25)
+        for k, (g, w) in enumerate(zip(got, want)):
+            assert np.array_equal(g.cpu().numpy(), w), (D, k)
+    assert want[1].max() >= 4
+
+
+@pytest.mark.parametrize("mc", [4, 64, 150])
+def test_fused_select_expand_optimized(device, mc):
+    rng = np.random.default_rng(11 + mc)
+    nn = 3000
+    ch = _table(rng, nn, mc, frac_rows=0.8)
+    visits, _, prior = _node_values(rng, nn, special=False)
+    visits[rng.random(nn) < 0.5] += 3
+    W = (np.round(rng.random(nn) * 32 - 16) / 8).astype(F)
+    W[rng.random(nn) < 0.02] = np.nan
+    roots = rng.integers(0, nn, 600).astype(np.int32)
+    roots[:3] = [-1, nn, 0]
+    print(f"fused_select_expand_optimized mc={mc}", flush=True)
+    for D in (1, 3, 40):
+        want = ref_np.fused_select_expand_optimized(roots, ch, visits, W, prior, D, 0.9)
+        got = torch_ops.fused_select_expand_optimized(*(_t(a, device) for a in
+                                                        (roots, ch, visits, W, prior)), D, 0.9)
+        assert np.array_equal(got[0].cpu().numpy(), want[0]), D
+        assert np.array_equal(got[1].cpu().numpy(), want[1]), D
+        assert _same_f32(got[2].cpu().numpy(), want[2]), D
+
+
+def test_fused_select_expand_optimized_chain_cap(device):
+    n = 40
+    ch = np.full((n, 2), -1, np.int32)
+    ch[:-1, 0] = np.arange(1, n)
+    visits = np.full(n, 3, np.int32)
+    W = np.zeros(n, F)
+    pri = np.full(n, 0.5, F)
+    p, L, _ = torch_ops.fused_select_expand_optimized(*(_t(a, device) for a in
+                                                        (np.zeros(1, np.int32), ch, visits, W,
+                                                         pri)), 50, 1.0)
+    assert int(L[0]) == 33 and p[0, :34].cpu().tolist() == list(range(33)) + [-1]
+
+
+def _empty_tree(max_nodes, max_children, max_edges, nc=0, ec=0):
+    """Tree arrays filled with markers, so that every write (and every missing one) shows."""
+    return dict(node_counter=np.array([nc], np.int32), edge_counter=np.array([ec], np.int32),
+                children=np.full(max_nodes * max_children, -1, np.int32),
+                parent_indices_out=np.full(max_nodes, -7, np.int32),
+                parent_actions_out=np.full(max_nodes, -7, np.int32),
+                node_priors_out=np.full(max_nodes, -7, F),
+                visit_counts_out=np.full(max_nodes, 9, np.int32),
+                value_sums_out=np.full(max_nodes, 9, F),
+                col_indices=np.full(max_edges, -7, np.int32),
+                edge_actions=np.full(max_edges, -7, np.int32),
+                edge_priors=np.full(max_edges, -7, F))
+
+
+def _tree_tensors(tr, device):
+    return {k: _t(v, device) for k, v in tr.items()}
+
+
+@pytest.mark.parametrize("case", ["fits", "overflow", "many"])
+def test_batched_add_children(device, case):
+    rng = np.random.default_rng({"fits": 1, "overflow": 2, "many": 3}[case])
+    mc = 12
+    B = {"fits": 300, "overflow": 500, "many": 3000}[case]
+    max_nodes = {"fits": 10_000, "overflow": 2500, "many": 40_000}[case]
+    max_edges = max_nodes - (300 if case == "overflow" else 0)
+    parents = rng.permutation(max_nodes + 50)[:B].astype(np.int32)  # unique; some >= max_nodes
+    parents[rng.random(B) < 0.02] = -1
+    nchild = rng.integers(-1, mc + 4, B).astype(np.int32)
+    acts = rng.integers(0, 361, B * mc).astype(np.int32)
+    pri = rng.random(B * mc).astype(F)
+    tr = _empty_tree(max_nodes, mc, max_edges, nc=17, ec=5)
+    dt = _tree_tensors(tr, device)
+    want = ref_np.batched_add_children(parents, acts, pri, nchild, tr, max_nodes, mc, max_edges)
+    print(f"batched_add_children {case}", flush=True)
+    acc = get_mcts_gpu_accelerator(device)
+    got = acc.batched_add_children(
+        _t(parents, device), _t(acts, device), _t(pri, device), _t(nchild, device),
+        dt["node_counter"], dt["edge_counter"], dt["children"], dt["parent_indices_out"],
+        dt["parent_actions_out"], dt["node_priors_out"], dt["visit_counts_out"],
+        dt["value_sums_out"], dt["col_indices"], dt["edge_actions"], dt["edge_priors"],
+        max_nodes, mc, max_edges)
+    assert np.array_equal(got.cpu().numpy(), want)
+    for k, v in tr.items():
+        g = dt[k].cpu().numpy()
+        assert (_same_f32(g, v) if v.dtype == F else np.array_equal(g, v)), k
+    written = int((want >= 0).sum())
+    if case == "overflow":
+        # items fit until the edges run out, none after
+        assert 0 < written and (want.reshape(B, mc)[:, 0] < 0).sum() > B // 4
+    else:
+        assert written > B * 3
+
+
+def test_accelerator_methods(device):
+    """The accelerator class forwards with the reference's argument order."""
+    rng = np.random.default_rng(5)
+    nn, mc = 500, 8
+    ch = _table(rng, nn, mc)
+    visits, q, prior = _node_values(rng, nn, special=False)
+    acc = get_mcts_gpu_accelerator(device)
+    assert acc is get_mcts_gpu_accelerator(device)
+    roots = np.zeros(64, np.int32)
+    exp = ch >= 0
+    want = ref_np.fused_select_expand(roots, ch, visits, q, prior, exp.any(1), 10, 1.0)
+    got = acc.fused_select_expand(roots=_t(roots, device), children=_t(ch, device),
+                                  visit_counts=_t(visits, device), q_values=_t(q, device),
+                                  prior_probs=_t(prior, device),
+                                  is_expanded=_t(exp.any(1), device), max_depth=10, c_puct=1.0)
+    assert all(np.array_equal(g.cpu().numpy(), w) for g, w in zip(got, want))
+    cur = rng.integers(0, nn, 100).astype(np.int32)
+    valid = np.ones(100, bool)
+    got = acc.find_expansion_nodes(_t(cur, device), _t(ch.reshape(-1), device),
+                                   _t(visits, device), _t(valid, device), 100, mc)
+    assert np.array_equal(got.cpu().numpy(),
+                          ref_np.find_expansion_nodes(cur, valid, 100, ch, visits))
+    st = acc.get_stats()
+    assert st["expansion_calls"] >= 1 and "libomq_tree_ops" in st["library"]
+    with pytest.raises(ValueError):
+        acc.batched_add_children(*([None] * 5))
