@@ -808,17 +808,54 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
   return first_end;
 }
 
+// First-unvisited prefix of a chain.  The reference takes the first unvisited child of a row
+// whenever one is left (CythonLockFreeTree.select_best_child_nogil returns at the first child
+// with no visits, cython_tree_optimized.pyx:451-452), and a pick makes its child visited (an
+// integer virtual loss >= 1).  So while unvisited children remain, rank r of the chain takes
+// the r-th of them in index order: the first npre = min(m, unvisited children) ranks are
+// decided from the children's visit counts alone.  Writes their picks to ch[0, npre) (each
+// child once: rank 0 among its picks) and every child's prefix count (0 or 1) to cnt_s[0, k),
+// which the chain starts from; returns npre.  (off: no virtual loss; nothing is taken.)
+template <int RMAX>
+__device__ __noinline__ int unvisited_prefix(const SelArgs& f, int64_t tb, int first, int k, int m,
+                                       bool on, uint32_t* ch, uint16_t* cnt_s) {
+  const int lane = lane_id();
+  int n[RMAX];
+#pragma unroll
+  for (int j = 0; j < RMAX; ++j) {
+    const int i = j * kWave + lane;
+    n[j] = 1;
+    if (on && i < k) n[j] = f.N[tb + first + 1 + i];
+  }
+  int npre = 0;
+#pragma unroll
+  for (int j = 0; j < RMAX; ++j) {
+    const int i = j * kWave + lane;
+    const bool u = i < k && n[j] == 0;
+    const uint64_t um = __ballot(u);
+    const int pos = npre + (int)__builtin_amdgcn_mbcnt_hi(
+                               (uint32_t)(um >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)um, 0u));
+    const bool pick = u && pos < m;
+    if (pick) ch[pos] = (uint32_t)i << 16;
+    if (i < k) cnt_s[i] = pick ? 1 : 0;
+    npre += __popcll(um);
+  }
+  wave_sync();
+  return min(npre, m);
+}
+
 // Chain of a row of k children, instantiated up to RMAX slots per lane (rows of at most
 // 64*RMAX children): a kernel holds only the widths its game model can produce, which keeps
-// its register demand within the 128 VGPRs of a 1024-thread workgroup.
-template <int RMAX>
+// its register demand within the 128 VGPRs of a 1024-thread workgroup.  WIDE: the kernel's
+// chains keep up to 256 registers (workgroups of at most 512 threads, one per CU).
+template <int RMAX, bool WIDE>
 __device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0,
                                      int m, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s,
                                      float4* cscr, int* progress) {
   const int r = (k + kWave - 1) / kWave;  // 1 <= r <= RMAX (checked by the caller)
-  // contender windows kept open across blocks in the kernels of up to 4 slots per lane (the
-  // wider kernels' chains have no registers left for it)
-  constexpr bool kPersist = RMAX <= 4;
+  // contender windows kept open across blocks in the kernels of up to 4 slots per lane and in
+  // the WIDE ones (the other wider kernels' chains have no registers left for it)
+  constexpr bool kPersist = RMAX <= 4 || WIDE;
   if (RMAX <= 1 || r <= 1)
     return run_chain<1, kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 2 && r == 2)
@@ -832,6 +869,27 @@ __device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, in
   if (RMAX >= 6 && r == 6)
     return run_chain<(RMAX >= 6 ? 6 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
   return run_chain<(RMAX >= 8 ? 8 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+}
+
+// A group's chain: the first-unvisited prefix, and the chain when the prefix does not take
+// every rank (the chain then derives the prefix's ranks again: starting it after them costs
+// the 6-slot kernel's chains about 60 spilled registers).  *all_prefix: every rank was taken by
+// the prefix (distinct children in index order, each picked once).
+template <int RMAX, bool WIDE>
+__device__ inline int group_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
+                                  const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
+                                  int* progress, bool* all_prefix) {
+  const int npre = unvisited_prefix<RMAX>(f, tb, first, k, m, c.vli > 0, ch, cnt_s);
+  *all_prefix = npre >= m;
+  if (npre >= m) {
+    if (progress != nullptr) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane_id() == 0)
+        __hip_atomic_store(progress, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    return -1;
+  }
+  return dispatch_chain<RMAX, WIDE>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
 }
 
 // Block-wide exclusive scan of a[0..n) in place (n <= 4 * NT); returns the total.  a may be
@@ -966,6 +1024,9 @@ struct SelTraits {
   // the 3-slot kernel spills with them), single members elsewhere (the leaf pass takes single
   // members only)
   static constexpr int kSmall = RMAX <= 2 ? kLaneGroup : 1;
+  // small groups decided by the first-unvisited rule one per thread (prefix_pass) in the
+  // kernels of 512 threads, whose chains have registers to spare for it
+  static constexpr bool kPrefixPass = RMAX >= 5;
 };
 
 
@@ -1236,6 +1297,157 @@ __device__ inline void leaf_pass(const SelArgs& f, const SelCfg& c, int t, int d
 }
 
 // Size class of a chain group of m members: 0 for the largest (m >= 2^15), 15 for m = 1.
+// Small groups decided by the first-unvisited rule, one group per thread, before a level's
+// chains.  A group of at most kPrefixMembers members whose node's first kPrefixWindow
+// children hold at least m unvisited ones takes them in index order (unvisited_prefix gives
+// the rule): member r goes to the r-th of them, each child a single-member group of the next
+// level at segment position seg + r.  A group at a leaf ends its members' paths there.  Both
+// log the group, write the path entries and apply the arrival's virtual loss as the chain loop
+// does.  The other groups stay chains, compacted in place to [0, kept) in their order.  Ends
+// with a barrier; sets sh.nbig[cur] to the kept count.
+constexpr int kPrefixMembers = 4;
+constexpr int kPrefixWindow = 8;
+
+template <int RMAX, int NT>
+__device__ inline void prefix_pass(const SelArgs& f, const SelCfg& c, int t, int d, int W,
+                                   int64_t tb, int64_t gmax, const LevelLds& L,
+                                   LevelShared<NT>& sh, int32_t* lfs, int32_t* lflag, int nb,
+                                   bool vl_done, bool sg) {
+  const SelArgs& w = f;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int cur = d & 1, nxt = cur ^ 1;
+  const int MW = w.max_wave, MD = w.max_depth_buf;
+  int32_t* N = f.N;
+  const bool big1 = !sg || 1 > SelTraits<RMAX>::kSmall;  // where single-member groups go
+  int kept_total = 0;
+  for (int c0 = 0; c0 < nb; c0 += NT) {
+    const int gi = c0 + tid;
+    bool keep = false, done = false, leaf = false;
+    uint32_t sl = 0, pn = 0;
+    int p = 0, seg = 0, m = 0, k = 0, first = 0, Np0 = 0, scan = 0;
+    uint32_t upos = 0u;  // bit j: child j of the window is taken
+    if (gi < nb) {
+      sl = L.gsl[cur * W + gi];
+      pn = L.gnode[cur * W + gi];
+      p = (int)pn;
+      seg = (int)(sl & 0xFFFFu);
+      m = (int)(sl >> 16);
+      keep = true;
+      if (m <= kPrefixMembers) {
+        Np0 = N[tb + p];
+        k = f.nchild[tb + p];
+        first = f.first[tb + p];
+        leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
+        if (!leaf && k > RMAX * kWave) {
+          atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
+          leaf = true;
+        }
+        if (leaf) {
+          done = true;
+        } else if (c.vli > 0) {
+          int nv[kPrefixWindow];
+#pragma unroll
+          for (int j = 0; j < kPrefixWindow; ++j)
+            nv[j] = j < k ? N[tb + first + 1 + j] : 1;
+          int got = 0;
+#pragma unroll
+          for (int j = 0; j < kPrefixWindow; ++j) {
+            const bool take = nv[j] == 0 && got < m;
+            upos |= take ? (1u << j) : 0u;
+            scan = take ? j + 1 : scan;
+            got += take ? 1 : 0;
+          }
+          done = got >= m;
+        }
+        keep = !done;
+      }
+    }
+    // the groups finished here: group log, path entries, the arrival's virtual loss
+    const uint64_t dm = __ballot(done);
+    if (dm != 0) {
+      // per-wave totals: group-log entries, statistics and the next level's groups (one
+      // atomic each)
+      const bool inner = done && !leaf;
+      int ntot;
+      const int mg = wave_excl_scan(inner ? m : 0, &ntot);
+      const int nleafm = wave_sum_i(done && leaf ? m : 0);
+      const int ninner = __popcll(__ballot(inner));
+      const int scans = wave_sum_i(inner ? scan : 0);
+      int gbase = 0, gb = 0;
+      if (lane == 0) {
+        gbase = sh.gbase + atomicAdd(&sh.gnext, __popcll(dm));
+        if (ntot > 0) gb = atomicAdd(big1 ? &sh.nbig[nxt] : &sh.nsmall[nxt], ntot);
+        atomicAdd(&sh.st[OMQ_ST_PATHNODES], (unsigned long long)__popcll(dm));
+        if (nleafm > 0)
+          atomicAdd(&sh.st[OMQ_ST_PATHENTRIES], (unsigned long long)nleafm * (d + 1));
+        if (ninner > 0) {
+          atomicAdd(&sh.st[OMQ_ST_INTERNAL], (unsigned long long)ninner);
+          atomicAdd(&sh.st[OMQ_ST_ROWSUM], (unsigned long long)scans);
+          atomicAdd(&sh.st[OMQ_ST_STEPS], (unsigned long long)ntot);
+        }
+      }
+      gbase = readlane_i(gbase, 0);
+      gb = readlane_i(gb, 0) + mg;
+      if (done) {
+        const int gid = gbase + (int)__builtin_amdgcn_mbcnt_hi(
+                                    (uint32_t)(dm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)dm, 0u));
+        *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, m);
+        if (vl_done) {
+          // the members' virtual loss is in N already
+        } else if (c.vl_atomic) {
+          atomicAdd(&N[tb + p], c.vli * m);
+        } else {
+          N[tb + p] = Np0 + c.vli * m;
+        }
+        const uint16_t* mem = L.buf + cur * W + seg;
+        const int s0 = mem[0];
+        if (leaf) lflag[s0] = 1;
+        uint32_t rest = upos;
+        for (int r = 0; r < m; ++r) {
+          const int s = mem[r];
+          w.paths[((int64_t)t * MW + s) * MD + d] = p;
+          w.gmembers[((int64_t)t * MD + d) * MW + seg + r] = (uint16_t)s;
+          if (leaf) {
+            w.path_len[(int64_t)t * MW + s] = d + 1;
+            w.leaves[(int64_t)t * MW + s] = p;
+            lfs[s] = s0;
+          } else {
+            const int j = __ffs(rest) - 1;  // the r-th child taken
+            rest &= rest - 1u;
+            const int g = big1 ? gb + r : W - 1 - (gb + r);
+            L.gnode[nxt * W + g] = (uint32_t)(first + 1 + j);
+            L.gsl[nxt * W + g] = (uint32_t)(seg + r) | (1u << 16);
+            L.buf[nxt * W + seg + r] = (uint16_t)s;
+          }
+        }
+      }
+    }
+    // the groups kept as chains, compacted in place (this chunk's entries were read above;
+    // every write lands below the chunk's end)
+    const uint64_t km = __ballot(keep);
+    const int wid = tid / kWave;
+    if (lane == 0) sh.wtot[wid] = __popcll(km);
+    __syncthreads();
+    int before = kept_total, total = kept_total;
+    for (int q = 0; q < NT / kWave; ++q) {
+      const int v = sh.wtot[q];
+      before += q < wid ? v : 0;
+      total += v;
+    }
+    if (keep) {
+      const int g = before + (int)__builtin_amdgcn_mbcnt_hi(
+                                 (uint32_t)(km >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)km, 0u));
+      L.gnode[cur * W + g] = pn;
+      L.gsl[cur * W + g] = sl;
+    }
+    kept_total = total;
+    __syncthreads();
+  }
+  if (tid == 0) sh.nbig[cur] = kept_total;
+  __syncthreads();
+}
+
 __device__ inline int size_class(int m) { return 15 - min(15, 31 - __clz(m)); }
 
 // Chain groups [0, nb) of a level reordered by size class, largest first, so that the dynamic
@@ -1338,7 +1550,8 @@ __device__ inline void level1_followers(const SelArgs& f, const SelCfg& c, int64
       if (lane == 0) N[tb + p] = Np0 + c.vli * m;
       const bool leaf = (k <= 0) || (first < 0) || (c.max_depth <= 2) || (k > RMAX * kWave);
       if (!leaf) {
-        dispatch_chain<RMAX>(f, tb, first, k, Np0, m, c, chs, cnt_s, cscr, nullptr);
+        bool allp;
+        group_chain<RMAX, false>(f, tb, first, k, Np0, m, c, chs, cnt_s, cscr, nullptr, &allp);
         if ((mm >> lane) & 1ull) {
           const int r = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32),
                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
@@ -1401,7 +1614,7 @@ __device__ inline int replay_picks(const uint16_t* mem, int m, int k, const uint
 //   vl_done_to: levels 1..vl_done_to have their virtual loss in N already (the overlap)
 //   glog_ctr:   counter of the tree's group-log entries (LDS or global)
 //   lfs, lflag: the tree's per-simulation leaf records (global)
-template <int RMAX, int NT>
+template <int RMAX, int NT, bool WIDE>
 __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int dend, int W,
                           const LevelLds& L, LevelShared<NT>& sh, int* glog_ctr, int32_t* lfs,
                           int32_t* lflag, bool pipe, int root_first, int vl_done_to) {
@@ -1445,6 +1658,11 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
         __syncthreads();
       }
     }
+    // small groups decided by the first-unvisited rule, one per thread (not where level 1
+    // replays the followers' picks)
+    if (Tr::kPrefixPass && !replay && sh.nbig[cur] > 0)
+      prefix_pass<RMAX, NT>(f, c, t, d, W, tb, gmax, L, sh, lfs, lflag, sh.nbig[cur], vl_done,
+                            sg);
     const int nb = sh.nbig[cur];
     // more chain groups than waves: the longest first
     if (nb > NW)
@@ -1522,13 +1740,34 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
       }
 
       uint32_t* ch = L.choice + seg;
+      bool allp = false;
       const int fe = replay ? replay_picks(mem, m, k, L.pick2, ch, cnt_s)
-                            : dispatch_chain<RMAX>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr,
-                                                   pipe && d == 0 ? &sh.progress : nullptr);
+                            : group_chain<RMAX, WIDE>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr,
+                                                pipe && d == 0 ? &sh.progress : nullptr, &allp);
       if (lane == 0) {
         atomicAdd(&sh.st[OMQ_ST_INTERNAL], 1ull);
-        atomicAdd(&sh.st[OMQ_ST_ROWSUM], (unsigned long long)k);
+        // (a row whose picks are all first-unvisited children is scanned up to its last pick)
+        atomicAdd(&sh.st[OMQ_ST_ROWSUM], (unsigned long long)(allp ? (ch[m - 1] >> 16) + 1 : k));
         atomicAdd(&sh.st[OMQ_ST_STEPS], (unsigned long long)m);
+      }
+
+      if (allp) {
+        // every member picked its own child, in index order: member r makes the single-member
+        // group of child ch[r] at segment position seg + r, the layout the general scatter
+        // below gives such picks
+        const bool big1 = !sg || 1 > Tr::kSmall;
+        int gb = 0;
+        if (lane == 0) gb = atomicAdd(big1 ? &sh.nbig[nxt] : &sh.nsmall[nxt], m);
+        gb = readlane_i(gb, 0);
+        for (int r = lane; r < m; r += kWave) {
+          const int i = (int)(ch[r] >> 16);
+          const int g = big1 ? gb + r : W - 1 - (gb + r);
+          gnode[nxt * W + g] = (uint32_t)(first + 1 + i);
+          gsl[nxt * W + g] = (uint32_t)(seg + r) | (1u << 16);
+          buf[nxt * W + seg + r] = mem[r];
+        }
+        wave_sync();
+        continue;
       }
 
       // exclusive scan of the child counts (blocks of B children per lane) -> offsets, and
@@ -1761,7 +2000,7 @@ __global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c)
   if (tid == 0) s_glog = 0;
   start_group<RMAX, NT>(L, sh, W, 0, 0, 0, W, nullptr);
   const int dend = SPLIT ? (pipe ? 2 : 1) : c.max_depth;
-  const int d = level_loop<RMAX, NT>(f, c, t, 0, dend, W, L, sh, &s_glog, lfs, lflag, pipe,
+  const int d = level_loop<RMAX, NT, NT <= 512>(f, c, t, 0, dend, W, L, sh, &s_glog, lfs, lflag, pipe,
                                      root_first, pipe ? 2 : -1);
   if (SPLIT) {
     export_tasks<NT>(f, t, d, pipe && d == 2, W, L, sh);
@@ -1843,7 +2082,7 @@ __global__ __launch_bounds__(kSubThreads, 4) void select_subtree_kernel(SelArgs 
     const int d0 = info & 255;
     const uint16_t* src = f.gmembers + ((int64_t)t * MD + d0) * MW + seg;
     start_group<RMAX, NT>(L, sh, W, d0, p, seg, m, src);
-    level_loop<RMAX, NT>(f, c, t, d0, c.max_depth, W, L, sh, f.gcount + t,
+    level_loop<RMAX, NT, false>(f, c, t, d0, c.max_depth, W, L, sh, f.gcount + t,
                          f.lfs + (int64_t)t * MW, f.lflag + (int64_t)t * MW, false, 0,
                          (info & 256) ? d0 : -1);
     __syncthreads();
@@ -1874,12 +2113,13 @@ constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];  // 0: not known yet
 std::atomic<bool> g_attr_set[kMaxDevices][3][9];
 
-// Threads of the whole-wave kernel.  (512 threads for the 6-slot kernel, which lets its chains
-// keep 256 registers, made C3's level-1 chains slower than the spills they save: 8 waves for
-// its 40-130 level-1 groups.)
+// Threads of the whole-wave kernel: 512 for the kernels of more than 4 slots per lane, whose
+// chains then keep up to 256 registers (at 1024 threads, 128: the 6-slot chains spilled 12-100
+// registers, depending on the code around them).  The first-unvisited prefix leaves their
+// levels below the root few chains, so 8 waves suffice there.
 template <int RMAX>
 constexpr int whole_threads() {
-  return 1024;
+  return RMAX >= 5 ? 512 : 1024;
 }
 
 template <int RMAX>
