@@ -582,9 +582,12 @@ __device__ __noinline__ uint32_t top64_threshold_near(RowKeys<R> keys, int k, ui
 
 // With `progress` set, the chain publishes its progress after every block of 64 ranks: the
 // block's picks are in ch first (workgroup-scope release), then *progress = ranks done.
-template <int R, bool PERSIST>
+// PARTIAL: ranks [0, npre) were taken by the first-unvisited prefix (unvisited_prefix), whose
+// counts (0 or 1) are in cnt_s; the chain starts at rank npre.  Else npre is 0 and cnt_s is
+// cleared here.
+template <int R, bool PERSIST, bool PARTIAL>
 __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
-                         const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
+                         int npre, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
                          int* progress) {
   const int lane = lane_id();
   const float vlf = c.vlf;
@@ -594,10 +597,11 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
   WideRow<R> x;
   float qbl = 0.0f;
   bool negcp = false;
+  int pre0 = 0;  // (R == 1) the lane's child was taken by the prefix
 #pragma unroll
   for (int j = 0; j < R; ++j) {
     const int i = j * kWave + lane;
-    if (i < k) cnt_s[i] = 0;
+    if (!PARTIAL && i < k) cnt_s[i] = 0;
     float d = 2.0f, w = 0.0f, cpv = 0.0f, qv = -__builtin_inff(), av = 0.0f;
     if (i < k) {
       const int64_t node = tb + first + 1 + i;  // child of edge first+i is node first+i+1
@@ -605,6 +609,11 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
       w = f.W[node];
       cpv = c.c_puct * f.P[node];
       d = (float)(1 + n);
+      if (PARTIAL) {
+        const int pre = cnt_s[i];  // a pick of the prefix: one virtual loss more
+        if (pre != 0) d = d + fvl;
+        if (j == 0) pre0 = pre;
+      }
       negcp = negcp || !(cpv >= 0.0f);
       if (child_state(d, w, cpv, i, vlf, &qv, &av)) qbl = fmaxf(qbl, __builtin_fabsf(qv));
     }
@@ -639,7 +648,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     y.q[0] = lane < k ? x.q[0] : kPadQ;  // (padding lanes: see lane_steps)
     y.ar[0] = x.ar[0];
     y.pb[0] = false;
-    y.cn[0] = 0;
+    y.cn[0] = pre0;
     if (lane < k) {
       child_state(y.den[0] + fvl, y.wv[0], y.cp[0], lane, vlf, &y.qn[0], &y.arn[0]);
     } else {
@@ -697,19 +706,20 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     conbits = 0u;
     wopen = false;
   };
-  for (int r0 = 0; r0 < m; r0 += kWave) {
+  for (int r0 = PARTIAL ? (npre / kWave) * kWave : 0; r0 < m; r0 += kWave) {
     const int Npl = Np0 + c.vli * (r0 + lane + 1);
     const float svec = sqrtf((float)Npl);
     const int rend = __builtin_amdgcn_readfirstlane(min(kWave, m - r0));
+    const int rs = PARTIAL ? max(0, npre - r0) : 0;  // the block's ranks taken by the prefix
     // lane rr of rec / rnk: the child picked at rank r0+rr and its rank among the chain's
     // picks of that child (the picked lane's count before the pick)
     uint32_t rec = kNoChild;
     uint32_t rnk = 0;
     if (R == 1) {
-      lane_steps<false>(y, svec, 0, rend, fvl, vlf, qb, kKeyFloor, exact_only ? 0u : kKeyInf,
+      lane_steps<false>(y, svec, rs, rend, fvl, vlf, qb, kKeyFloor, exact_only ? 0u : kKeyInf,
                         k, r0, &first_end, &rec, &rnk);
     } else {
-      int rr = 0;
+      int rr = rs;
       bool try_window = !exact_only;
       if (PERSIST && wopen) {
         // ---- the open window continues, with its bound for this block's last rank ----
@@ -794,7 +804,8 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
         ++rr;
       }
     }
-    if (lane < rend) ch[r0 + lane] = rec != kNoChild ? ((rec << 16) | rnk) : kNoChild;
+    if (lane >= rs && lane < rend)
+      ch[r0 + lane] = rec != kNoChild ? ((rec << 16) | rnk) : kNoChild;
     if (progress != nullptr) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0)
@@ -850,31 +861,32 @@ __device__ __noinline__ int unvisited_prefix(const SelArgs& f, int64_t tb, int f
 // chains keep up to 256 registers (workgroups of at most 512 threads, one per CU).
 template <int RMAX, bool WIDE>
 __device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0,
-                                     int m, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s,
+                                     int m, int npre, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s,
                                      float4* cscr, int* progress) {
   const int r = (k + kWave - 1) / kWave;  // 1 <= r <= RMAX (checked by the caller)
   // contender windows kept open across blocks in the kernels of up to 4 slots per lane and in
   // the WIDE ones (the other wider kernels' chains have no registers left for it)
   constexpr bool kPersist = RMAX <= 4 || WIDE;
   if (RMAX <= 1 || r <= 1)
-    return run_chain<1, kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<1, kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 2 && r == 2)
-    return run_chain<(RMAX >= 2 ? 2 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 2 ? 2 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 3 && r == 3)
-    return run_chain<(RMAX >= 3 ? 3 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 3 ? 3 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 4 && r == 4)
-    return run_chain<(RMAX >= 4 ? 4 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 4 ? 4 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 5 && r == 5)
-    return run_chain<(RMAX >= 5 ? 5 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 5 ? 5 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
   if (RMAX >= 6 && r == 6)
-    return run_chain<(RMAX >= 6 ? 6 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
-  return run_chain<(RMAX >= 8 ? 8 : 1), kPersist>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 6 ? 6 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
+  return run_chain<(RMAX >= 8 ? 8 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
 }
 
 // A group's chain: the first-unvisited prefix, and the chain when the prefix does not take
-// every rank (the chain then derives the prefix's ranks again: starting it after them costs
-// the 6-slot kernel's chains about 60 spilled registers).  *all_prefix: every rank was taken by
-// the prefix (distinct children in index order, each picked once).
+// every rank.  The WIDE kernels' chains start after the prefix; the others derive its ranks
+// again (starting after them cost the 1024-thread chains up to 60 spilled registers).
+// *all_prefix: every rank was taken by the prefix (distinct children in index order, each
+// picked once).
 template <int RMAX, bool WIDE>
 __device__ inline int group_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
                                   const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
@@ -889,7 +901,14 @@ __device__ inline int group_chain(const SelArgs& f, int64_t tb, int first, int k
     }
     return -1;
   }
-  return dispatch_chain<RMAX, WIDE>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr, progress);
+  // (the WIDE kernels' chains start after the prefix; the others derive its ranks again)
+  if (WIDE && npre > 0 && progress != nullptr) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane_id() == 0)
+      __hip_atomic_store(progress, npre, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  return dispatch_chain<RMAX, WIDE>(f, tb, first, k, Np0, m, WIDE ? npre : 0, c, ch, cnt_s,
+                                    cscr, progress);
 }
 
 // Block-wide exclusive scan of a[0..n) in place (n <= 4 * NT); returns the total.  a may be
@@ -1007,6 +1026,9 @@ struct LevelShared {
 // order.
 constexpr int kLaneGroup = 2;
 
+// Kernels of at least this many slots per lane run 512-thread workgroups (whole_threads).
+constexpr int kWideRmax = 4;
+
 // Single-member groups are kept apart from the chain groups in the kernels with a lane pass
 // (rows of at most 192 children) or a leaf pass (256 and 384); the 8-slot kernel keeps every
 // group a chain (the passes' registers would add spills to its chains).
@@ -1026,7 +1048,7 @@ struct SelTraits {
   static constexpr int kSmall = RMAX <= 2 ? kLaneGroup : 1;
   // small groups decided by the first-unvisited rule one per thread (prefix_pass) in the
   // kernels of 512 threads, whose chains have registers to spare for it
-  static constexpr bool kPrefixPass = RMAX >= 5;
+  static constexpr bool kPrefixPass = RMAX >= kWideRmax;
 };
 
 
@@ -2119,7 +2141,7 @@ std::atomic<bool> g_attr_set[kMaxDevices][3][9];
 // levels below the root few chains, so 8 waves suffice there.
 template <int RMAX>
 constexpr int whole_threads() {
-  return RMAX >= 5 ? 512 : 1024;
+  return RMAX >= kWideRmax ? 512 : 1024;
 }
 
 template <int RMAX>
