@@ -34,8 +34,10 @@ def algorithmic_bytes(st: dict, sims: int) -> dict:
     """Compulsory HBM bytes of each tree-operation kernel family over the timed region,
     from the device counters (the stats slots OMQ_ST_* of omq_tree_ops.h):
       select    16 B per visited node (row header N, first, nchild + N write of the virtual
-                loss) + 12 B per child of each row scanned (N, W, P) + 4 B per path entry
-                (path output) + 8 B per simulation (leaf and path length)
+                loss) + 12 B per child of each row scanned (N, W, P; a row whose picks are all
+                first-unvisited children is scanned up to its last pick, where the reference's
+                scan stops) + 4 B per path entry (path output) + 8 B per simulation (leaf and
+                path length)
       leaf_info 8 B per path entry below the root of each unique leaf's path (the entry and its
                 node's action) + 20 B per unique leaf (first simulation, path length, key,
                 legal count)

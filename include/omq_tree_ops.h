@@ -161,7 +161,8 @@ typedef struct omq_wave {
 
 /* stats counters (per tree, accumulated over waves) */
 #define OMQ_ST_INTERNAL 0     /* groups that selected a child (distinct internal nodes per wave) */
-#define OMQ_ST_ROWSUM 1       /* sum of row lengths read by those groups */
+#define OMQ_ST_ROWSUM 1       /* sum of row lengths read by those groups (a row whose picks
+                                 are all first-unvisited children: up to its last pick) */
 #define OMQ_ST_PATHNODES 2    /* distinct path nodes (groups) */
 #define OMQ_ST_PATHENTRIES 3  /* sum over simulations of path length */
 #define OMQ_ST_ULEAVES 4      /* unique leaves */
