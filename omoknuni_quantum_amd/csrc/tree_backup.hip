@@ -15,7 +15,7 @@ namespace omq {
 
 constexpr int kBackupThreads = 256;
 constexpr int kBigGroup = 32;
-constexpr int kBigChunk = 4;  // member values per lane held per chunk of a big group
+constexpr int kBigChunk = 8;  // member values per lane held per chunk of a big group
 
 // signed value per simulation: v(leaf), negated when the leaf depth is odd in leaf-positive
 // mode, so that the contribution at depth d is (d odd ? -sv : sv)
@@ -100,20 +100,27 @@ __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_fores
       const uint16_t* bmem = w.gmembers + ((int64_t)t * MD + bd) * MW + bseg;
       const bool odd = bd & 1;
       float acc = f.value_sums[tb + bp];
-      // chunks of kBigChunk*64 members: the next chunk's values are loaded while the current
-      // one is folded in order
+      // chunks of kBigChunk*64 members, software-pipelined over the two dependent loads: while
+      // chunk c is folded in order, the values of chunk c+1 (from member ids loaded one chunk
+      // earlier) and the member ids of chunk c+2 are in flight
+      constexpr int kCh = kBigChunk * kWave;
       float xa[kBigChunk], xb[kBigChunk];
+      int ib[kBigChunk];
 #pragma unroll
       for (int u = 0; u < kBigChunk; ++u) {
         const int c = u * kWave + lane;
         xa[u] = c < bm ? sv(bmem[c]) : 0.0f;
+        const int c1 = kCh + c;
+        ib[u] = c1 < bm ? (int)bmem[c1] : 0;
       }
-      for (int c0 = 0; c0 < bm; c0 += kBigChunk * kWave) {
-        const int cn = c0 + kBigChunk * kWave;
+      for (int c0 = 0; c0 < bm; c0 += kCh) {
+        const int cn = c0 + kCh;
 #pragma unroll
         for (int u = 0; u < kBigChunk; ++u) {
           const int c = cn + u * kWave + lane;
-          xb[u] = c < bm ? sv(bmem[c]) : 0.0f;
+          xb[u] = c < bm ? sv(ib[u]) : 0.0f;
+          const int c2 = cn + kCh + u * kWave + lane;
+          ib[u] = c2 < bm ? (int)bmem[c2] : 0;
         }
 #pragma unroll
         for (int u = 0; u < kBigChunk; ++u) {
