@@ -1681,8 +1681,9 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
       }
     }
     // small groups decided by the first-unvisited rule, one per thread (not where level 1
-    // replays the followers' picks)
-    if (Tr::kPrefixPass && !replay && sh.nbig[cur] > 0)
+    // replays the followers' picks; not for a level of at most one chain group per wave,
+    // whose chains take their prefixes themselves without the pass's barriers)
+    if (Tr::kPrefixPass && !replay && sh.nbig[cur] > NW)
       prefix_pass<RMAX, NT>(f, c, t, d, W, tb, gmax, L, sh, lfs, lflag, sh.nbig[cur], vl_done,
                             sg);
     const int nb = sh.nbig[cur];
