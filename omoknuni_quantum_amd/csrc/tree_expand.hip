@@ -181,26 +181,46 @@ __global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f,
     s_new = 0;
     s_fail = 0;
   }
-  for (int u = tid; u < U; u += kPlanThreads) {
-    const int leaf = w.uleaf[wb + u];
-    const int L = w.ulegal[wb + u];
-    int k = 0;
-    if (f.num_children[tb + leaf] == 0 && L > 0) {
-      if (c.policy == OMQ_EXPAND_FULL) {
-        k = L;
-      } else if (leaf == 0) {
-        const int N0 = f.visit_counts[tb] - c.vli * c.W;
-        const int mc = pw_root_mc(L, N0);
-        k = min(L > mc ? mc : L, 8);
-      } else {
-        k = min(L, 3);
+  // four leaves per thread at a time, so that their two dependent loads (the leaf, then its
+  // row length) are in flight together
+  constexpr int kPlanBatch = 4;
+  for (int u0 = tid; u0 < U; u0 += kPlanBatch * kPlanThreads) {
+    int leafv[kPlanBatch], Lv[kPlanBatch], nchv[kPlanBatch];
+#pragma unroll
+    for (int j = 0; j < kPlanBatch; ++j) {
+      const int u = u0 + j * kPlanThreads;
+      leafv[j] = u < U ? w.uleaf[wb + u] : 0;
+      Lv[j] = u < U ? w.ulegal[wb + u] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kPlanBatch; ++j) {
+      const int u = u0 + j * kPlanThreads;
+      nchv[j] = u < U ? f.num_children[tb + leafv[j]] : 1;
+    }
+#pragma unroll
+    for (int j = 0; j < kPlanBatch; ++j) {
+      const int u = u0 + j * kPlanThreads;
+      if (u >= U) break;
+      const int leaf = leafv[j];
+      const int L = Lv[j];
+      int k = 0;
+      if (nchv[j] == 0 && L > 0) {
+        if (c.policy == OMQ_EXPAND_FULL) {
+          k = L;
+        } else if (leaf == 0) {
+          const int N0 = f.visit_counts[tb] - c.vli * c.W;
+          const int mc = pw_root_mc(L, N0);
+          k = min(L > mc ? mc : L, 8);
+        } else {
+          k = min(L, 3);
+        }
       }
+      if (k > OMQ_MAX_ROW) {  // a selection row must fit the register tile
+        atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
+        k = 0;
+      }
+      want[u] = k;
     }
-    if (k > OMQ_MAX_ROW) {  // a selection row must fit the register tile
-      atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
-      k = 0;
-    }
-    want[u] = k;
   }
   __syncthreads();
   // exclusive scan over contiguous chunks
@@ -222,6 +242,7 @@ __global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f,
   // excl offsets into a second pass; want[] keeps k, offsets go to uedge directly
   int run = wbase + wex;
   if (all_fit) {
+    int n_exp = 0;  // (the thread's leaves expanded; their children are its chunk's sum)
     for (int i = lo; i < hi; ++i) {
       const int k = want[i];
       w.uedge[wb + i] = k > 0 ? base + run - 1 : -1;
@@ -230,10 +251,15 @@ __global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f,
         const int leaf = w.uleaf[wb + i];
         f.first_child[tb + leaf] = base + run - 1;
         f.num_children[tb + leaf] = k;
-        atomicAdd(&s_exp, 1ull);
-        atomicAdd(&s_new, (unsigned long long)k);
+        ++n_exp;
       }
       run += k;
+    }
+    // one atomic per wave (the per-leaf atomics on one address serialized)
+    const int we = wave_sum_i(n_exp);
+    if (lane_id() == 0 && we > 0) {
+      atomicAdd(&s_exp, (unsigned long long)we);
+      atomicAdd(&s_new, (unsigned long long)wt);
     }
     if (tid == 0) s_total = total;
   } else if (tid < kWave) {
