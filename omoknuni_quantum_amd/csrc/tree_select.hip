@@ -1077,44 +1077,68 @@ __device__ inline void small_groups_body(const SelArgs& f, const SelCfg& c, int 
     if (g0 >= ns) break;
     const int gi = W - 1 - (g0 + lane);
     const uint32_t sl = g0 + lane < ns ? gsl[cur * W + gi] : 0u;
-    const int m = (int)(sl >> 16);
-    if (m < 1 || m > kSmallGroup) continue;
-    const int p = (int)gnode[cur * W + gi];
-    const int seg = (int)(sl & 0xFFFFu);
+    const int m0 = (int)(sl >> 16);
+    const bool valid = m0 >= 1 && m0 <= kSmallGroup;
+    const int m = valid ? m0 : 0;
+    // group-log ids and statistics per wave (one LDS atomic each, not one per lane)
+    const uint64_t vm = __ballot(valid);
+    if (vm == 0) continue;
+    int gbase = 0;
+    if (lane == 0) gbase = sh.gbase + atomicAdd(&sh.gnext, __popcll(vm));
+    gbase = readlane_i(gbase, 0);
+    int p = 0, seg = 0, Np0 = 0, k = 0, first = 0;
     int mem[kSmallGroup];
 #pragma unroll
-    for (int r = 0; r < kSmallGroup; ++r) mem[r] = r < m ? (int)buf[cur * W + seg + r] : 0;
-    const int gid = sh.gbase + atomicAdd(&sh.gnext, 1);
-    *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, m);
+    for (int r = 0; r < kSmallGroup; ++r) mem[r] = 0;
+    bool leaf = true;
+    if (valid) {
+      p = (int)gnode[cur * W + gi];
+      seg = (int)(sl & 0xFFFFu);
 #pragma unroll
-    for (int r = 0; r < kSmallGroup; ++r) {
-      if (r < m) {
-        w.paths[((int64_t)t * MW + mem[r]) * MD + d] = p;
-        w.gmembers[((int64_t)t * MD + d) * MW + seg + r] = (uint16_t)mem[r];
+      for (int r = 0; r < kSmallGroup; ++r) mem[r] = r < m ? (int)buf[cur * W + seg + r] : 0;
+      const int gid = gbase + (int)__builtin_amdgcn_mbcnt_hi(
+                                  (uint32_t)(vm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)vm, 0u));
+      *reinterpret_cast<int4*>(w.glog + ((int64_t)t * gmax + gid) * 4) = make_int4(p, d, seg, m);
+#pragma unroll
+      for (int r = 0; r < kSmallGroup; ++r) {
+        if (r < m) {
+          w.paths[((int64_t)t * MW + mem[r]) * MD + d] = p;
+          w.gmembers[((int64_t)t * MD + d) * MW + seg + r] = (uint16_t)mem[r];
+        }
+      }
+      Np0 = N[tb + p];
+      k = f.nchild[tb + p];
+      first = f.first[tb + p];
+      if (vl_done)
+        Np0 -= c.vli * m;  // the members' virtual loss is in N already
+      else if (c.vl_atomic)
+        atomicAdd(&N[tb + p], c.vli * m);
+      else
+        N[tb + p] = Np0 + c.vli * m;
+      leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
+      if (!leaf && k > RMAX * kWave) {
+        atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
+        leaf = true;
       }
     }
-    int Np0 = N[tb + p];
-    const int k = f.nchild[tb + p];
-    const int first = f.first[tb + p];
-    if (vl_done)
-      Np0 -= c.vli * m;  // the members' virtual loss is in N already
-    else if (c.vl_atomic)
-      atomicAdd(&N[tb + p], c.vli * m);
-    else
-      N[tb + p] = Np0 + c.vli * m;
-    atomicAdd(&sh.st[OMQ_ST_PATHNODES], 1ull);
-    bool leaf = (k <= 0) || (first < 0) || (d == c.max_depth - 1);
-    if (!leaf && k > RMAX * kWave) {
-      atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
-      leaf = true;
+    {
+      const bool inner = valid && !leaf;
+      const int ninner = __popcll(__ballot(inner));
+      const int rows = wave_sum_i(inner ? k : 0);
+      const int steps = wave_sum_i(inner ? m : 0);
+      if (lane == 0) {
+        atomicAdd(&sh.st[OMQ_ST_PATHNODES], (unsigned long long)__popcll(vm));
+        if (ninner > 0) {
+          atomicAdd(&sh.st[OMQ_ST_INTERNAL], (unsigned long long)ninner);
+          atomicAdd(&sh.st[OMQ_ST_ROWSUM], (unsigned long long)rows);
+          atomicAdd(&sh.st[OMQ_ST_STEPS], (unsigned long long)steps);
+        }
+      }
     }
     int pick[kSmallGroup];
 #pragma unroll
     for (int r = 0; r < kSmallGroup; ++r) pick[r] = -1;
-    if (!leaf) {
-      atomicAdd(&sh.st[OMQ_ST_INTERNAL], 1ull);
-      atomicAdd(&sh.st[OMQ_ST_ROWSUM], (unsigned long long)k);
-      atomicAdd(&sh.st[OMQ_ST_STEPS], (unsigned long long)m);
+    if (valid && !leaf) {
 #pragma unroll
       for (int r = 0; r < kSmallGroup; ++r) {
         if (r >= m) break;
@@ -1162,6 +1186,34 @@ __device__ inline void small_groups_body(const SelArgs& f, const SelCfg& c, int 
         if (pick[r] < 0) atomicOr(&w.status[0], OMQ_STATUS_NOCHILD);
       }
     }
+    // the next level's groups (each distinct child: at most kSmallGroup members, a small
+    // group) and the members whose path ends here, counted per wave
+    int ndist = 0, nend = 0;
+#pragma unroll
+    for (int r = 0; r < kSmallGroup; ++r) {
+      if (r >= m) break;
+      if (pick[r] < 0) {
+        ++nend;
+        continue;
+      }
+      bool seen = false;
+#pragma unroll
+      for (int r2 = 0; r2 < kSmallGroup - 1; ++r2)
+        if (r2 < r && pick[r2] == pick[r]) seen = true;
+      ndist += seen ? 0 : 1;
+    }
+    int dtot;
+    int sbase = wave_excl_scan(ndist, &dtot);
+    const int ends = wave_sum_i(nend);
+    {
+      int sb = 0;
+      if (lane == 0) {
+        if (dtot > 0) sb = atomicAdd(&sh.nsmall[nxt], dtot);
+        if (ends > 0) atomicAdd(&sh.st[OMQ_ST_PATHENTRIES], (unsigned long long)ends * (d + 1));
+      }
+      sbase += readlane_i(sb, 0);
+    }
+    if (!valid) continue;
     // children in order of first pick; members of a child contiguous, in rank order
     int pos = seg;
     int s_end = -1;
@@ -1173,7 +1225,6 @@ __device__ inline void small_groups_body(const SelArgs& f, const SelCfg& c, int 
         w.path_len[(int64_t)t * MW + mem[r]] = d + 1;
         w.leaves[(int64_t)t * MW + mem[r]] = p;
         lfs[mem[r]] = s_end;
-        atomicAdd(&sh.st[OMQ_ST_PATHENTRIES], (unsigned long long)(d + 1));
         continue;
       }
       bool seen = false;
@@ -1189,8 +1240,7 @@ __device__ inline void small_groups_body(const SelArgs& f, const SelCfg& c, int 
           ++cntc;
         }
       }
-      const int g = cntc > kSmallGroup ? atomicAdd(&sh.nbig[nxt], 1)
-                                       : W - 1 - atomicAdd(&sh.nsmall[nxt], 1);
+      const int g = W - 1 - sbase++;  // (cntc <= m <= kSmallGroup: a small group)
       gnode[nxt * W + g] = (uint32_t)(first + 1 + pick[r]);
       gsl[nxt * W + g] = (uint32_t)pos | ((uint32_t)cntc << 16);
       pos += cntc;
