@@ -300,6 +300,9 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
   const uint32_t kspan = khi > kbase ? khi - kbase : 0u;
   // the lane whose state after its next pick is pending (the previous step's pick), or -1
   int pl = __builtin_amdgcn_readfirstlane(lane_pending(y));
+  // the ranks are uniform; said explicitly, so that the step loop's counter and exit stay in
+  // scalar registers whatever the caller's rr was derived from
+  rr = __builtin_amdgcn_readfirstlane(rr);
   while (rr < rend) {
     // ---- steps with a single candidate: one exit, at the bottom; a step that is not taken
     // here changes nothing but the pending state, and nothing of it is kept past the loop.
@@ -710,7 +713,9 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     const int Npl = Np0 + c.vli * (r0 + lane + 1);
     const float svec = sqrtf((float)Npl);
     const int rend = __builtin_amdgcn_readfirstlane(min(kWave, m - r0));
-    const int rs = PARTIAL ? max(0, npre - r0) : 0;  // the block's ranks taken by the prefix
+    // the block's ranks taken by the prefix (npre is uniform: a call's result is not known
+    // to be, so it is made so here)
+    const int rs = PARTIAL ? __builtin_amdgcn_readfirstlane(max(0, npre - r0)) : 0;
     // lane rr of rec / rnk: the child picked at rank r0+rr and its rank among the chain's
     // picks of that child (the picked lane's count before the pick)
     uint32_t rec = kNoChild;
