@@ -224,12 +224,6 @@ struct Row {
   int cn[R];            // picks of the child in this chain so far
 };
 
-// The lane of y whose next state is pending (pb set), or -1.
-__device__ inline int lane_pending(const Row<1>& y) {
-  const uint64_t m = __ballot(y.pb[0]);
-  return m ? lowest_lane(m) : -1;
-}
-
 // Wave max of a float as order-preserving keys (made uniform).
 __device__ inline float wave_max_key(float x) { return funkey(wave_max_u32(fkey(x))); }
 
@@ -298,15 +292,22 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
   // A in range: (Ak - kbase) < kspan as unsigned
   const uint32_t kbase = klo + 1u;
   const uint32_t kspan = khi > kbase ? khi - kbase : 0u;
-  // the lane whose state after its next pick is pending (the previous step's pick), or -1
-  int pl = __builtin_amdgcn_readfirstlane(lane_pending(y));
+  // the lane whose state after its next pick is pending (the previous step's pick), if any, as
+  // a lane mask
+  uint64_t pm = __ballot(y.pb[0]);
   // the ranks are uniform; said explicitly, so that the step loop's counter and exit stay in
   // scalar registers whatever the caller's rr was derived from
   rr = __builtin_amdgcn_readfirstlane(rr);
   while (rr < rend) {
-    // ---- steps with a single candidate: one exit, at the bottom; a step that is not taken
-    // here changes nothing but the pending state, and nothing of it is kept past the loop.
-    // The flags are scalar (from the ballot), so the loop keeps no lane masks across steps.
+    // ---- steps with a single candidate: two exits, at the bottom.  The candidates of a step
+    // take their next state at once (the single candidate when the step is taken), so that
+    // the next step's scores wait only for the compare with the wave max, not for the scalar
+    // test of the step; a step that is not taken puts their state back after the loop.  Apart
+    // from that, it changes nothing but the pending state, and nothing of it is kept past the
+    // loop.
+    int inc = 1;
+    uint64_t cm = 0;
+    float qs = 0.0f, as = 0.0f, dsv = 0.0f;
     for (;;) {
       const float s = readlane_f(svec, rr);
       const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
@@ -346,48 +347,73 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       OMQ_PIN(ax);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x142, 0xA);  // row_bcast:15
-      const bool pb = lane == pl;
-      y.qn[0] = pb ? qx : y.qn[0];
-      y.arn[0] = pb ? ax : y.arn[0];
+      const bool pbl = __builtin_amdgcn_inverse_ballot_w64(pm);
+      y.qn[0] = pbl ? qx : y.qn[0];
+      y.arn[0] = pbl ? ax : y.arn[0];
+      qs = y.q[0];
+      as = y.ar[0];
+      dsv = y.den[0];
       OMQ_PIN(y.qn[0]);
       OMQ_PIN(y.arn[0]);
+      OMQ_PIN(qs);
+      OMQ_PIN(as);
+      OMQ_PIN(dsv);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x143, 0xC);  // row_bcast:31
       const uint32_t Ak = (uint32_t)__builtin_amdgcn_readlane(v, 63);
-      const uint64_t cm = __ballot(hk >= Ak);
+      const bool cand = hk >= Ak;
+      // the candidates take their next state now (d2 is the denominator after a pick)
+      y.q[0] = cand ? y.qn[0] : y.q[0];
+      y.ar[0] = cand ? y.arn[0] : y.ar[0];
+      y.den[0] = cand ? d2 : y.den[0];
+      y.cn[0] = cand ? y.cn[0] + 1 : y.cn[0];
+      OMQ_PIN(y.q[0]);
+      OMQ_PIN(y.ar[0]);
+      OMQ_PIN(y.den[0]);
+      OMQ_PIN(y.cn[0]);
+      OMQ_SCHED_FENCE();
+      cm = __ballot(cand);
       // The step is taken when A is in range and it has a single candidate l.  (s_ff1 of an
       // empty mask gives -1: then any lane will do for the writes below, which the step that
-      // takes rank rr later repeats.)  inc = taken ? 1 : 0 and lt = taken ? l : -1 are formed
-      // in scalar registers (as plain C the compiler routes them through vector registers).
+      // takes rank rr later repeats.)  inc = taken ? 1 : 0 is formed in scalar registers (as
+      // plain C the compiler routes it through vector registers).
       const int pc = __popcll(cm);
-      int l, inc, lt;
+      int l;
       asm("s_ff1_i32_b64 %0, %1" : "=s"(l) : "s"(cm));
-      asm("s_sub_u32 %0, %2, %3\n\t"
-          "s_cmp_lt_u32 %0, %4\n\t"
-          "s_cselect_b32 %0, %5, 0\n\t"
+      asm("s_sub_u32 %0, %1, %2\n\t"
+          "s_cmp_lt_u32 %0, %3\n\t"
+          "s_cselect_b32 %0, %4, 0\n\t"
           "s_cmp_eq_u32 %0, 1\n\t"
-          "s_cselect_b32 %0, 1, 0\n\t"
-          "s_cselect_b32 %1, %6, -1"
-          : "=&s"(inc), "=&s"(lt)
-          : "s"(Ak), "s"(kbase), "s"(kspan), "s"(pc), "s"(l)
+          "s_cselect_b32 %0, 1, 0"
+          : "=&s"(inc)
+          : "s"(Ak), "s"(kbase), "s"(kspan), "s"(pc)
           : "scc");
-      // the step's pick, if taken; the pending state is final now
-      const bool hit = lane == lt;
-      y.q[0] = hit ? y.qn[0] : y.q[0];
-      y.ar[0] = hit ? y.arn[0] : y.ar[0];
-      y.den[0] = hit ? y.den[0] + fvl : y.den[0];
-      y.cn[0] = hit ? y.cn[0] + 1 : y.cn[0];
-      pl = lt;
       // lane rr := pick / its rank.  The lane select goes through m0, which the "{m0}"
       // operand hands to the compiler (v_writelane may read only one SGPR besides m0).
       const int rk = readlane_i(y.cn[0], l) - 1;
       asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rec) : "s"(l), "{m0}"(rr));
       asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rnk) : "s"(rk), "{m0}"(rr));
-      rr += inc;
+      pm = cm;  // (a taken step's single candidate: its pick)
+      // (the next rank does not wait for the test either; an untaken step's rank is given
+      // back below)
+      rr += 1;
       if (inc == 0 || rr >= rend) break;
     }
-    y.pb[0] = lane == pl;
-    if (rr >= rend) return rr;
+    if (inc != 0) {
+      y.pb[0] = __builtin_amdgcn_inverse_ballot_w64(pm);
+      return rr;
+    }
+    // not taken: the candidates' state as it was; the previous pick's next state is final
+    {
+      rr -= 1;
+      const bool cand = __builtin_amdgcn_inverse_ballot_w64(cm);
+      y.q[0] = qs;
+      y.ar[0] = as;
+      y.den[0] = dsv;
+      y.cn[0] = cand ? y.cn[0] - 1 : y.cn[0];
+      pm = 0;
+    }
+
     // ---- the step at rr was not taken above (its state is as it was, nothing pending): its
     // candidates again, then the window's end or the exact comparison ----
     const float s = readlane_f(svec, rr);
@@ -405,14 +431,13 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     y.ar[0] = hit ? y.arn[0] : y.ar[0];
     y.den[0] = hit ? y.den[0] + fvl : y.den[0];
     y.cn[0] = hit ? y.cn[0] + 1 : y.cn[0];
-    y.pb[0] = hit;
-    pl = win >= 0 ? win : -1;
+    pm = __ballot(hit);
     const int rk = readlane_i(y.cn[0], win & (kWave - 1)) - 1;
     asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rec) : "s"(win), "{m0}"(rr));
     asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rnk) : "s"(rk), "{m0}"(rr));
     ++rr;
   }
-  y.pb[0] = lane == pl;
+  y.pb[0] = __builtin_amdgcn_inverse_ballot_w64(pm);
   return rr;
 }
 
