@@ -305,7 +305,8 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     // test of the step; a step that is not taken puts their state back after the loop.  Apart
     // from that, it changes nothing but the pending state, and nothing of it is kept past the
     // loop.
-    int inc = 1;
+    rr = __builtin_amdgcn_readfirstlane(rr);
+    int pc = 1, pen = 0;
     uint64_t cm = 0;
     float qs = 0.0f, as = 0.0f, dsv = 0.0f;
     for (;;) {
@@ -372,22 +373,30 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       OMQ_PIN(y.den[0]);
       OMQ_PIN(y.cn[0]);
       OMQ_SCHED_FENCE();
+      // The step is taken when A is in range and it has a single candidate l; the loop goes
+      // on while the next rank is in the block too.  Both conditions besides the candidate
+      // count are folded into pen (bit 1: A out of range, bit 2: the block's last rank), formed
+      // in scalar registers while the compare runs (as plain C the compiler routes them
+      // through vector registers), so that the branch waits only for pc + pen == 1.
+      {
+        int tmp;
+        asm("s_sub_u32 %0, %2, %3\n\t"
+            "s_cmp_lt_u32 %0, %4\n\t"
+            "s_cselect_b32 %0, 0, 2\n\t"
+            "s_cmp_lt_i32 %5, %6\n\t"
+            "s_cselect_b32 %1, 0, 4\n\t"
+            "s_or_b32 %0, %0, %1"
+            : "=&s"(pen), "=&s"(tmp)
+            : "s"(Ak), "s"(kbase), "s"(kspan), "s"(__builtin_amdgcn_readfirstlane(rr + 1)),
+              "s"(rend)
+            : "scc");
+      }
       cm = __ballot(cand);
-      // The step is taken when A is in range and it has a single candidate l.  (s_ff1 of an
-      // empty mask gives -1: then any lane will do for the writes below, which the step that
-      // takes rank rr later repeats.)  inc = taken ? 1 : 0 is formed in scalar registers (as
-      // plain C the compiler routes it through vector registers).
-      const int pc = __popcll(cm);
+      pc = __popcll(cm);
+      // (s_ff1 of an empty mask gives -1: then any lane will do for the writes below, which
+      // the step that takes rank rr later repeats.)
       int l;
       asm("s_ff1_i32_b64 %0, %1" : "=s"(l) : "s"(cm));
-      asm("s_sub_u32 %0, %1, %2\n\t"
-          "s_cmp_lt_u32 %0, %3\n\t"
-          "s_cselect_b32 %0, %4, 0\n\t"
-          "s_cmp_eq_u32 %0, 1\n\t"
-          "s_cselect_b32 %0, 1, 0"
-          : "=&s"(inc)
-          : "s"(Ak), "s"(kbase), "s"(kspan), "s"(pc)
-          : "scc");
       // lane rr := pick / its rank.  The lane select goes through m0, which the "{m0}"
       // operand hands to the compiler (v_writelane may read only one SGPR besides m0).
       const int rk = readlane_i(y.cn[0], l) - 1;
@@ -397,9 +406,9 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       // (the next rank does not wait for the test either; an untaken step's rank is given
       // back below)
       rr += 1;
-      if (inc == 0 || rr >= rend) break;
+      if (pc + pen != 1) break;
     }
-    if (inc != 0) {
+    if (pc == 1 && (pen & 2) == 0) {  // the last step was taken: the block's end
       y.pb[0] = __builtin_amdgcn_inverse_ballot_w64(pm);
       return rr;
     }
@@ -412,6 +421,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       y.den[0] = dsv;
       y.cn[0] = cand ? y.cn[0] - 1 : y.cn[0];
       pm = 0;
+      y.pb[0] = false;
     }
 
     // ---- the step at rr was not taken above (its state is as it was, nothing pending): its
@@ -425,7 +435,9 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     const int win = __builtin_amdgcn_readfirstlane(
         exact_pick<1>(y.den, y.wv, y.cp, cand ? 1u : 0u, !in_range, k, s, vlf));
     if (WINDOW && win < 0) return rr;  // (no child scores above -1e9: not a window step)
-    if (!WINDOW && win < 0 && *first_end < 0) *first_end = r0 + rr;
+    // (first_end is uniform: said so, so that the ranks stay uniform after this branch)
+    if (!WINDOW && win < 0 && __builtin_amdgcn_readfirstlane(*first_end) < 0)
+      *first_end = r0 + rr;
     const bool hit = win >= 0 && lane == win;
     y.q[0] = hit ? y.qn[0] : y.q[0];
     y.ar[0] = hit ? y.arn[0] : y.ar[0];
@@ -821,7 +833,7 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
         // ---- one step over the whole row ----
         const float s = readlane_f(svec, rr);
         const int win = wide_step<R>(x, s, fvl, vlf, qbt_eff, exact_only, k);
-        if (win < 0 && first_end < 0) first_end = r0 + rr;
+        if (win < 0 && __builtin_amdgcn_readfirstlane(first_end) < 0) first_end = r0 + rr;
         int rk = 0;
         if (win >= 0) {
           rk = cnt_s[win];
