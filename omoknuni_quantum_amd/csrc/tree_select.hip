@@ -213,6 +213,29 @@ __device__ inline int exact_pick(const float* den, const float* wv, const float*
   return bk != 0u ? bidx : -1;
 }
 
+// exact_pick for one child per lane, lanes in index order (a row of at most 64 children, or a
+// contender window): the candidates' exact keys (an unvisited child's by its lane, which orders
+// as its index does) go through one wave max, and the lowest lane holding it is the pick; -1
+// when no candidate scores above -1e9.
+__device__ inline int exact_pick_lane(float den, float wv, float cp, bool cand, float s,
+                                      float vlf) {
+  const int lane = lane_id();
+  uint32_t kx = 0u;
+  if (cand) {
+    if (den == 1.0f) {
+      kx = 0xFFFF0000u | (uint32_t)(0xFFFF - lane);
+    } else {
+      const float qe = wv / ((den - 1.0f) + vlf);
+      float sc = qe + (cp * s) / den;
+      sc = sc + 0.0f;  // -0 -> +0, so that equal scores compare equal
+      kx = (sc > -1e9f) ? fkey(sc) : 0u;
+    }
+  }
+  const uint32_t bk = wave_max_u32(kx);
+  if (bk == 0u) return -1;
+  return lowest_lane(__ballot(kx == bk));
+}
+
 // Selection state of the children held by a lane (R slots).
 template <int R>
 struct Row {
@@ -307,6 +330,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     // loop.
     rr = __builtin_amdgcn_readfirstlane(rr);
     int pc = 1, pen = 0;
+    uint32_t Akl = 0u;
     uint64_t cm = 0;
     float qs = 0.0f, as = 0.0f, dsv = 0.0f;
     for (;;) {
@@ -393,6 +417,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       }
       cm = __ballot(cand);
       pc = __popcll(cm);
+      Akl = Ak;
       // (s_ff1 of an empty mask gives -1: then any lane will do for the writes below, which
       // the step that takes rank rr later repeats.)
       int l;
@@ -424,16 +449,14 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       y.pb[0] = false;
     }
 
-    // ---- the step at rr was not taken above (its state is as it was, nothing pending): its
-    // candidates again, then the window's end or the exact comparison ----
+    // ---- the step at rr was not taken above (its state is as it was, nothing pending): the
+    // window's end, or the exact comparison among its candidates (every child when A is out of
+    // range), whose wave max and candidates the loop's last step left in Akl and cm ----
     const float s = readlane_f(svec, rr);
-    const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
-    const uint32_t Ak = wave_max_u32(fkey(ap));
-    const bool cand = raised_key(ap, y.q[0], qw) >= Ak;
-    const bool in_range = Ak - kbase < kspan;
+    const bool in_range = Akl - kbase < kspan;
     if (WINDOW && !in_range) return rr;
-    const int win = __builtin_amdgcn_readfirstlane(
-        exact_pick<1>(y.den, y.wv, y.cp, cand ? 1u : 0u, !in_range, k, s, vlf));
+    const bool cand = in_range ? __builtin_amdgcn_inverse_ballot_w64(cm) : lane < k;
+    const int win = exact_pick_lane(y.den[0], y.wv[0], y.cp[0], cand, s, vlf);
     if (WINDOW && win < 0) return rr;  // (no child scores above -1e9: not a window step)
     // (first_end is uniform: said so, so that the ranks stay uniform after this branch)
     if (!WINDOW && win < 0 && __builtin_amdgcn_readfirstlane(*first_end) < 0)
