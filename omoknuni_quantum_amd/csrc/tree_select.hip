@@ -214,22 +214,26 @@ __device__ inline int exact_pick(const float* den, const float* wv, const float*
 }
 
 // exact_pick for one child per lane, lanes in index order (a row of at most 64 children, or a
-// contender window): the candidates' exact keys (an unvisited child's by its lane, which orders
-// as its index does) go through one wave max, and the lowest lane holding it is the pick; -1
-// when no candidate scores above -1e9.
-__device__ inline int exact_pick_lane(float den, float wv, float cp, bool cand, float s,
+// contender window), among the candidate lanes cm: their exact keys (an unvisited child's by its
+// lane, which orders as its index does), the largest key's lowest lane being the pick; -1 when
+// no candidate scores above -1e9.  The keys are formed in every lane (a select, not a branch);
+// two candidates, the common case, are compared in scalar registers, more by one wave max.
+__device__ inline int exact_pick_lane(float den, float wv, float cp, uint64_t cm, float s,
                                       float vlf) {
   const int lane = lane_id();
-  uint32_t kx = 0u;
-  if (cand) {
-    if (den == 1.0f) {
-      kx = 0xFFFF0000u | (uint32_t)(0xFFFF - lane);
-    } else {
-      const float qe = wv / ((den - 1.0f) + vlf);
-      float sc = qe + (cp * s) / den;
-      sc = sc + 0.0f;  // -0 -> +0, so that equal scores compare equal
-      kx = (sc > -1e9f) ? fkey(sc) : 0u;
-    }
+  const float qe = wv / ((den - 1.0f) + vlf);
+  float sc = qe + (cp * s) / den;
+  sc = sc + 0.0f;  // -0 -> +0, so that equal scores compare equal
+  uint32_t kx = (sc > -1e9f) ? fkey(sc) : 0u;
+  kx = den == 1.0f ? 0xFFFF0000u | (uint32_t)(0xFFFF - lane) : kx;
+  kx = __builtin_amdgcn_inverse_ballot_w64(cm) ? kx : 0u;
+  if (__popcll(cm) == 2) {
+    const int l1 = lowest_lane(cm);
+    const int l2 = lowest_lane(cm & (cm - 1));
+    const uint32_t k1 = (uint32_t)readlane_i((int)kx, l1);
+    const uint32_t k2 = (uint32_t)readlane_i((int)kx, l2);
+    const uint32_t bk = max(k1, k2);
+    return bk == 0u ? -1 : (k2 > k1 ? l2 : l1);
   }
   const uint32_t bk = wave_max_u32(kx);
   if (bk == 0u) return -1;
@@ -455,8 +459,8 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     const float s = readlane_f(svec, rr);
     const bool in_range = Akl - kbase < kspan;
     if (WINDOW && !in_range) return rr;
-    const bool cand = in_range ? __builtin_amdgcn_inverse_ballot_w64(cm) : lane < k;
-    const int win = exact_pick_lane(y.den[0], y.wv[0], y.cp[0], cand, s, vlf);
+    const uint64_t cset = in_range ? cm : __ballot(lane < k);
+    const int win = exact_pick_lane(y.den[0], y.wv[0], y.cp[0], cset, s, vlf);
     if (WINDOW && win < 0) return rr;  // (no child scores above -1e9: not a window step)
     // (first_end is uniform: said so, so that the ranks stay uniform after this branch)
     if (!WINDOW && win < 0 && __builtin_amdgcn_readfirstlane(*first_end) < 0)
