@@ -1115,6 +1115,8 @@ struct SelTraits {
   // the 3-slot kernel spills with them), single members elsewhere (the leaf pass takes single
   // members only)
   static constexpr int kSmall = RMAX <= 2 ? kLaneGroup : 1;
+  // children whose loads a lane of the lane pass has in flight at a time
+  static constexpr int kLaneRound = RMAX <= 2 ? 8 : 4;
   // small groups decided by the first-unvisited rule one per thread (prefix_pass) in the
   // kernels of 512 threads, whose chains have registers to spare for it
   static constexpr bool kPrefixPass = RMAX >= kWideRmax;
@@ -1127,6 +1129,7 @@ __device__ inline void small_groups_body(const SelArgs& f, const SelCfg& c, int 
                                          LevelShared<NT>& sh, int32_t* lfs, int32_t* lflag,
                                          bool vl_done) {
   constexpr int kSmallGroup = SelTraits<RMAX>::kSmall;
+  constexpr int kLaneRound = SelTraits<RMAX>::kLaneRound;
   const SelArgs& w = f;
   const int cur = d & 1, nxt = cur ^ 1;
   const int MW = w.max_wave, MD = w.max_depth_buf;
@@ -1216,21 +1219,21 @@ __device__ inline void small_groups_body(const SelArgs& f, const SelCfg& c, int 
         const float sp = sqrtf((float)Np);
         float best = -1e9f;
         int bi = -1, unv = -1;
-        // the row in order, four children's loads in flight at a time; the first unvisited
-        // child ends the scan (it is the reference's pick)
+        // the row in order, kLaneRound children's loads in flight at a time; the first
+        // unvisited child ends the scan (it is the reference's pick)
         const int64_t row = tb + first + 1;
-        for (int i0 = 0; i0 < k && unv < 0; i0 += 4) {
-          int n4[4];
-          float w4[4], p4[4];
+        for (int i0 = 0; i0 < k && unv < 0; i0 += kLaneRound) {
+          int n4[kLaneRound];
+          float w4[kLaneRound], p4[kLaneRound];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < kLaneRound; ++j) {
             const bool in = i0 + j < k;
             n4[j] = in ? N[row + i0 + j] : 1;
             w4[j] = in ? f.W[row + i0 + j] : 0.0f;
             p4[j] = in ? f.P[row + i0 + j] : 0.0f;
           }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < kLaneRound; ++j) {
             const int i = i0 + j;
             int n = n4[j];
 #pragma unroll
