@@ -459,8 +459,21 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     const float s = readlane_f(svec, rr);
     const bool in_range = Akl - kbase < kspan;
     if (WINDOW && !in_range) return rr;
-    const uint64_t cset = in_range ? cm : __ballot(lane < k);
-    const int win = exact_pick_lane(y.den[0], y.wv[0], y.cp[0], cset, s, vlf);
+    uint64_t cset = in_range ? cm : __ballot(lane < k);
+    if (in_range && __popcll(cm) >= 2) {
+      // The candidates again, against the margin of the lane m that holds A: QW only stands
+      // for |Q_m| in the argument at raised_key, so |qa_m| (1 + 2^-20) >= |Q_m| does too, and
+      // is usually far below the chain's bound.  The exact argmax is in both sets, so in their
+      // intersection; when that is one lane, it is the pick.
+      const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
+      const int m = lowest_lane(__ballot(fkey(ap) == Akl));
+      const float qam = __builtin_fabsf(readlane_f(y.q[0], m));
+      const float qwm = __builtin_fmaf(qam, 0x1p-20f, qam);
+      cset &= __ballot(raised_key(ap, y.q[0], qwm) >= Akl);
+    }
+    const int win = __builtin_amdgcn_readfirstlane(
+        __popcll(cset) == 1 ? lowest_lane(cset)
+                            : exact_pick_lane(y.den[0], y.wv[0], y.cp[0], cset, s, vlf));
     if (WINDOW && win < 0) return rr;  // (no child scores above -1e9: not a window step)
     // (first_end is uniform: said so, so that the ranks stay uniform after this branch)
     if (!WINDOW && win < 0 && __builtin_amdgcn_readfirstlane(*first_end) < 0)
