@@ -158,14 +158,23 @@ class WaveEngine:
         b = torch.as_tensor(np.ascontiguousarray(boards, dtype=np.int8)).reshape(-1)
         if b.numel() != self.T * self.A:
             raise ValueError(f"boards hold {b.numel()} cells, expected {self.T} x {self.A}")
-        self.root_boards = b.to(self.device)
-        self.root_player = None
+        self.root_boards = self._reuse(self.root_boards, b)
+        rp = None
         if root_player is not None:
             rp = torch.as_tensor(np.ascontiguousarray(root_player, dtype=np.int32)).reshape(-1)
             if rp.numel() != self.T:
                 raise ValueError("one root player per tree")
-            self.root_player = rp.to(self.device)
+        self.root_player = None if rp is None else self._reuse(self.root_player, rp)
         self.rule = int(rule)
+
+    def _reuse(self, cur: torch.Tensor | None, x: torch.Tensor) -> torch.Tensor:
+        """x on the device, in cur's storage when cur has its size and type: root inputs keep
+        their addresses from one position to the next, so that a recorded search (whose
+        kernels hold those addresses) stays valid."""
+        if cur is not None and cur.numel() == x.numel() and cur.dtype == x.dtype:
+            cur.copy_(x)
+            return cur
+        return x.to(self.device)
 
     def set_go_rules(self, boards, flags: int = _lib.OMQ_GO_KO, root_player=None,
                      root_passes=None, root_ko=None) -> None:
@@ -189,18 +198,18 @@ class WaveEngine:
         if b.numel() != self.T * cells:
             raise ValueError(f"boards hold {b.numel()} points, expected {self.T} x {cells}")
 
-        def per_tree(x, name):
+        def per_tree(cur, x, name):
             if x is None:
                 return None
             v = torch.as_tensor(np.ascontiguousarray(x, dtype=np.int32)).reshape(-1)
             if v.numel() != self.T:
                 raise ValueError(f"one {name} per tree")
-            return v.to(self.device)
+            return self._reuse(cur, v)
 
-        self.root_boards = b.to(self.device)
-        self.root_player = per_tree(root_player, "root player")
-        self.root_passes = per_tree(root_passes, "root pass count")
-        self.root_ko = per_tree(root_ko, "ko point")
+        self.root_boards = self._reuse(self.root_boards, b)
+        self.root_player = per_tree(self.root_player, root_player, "root player")
+        self.root_passes = per_tree(self.root_passes, root_passes, "root pass count")
+        self.root_ko = per_tree(self.root_ko, root_ko, "ko point")
         if self.umask is None:
             self.umask = torch.zeros(self.T * self.MW * self.model.legal_words,
                                      dtype=torch.int32, device=self.device)
@@ -363,6 +372,18 @@ class WaveEngine:
         mark("backup")
         self.backup(wave_size)
         mark(None)
+
+    def launch_signature(self) -> tuple:
+        """Everything on the host side that a wave's launches take as arguments besides the
+        wave size: search parameters, noise on or off, and the addresses of the rule inputs.
+        Two searches with the same signature and wave sizes launch the same kernels with the
+        same arguments (the tree, wave and root buffers keep their addresses)."""
+        ptr = lambda x: 0 if x is None else x.data_ptr()  # noqa: E731
+        p = self.params
+        return (p.c_puct, p.virtual_loss, p.max_depth, p.expand_policy, p.sign_mode, p.w_mode,
+                p.vl_atomic, p.dirichlet_epsilon, self.has_noise, self.rule, self.go_flags,
+                ptr(self.root_boards), ptr(self.root_player), ptr(self.root_passes),
+                ptr(self.root_ko), int(self.wave.umask or 0))
 
     def search(self, num_simulations: int, wave_size: int, evaluator, timer=None) -> None:
         """MCTS.search on every tree: reset, root expansion (one-simulation wave on the lone

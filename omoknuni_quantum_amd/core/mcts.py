@@ -129,6 +129,7 @@ class MCTS:
         self._roots_key: Optional[bytes] = None
         self._boards: Optional[torch.Tensor] = None
         self._eval = None
+        self._graphs: dict = {}  # recorded searches by launch signature (use_cuda_graphs)
         self._search_count = 0
         self.last_selected_action = None
         self._initialize_statistics()
@@ -399,23 +400,64 @@ class MCTS:
         if num_sims == 0:  # mcts.py:1022-1030 (a configured count of 0)
             return np.full((self.engine.T, self.action_size), 1.0 / self.action_size)
         eng = self.engine
-        if int(eng.nchild[0].item()) == 0 and int(eng.num_nodes[0].item()) == 1:
-            eng.run_wave(1, self._eval)  # root expansion with its own backup
-        done = 0
-        first = True
-        while done < num_sims:
-            w = min(self.wave, num_sims - done)
-            eng.run_wave(w, self._eval)
-            done += w
-            if first:
-                eng.check_status()  # (a device error stops the search after its first wave)
-                first = False
+        fresh = int(eng.nchild[0].item()) == 0 and int(eng.num_nodes[0].item()) == 1
+        key = self._graph_key(num_sims, fresh)
+        if key is not None:
+            self._graph_waves(key, num_sims, fresh)
+        else:
+            self._waves(num_sims, fresh, check_first=True)
         eng.check_status()
         policy = eng.root_policies()
         elapsed = time.perf_counter() - start
         self._search_count += 1
         self._update_statistics(num_sims * eng.T, elapsed)
         return policy
+
+    def _waves(self, num_sims: int, fresh: bool, check_first: bool = False) -> None:
+        """The search's waves: the root expansion of a lone root (its own backup), then waves
+        of min(wave, remaining) simulations."""
+        eng = self.engine
+        if fresh:
+            eng.run_wave(1, self._eval)
+        done = 0
+        while done < num_sims:
+            w = min(self.wave, num_sims - done)
+            eng.run_wave(w, self._eval)
+            done += w
+            if check_first and done == w:
+                eng.check_status()  # (a device error stops the search after its first wave)
+
+    def _graph_key(self, num_sims: int, fresh: bool):
+        """Launch signature of this search's waves when they can be recorded as a HIP graph
+        (config.use_cuda_graphs, as the reference's flag of that name, mcts_config.py:96, and
+        an evaluator that launches device work only and says so with graph_key()); None
+        otherwise."""
+        gk = getattr(self._eval, "graph_key", None)
+        if not self.config.use_cuda_graphs or gk is None or self.device.type != "cuda":
+            return None
+        return (num_sims, self.wave, fresh, self.engine.launch_signature(), gk())
+
+    def _graph_waves(self, key, num_sims: int, fresh: bool) -> None:
+        """The waves as one graph launch.  The first search of a signature runs eagerly (on a
+        side stream, which also sets every kernel attribute) and is then recorded; later ones
+        replay the recording, which reads the roots and trees from the same buffers."""
+        g = self._graphs.get(key)
+        if g is not None:
+            g.replay()
+            return
+        cur = torch.cuda.current_stream(self.device)
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            self._waves(num_sims, fresh, check_first=True)
+        cur.wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._waves(num_sims, fresh)
+        if len(self._graphs) >= 8:
+            self._graphs.pop(next(iter(self._graphs)))
+        self._graphs[key] = g
 
     def _update_statistics(self, num_simulations: int, elapsed_time: float):
         # mcts.py:1442-1456

@@ -22,6 +22,11 @@ class SyntheticEvaluator:
         self.logit_scale = float(logit_scale)
         self.stats = {"evaluations": 0, "batch_evaluations": 0}
 
+    def graph_key(self) -> tuple:
+        """evaluate_wave only launches a kernel whose one host argument is logit_scale, so a
+        search with it can be recorded as a HIP graph (MCTS use_cuda_graphs)."""
+        return ("synthetic", self.logit_scale)
+
     def evaluate_wave(self, engine) -> None:
         lib = _lib.load()
         _lib.check(lib.omq_synthetic_evaluate(engine.forest_ref, engine.wave_ref,
