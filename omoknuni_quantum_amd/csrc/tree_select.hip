@@ -1128,8 +1128,10 @@ struct SelTraits {
   // the 3-slot kernel spills with them), single members elsewhere (the leaf pass takes single
   // members only)
   static constexpr int kSmall = RMAX <= 2 ? kLaneGroup : 1;
-  // children whose loads a lane of the lane pass has in flight at a time
-  static constexpr int kLaneRound = RMAX <= 2 ? 8 : 4;
+  // children whose loads a lane of the lane pass has in flight at a time: as many as the
+  // kernel has registers for without spilling (the 3-slot kernel spills already; the 4-slot
+  // kernel's 225-child rows: C5 select 47.4 -> 46.3 us with 16, 47.8 with 32)
+  static constexpr int kLaneRound = RMAX <= 2 ? 8 : RMAX == 4 ? 16 : 4;
   // small groups decided by the first-unvisited rule one per thread (prefix_pass) in the
   // kernels of 512 threads, whose chains have registers to spare for it
   static constexpr bool kPrefixPass = RMAX >= kWideRmax;
