@@ -121,7 +121,9 @@ __device__ inline uint32_t wave_max_rows(uint32_t x) {
 // E = (|A| + QB) * 2^-20.5.  The child with ap = A has exact score >= A - E; a child w whose
 // exact score reaches the maximum then has ap_w >= A - 2E (|ap_w| <= |A| + 2E keeps e_w <= E).
 // So the exact argmax is among the candidates ap >= T = A - (|A| + QB) * 2^-19 (a further
-// factor 2^0.5 of margin).  A single candidate is the exact argmax; otherwise the candidates
+// factor 2^0.5 of margin).  (That is the test of the steps over a whole row, whose states all
+// use refined reciprocals; the steps over one child per lane use raised keys instead, with the
+// argument at raised_key, which also covers states formed with the hardware reciprocal.)  A single candidate is the exact argmax; otherwise the candidates
 // are scored exactly (two correctly rounded divisions each) and compared in scalar registers.
 // No candidate (NaN or infinite scores), a negative c*P or QB >= 1e8 scores every child
 // exactly.
@@ -259,13 +261,19 @@ __device__ inline float wave_max_key(float x) { return funkey(wave_max_u32(fkey(
 // step's maximum (the chain's QB, or the window's contenders' bound).
 //
 // Why the exact argmax w is a candidate (hi_w >= A, A = max ap, held by lane m): each lane's
-// |ap - sc| <= e = 7u (|ap| + |Q|) (1 + 2^-20), u = 2^-24 (the argument above run_chain's
-// helpers, written per child: 4u U from the two U's, 3u |Q| from qa and Q, u |ap| + u |sc| from
-// the last roundings, and U <= |ap| + |Q|).  Then sc_w >= sc_m >= A - e_m and ap_w >= A - e_m
-// - e_w; with |A| <= |ap_w| + e_m + e_w and |Q_m| <= QW, e_m + e_w <= 7u X (1 + 8u) for
-// X = 2|ap_w| + |qa_w| + QW.  hi_w is the rounded ap_w + fl(fl(2|ap_w| + |qa_w|) + QW) M >=
-// ap_w + X (1 - 2u) M, and M > 1.6 * 7u covers it; rounding to nearest keeps a real value >= A
-// (a float) >= A.  The lane holding A has hi >= ap = A.
+// |ap - sc| <= e = 8.1u (|ap| + |Q|) (1 + 2^-20), u = 2^-24 (the argument above run_chain's
+// helpers, written per child).  A lane's reciprocals r (of d) and r' are Newton-refined
+// (|r d - 1| <= u (1 + 2^-20)) or, in the state after a pick that a step forms, the hardware
+// reciprocal alone: |r d - 1| <= 2^-23.38 = 1.54u, the largest error of v_rcp_f32 over every
+// float in [1, 2^24], which holds every denominator here (tests/test_gpu_rcp_bound.py).  So
+// |qa - Q| <= (1.54u + 2u) |Q| (the reciprocal, qa's product, Q's quotient) and the U's differ
+// by (1.54u + u + 2u) U (the reciprocal, a's product, the exact U's product and quotient);
+// with u |ap| + u |sc| from the last roundings and U <= |ap| + |Q|, e <= 8.1u (|ap| + |Q|).
+// Then sc_w >= sc_m >= A - e_m and ap_w >= A - e_m - e_w; with |A| <= |ap_w| + e_m + e_w and
+// |Q_m| <= QW, e_m + e_w <= 8.1u X (1 + 9u) for X = 2|ap_w| + |qa_w| + QW.  hi_w is the rounded
+// ap_w + fl(fl(2|ap_w| + |qa_w|) + QW) M >= ap_w + X (1 - 2u) M, and M = 11.3u > 8.1u
+// (1 + 9u) / (1 - 2u) covers it; rounding to nearest keeps a real value >= A (a float) >= A.
+// The lane holding A has hi >= ap = A.
 constexpr float kMarg = 0x1.6a09e8p-21f;
 __device__ inline uint32_t raised_key(float ap, float qa, float qw) {
   const float x = (2.0f * __builtin_fabsf(ap) + __builtin_fabsf(qa)) + qw;
@@ -341,7 +349,8 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       const float s = readlane_f(svec, rr);
       const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
       // The wave max of the keys is interleaved with the raised key and with the pending state
-      // after the next pick of the previous step's child (both independent of it).
+      // after the next pick of the previous step's child (both independent of it).  That state
+      // takes the hardware reciprocals as they are (the argument at raised_key covers them).
       int v = (int)fkey(ap);
       float d2 = y.den[0] + fvl;
       float e2 = (d2 - 1.0f) + vlf;
@@ -355,14 +364,8 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       OMQ_PIN(r2);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x112, 0xF);  // row_shr:2
-      float t1 = __builtin_fmaf(-e2, r1, 1.0f);
-      float t2 = __builtin_fmaf(-d2, r2, 1.0f);
-      OMQ_PIN(t1);
-      OMQ_PIN(t2);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x114, 0xF);  // row_shr:4
-      r1 = __builtin_fmaf(r1, t1, r1);
-      r2 = __builtin_fmaf(r2, t2, r2);
       uint32_t hk = raised_key(ap, y.q[0], qw);
       OMQ_PIN(r1);
       OMQ_PIN(r2);
