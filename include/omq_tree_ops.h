@@ -179,6 +179,11 @@ typedef struct omq_wave {
 #define OMQ_STATUS_ROWLIMIT 2   /* a row longer than OMQ_MAX_ROW was met or refused */
 #define OMQ_STATUS_STALL 4      /* a bounded wait inside omq_select ran out (internal error: the
                                    wave's selection is incomplete) */
+#define OMQ_STATUS_COUNTLIMIT 8 /* omq_select met a root with 1 + N + virtual_loss * wave >= 2^24:
+                                   the selection keeps a row's visit counts as floats advanced
+                                   by the virtual loss, which are exact only below 2^24 (every
+                                   node's count is at most its root's); the wave's picks may
+                                   then differ from the reference's */
 
 /* ---- library ---------------------------------------------------------------------- */
 int omq_abi_version(void);

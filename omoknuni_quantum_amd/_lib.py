@@ -27,7 +27,7 @@ STAT_NAMES = [
     "internal", "rowsum", "pathnodes", "pathentries", "uleaves", "expanded", "newchild",
     "sims", "steps", "capfail", "uleafpath",
 ]
-OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT, OMQ_STATUS_STALL = 1, 2, 4
+OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT, OMQ_STATUS_STALL, OMQ_STATUS_COUNTLIMIT = 1, 2, 4, 8
 OMQ_RULE_FREESTYLE, OMQ_RULE_RENJU = 0, 1
 OMQ_TERM_NONE, OMQ_TERM_WIN1, OMQ_TERM_WIN2, OMQ_TERM_DRAW, OMQ_TERM_END = 0, 1, 2, 3, 4
 OMQ_GO_KO, OMQ_GO_SUICIDE = 1, 2

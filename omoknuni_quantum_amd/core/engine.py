@@ -426,6 +426,9 @@ class WaveEngine:
         if st & _lib.OMQ_STATUS_ROWLIMIT:
             raise _lib.OmqError(f"a node has more than {_lib.OMQ_MAX_ROW} legal actions; "
                                 "its expansion was refused by the library")
+        if st & _lib.OMQ_STATUS_COUNTLIMIT:
+            raise _lib.OmqError("a root's visit count plus the wave's virtual loss reached 2^24; "
+                                "the selection's float visit counts are exact only below it")
 
     def root_policies(self, device: bool = False):
         """pi[t, a] = N(child_a) / sum N over the root's children (mcts.py:1069-1137): uniform

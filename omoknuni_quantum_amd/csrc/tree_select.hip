@@ -2160,7 +2160,13 @@ __global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c)
     lflag[s] = 0;
     if (L.pick2 != nullptr) L.pick2[s] = kPickNone;
   }
-  if (tid == 0) s_glog = 0;
+  if (tid == 0) {
+    s_glog = 0;
+    // the chains keep a row's counts as floats (1 + N) advanced by the virtual loss, exact
+    // while below 2^24; every node's count is at most its root's
+    if ((int64_t)f.N[tb] + 1 + (int64_t)c.vli * W >= (int64_t)(1 << 24))
+      atomicOr(&f.status[0], OMQ_STATUS_COUNTLIMIT);
+  }
   start_group<RMAX, NT>(L, sh, W, 0, 0, 0, W, nullptr);
   const int dend = SPLIT ? (pipe ? 2 : 1) : c.max_depth;
   const int d = level_loop<RMAX, NT, NT <= 512>(f, c, t, 0, dend, W, L, sh, &s_glog, lfs, lflag, pipe,

@@ -171,3 +171,28 @@ def test_torch_ops_match_reference_kernel_semantics(device):
     torch.ops.omq.batch_remove_virtual_loss(idx, vl)
     torch.cuda.synchronize()
     assert int(vl.abs().sum()) == 0
+
+
+def test_count_limit_is_reported(device):
+    """A root whose visit count plus the wave's virtual loss reaches 2^24 (forced from the
+    host) sets OMQ_STATUS_COUNTLIMIT, and check_status raises; below it nothing is set."""
+    wl = get("C2").scaled(num_trees=2, num_simulations=256, capacity=50_000)
+    eng, orc, ev = make_pair(wl, device=device)
+    eng.reset()
+    eng.run_wave(1, ev)
+    W = wl.wave_size
+    vl = int(wl.virtual_loss)
+    eng.N[0] = (1 << 24) - 1 - vl * W - 1  # tree 0: one below the limit
+    eng.select(W)
+    torch.cuda.synchronize()
+    assert int(eng.status[0].item()) & _lib.OMQ_STATUS_COUNTLIMIT == 0
+    eng.reset()
+    eng.run_wave(1, ev)
+    eng.N[eng.cap] = (1 << 24) - 1 - vl * W  # tree 1: at the limit
+    eng.select(W)
+    torch.cuda.synchronize()
+    assert int(eng.status[0].item()) & _lib.OMQ_STATUS_COUNTLIMIT
+    with pytest.raises(_lib.OmqError, match="2\\^24"):
+        eng.check_status()
+    eng.reset()
+    eng.check_status()
