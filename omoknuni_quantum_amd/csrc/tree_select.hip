@@ -138,8 +138,8 @@ __device__ inline uint32_t wave_max_rows(uint32_t x) {
 // visited child, and a lower index dominates a higher one by a factor >= 1 + 2^-10, so the
 // lowest-index unvisited child is the single candidate, as the reference's first-unvisited
 // rule requires.  A padding child (index >= k) carries qa = -inf, a = 0.  Every child's state
-// after its next pick is kept too, so a pick is a register select; the state after the
-// following pick is computed during the next step's wave max, off the pick's dependency chain.
+// after its next pick is kept too, so a pick is a register select; each step forms every
+// child's state after its next pick anew during its wave max, off the pick's dependency chain.
 // The parent's sqrt for ranks r0..r0+63 is computed once per 64 steps (lane l holds rank
 // r0+l); the 64 picks of a block are kept one per lane, and their ranks are counted after the
 // block.
@@ -249,7 +249,6 @@ struct Row {
   float qn[R], arn[R];  // state after the next pick
   float den[R];         // (float)(1 + N) including this chain's picks
   float wv[R], cp[R];   // W and c_puct * P
-  bool pb[R];           // the previous step's pick, whose next state is still pending
   int cn[R];            // picks of the child in this chain so far
 };
 
@@ -327,9 +326,6 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
   // A in range: (Ak - kbase) < kspan as unsigned
   const uint32_t kbase = klo + 1u;
   const uint32_t kspan = khi > kbase ? khi - kbase : 0u;
-  // the lane whose state after its next pick is pending (the previous step's pick), if any, as
-  // a lane mask
-  uint64_t pm = __ballot(y.pb[0]);
   // the ranks are uniform; said explicitly, so that the step loop's counter and exit stay in
   // scalar registers whatever the caller's rr was derived from
   rr = __builtin_amdgcn_readfirstlane(rr);
@@ -348,9 +344,11 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     for (;;) {
       const float s = readlane_f(svec, rr);
       const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
-      // The wave max of the keys is interleaved with the raised key and with the pending state
-      // after the next pick of the previous step's child (both independent of it).  That state
-      // takes the hardware reciprocals as they are (the argument at raised_key covers them).
+      // The wave max of the keys is interleaved with the raised key and with every lane's
+      // state after its next pick (both independent of it).  That state follows from the
+      // lane's current count, so it is formed anew each step: only the previous step's pick
+      // changes it.  It takes the hardware reciprocals as they are (the argument at
+      // raised_key covers them).
       int v = (int)fkey(ap);
       float d2 = y.den[0] + fvl;
       float e2 = (d2 - 1.0f) + vlf;
@@ -373,20 +371,15 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x118, 0xF);  // row_shr:8
       // a picked child is visited afterwards (virtual loss >= 1 here)
-      float qx = y.wv[0] * r1;
-      float ax = y.cp[0] * r2;
-      OMQ_PIN(qx);
-      OMQ_PIN(ax);
+      y.qn[0] = y.wv[0] * r1;
+      y.arn[0] = y.cp[0] * r2;
+      OMQ_PIN(y.qn[0]);
+      OMQ_PIN(y.arn[0]);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x142, 0xA);  // row_bcast:15
-      const bool pbl = __builtin_amdgcn_inverse_ballot_w64(pm);
-      y.qn[0] = pbl ? qx : y.qn[0];
-      y.arn[0] = pbl ? ax : y.arn[0];
       qs = y.q[0];
       as = y.ar[0];
       dsv = y.den[0];
-      OMQ_PIN(y.qn[0]);
-      OMQ_PIN(y.arn[0]);
       OMQ_PIN(qs);
       OMQ_PIN(as);
       OMQ_PIN(dsv);
@@ -434,17 +427,13 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       const int rk = readlane_i(y.cn[0], l) - 1;
       asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rec) : "s"(l), "{m0}"(rr));
       asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rnk) : "s"(rk), "{m0}"(rr));
-      pm = cm;  // (a taken step's single candidate: its pick)
       // (the next rank does not wait for the test either; an untaken step's rank is given
       // back below)
       rr += 1;
       if (pc + pen != 1) break;
     }
-    if (pc == 1 && (pen & 2) == 0) {  // the last step was taken: the block's end
-      y.pb[0] = __builtin_amdgcn_inverse_ballot_w64(pm);
-      return rr;
-    }
-    // not taken: the candidates' state as it was; the previous pick's next state is final
+    if (pc == 1 && (pen & 2) == 0) return rr;  // the last step was taken: the block's end
+    // not taken: the candidates' state as it was
     {
       rr -= 1;
       const bool cand = __builtin_amdgcn_inverse_ballot_w64(cm);
@@ -452,8 +441,6 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       y.ar[0] = as;
       y.den[0] = dsv;
       y.cn[0] = cand ? y.cn[0] - 1 : y.cn[0];
-      pm = 0;
-      y.pb[0] = false;
     }
 
     // ---- the step at rr was not taken above (its state is as it was, nothing pending): the
@@ -486,13 +473,11 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     y.ar[0] = hit ? y.arn[0] : y.ar[0];
     y.den[0] = hit ? y.den[0] + fvl : y.den[0];
     y.cn[0] = hit ? y.cn[0] + 1 : y.cn[0];
-    pm = __ballot(hit);
     const int rk = readlane_i(y.cn[0], win & (kWave - 1)) - 1;
     asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rec) : "s"(win), "{m0}"(rr));
     asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rnk) : "s"(rk), "{m0}"(rr));
     ++rr;
   }
-  y.pb[0] = __builtin_amdgcn_inverse_ballot_w64(pm);
   return rr;
 }
 
@@ -730,7 +715,6 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     y.cp[0] = x.cp[0];
     y.q[0] = lane < k ? x.q[0] : kPadQ;  // (padding lanes: see lane_steps)
     y.ar[0] = x.ar[0];
-    y.pb[0] = false;
     y.cn[0] = pre0;
     if (lane < k) {
       child_state(y.den[0] + fvl, y.wv[0], y.cp[0], lane, vlf, &y.qn[0], &y.arn[0]);
@@ -848,7 +832,6 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
           y.den[0] = e.x;
           y.wv[0] = e.y;
           y.cp[0] = e.z;
-          y.pb[0] = false;
           y.cn[0] = lane < ncon ? (int)cnt_s[cidx] : 0;
           if (lane < ncon) {
             child_state(y.den[0], y.wv[0], y.cp[0], cidx, vlf, &y.q[0], &y.ar[0]);
