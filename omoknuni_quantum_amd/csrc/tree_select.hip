@@ -340,7 +340,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     int pc = 1, pen = 0;
     uint32_t Akl = 0u;
     uint64_t cm = 0;
-    float qs = 0.0f, as = 0.0f, dsv = 0.0f;
+    float qs = 0.0f;
     for (;;) {
       const float s = readlane_f(svec, rr);
       const float ap = __builtin_fmaf(s, y.ar[0], y.q[0]);
@@ -378,11 +378,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x142, 0xA);  // row_bcast:15
       qs = y.q[0];
-      as = y.ar[0];
-      dsv = y.den[0];
       OMQ_PIN(qs);
-      OMQ_PIN(as);
-      OMQ_PIN(dsv);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x143, 0xC);  // row_bcast:31
       const uint32_t Ak = (uint32_t)__builtin_amdgcn_readlane(v, 63);
@@ -433,14 +429,19 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       if (pc + pen != 1) break;
     }
     if (pc == 1 && (pen & 2) == 0) return rr;  // the last step was taken: the block's end
-    // not taken: the candidates' state as it was
+    // not taken: the candidates' state as it was.  qa comes back from its copy; the count, the
+    // denominator (integral and below 2^24, so the subtraction is exact) and a follow from it
+    // (a = 0 for an unvisited child; c*P = 0 on a padding lane)
     {
       rr -= 1;
       const bool cand = __builtin_amdgcn_inverse_ballot_w64(cm);
       y.q[0] = qs;
-      y.ar[0] = as;
-      y.den[0] = dsv;
-      y.cn[0] = cand ? y.cn[0] - 1 : y.cn[0];
+      if (cand) {
+        const float d = y.den[0] - fvl;
+        y.den[0] = d;
+        y.cn[0] -= 1;
+        y.ar[0] = d == 1.0f ? 0.0f : y.cp[0] * refined_rcp(d);
+      }
     }
 
     // ---- the step at rr was not taken above (its state is as it was, nothing pending): the
