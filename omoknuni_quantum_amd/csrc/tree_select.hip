@@ -309,7 +309,8 @@ static_assert(kKeyInf == (__builtin_bit_cast(uint32_t, __builtin_inff()) ^ 0x800
 // comparison among its candidates (all children when A is out of range) and comes back.
 // Keeping the rare step out of the loop body leaves the common step without the register
 // copies that joining the two paths inside it costs.  Lane r of rec / rnk receives the pick at
-// rank r (the lane, or -1 for none) and its rank among the chain's earlier picks of that child.
+// rank r (the lane, or -1 for none) and the chain's picks of that child up to and including it
+// (its rank among them plus one).
 //   WINDOW: contender window; klo is also at least the largest raised key of the
 //           non-contenders at the block's last rank, which bounds their raised keys over the
 //           whole window (ap and hi only grow with s).  With A above it, no non-contender is a
@@ -420,7 +421,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       asm("s_ff1_i32_b64 %0, %1" : "=s"(l) : "s"(cm));
       // lane rr := pick / its rank.  The lane select goes through m0, which the "{m0}"
       // operand hands to the compiler (v_writelane may read only one SGPR besides m0).
-      const int rk = readlane_i(y.cn[0], l) - 1;
+      const int rk = readlane_i(y.cn[0], l);
       asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rec) : "s"(l), "{m0}"(rr));
       asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rnk) : "s"(rk), "{m0}"(rr));
       // (the next rank does not wait for the test either; an untaken step's rank is given
@@ -474,7 +475,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     y.ar[0] = hit ? y.arn[0] : y.ar[0];
     y.den[0] = hit ? y.den[0] + fvl : y.den[0];
     y.cn[0] = hit ? y.cn[0] + 1 : y.cn[0];
-    const int rk = readlane_i(y.cn[0], win & (kWave - 1)) - 1;
+    const int rk = readlane_i(y.cn[0], win & (kWave - 1));
     asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rec) : "s"(win), "{m0}"(rr));
     asm volatile("v_writelane_b32 %0, %1, m0" : "+v"(*rnk) : "s"(rk), "{m0}"(rr));
     ++rr;
@@ -781,8 +782,8 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
     // the block's ranks taken by the prefix (npre is uniform: a call's result is not known
     // to be, so it is made so here)
     const int rs = PARTIAL ? __builtin_amdgcn_readfirstlane(max(0, npre - r0)) : 0;
-    // lane rr of rec / rnk: the child picked at rank r0+rr and its rank among the chain's
-    // picks of that child (the picked lane's count before the pick)
+    // lane rr of rec / rnk: the child picked at rank r0+rr and the chain's picks of that child
+    // up to and including it (the picked lane's count after the pick: its rank plus one)
     uint32_t rec = kNoChild;
     uint32_t rnk = 0;
     if (R == 1) {
@@ -869,12 +870,12 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
           wave_sync();
         }
         rec = (lane == rr) ? (uint32_t)win : rec;
-        rnk = (lane == rr) ? (uint32_t)rk : rnk;
+        rnk = (lane == rr) ? (uint32_t)(rk + 1) : rnk;
         ++rr;
       }
     }
     if (lane >= rs && lane < rend)
-      ch[r0 + lane] = rec != kNoChild ? ((rec << 16) | rnk) : kNoChild;
+      ch[r0 + lane] = rec != kNoChild ? ((rec << 16) | (rnk - 1u)) : kNoChild;
     if (progress != nullptr) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0)
