@@ -350,38 +350,51 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       // lane's current count, so it is formed anew each step: only the previous step's pick
       // changes it.  It takes the hardware reciprocals as they are (the argument at
       // raised_key covers them).
+      // Two independent instructions sit between consecutive DPP steps (a DPP source needs
+      // two wait states after its write), so the wave max runs without hazard nops.  Each group
+      // pins its inputs first, which keeps its instructions after the previous DPP step.  The
+      // raised key is raised_key's expression, split across the groups.
       int v = (int)fkey(ap);
       float d2 = y.den[0] + fvl;
-      float e2 = (d2 - 1.0f) + vlf;
-      OMQ_PIN(d2);
-      OMQ_PIN(e2);
+      float e1 = d2 - 1.0f;
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x111, 0xF);  // row_shr:1
-      float r1 = __builtin_amdgcn_rcpf(e2);
+      OMQ_PIN(d2);
+      OMQ_PIN(e1);
+      float e2 = e1 + vlf;
       float r2 = __builtin_amdgcn_rcpf(d2);
-      OMQ_PIN(r1);
-      OMQ_PIN(r2);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x112, 0xF);  // row_shr:2
+      OMQ_PIN(e2);
+      float apc = ap;
+      OMQ_PIN(apc);
+      float r1 = __builtin_amdgcn_rcpf(e2);
+      float x1 = 2.0f * __builtin_fabsf(apc);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x114, 0xF);  // row_shr:4
-      uint32_t hk = raised_key(ap, y.q[0], qw);
-      OMQ_PIN(r1);
-      OMQ_PIN(r2);
-      OMQ_PIN(hk);
+      OMQ_PIN(x1);
+      float qc = y.q[0];
+      OMQ_PIN(qc);
+      float x2 = x1 + __builtin_fabsf(qc);
+      qs = qc;
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x118, 0xF);  // row_shr:8
+      OMQ_PIN(x2);
+      OMQ_PIN(r2);
+      float x3 = x2 + qw;
       // a picked child is visited afterwards (virtual loss >= 1 here)
-      y.qn[0] = y.wv[0] * r1;
       y.arn[0] = y.cp[0] * r2;
-      OMQ_PIN(y.qn[0]);
-      OMQ_PIN(y.arn[0]);
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x142, 0xA);  // row_bcast:15
-      qs = y.q[0];
-      OMQ_PIN(qs);
+      OMQ_PIN(x3);
+      OMQ_PIN(r1);
+      const float hi = __builtin_fmaf(x3, kMarg, apc);
+      y.qn[0] = y.wv[0] * r1;
       OMQ_SCHED_FENCE();
       OMQ_DPP_MAX(v, 0x143, 0xC);  // row_bcast:31
+      float hic = hi;
+      OMQ_PIN(hic);
+      const uint32_t hk = fkey(hic);
       const uint32_t Ak = (uint32_t)__builtin_amdgcn_readlane(v, 63);
       const bool cand = hk >= Ak;
       // the candidates take their next state now (d2 is the denominator after a pick)
