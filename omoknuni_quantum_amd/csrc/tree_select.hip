@@ -1112,7 +1112,9 @@ struct LevelShared {
 constexpr int kLaneGroup = 2;
 
 // Kernels of at least this many slots per lane run 512-thread workgroups (whole_threads).
-constexpr int kWideRmax = 4;
+// (The 3-slot kernel at 1024 threads, with the level-1 followers, spilled 62 registers; at 512
+// threads it spills none, and a Go 13 x 13 wave's select went 182 -> 170 us.)
+constexpr int kWideRmax = 3;
 
 // Single-member groups are kept apart from the chain groups in the kernels with a lane pass
 // (rows of at most 192 children) or a leaf pass (256 and 384); the 8-slot kernel keeps every
@@ -1969,20 +1971,40 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
       }
       wave_sync();
 
-      // scatter the members to their child's segment (rank keeps simulation order)
+      // scatter the members to their child's segment (rank keeps simulation order), kSU
+      // members per lane at a time: their reads are issued together (they come from this
+      // level's half of buf and from ch and cnt_s, none of which the writes to the next
+      // level's half touch).  Two in the 1024-thread kernels, whose registers are fewer.
+      constexpr int kSU = NT <= 512 ? 4 : 2;
       const int s_end = fe >= 0 ? (int)mem[fe] : -1;
-      for (int r = lane; r < m; r += kWave) {
-        const int s = mem[r];
-        const uint32_t cv = ch[r];
-        if (cv == kNoChild) {
-          w.path_len[(int64_t)t * MW + s] = d + 1;
-          w.leaves[(int64_t)t * MW + s] = p;
-          lfs[s] = s_end;
-          atomicAdd(&sh.st[OMQ_ST_PATHENTRIES], (unsigned long long)(d + 1));
-        } else {
-          const int i = (int)(cv >> 16);
-          const int rk = (int)(cv & 0xFFFFu);
-          buf[nxt * W + seg + cnt_s[i] + rk] = (uint16_t)s;
+      for (int r0 = lane; r0 < m; r0 += kSU * kWave) {
+        int sv[kSU];
+        uint32_t cvv[kSU];
+#pragma unroll
+        for (int u = 0; u < kSU; ++u) {
+          const int r = r0 + u * kWave;
+          sv[u] = r < m ? (int)mem[r] : 0;
+          cvv[u] = r < m ? ch[r] : 0u;
+        }
+        int off[kSU];
+#pragma unroll
+        for (int u = 0; u < kSU; ++u) {
+          const bool to_child = r0 + u * kWave < m && cvv[u] != kNoChild;
+          off[u] = to_child ? (int)cnt_s[cvv[u] >> 16] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kSU; ++u) {
+          if (r0 + u * kWave >= m) break;
+          const int s = sv[u];
+          const uint32_t cv = cvv[u];
+          if (cv == kNoChild) {
+            w.path_len[(int64_t)t * MW + s] = d + 1;
+            w.leaves[(int64_t)t * MW + s] = p;
+            lfs[s] = s_end;
+            atomicAdd(&sh.st[OMQ_ST_PATHENTRIES], (unsigned long long)(d + 1));
+          } else {
+            buf[nxt * W + seg + off[u] + (int)(cv & 0xFFFFu)] = (uint16_t)s;
+          }
         }
       }
       if (fe >= 0 && lane == 0) {
@@ -2138,7 +2160,8 @@ __device__ inline void export_tasks(const SelArgs& f, int t, int d, bool vl_done
 template <int RMAX, int NT, bool SPLIT>
 __global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c) {
   // the level overlap in the kernels whose chains keep their registers with a second copy of
-  // the chain code (the followers'), with a full workgroup of followers
+  // the chain code (the followers'), with a full workgroup of followers (the 1- and 2-slot
+  // kernels: every kernel of more slots runs 512 threads)
   constexpr bool kPipe = RMAX <= 3 && NT == 1024;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ LevelShared<NT> sh;
