@@ -330,6 +330,10 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
   // the ranks are uniform; said explicitly, so that the step loop's counter and exit stay in
   // scalar registers whatever the caller's rr was derived from
   rr = __builtin_amdgcn_readfirstlane(rr);
+  // (the row's W and c*P in registers before the loop, so that no wait for their loads is left
+  // inside it)
+  OMQ_PIN(y.wv[0]);
+  OMQ_PIN(y.cp[0]);
   while (rr < rend) {
     // ---- steps with a single candidate: two exits, at the bottom.  The candidates of a step
     // take their next state at once (the single candidate when the step is taken), so that
