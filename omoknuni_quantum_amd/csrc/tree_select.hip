@@ -303,8 +303,8 @@ static_assert(kKeyInf == (__builtin_bit_cast(uint32_t, __builtin_inff()) ^ 0x800
 // ap can only add candidates (a NaN hi), which sends the step to the exact comparison.
 // Padding lanes hold qa = kPadQ, a = 0: their hi stays finite and below any A above -1e9.
 //
-// A pick advances the picked lane to its next state (a register select); that lane's state
-// after its following pick is computed during the next step's wave max.  The steps with a
+// A pick advances the picked lane to its next state (a register select); every lane's state
+// after its next pick is formed anew during each step's wave max.  The steps with a
 // single candidate run in a loop of their own; any other step leaves that loop for the exact
 // comparison among its candidates (all children when A is out of range) and comes back.
 // Keeping the rare step out of the loop body leaves the common step without the register
@@ -339,8 +339,8 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
     // take their next state at once (the single candidate when the step is taken), so that
     // the next step's scores wait only for the compare with the wave max, not for the scalar
     // test of the step; a step that is not taken puts their state back after the loop.  Apart
-    // from that, it changes nothing but the pending state, and nothing of it is kept past the
-    // loop.
+    // from that, it changes nothing but the states after the next pick (formed anew every
+    // step), and nothing of it is kept past the loop.
     rr = __builtin_amdgcn_readfirstlane(rr);
     int pc = 1, pen = 0;
     uint32_t Akl = 0u;
@@ -462,7 +462,7 @@ __device__ inline int lane_steps(Row<1>& y, float svec, int rr, int rend, float 
       }
     }
 
-    // ---- the step at rr was not taken above (its state is as it was, nothing pending): the
+    // ---- the step at rr was not taken above (its state is as it was): the
     // window's end, or the exact comparison among its candidates (every child when A is out of
     // range), whose wave max and candidates the loop's last step left in Akl and cm ----
     const float s = readlane_f(svec, rr);
