@@ -204,9 +204,15 @@ __device__ inline int sparse_legal_list(const omq_forest& f, uint64_t k, int* li
     r = (int)((uint32_t)(splitmix64(k ^ ((uint64_t)(jl + 1) * kSaltFloyd)) >> 32) %
               (uint32_t)(jl + 1));
   // With no two equal draws, every step adds its own draw; otherwise the steps are replayed
-  // in order, a draw already taken being replaced by j_i.
+  // in order, a draw already taken being replaced by j_i.  The pass that looks for equal draws
+  // also ranks the draws, which is the rank sort of the sampled values when they are distinct.
   bool dup = false;
-  for (int i = 0; i < n; ++i) dup = dup || (lane > i && readlane_i(r, i) == r);
+  int rank = 0;
+  for (int i = 0; i < n; ++i) {
+    const int v = readlane_i(r, i);
+    dup = dup || (lane > i && v == r);
+    rank += (lane < n && v < r) ? 1 : 0;
+  }
   int mine = r;  // lane i holds the i-th sampled value
   if (__ballot(dup && lane < n) != 0) {
     mine = -1;
@@ -215,12 +221,12 @@ __device__ inline int sparse_legal_list(const omq_forest& f, uint64_t k, int* li
       const bool hit = __ballot(lane < i && mine == ri) != 0;
       if (lane == i) mine = hit ? A - n + i : ri;
     }
-  }
-  // rank sort (values are distinct)
-  int rank = 0;
-  for (int i = 0; i < n; ++i) {
-    const int v = readlane_i(mine, i);
-    rank += (lane < n && v < mine) ? 1 : 0;
+    // rank sort of the replayed values (distinct)
+    rank = 0;
+    for (int i = 0; i < n; ++i) {
+      const int v = readlane_i(mine, i);
+      rank += (lane < n && v < mine) ? 1 : 0;
+    }
   }
   if (lane < n) list[rank] = mine;
   wave_sync();

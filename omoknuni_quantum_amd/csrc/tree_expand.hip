@@ -425,17 +425,25 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
         if (lane == 0 && bi < n) l.bits[bi >> 5] |= 1u << (bi & 31);
         wave_sync();
       }
-      if (lane == 0) {
-        int j = 0;
-        for (int i = 0; i < n; ++i) {
-          if ((l.bits[i >> 5] >> (i & 31)) & 1u) {
-            l.val[j] = l.val[i];
-            l.list[j] = l.list[i];
-            ++j;
-          }
+      // the chosen entries compacted in order, 64 at a time: a chunk's entries are read before
+      // any is written, and its writes land below the next chunk's entries (j <= i)
+      int j0 = 0;
+      for (int c0 = 0; c0 < n; c0 += kWave) {
+        const int i = c0 + lane;
+        const bool keep = i < n && ((l.bits[i >> 5] >> (i & 31)) & 1u);
+        const double v = keep ? l.val[i] : 0.0;
+        const int a = keep ? l.list[i] : 0;
+        const uint64_t b = __ballot(keep);
+        wave_sync();
+        if (keep) {
+          const int j = j0 + (int)__builtin_amdgcn_mbcnt_hi(
+                                 (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+          l.val[j] = v;
+          l.list[j] = a;
         }
+        j0 += __popcll(b);
+        wave_sync();
       }
-      wave_sync();
       nch = sel;
       if (noisy) {
         double dpart = 0.0;
