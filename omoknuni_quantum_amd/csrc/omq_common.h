@@ -192,8 +192,10 @@ __device__ inline int sparse_legal_count(const omq_forest& f, uint64_t k) {
 
 // Sorted legal list of a SPARSE-model node: Floyd's sampling of n distinct values of
 // [0, A) (Bentley & Floyd, "A sample of brilliance", CACM 30(9), 1987), then sorted by rank.
-// Requires n <= 64.  `list` is wave-private LDS of at least n entries.  Returns n.
-__device__ inline int sparse_legal_list(const omq_forest& f, uint64_t k, int* list) {
+// Requires n <= 64.  `list` is wave-private LDS of at least n entries; `bm` is wave-private LDS
+// of f.legal_words words (a scratch bitmap of [0, A), used when it covers A).  Returns n.
+__device__ inline int sparse_legal_list(const omq_forest& f, uint64_t k, int* list,
+                                        uint32_t* bm) {
   const int lane = lane_id();
   const int A = f.num_actions;
   const int n = sparse_legal_count(f, k);
@@ -204,14 +206,43 @@ __device__ inline int sparse_legal_list(const omq_forest& f, uint64_t k, int* li
     r = (int)((uint32_t)(splitmix64(k ^ ((uint64_t)(jl + 1) * kSaltFloyd)) >> 32) %
               (uint32_t)(jl + 1));
   // With no two equal draws, every step adds its own draw; otherwise the steps are replayed
-  // in order, a draw already taken being replaced by j_i.  The pass that looks for equal draws
-  // also ranks the draws, which is the rank sort of the sampled values when they are distinct.
+  // in order, a draw already taken being replaced by j_i.  The test for equal draws also ranks
+  // the draws, which is the rank sort of the sampled values when they are distinct.
   bool dup = false;
   int rank = 0;
-  for (int i = 0; i < n; ++i) {
-    const int v = readlane_i(r, i);
-    dup = dup || (lane > i && v == r);
-    rank += (lane < n && v < r) ? 1 : 0;
+  const int nw = (A + 31) >> 5;
+  if (f.legal_words >= nw && nw <= 3 * kWave) {
+    // the draws as bits of an LDS bitmap: an OR that finds its bit set has an equal draw
+    for (int i = lane; i < nw; i += kWave) bm[i] = 0u;
+    wave_sync();
+    uint32_t old = 0u;
+    if (lane < n) old = atomicOr(&bm[r >> 5], 1u << (r & 31));
+    dup = lane < n && ((old >> (r & 31)) & 1u);
+    wave_sync();
+    if (__ballot(dup) == 0) {
+      // a draw's rank is the number of bits below it: lane l holds words 3l .. 3l+2, whose
+      // popcounts are scanned over the lanes; a draw in word v takes the scan at lane v / 3,
+      // the counts of the lane's words before v, and the bits below it in word v
+      const uint32_t x0 = 3 * lane < nw ? bm[3 * lane] : 0u;
+      const uint32_t x1 = 3 * lane + 1 < nw ? bm[3 * lane + 1] : 0u;
+      const uint32_t x2 = 3 * lane + 2 < nw ? bm[3 * lane + 2] : 0u;
+      const int c0 = __popc(x0), c1 = __popc(x1);
+      int tot;
+      const int e = wave_excl_scan(c0 + c1 + __popc(x2), &tot);
+      const int v = lane < n ? (r >> 5) : 0;
+      const int src = v / 3, sub = v - 3 * src;
+      const int pe = __shfl(e, src, kWave), p0 = __shfl(c0, src, kWave),
+                p1 = __shfl(c1, src, kWave);
+      const uint32_t xv = bm[v];
+      rank = pe + (sub >= 1 ? p0 : 0) + (sub == 2 ? p1 : 0) +
+             __popc(xv & ((1u << (r & 31)) - 1u));
+    }
+  } else {
+    for (int i = 0; i < n; ++i) {
+      const int v = readlane_i(r, i);
+      dup = dup || (lane > i && v == r);
+      rank += (lane < n && v < r) ? 1 : 0;
+    }
   }
   int mine = r;  // lane i holds the i-th sampled value
   if (__ballot(dup && lane < n) != 0) {
@@ -300,7 +331,7 @@ __device__ inline int board_legal_list(const omq_forest& f, const uint32_t* mask
 __device__ inline int leaf_legal_list(const omq_forest& f, const omq_wave& w, int t, int u,
                                       uint32_t* mask, int* list) {
   if (f.game == OMQ_GAME_SPARSE) {
-    return sparse_legal_list(f, w.ukey[(int64_t)t * w.max_wave + u], list);
+    return sparse_legal_list(f, w.ukey[(int64_t)t * w.max_wave + u], list, mask);
   }
   if (w.umask != nullptr) {
     leaf_umask(f, w, t, u, mask);

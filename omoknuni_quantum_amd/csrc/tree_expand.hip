@@ -366,7 +366,7 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
   }
   int n;
   if (f.game == OMQ_GAME_SPARSE) {
-    n = sparse_legal_list(f, w.ukey[wb + u], l.list);
+    n = sparse_legal_list(f, w.ukey[wb + u], l.list, l.mask);
   } else if (w.umask != nullptr) {
     leaf_umask(f, w, t, u, l.mask);  // (its barrier also orders spol)
     n = board_legal_list(f, l.mask, l.list);
