@@ -88,10 +88,21 @@ __global__ __launch_bounds__(kLeafInfoThreads) void leaf_info_kernel(omq_forest 
     const uint32_t* root = f.root_legal + (int64_t)t * f.legal_words;
     uint64_t key = f.root_keys[t];
     int taken = 0;
-    for (int d = 1; d < L; ++d) {
-      const int a = f.actions[tb + path[d]];
-      key = child_key(key, a);
-      if (board && a != pass && a >= 0 && a < f.num_actions) taken += (root[a >> 5] >> (a & 31)) & 1u;
+    // eight depths at a time: their path entries, then their actions, in flight together
+    constexpr int kB = 8;
+    for (int d0 = 1; d0 < L; d0 += kB) {
+      int pv[kB], av[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) pv[j] = d0 + j < L ? path[d0 + j] : 0;
+#pragma unroll
+      for (int j = 0; j < kB; ++j) av[j] = d0 + j < L ? f.actions[tb + pv[j]] : 0;
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        if (d0 + j >= L) break;
+        const int a = av[j];
+        key = child_key(key, a);
+        if (board && a != pass && a >= 0 && a < f.num_actions) taken += (root[a >> 5] >> (a & 31)) & 1u;
+      }
     }
     int count;
     if (board) {
@@ -345,6 +356,7 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
   const int leaf = w.uleaf[wb + u];
   const int cbase = w.uedge[wb + u] + 1;  // node id of the first child
   const int s0 = w.ufirst[wb + u];
+  const uint64_t ukey = f.game == OMQ_GAME_SPARSE ? w.ukey[wb + u] : 0ull;
   const float* pol = w.policy + (wb + u) * (int64_t)f.num_actions;
   const bool staged = stage_policy(f);
   float prow[kStageMaxA / kWave];
@@ -366,7 +378,7 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
   }
   int n;
   if (f.game == OMQ_GAME_SPARSE) {
-    n = sparse_legal_list(f, w.ukey[wb + u], l.list, l.mask);
+    n = sparse_legal_list(f, ukey, l.list, l.mask);
   } else if (w.umask != nullptr) {
     leaf_umask(f, w, t, u, l.mask);  // (its barrier also orders spol)
     n = board_legal_list(f, l.mask, l.list);
