@@ -141,12 +141,17 @@ __global__ void synth_eval_kernel(omq_forest f, omq_wave w, float scale) {
   const uint64_t key = w.ukey[wb + u];
   const int n = leaf_legal_list(f, w, t, u, l.mask, l.list);
   float* row = w.policy + (wb + u) * (int64_t)f.num_actions;
+  // the scaled logits are kept in the wave's LDS (exactly, as doubles) for the second pass
   float mx = -__builtin_inff();
-  for (int i = lane; i < n; i += kWave) mx = fmaxf(mx, scale * key_normal(key, l.list[i]));
+  for (int i = lane; i < n; i += kWave) {
+    const float z = scale * key_normal(key, l.list[i]);
+    l.val[i] = (double)z;
+    mx = fmaxf(mx, z);
+  }
   mx = wave_max_f32(mx);
   float part = 0.0f;
   for (int i = lane; i < n; i += kWave) {
-    const float e = exp_cw(scale * key_normal(key, l.list[i]) - mx);
+    const float e = exp_cw((float)l.val[i] - mx);
     l.val[i] = (double)e;
     part = part + e;
   }
