@@ -219,24 +219,58 @@ __device__ inline int sparse_legal_list(const omq_forest& f, uint64_t k, int* li
     if (lane < n) old = atomicOr(&bm[r >> 5], 1u << (r & 31));
     dup = lane < n && ((old >> (r & 31)) & 1u);
     wave_sync();
-    if (__ballot(dup) == 0) {
-      // a draw's rank is the number of bits below it: lane l holds words 3l .. 3l+2, whose
-      // popcounts are scanned over the lanes; a draw in word v takes the scan at lane v / 3,
-      // the counts of the lane's words before v, and the bits below it in word v
+    // a value's rank is the number of bits below it: lane l holds words 3l .. 3l+2, whose
+    // popcounts are scanned over the lanes; a value in word v takes the scan at lane v / 3, the
+    // counts of that lane's words before v, and the bits below it in word v
+    auto rank_of = [&](int x) -> int {
       const uint32_t x0 = 3 * lane < nw ? bm[3 * lane] : 0u;
       const uint32_t x1 = 3 * lane + 1 < nw ? bm[3 * lane + 1] : 0u;
       const uint32_t x2 = 3 * lane + 2 < nw ? bm[3 * lane + 2] : 0u;
       const int c0 = __popc(x0), c1 = __popc(x1);
       int tot;
       const int e = wave_excl_scan(c0 + c1 + __popc(x2), &tot);
-      const int v = lane < n ? (r >> 5) : 0;
+      const int v = lane < n ? (x >> 5) : 0;
       const int src = v / 3, sub = v - 3 * src;
       const int pe = __shfl(e, src, kWave), p0 = __shfl(c0, src, kWave),
                 p1 = __shfl(c1, src, kWave);
       const uint32_t xv = bm[v];
-      rank = pe + (sub >= 1 ? p0 : 0) + (sub == 2 ? p1 : 0) +
-             __popc(xv & ((1u << (r & 31)) - 1u));
+      return pe + (sub >= 1 ? p0 : 0) + (sub == 2 ? p1 : 0) +
+             __popc(xv & ((1u << (x & 31)) - 1u));
+    };
+    const uint64_t fl0 = __ballot(dup);
+    if (fl0 != 0) {
+      // Floyd's steps without replaying them: step i takes j_i instead of its draw when the
+      // draw is already in the set, that is when an earlier lane drew the same value (D), or
+      // when the draw is j_k of an earlier step k that took j_k.  The second rule links a step
+      // to one earlier step, so the rounds below settle it (at most n of them).
+      bool D = false;
+      uint64_t fl = fl0;
+      for (int it = 0; it < kWave && fl != 0; ++it) {
+        const int v = readlane_i(r, lowest_lane(fl));
+        const uint64_t eq = __ballot(lane < n && r == v);
+        D = D || (lane < n && r == v && lane > lowest_lane(eq));
+        fl &= ~eq;
+      }
+      const int kk = r - (A - n);
+      const bool link = lane < n && kk >= 0 && kk < lane;
+      bool col = D;
+      for (int it = 0; it < n; ++it) {
+        const int ck = __shfl((int)col, link ? kk : lane, kWave);
+        const bool nc = D || (link && ck != 0);
+        const bool changed = __ballot(nc != col) != 0;
+        col = nc;
+        if (!changed) break;
+      }
+      if (col) r = A - n + lane;
+      // the sampled values are distinct now: their bitmap ranks them
+      wave_sync();
+      for (int i = lane; i < nw; i += kWave) bm[i] = 0u;
+      wave_sync();
+      if (lane < n) atomicOr(&bm[r >> 5], 1u << (r & 31));
+      wave_sync();
+      dup = false;
     }
+    rank = rank_of(r);
   } else {
     for (int i = 0; i < n; ++i) {
       const int v = readlane_i(r, i);
