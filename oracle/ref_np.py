@@ -63,11 +63,25 @@ SELECT_VARIANTS = (
 )
 
 
+# Planted misreadings of the capacity rule of expand_node (cython_tree_optimized.pyx:242-246:
+# a leaf whose n children do not fit is refused whole, and later leaves are still tried), used
+# only by the tests that show the capacity checks fail on each of them.  None is the rule.
+CAP_VARIANTS = (
+    "first_fail",  # after the first refusal of a wave, every later leaf of it refused too
+    "partial",     # a leaf that does not fit gets as many children as still fit
+)
+
+
 class NpTree:
-    def __init__(self, cap: int, c_puct: float, vl: float, variant: str | None = None):
+    def __init__(self, cap: int, c_puct: float, vl: float, variant: str | None = None,
+                 cap_variant: str | None = None):
         if variant is not None and variant not in SELECT_VARIANTS:
             raise ValueError(f"unknown selection variant {variant!r}")
+        if cap_variant is not None and cap_variant not in CAP_VARIANTS:
+            raise ValueError(f"unknown capacity variant {cap_variant!r}")
         self.variant = variant
+        self.cap_variant = cap_variant
+        self.wave_refused = False  # a refusal happened in the current wave (first_fail)
         self.inflight = np.zeros(cap, np.int32)  # simulations of the current wave per node
         self.cap = cap
         self.c = F(c_puct)
@@ -140,8 +154,16 @@ class NpTree:
 
     def expand(self, leaf: int, actions, priors) -> bool:
         k = len(actions)
-        if self.expanded[leaf] or k == 0 or self.num_nodes + k > self.cap:
+        if self.expanded[leaf] or k == 0:
             return False
+        if self.cap_variant == "first_fail" and self.wave_refused:
+            return False
+        if self.num_nodes + k > self.cap:
+            if self.cap_variant == "partial" and self.num_nodes < self.cap:
+                k = self.cap - self.num_nodes
+            else:
+                self.wave_refused = True
+                return False
         fe, fc = self.num_edges, self.num_nodes
         self.num_edges += k
         self.num_nodes += k
@@ -220,22 +242,57 @@ PW_VARIANTS = (
 )
 
 
+# Planted misreadings of the root Dirichlet mix (optimized_wave_search.py:384-392 under numpy's
+# promotion: float32 priors times the Python float 1 - eps stay float32, the float64 noise
+# term promotes the sum to float64; cython_tree_optimized.pyx:569-572 rounds it to float32),
+# used only by the tests that show the mix checks fail on each of them.  None is the rule.
+MIX_VARIANTS = (
+    "mix_f32",           # the whole mix in float32 (noise rounded to float32 first)
+    "w_double",          # (1 - eps) * p formed in float64 instead of float32
+    "renorm_double",     # the legal renormalisation p / S kept in float64 before the mix
+    "mixed_rounded",     # the mixed prior rounded to float32 before the widening's renorm
+    "renorm_after_mix",  # under 'full', the mixed priors renormalised by their sum
+    "pw_renorm_f32",     # the widening's renormalisation of noisy priors in float32
+)
+
+
 def choose_children(legal, pol_row, is_root, policy, root_visits, noise=None, eps=0.0,
-                    pw_variant=None):
+                    pw_variant=None, mix_variant=None):
     """Expansion of one leaf (optimized_wave_search.py:377-415): legal priors renormalised by
     their canonical sum, Dirichlet at the root, 'full' or progressive widening; returns
     (actions, priors) in ascending action order.  pw_variant plants a misreading of
-    PW_VARIANTS."""
+    PW_VARIANTS, mix_variant one of MIX_VARIANTS."""
     if pw_variant is not None and pw_variant not in PW_VARIANTS:
         raise ValueError(f"unknown widening variant {pw_variant!r}")
+    if mix_variant is not None and mix_variant not in MIX_VARIANTS:
+        raise ValueError(f"unknown mix variant {mix_variant!r}")
+    mv = mix_variant
     legal = list(legal)
     n = len(legal)
     pf = [F(pol_row[a]) for a in legal]
     S = sum64(pf)
-    pf = [F(p / S) for p in pf]
+    if mv == "renorm_double":
+        pr = [float(p) / float(S) for p in pf]
+    else:
+        pr = [float(F(p / S)) for p in pf]
+    pf = [F(p) for p in pr]
     noisy = is_root and noise is not None and eps > 0
     w32 = F(1.0 - eps)
-    pd = [float(F(w32 * p)) + eps * float(noise[i]) if noisy else float(p) for i, p in enumerate(pf)]
+
+    def mix(i):
+        if mv == "mix_f32":
+            return float(F(F(w32 * pf[i]) + F(F(eps) * F(noise[i]))))
+        if mv == "w_double":
+            return (1.0 - eps) * pr[i] + eps * float(noise[i])
+        if mv == "renorm_double":
+            return float(w32) * pr[i] + eps * float(noise[i])
+        x = float(F(w32 * pf[i])) + eps * float(noise[i])
+        return float(F(x)) if mv == "mixed_rounded" else x
+
+    pd = [mix(i) if noisy else float(p) for i, p in enumerate(pf)]
+    if noisy and mv == "renorm_after_mix" and policy == "full":
+        Sm = sum64d(pd)
+        pd = [x / Sm for x in pd]
     chosen = list(range(n))
     k = n
     if policy == "reference_pw":
@@ -249,7 +306,7 @@ def choose_children(legal, pol_row, is_root, policy, root_visits, noise=None, ep
         if n > sel:
             order = sorted(range(n), key=lambda i: (-pd[i], i))[:sel]
             chosen = sorted(order)
-            if noisy:
+            if noisy and mv != "pw_renorm_f32":
                 Sd = sum64d([pd[i] for i in chosen])
                 for i in chosen:
                     pd[i] = pd[i] / Sd
@@ -420,6 +477,7 @@ def np_wave(tree: NpTree, W: int, max_depth: int, legal_of, pol_rows, vals, poli
     from pol_rows/vals (row u for the u-th unique leaf), expansion, then backup in order.
     terminal_of(path actions), when given, names the terminal leaves, which are evaluated and
     backed up but not expanded (optimized_wave_search.py:374-376); the root never is."""
+    tree.wave_refused = False
     paths = [tree.select_path(max_depth) for _ in range(W)]
     leaves = [p[-1] for p in paths]
     uniq = []

@@ -10,18 +10,17 @@ from omoknuni_quantum_amd.synthetic.workloads import get
 from oracle.oracle import Oracle
 
 
-@pytest.mark.gpu
-def test_c5_resnet_replay_parity(device):
-    wl = get("C5").scaled(num_trees=4, num_simulations=96, capacity=50_000)
+def _replay_parity(wl, device, num_blocks, channels):
     params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth)
     eng = WaveEngine(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth, device,
                      params)
     keys, legal, noise = wl.root_inputs()
     eng.set_roots(keys, legal, noise)
     boards = torch.from_numpy(wl.boards()).to(device)
-    ev = ResNetEvaluator(eng, boards, num_blocks=2, channels=32, record=True)
+    ev = ResNetEvaluator(eng, boards, num_blocks=num_blocks, channels=channels, record=True)
     eng.search(wl.num_simulations, wl.wave_size, ev)
     torch.cuda.synchronize()
+    eng.check_status()
     sizes = [1] + [wl.wave_size] * (wl.num_simulations // wl.wave_size)
     assert len(ev.calls) == len(sizes)
     pol0 = ev.calls[1][0]
@@ -39,6 +38,23 @@ def test_c5_resnet_replay_parity(device):
             assert np.array_equal(g[k], o[k]), (t, k)
         for k in ("W", "P"):
             assert np.array_equal(g[k].view(np.int32), o[k].view(np.int32)), (t, k)
+        assert int(g["N"][0]) == 2 + wl.num_simulations
+
+
+@pytest.mark.gpu
+def test_c5_resnet_replay_parity(device):
+    wl = get("C5").scaled(num_trees=4, num_simulations=96, capacity=50_000)
+    _replay_parity(wl, device, num_blocks=2, channels=32)
+
+
+@pytest.mark.gpu
+def test_c5_full_network_fullcount_replay_parity(device):
+    """C5's own network (10 blocks x 128 channels, bf16) on two trees at C5's full simulation
+    count, wave and capacity (1600 simulations in waves of 16 slots per tree, 400k nodes)."""
+    wl = get("C5").scaled(num_trees=2)
+    assert wl.num_simulations == 1600 and wl.wave_size == 16 and wl.capacity == 400_000
+    print(f"[c5] T={wl.num_trees} sims={wl.num_simulations} W={wl.wave_size}", flush=True)
+    _replay_parity(wl, device, num_blocks=10, channels=128)
 
 
 def test_resnet_architecture_shapes():

@@ -45,9 +45,19 @@ CASES = {
     # thousands of refused expansions per tree) and C4's 2048-simulation waves
     "C3-fullcount": ("C3", {"num_trees": 2}),
     "C4-fullcount": ("C4", {"num_trees": 2}),
+    # C2 at its full simulation count and capacity on two trees (1600 simulations, waves of 256)
+    "C2-fullcount": ("C2", {"num_trees": 2}),
+    # tiny capacities: the capacity-full rule at every fill level (first fit in first-occurrence
+    # order, refused leaves backed up), with 1-10 children per leaf or counts falling by depth
+    "capacity-sparse-60": ("C4", {"model": games.chess_sparse(64, 1, 10), "num_trees": 16,
+                                  "num_simulations": 192, "wave_size": 16, "capacity": 60}),
+    "capacity-sparse-150": ("C4", {"model": games.chess_sparse(64, 1, 10), "num_trees": 16,
+                                   "num_simulations": 192, "wave_size": 16, "capacity": 150}),
+    "capacity-gomoku5": ("C2", {"model": games.gomoku(5), "max_stones": 17, "num_trees": 16,
+                                "num_simulations": 192, "wave_size": 16, "capacity": 55}),
 }
 # compared after every wave, except the full-count cases (every third wave and the last)
-CHECK_EVERY = {"C3-fullcount": 3, "C4-fullcount": 3}
+CHECK_EVERY = {"C3-fullcount": 3, "C4-fullcount": 3, "C2-fullcount": 2}
 
 
 @pytest.mark.gpu

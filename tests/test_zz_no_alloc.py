@@ -82,3 +82,21 @@ def test_noalloc_shift_matches_workspace_entry(device, order):
         b.run_wave(wl.wave_size, ev)
         torch.cuda.synchronize()
         _compare(a, b, f"{wl.name} continued")
+
+
+def test_noalloc_shift_over_limit_leaves_forest_unchanged(device):
+    """A searched forest beyond the library's workspace (2 trees x 600k nodes > 1,048,576):
+    OMQ_E_LIMIT, and nothing is launched, so every tree stays as it was."""
+    wl = get("C4").scaled(num_trees=2, num_simulations=512, wave_size=256, capacity=600_000,
+                          name="over-limit")
+    assert wl.num_trees * wl.capacity * _lib.OMQ_SHIFT_WORKSPACE_PER_NODE > \
+        _lib.OMQ_NOALLOC_SHIFT_INTS
+    print(f"[no-alloc] {wl.name}: T={wl.num_trees} capacity={wl.capacity}", flush=True)
+    a, b = _searched_pair(wl, device)
+    roots = torch.from_numpy(_most_visited_children(b)).to(b.device)
+    lib = _lib.load()
+    rc = lib.omq_shift_root_noalloc(b.forest_ref, roots.data_ptr(), b.stream_handle())
+    assert rc == _lib.OMQ_E_LIMIT
+    assert "omq_shift_root_noalloc" in lib.omq_last_error().decode()
+    torch.cuda.synchronize()
+    _compare(a, b, "over-limit, refused")
