@@ -10,7 +10,7 @@ at the top level, then every other workload of the benchmark under "configs", ea
 roofline, CPU baseline and full-size parity check.
 
     python bench.py [--steps K] [--warmup W] [--config C3] [--configs all|none|C1,C2,...]
-                    [--cpu-baseline auto|skip] [--select-schedule auto|whole|split]
+                    [--cpu-baseline auto|skip]
 """
 from __future__ import annotations
 
@@ -56,7 +56,6 @@ def algorithmic_bytes(st: dict, sims: int) -> dict:
     }
 
 
-SCHEDULES = {"auto": 0, "whole": 1, "split": 2}
 
 KERNEL_OF_PHASE = {"select": "select_root_kernel", "leaf_info": "leaf_info_kernel",
                    "expand": "expand_write_kernel", "backup": "backup_groups_kernel"}
@@ -183,7 +182,7 @@ def measure(name: str, args, steps: int, warmup: int, extras: bool) -> dict:
                    "simulations_per_tree": wl.num_simulations, "wave": wl.wave_size,
                    "capacity": wl.capacity, "game": wl.model.kind,
                    "actions": wl.model.num_actions, "w_mode": args.w_mode,
-                   "vl_atomic": bool(args.vl_atomic), "select_schedule": args.select_schedule,
+                   "vl_atomic": bool(args.vl_atomic),
                    "parallelism": "none (1 GPU)"},
         "roofline": roofline,
         "tree_op_ms_per_step": round(tree_ms / steps, 4),
@@ -222,8 +221,8 @@ def measure(name: str, args, steps: int, warmup: int, extras: bool) -> dict:
 def run(args) -> dict:
     from omoknuni_quantum_amd import _lib
 
-    _lib.check(_lib.load().omq_select_options(SCHEDULES[args.select_schedule],
-                                              _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
+    _lib.check(_lib.load().omq_select_options(_lib.OMQ_SPIN_LIMIT_DEFAULT),
+               "omq_select_options")
     head = measure(args.config, args, args.steps, args.warmup, extras=True)
     out = {
         "metric": METRIC,
@@ -502,9 +501,6 @@ def main():
                          "a comma-separated list of C1..C5")
     ap.add_argument("--trees", type=int, default=0, help="override the workload's tree count")
     ap.add_argument("--w-mode", choices=("ordered", "atomic"), default="ordered")
-    ap.add_argument("--select-schedule", choices=tuple(SCHEDULES), default="auto",
-                    help="omq_select schedule: by size (auto), one workgroup per tree (whole), "
-                         "or root chains and subtree tasks (split)")
     ap.add_argument("--vl-atomic", action="store_true")
     ap.add_argument("--cpu-baseline", choices=("auto", "skip"), default="auto")
     ap.add_argument("--cpu-trees", type=int, default=0,

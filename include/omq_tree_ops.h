@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define OMQ_ABI_VERSION 2
+#define OMQ_ABI_VERSION 3
 
 /* error codes */
 #define OMQ_OK 0
@@ -146,8 +146,7 @@ typedef struct omq_wave {
   int64_t* stats;           /* [T*OMQ_NSTATS] accumulated operation counters */
   int32_t* status;          /* [4] device-side error flags (bit set, never cleared by the library) */
   int32_t* sel_scratch;     /* [OMQ_SEL_SCRATCH_INTS(T, max_wave)] omq_select's scratch: per-
-                               simulation leaf records and the subtree tasks of its split
-                               schedule (no contents to keep between calls) */
+                               simulation leaf records (no contents to keep between calls) */
   uint32_t* umask;          /* NULL, or [T*max_wave*legal_words]: legal-action masks of the unique
                                leaves, written by omq_go_rules.  When it is not NULL,
                                omq_synthetic_evaluate and omq_expand take a board leaf's legal
@@ -156,8 +155,11 @@ typedef struct omq_wave {
                                path's cells. */
 } omq_wave;
 
+/* default bound of the polls of a wait inside omq_select (omq_select_options) */
+#define OMQ_SPIN_LIMIT_DEFAULT (1 << 22)
+
 /* int32 entries of omq_wave::sel_scratch for T trees of max_wave simulations */
-#define OMQ_SEL_SCRATCH_INTS(T, MW) (4 * (int64_t)(T) * (MW) + 10 * (int64_t)(T) + 16)
+#define OMQ_SEL_SCRATCH_INTS(T, MW) (2 * (int64_t)(T) * (MW))
 
 /* stats counters (per tree, accumulated over waves) */
 #define OMQ_ST_INTERNAL 0     /* groups that selected a child (distinct internal nodes per wave) */
@@ -206,16 +208,16 @@ int omq_forest_reset(const omq_forest* f, void* stream);
 int omq_select(const omq_forest* f, const omq_wave* w, int32_t wave_size, float c_puct,
                float virtual_loss, int32_t max_depth, int32_t vl_atomic, void* stream);
 
-/* Process-wide options of omq_select, for tests and tuning; no counterpart in the reference.
- * - split_mode.  0 (default) and 1 run each tree's whole wave in one workgroup.  2 takes the
- *   split schedule (forests of at most 128 trees): the root chains in one workgroup per tree,
- *   then the subtrees below them as tasks spread over the whole chip, then the unique-leaf
- *   pass.  Both schedules give the same results; the split one measured slower.
- * - spin_limit.  Bound of the polls of a wait inside omq_select (default 2^22, at least 0).
- *   Running out sets OMQ_STATUS_STALL, and the simulations it held up end their paths early;
- *   the trees must then be reset.
- * Returns OMQ_E_ARG for an unknown mode or a negative limit. */
-int omq_select_options(int32_t split_mode, int32_t spin_limit);
+/* Process-wide option of omq_select, for tests; no counterpart in the reference.
+ * spin_limit bounds the polls of a wait inside omq_select (default OMQ_SPIN_LIMIT_DEFAULT,
+ * at least 0).  Running out sets OMQ_STATUS_STALL, and the simulations it held up end their
+ * paths early; the trees must then be reset.  The value is read at each omq_select call, so a
+ * recorded graph keeps the value of its recording.  Returns OMQ_E_ARG for a negative limit. */
+int omq_select_options(int32_t spin_limit);
+
+/* The spin limit omq_select launches with (for callers that record graphs and key them by
+ * the launch arguments); no counterpart in the reference. */
+int32_t omq_select_spin_limit(void);
 
 /* Compute the hash key and the number of legal actions of every unique leaf of the wave.
  * (Game-model step between selection and evaluation; no reference counterpart in the

@@ -13,7 +13,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libomq_tree_ops.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # constants of include/omq_tree_ops.h
 OMQ_OK, OMQ_E_ARG, OMQ_E_LAUNCH, OMQ_E_LIMIT = 0, -1, -2, -3
@@ -63,7 +63,7 @@ class OmqWave(ctypes.Structure):
 
 def sel_scratch_ints(T: int, MW: int) -> int:
     """OMQ_SEL_SCRATCH_INTS of include/omq_tree_ops.h."""
-    return 4 * T * MW + 10 * T + 16
+    return 2 * T * MW
 
 
 OMQ_SPIN_LIMIT_DEFAULT = 1 << 22
@@ -78,7 +78,8 @@ SIGNATURES = {
     "omq_forest_reset": (ctypes.c_int, [_FP, _p]),
     "omq_select": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, ctypes.c_float, _i32, _i32, _p]),
     "omq_leaf_info": (ctypes.c_int, [_FP, _WP, _p]),
-    "omq_select_options": (ctypes.c_int, [_i32, _i32]),
+    "omq_select_options": (ctypes.c_int, [_i32]),
+    "omq_select_spin_limit": (ctypes.c_int32, []),
     "omq_synthetic_evaluate": (ctypes.c_int, [_FP, _WP, ctypes.c_float, _p]),
     "omq_expand": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _p, ctypes.c_double, _p]),
     "omq_backup": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _i32, _p]),

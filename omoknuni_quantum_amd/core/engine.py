@@ -375,15 +375,17 @@ class WaveEngine:
 
     def launch_signature(self) -> tuple:
         """Everything on the host side that a wave's launches take as arguments besides the
-        wave size: search parameters, noise on or off, and the addresses of the rule inputs.
-        Two searches with the same signature and wave sizes launch the same kernels with the
-        same arguments (the tree, wave and root buffers keep their addresses)."""
+        wave size: search parameters, noise on or off, the addresses of the rule inputs and
+        the library's process-wide spin limit (omq_select_options).  Two searches with the
+        same signature and wave sizes launch the same kernels with the same arguments (the
+        tree, wave and root buffers keep their addresses)."""
         ptr = lambda x: 0 if x is None else x.data_ptr()  # noqa: E731
         p = self.params
         return (p.c_puct, p.virtual_loss, p.max_depth, p.expand_policy, p.sign_mode, p.w_mode,
                 p.vl_atomic, p.dirichlet_epsilon, self.has_noise, self.rule, self.go_flags,
                 ptr(self.root_boards), ptr(self.root_player), ptr(self.root_passes),
-                ptr(self.root_ko), int(self.wave.umask or 0))
+                ptr(self.root_ko), int(self.wave.umask or 0),
+                int(self.lib.omq_select_spin_limit()))
 
     def search(self, num_simulations: int, wave_size: int, evaluator, timer=None) -> None:
         """MCTS.search on every tree: reset, root expansion (one-simulation wave on the lone

@@ -12,7 +12,8 @@ namespace omq {
 size_t select_lds_bytes(int W);
 hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_puct,
                          float virtual_loss, int max_depth, int vl_atomic, hipStream_t stream);
-void select_set_options(int split_mode, int spin_limit);
+void select_set_options(int spin_limit);
+int select_spin_limit();
 hipError_t launch_leaf_info(const omq_forest& f, const omq_wave& w, int W, hipStream_t st);
 hipError_t launch_synth_eval(const omq_forest& f, const omq_wave& w, int W, float scale,
                              hipStream_t st);
@@ -197,14 +198,13 @@ int omq_select(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
                     "omq_select");
 }
 
-int omq_select_options(int32_t split_mode, int32_t spin_limit) {
-  if (split_mode < 0 || split_mode > 2)
-    return fail(OMQ_E_ARG, "split_mode %d is not 0 (automatic), 1 (whole) or 2 (split)",
-                split_mode);
+int omq_select_options(int32_t spin_limit) {
   if (spin_limit < 0) return fail(OMQ_E_ARG, "spin_limit %d < 0", spin_limit);
-  omq::select_set_options(split_mode, spin_limit);
+  omq::select_set_options(spin_limit);
   return OMQ_OK;
 }
+
+int32_t omq_select_spin_limit(void) { return omq::select_spin_limit(); }
 
 int omq_leaf_info(const omq_forest* f, const omq_wave* w, void* stream) {
   int rc = check_forest(f);

@@ -69,11 +69,6 @@ struct SelArgs {
   // selection scratch (omq_wave::sel_scratch)
   int32_t* lflag;  // [T*max_wave] 1 for the first simulation of a leaf group
   int32_t* lfs;    // [T*max_wave] first simulation of a simulation's leaf group
-  int32_t* tasks;  // [T*max_wave*2] subtree tasks: node, seg | members << 16
-  int32_t* ntask;  // [T] subtree tasks of a tree
-  int32_t* tinfo;  // [T] level of a tree's tasks, + 256 when its virtual loss is applied
-  int32_t* tcls;   // [T*8] tasks per size class
-  int32_t* ctl;    // [16] the subtree kernel's task counter
 };
 
 // Max of a uint32 over the 64 lanes, made uniform: DPP row shifts 1,2,4,8 (each a single
@@ -2099,69 +2094,10 @@ __device__ inline void flush_stats(const SelArgs& w, int t, LevelShared<NT>& sh)
               sh.st[tid]);
 }
 
-// ---- Subtree tasks ---------------------------------------------------------------------
-// The groups of one level below the root chain are independent: the members of a group only
-// ever meet the nodes of its node's subtree.  In the split schedule the root kernel stops at
-// that level and hands its groups over as subtree tasks; the subtree kernel's workgroups take
-// them from a global counter, largest size class first over all trees (the longest subtrees
-// start first), and each runs the level loop of its subtree in LDS.  No workgroup waits for
-// another; the kernel boundaries order the root kernel, the subtree kernel and the finish.
-constexpr int kTaskClasses = 8;
-constexpr int kSplitMaxTrees = 128;  // trees of a forest for the split schedule (LDS table)
-constexpr int kSubThreads = 256;
-
-// Size class of a subtree task of m members: 0 for m >= 128, ..., 7 for m = 1.
-__device__ inline int task_class(int m) { return 7 - min(7, 31 - __clz(m)); }
-
-// The groups of level d (in L / sh at parity d & 1) as subtree tasks of tree t: members copied
-// to gmembers level d (their place in the group log), tasks written in size-class order with
-// the per-class counts, and the tree's task level (d, plus 256 when the level's virtual loss is
-// in N already).  Called by every thread of the workgroup.
-template <int NT>
-__device__ inline void export_tasks(const SelArgs& f, int t, int d, bool vl_done, int W,
-                                    const LevelLds& L, LevelShared<NT>& sh) {
-  const int tid = threadIdx.x;
-  const int cur = d & 1;
-  const int MW = f.max_wave, MD = f.max_depth_buf;
-  const int nb = sh.nbig[cur];
-  const int ns = sh.nsmall[cur];
-  const int n = nb + ns;
-  if (n > 0)
-    for (int s = tid; s < W; s += NT)
-      f.gmembers[((int64_t)t * MD + d) * MW + s] = L.buf[cur * W + s];
-  if (tid < kTaskClasses) sh.hist[tid] = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += NT) {
-    const int gi = i < nb ? i : W - 1 - (i - nb);
-    atomicAdd(&sh.hist[task_class((int)(L.gsl[cur * W + gi] >> 16))], 1);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int k = 0; k < kTaskClasses; ++k) {
-      const int v = sh.hist[k];
-      f.tcls[t * kTaskClasses + k] = v;
-      sh.hist[kTaskClasses + k] = run;
-      run += v;
-    }
-    f.ntask[t] = n;
-    f.tinfo[t] = d | (vl_done ? 256 : 0);
-  }
-  __syncthreads();
-  int32_t* tasks = f.tasks + (int64_t)t * MW * 2;
-  for (int i = tid; i < n; i += NT) {
-    const int gi = i < nb ? i : W - 1 - (i - nb);
-    const uint32_t sl = L.gsl[cur * W + gi];
-    const int pos = atomicAdd(&sh.hist[kTaskClasses + task_class((int)(sl >> 16))], 1);
-    tasks[2 * pos] = (int)L.gnode[cur * W + gi];
-    tasks[2 * pos + 1] = (int)sl;
-  }
-}
-
 // ---- Kernels ---------------------------------------------------------------------------
-// The root kernel: one workgroup per tree.  SPLIT: levels below dend are left to the subtree
-// kernel as tasks; otherwise the whole selection runs here, with the unique-leaf pass.
-template <int RMAX, int NT, bool SPLIT>
+// The select kernel: one workgroup per tree runs every level of its tree's wave, then the
+// unique-leaf pass.
+template <int RMAX, int NT>
 __global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c) {
   // the level overlap in the kernels whose chains keep their registers with a second copy of
   // the chain code (the followers'), with a full workgroup of followers (the 1- and 2-slot
@@ -2195,106 +2131,13 @@ __global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c)
       atomicOr(&f.status[0], OMQ_STATUS_COUNTLIMIT);
   }
   start_group<RMAX, NT>(L, sh, W, 0, 0, 0, W, nullptr);
-  const int dend = SPLIT ? (pipe ? 2 : 1) : c.max_depth;
-  const int d = level_loop<RMAX, NT, NT <= 512>(f, c, t, 0, dend, W, L, sh, &s_glog, lfs, lflag, pipe,
-                                     root_first, pipe ? 2 : -1);
-  if (SPLIT) {
-    export_tasks<NT>(f, t, d, pipe && d == 2, W, L, sh);
-  } else {
-    __syncthreads();
-    finish_tree<NT>(f, t, W, lfs, lflag, sh.wtot);
-  }
+  level_loop<RMAX, NT, NT <= 512>(f, c, t, 0, c.max_depth, W, L, sh, &s_glog, lfs, lflag, pipe,
+                                  root_first, pipe ? 2 : -1);
   __syncthreads();
-  if (tid == 0) f.gcount[t] = s_glog;  // (the subtree kernel adds its groups)
+  finish_tree<NT>(f, t, W, lfs, lflag, sh.wtot);
+  __syncthreads();
+  if (tid == 0) f.gcount[t] = s_glog;
   flush_stats<NT>(f, t, sh);
-}
-
-// The subtree kernel: persistent workgroups dealing the subtree tasks of every tree.
-template <int RMAX>
-__global__ __launch_bounds__(kSubThreads, 4) void select_subtree_kernel(SelArgs f, SelCfg c) {
-  constexpr int NT = kSubThreads;
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ LevelShared<NT> sh;
-  __shared__ int s_off[kTaskClasses * kSplitMaxTrees];  // first global index of (class, tree)
-  __shared__ int s_base[kTaskClasses + 1];               // first global index of a class
-  __shared__ int s_job[3];                               // tree, node, seg | m << 16
-  const int W = c.W;
-  const LevelLds L = carve_level_lds<NT>(smem, W, false);
-  const int tid = threadIdx.x;
-  const int T = f.num_trees;
-  const int MW = f.max_wave, MD = f.max_depth_buf;
-  // global task order: size class, then tree, then the tree's order
-  for (int i = tid; i < kTaskClasses * T; i += NT) {
-    const int k = i / T, tt = i - k * T;
-    s_off[i] = f.tcls[tt * kTaskClasses + k];
-  }
-  __syncthreads();
-  if (tid < kTaskClasses) {  // per class: exclusive prefix over the trees, in place
-    int run = 0;
-    for (int tt = 0; tt < T; ++tt) {
-      const int v = s_off[tid * T + tt];
-      s_off[tid * T + tt] = run;
-      run += v;
-    }
-    s_base[tid + 1] = run;  // class total, for now
-  }
-  __syncthreads();
-  if (tid == 0) {
-    s_base[0] = 0;
-    for (int k = 0; k < kTaskClasses; ++k) s_base[k + 1] += s_base[k];
-  }
-  __syncthreads();
-  for (int i = tid; i < kTaskClasses * T; i += NT) s_off[i] += s_base[i / T];
-  __syncthreads();
-  const int ntot = s_base[kTaskClasses];
-  // Tasks are dealt round-robin in the global order (largest size class first): workgroup b
-  // takes tasks b, b + grid, ...  (A shared task counter would put every workgroup's fetch
-  // behind one contended device-scope atomic.)
-  for (int g = blockIdx.x; g < ntot; g += gridDim.x) {
-    if (tid == 0) {
-      {
-        int k = 0;
-        while (k + 1 < kTaskClasses && s_base[k + 1] <= g) ++k;
-        int lo = 0, hi = T - 1;  // the last tree whose class-k range starts at or before g
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (s_off[k * T + mid] <= g) lo = mid; else hi = mid - 1;
-        }
-        const int tt = lo;
-        int cstart = 0;
-        for (int k2 = 0; k2 < k; ++k2) cstart += f.tcls[tt * kTaskClasses + k2];
-        const int i = cstart + (g - s_off[k * T + tt]);
-        const int32_t* tasks = f.tasks + (int64_t)tt * MW * 2;
-        s_job[0] = tt;
-        s_job[1] = tasks[2 * i];
-        s_job[2] = tasks[2 * i + 1];
-      }
-    }
-    __syncthreads();
-    const int t = s_job[0], p = s_job[1];
-    const uint32_t sl = (uint32_t)s_job[2];
-    const int seg = (int)(sl & 0xFFFFu), m = (int)(sl >> 16);
-    const int info = f.tinfo[t];
-    const int d0 = info & 255;
-    const uint16_t* src = f.gmembers + ((int64_t)t * MD + d0) * MW + seg;
-    start_group<RMAX, NT>(L, sh, W, d0, p, seg, m, src);
-    level_loop<RMAX, NT, false>(f, c, t, d0, c.max_depth, W, L, sh, f.gcount + t,
-                         f.lfs + (int64_t)t * MW, f.lflag + (int64_t)t * MW, false, 0,
-                         (info & 256) ? d0 : -1);
-    __syncthreads();
-    flush_stats<NT>(f, t, sh);
-    __syncthreads();
-  }
-}
-
-// The unique-leaf pass of the split schedule: one workgroup per tree.
-constexpr int kFinishThreads = 1024;
-__global__ __launch_bounds__(kFinishThreads) void select_finish_kernel(SelArgs f, SelCfg c) {
-  __shared__ int s_wtot[kFinishThreads / kWave];
-  const int t = blockIdx.x;
-  const int MW = f.max_wave;
-  finish_tree<kFinishThreads>(f, t, c.W, f.lfs + (int64_t)t * MW, f.lflag + (int64_t)t * MW,
-                              s_wtot);
 }
 
 }  // namespace omq
@@ -2303,11 +2146,9 @@ __global__ __launch_bounds__(kFinishThreads) void select_finish_kernel(SelArgs f
 namespace omq {
 
 namespace {
-std::atomic<int> g_split_mode{0};          // 0 automatic, 1 whole, 2 split
-std::atomic<int> g_spin_limit{1 << 22};    // polls of a follower's bounded wait
+std::atomic<int> g_spin_limit{OMQ_SPIN_LIMIT_DEFAULT};  // polls of a follower's bounded wait
 constexpr int kMaxDevices = 64;
-std::atomic<int> g_cu_count[kMaxDevices];  // 0: not known yet
-std::atomic<bool> g_attr_set[kMaxDevices][3][9];
+std::atomic<bool> g_attr_set[kMaxDevices][9];
 
 // Threads of the whole-wave kernel: 512 for the kernels of more than 4 slots per lane, whose
 // chains then keep up to 256 registers (at 1024 threads, 128: the 6-slot chains spilled 12-100
@@ -2319,27 +2160,20 @@ constexpr int whole_threads() {
 }
 
 template <int RMAX>
-const void* root_kernel(bool split) {
-  if (!split) return (const void*)select_root_kernel<RMAX, whole_threads<RMAX>(), false>;
-  if (RMAX <= 3) return (const void*)select_root_kernel<RMAX, 1024, true>;
-  return (const void*)select_root_kernel<RMAX, 256, true>;
+const void* root_kernel() {
+  return (const void*)select_root_kernel<RMAX, whole_threads<RMAX>()>;
 }
 
-struct SelKernels {
-  const void* root;
-  const void* sub;
-  int root_threads;
+struct SelKernel {
+  const void* fn;
+  int threads;
 };
 
-SelKernels pick_kernels(int rmax, bool split) {
-  SelKernels k{};
+SelKernel pick_kernel(int rmax) {
   switch (rmax) {
-#define OMQ_PICK(R)                                            \
-  case R:                                                      \
-    k.root = root_kernel<R>(split);                            \
-    k.sub = (const void*)select_subtree_kernel<R>;             \
-    k.root_threads = split ? (R > 3 ? 256 : 1024) : whole_threads<R>(); \
-    break;
+#define OMQ_PICK(R) \
+  case R:           \
+    return SelKernel{root_kernel<R>(), whole_threads<R>()};
     OMQ_PICK(1)
     OMQ_PICK(2)
     OMQ_PICK(3)
@@ -2350,18 +2184,14 @@ SelKernels pick_kernels(int rmax, bool split) {
     OMQ_PICK(8)
 #undef OMQ_PICK
   }
-  return k;
 }
 }  // namespace
 
-void select_set_options(int split_mode, int spin_limit) {
-  g_split_mode.store(split_mode, std::memory_order_relaxed);
+void select_set_options(int spin_limit) {
   g_spin_limit.store(spin_limit, std::memory_order_relaxed);
 }
 
-bool select_split_fits(int num_trees, int W) {
-  return num_trees <= kSplitMaxTrees && W >= 1;
-}
+int select_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
 size_t select_lds_bytes(int W) { return level_lds_bytes<1024>(W, true); }
 
@@ -2380,29 +2210,18 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   int rmax = (max_row + kWave - 1) / kWave;
   if (rmax < 1) rmax = 1;
   if (rmax > 6) rmax = 8;
-  // The schedule: one workgroup per tree unless the split schedule is asked for (it measured
-  // slower on every workload: a subtree task pays a few microseconds of barriers and dependent
-  // loads per level, and the largest subtree of a wave runs on one workgroup).
-  const int mode = g_split_mode.load(std::memory_order_relaxed);
-  const bool split = select_split_fits(f.num_trees, W) && mode == 2;
-  const SelKernels k = pick_kernels(rmax, split);
+  const SelKernel k = pick_kernel(rmax);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   const bool cache = dev >= 0 && dev < kMaxDevices;
   // the LDS limit is raised once per device and kernel (the attribute is idempotent, so two
   // threads racing here both set it)
-  const int slot = split ? 1 : 0;
-  if (!cache || !g_attr_set[dev][slot][rmax].load(std::memory_order_acquire)) {
-    e = hipFuncSetAttribute(k.root, hipFuncAttributeMaxDynamicSharedMemorySize,
+  if (!cache || !g_attr_set[dev][rmax].load(std::memory_order_acquire)) {
+    e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)level_lds_bytes<1024>(OMQ_MAX_WAVE, true));
     if (e != hipSuccess) return e;
-    if (split) {
-      e = hipFuncSetAttribute(k.sub, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)level_lds_bytes<kSubThreads>(OMQ_MAX_WAVE, false));
-      if (e != hipSuccess) return e;
-    }
-    if (cache) g_attr_set[dev][slot][rmax].store(true, std::memory_order_release);
+    if (cache) g_attr_set[dev][rmax].store(true, std::memory_order_release);
   }
   SelArgs a;
   a.N = f.visit_counts;
@@ -2429,40 +2248,10 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   const int64_t TM = (int64_t)f.num_trees * w.max_wave;
   a.lflag = w.sel_scratch;
   a.lfs = w.sel_scratch + TM;
-  a.tasks = w.sel_scratch + 2 * TM;
-  a.ntask = w.sel_scratch + 4 * TM;
-  a.tinfo = a.ntask + f.num_trees;
-  a.tcls = a.tinfo + f.num_trees;
-  a.ctl = a.tcls + (int64_t)f.num_trees * kTaskClasses;
   void* args[] = {&a, &c};
-  const size_t lds_root = k.root_threads == 1024  ? level_lds_bytes<1024>(W, true)
-                          : k.root_threads == 512 ? level_lds_bytes<512>(W, false)
-                                                  : level_lds_bytes<256>(W, false);
-  e = hipLaunchKernel(k.root, dim3(f.num_trees), dim3(k.root_threads), args, lds_root, stream);
-  if (e != hipSuccess) return e;
-  e = hipGetLastError();
-  if (e != hipSuccess || !split) return e;
-  // Subtree workgroups: as many as fit on the chip at once (at most 4 per CU: the chains'
-  // 128 registers per lane), and no more than the simulations could make tasks.
-  int cus = cache ? g_cu_count[dev].load(std::memory_order_relaxed) : 0;
-  if (cus <= 0) {
-    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return e;
-    if (cache) g_cu_count[dev].store(cus, std::memory_order_relaxed);
-  }
-  const size_t lds_sub = level_lds_bytes<kSubThreads>(W, false) + 8 * 1024;
-  int per_cu = (int)((160 * 1024) / lds_sub);
-  per_cu = per_cu < 1 ? 1 : (per_cu > 4 ? 4 : per_cu);
-  int64_t blocks = (int64_t)cus * per_cu;
-  if (blocks > TM) blocks = TM;
-  if (blocks < 1) blocks = 1;
-  e = hipLaunchKernel(k.sub, dim3((unsigned)blocks), dim3(kSubThreads), args,
-                      level_lds_bytes<kSubThreads>(W, false), stream);
-  if (e != hipSuccess) return e;
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  e = hipLaunchKernel((const void*)select_finish_kernel, dim3(f.num_trees), dim3(kFinishThreads),
-                      args, 0, stream);
+  const size_t lds = k.threads == 1024 ? level_lds_bytes<1024>(W, true)
+                                       : level_lds_bytes<512>(W, false);
+  e = hipLaunchKernel(k.fn, dim3(f.num_trees), dim3(k.threads), args, lds, stream);
   if (e != hipSuccess) return e;
   return hipGetLastError();
 }

@@ -71,32 +71,6 @@ def test_wave_parity(case, device):
     assert n >= 2
 
 
-# The split schedule of omq_select (root chains, then subtree tasks over the whole chip, then
-# the unique-leaf pass; omq_select_options split_mode 2) must give the same waves.
-SPLIT_CASES = ["C2-small", "C3-small", "C3-capacity", "C4-small", "overlap-ragged",
-               "overlap-depth2", "overlap-knobs", "uniform-priors-C2", "negative-cpuct"]
-
-
-@pytest.fixture
-def split_schedule():
-    from omoknuni_quantum_amd import _lib
-
-    lib = _lib.load()
-    _lib.check(lib.omq_select_options(2, _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
-    yield
-    _lib.check(lib.omq_select_options(0, _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
-
-
-@pytest.mark.gpu
-@pytest.mark.parametrize("case", SPLIT_CASES)
-def test_wave_parity_split_schedule(case, device, split_schedule):
-    name, kw = CASES[case]
-    wl = get(name).scaled(name=case + "-split", **kw)
-    print(f"[parity split] {case}: T={wl.num_trees} sims={wl.num_simulations} "
-          f"W={wl.wave_size}", flush=True)
-    assert run_parity(wl, check_every=1, device=device) >= 2
-
-
 @pytest.mark.gpu
 def test_follower_wait_running_out(device):
     """A follower whose bounded wait runs out (spin limit 0, set from the host) sets
@@ -116,11 +90,11 @@ def test_follower_wait_running_out(device):
     eng.run_wave(1, ev)
     eng.run_wave(wl.wave_size, ev)  # an expanded first level, so that the overlap runs
     try:
-        _lib.check(lib.omq_select_options(0, 0), "omq_select_options")
+        _lib.check(lib.omq_select_options(0), "omq_select_options")
         eng.select(wl.wave_size)
         torch.cuda.synchronize()
     finally:
-        _lib.check(lib.omq_select_options(0, _lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
+        _lib.check(lib.omq_select_options(_lib.OMQ_SPIN_LIMIT_DEFAULT), "omq_select_options")
     assert int(eng.status[0].item()) & _lib.OMQ_STATUS_STALL
     with pytest.raises(_lib.OmqError):
         eng.check_status()
