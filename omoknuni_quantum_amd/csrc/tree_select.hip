@@ -667,9 +667,23 @@ __device__ __noinline__ uint32_t top64_threshold_near(RowKeys<R> keys, int k, ui
 // PARTIAL: ranks [0, npre) were taken by the first-unvisited prefix (unvisited_prefix), whose
 // counts (0 or 1) are in cnt_s; the chain starts at rank npre.  Else npre is 0 and cnt_s is
 // cleared here.
+// What a chain reads of the forest and the configuration, passed by value: a chain the
+// compiler keeps out of line then takes them in registers (a reference to the kernel's SelArgs
+// would make every lane store a copy of the whole argument block in its private memory).
+struct ChainRows {
+  const int32_t* N;
+  const float* W;
+  const float* P;
+};
+struct ChainCfg {
+  float c_puct;
+  float vlf;
+  int vli;
+};
+
 template <int R, bool PERSIST, bool PARTIAL>
-__device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
-                         int npre, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
+__device__ int run_chain(ChainRows f, int64_t tb, int first, int k, int Np0, int m, int npre,
+                         ChainCfg c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
                          int* progress) {
   const int lane = lane_id();
   const float vlf = c.vlf;
@@ -912,15 +926,15 @@ __device__ int run_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0
 // child once: rank 0 among its picks) and every child's prefix count (0 or 1) to cnt_s[0, k),
 // which the chain starts from; returns npre.  (off: no virtual loss; nothing is taken.)
 template <int RMAX>
-__device__ __noinline__ int unvisited_prefix(const SelArgs& f, int64_t tb, int first, int k, int m,
-                                       bool on, uint32_t* ch, uint16_t* cnt_s) {
+__device__ __noinline__ int unvisited_prefix(const int32_t* N, int64_t tb, int first, int k, int m,
+                                             bool on, uint32_t* ch, uint16_t* cnt_s) {
   const int lane = lane_id();
   int n[RMAX];
 #pragma unroll
   for (int j = 0; j < RMAX; ++j) {
     const int i = j * kWave + lane;
     n[j] = 1;
-    if (on && i < k) n[j] = f.N[tb + first + 1 + i];
+    if (on && i < k) n[j] = N[tb + first + 1 + i];
   }
   int npre = 0;
 #pragma unroll
@@ -948,22 +962,24 @@ __device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, in
                                      int m, int npre, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s,
                                      float4* cscr, int* progress) {
   const int r = (k + kWave - 1) / kWave;  // 1 <= r <= RMAX (checked by the caller)
+  const ChainRows rows{f.N, f.W, f.P};
+  const ChainCfg cc{c.c_puct, c.vlf, c.vli};
   // contender windows kept open across blocks in the kernels of up to 4 slots per lane and in
   // the WIDE ones (the other wider kernels' chains have no registers left for it)
   constexpr bool kPersist = RMAX <= 4 || WIDE;
   if (RMAX <= 1 || r <= 1)
-    return run_chain<1, kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
+    return run_chain<1, kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
   if (RMAX >= 2 && r == 2)
-    return run_chain<(RMAX >= 2 ? 2 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 2 ? 2 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
   if (RMAX >= 3 && r == 3)
-    return run_chain<(RMAX >= 3 ? 3 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 3 ? 3 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
   if (RMAX >= 4 && r == 4)
-    return run_chain<(RMAX >= 4 ? 4 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 4 ? 4 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
   if (RMAX >= 5 && r == 5)
-    return run_chain<(RMAX >= 5 ? 5 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 5 ? 5 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
   if (RMAX >= 6 && r == 6)
-    return run_chain<(RMAX >= 6 ? 6 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
-  return run_chain<(RMAX >= 8 ? 8 : 1), kPersist, WIDE>(f, tb, first, k, Np0, m, npre, c, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 6 ? 6 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
+  return run_chain<(RMAX >= 8 ? 8 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
 }
 
 // A group's chain: the first-unvisited prefix, and the chain when the prefix does not take
@@ -975,7 +991,7 @@ template <int RMAX, bool WIDE>
 __device__ inline int group_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
                                   const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
                                   int* progress, bool* all_prefix) {
-  const int npre = unvisited_prefix<RMAX>(f, tb, first, k, m, c.vli > 0, ch, cnt_s);
+  const int npre = unvisited_prefix<RMAX>(f.N, tb, first, k, m, c.vli > 0, ch, cnt_s);
   *all_prefix = npre >= m;
   if (npre >= m) {
     if (progress != nullptr) {
