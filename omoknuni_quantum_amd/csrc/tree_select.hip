@@ -812,6 +812,27 @@ __device__ int run_chain(ChainRows f, int64_t tb, int first, int k, int Np0, int
     // up to and including it (the picked lane's count after the pick: its rank plus one)
     uint32_t rec = kNoChild;
     uint32_t rnk = 0;
+    // Window steps from rank rr of the block on.  A step is the window's while its maximum
+    // key exceeds every non-contender's raised key at that step; those keys only grow with s,
+    // so a bound taken at a later rank holds for every rank before it.  The bound is taken
+    // at the end of a segment of ranks and renewed for the next segment while the window
+    // holds.  Where the block raises the parent count by 1/16 or more (s grows 3 % or more
+    // over it), a bound at the block's end ends windows early, so the segments are 32 ranks
+    // there; elsewhere one bound per block costs less (C2 select 68.0 -> 62.4 us, C3
+    // 232.5 -> 225.3 us, against 64-rank segments everywhere; 16- and 8-rank segments
+    // measured slower).
+    const int npb = Np0 + c.vli * r0;  // the parent count at the block's first rank
+    const int seg = npb >= 16 * kWave * c.vli ? kWave : kWave / 2;
+    auto window_steps = [&](int rr) {
+      while (rr < rend) {
+        const int se = __builtin_amdgcn_readfirstlane(min(rend, rr + seg));
+        const uint32_t ubk = noncon_bound(readlane_f(svec, se - 1));
+        rr = lane_steps<true>(y, svec, rr, se, fvl, vlf, qb, ubk, kKeyInf, ncon, r0,
+                              &first_end, &rec, &rnk);
+        if (rr < se) break;
+      }
+      return rr;
+    };
     if (R == 1) {
       lane_steps<false>(y, svec, rs, rend, fvl, vlf, qb, kKeyFloor, exact_only ? 0u : kKeyInf,
                         k, r0, &first_end, &rec, &rnk);
@@ -819,10 +840,8 @@ __device__ int run_chain(ChainRows f, int64_t tb, int first, int k, int Np0, int
       int rr = rs;
       bool try_window = !exact_only;
       if (PERSIST && wopen) {
-        // ---- the open window continues, with its bound for this block's last rank ----
-        const uint32_t ubk = noncon_bound(readlane_f(svec, rend - 1));
-        rr = lane_steps<true>(y, svec, 0, rend, fvl, vlf, qb, ubk, kKeyInf, ncon, r0,
-                              &first_end, &rec, &rnk);
+        // ---- the open window continues ----
+        rr = window_steps(0);
         const int ci = __shfl(cidx, (int)(rec & 63u), 64);
         if (lane < rr) rec = (uint32_t)ci;
         if (rr < rend) close_window();  // (a fresh window may follow in this block)
@@ -854,7 +873,6 @@ __device__ int run_chain(ChainRows f, int64_t tb, int first, int k, int Np0, int
             conbits |= con ? (1u << j) : 0u;
             base += __popcll(cm);
           }
-          const uint32_t ubk = noncon_bound(readlane_f(svec, rend - 1));
           ncon = base;
           wave_sync();
           const float4 e = lane < ncon ? cscr[lane] : make_float4(2.0f, 0.0f, 0.0f, 0.0f);
@@ -874,8 +892,7 @@ __device__ int run_chain(ChainRows f, int64_t tb, int first, int k, int Np0, int
           const int rr0 = rr;
           // window steps record the picked lane; the lanes become child indices below.  A
           // window step always picks (no candidate or an unsafe threshold aborts it first).
-          rr = lane_steps<true>(y, svec, rr, rend, fvl, vlf, qb, ubk, kKeyInf, ncon, r0,
-                                &first_end, &rec, &rnk);
+          rr = window_steps(rr);
           {
             const int ci = __shfl(cidx, (int)(rec & 63u), 64);
             if (lane >= rr0 && lane < rr) rec = (uint32_t)ci;
