@@ -150,6 +150,23 @@ __device__ inline uint32_t wave_max_u32(uint32_t x) {
 // from +0, the elements whose index is congruent to l mod 64; the 64 partial sums are then
 // combined by the xor butterfly with distances 32,16,8,4,2,1.  Every lane ends with the same
 // value.  (The host restatement of this order must match it exactly.)
+// Workgroups are dispatched to the chip's XCDs round-robin in linear order (workgroup i to XCD
+// i mod kXcds, as its (i / kXcds)-th).  xcd_block gives each XCD one contiguous run of the
+// grid's blocks instead: block i takes logical block start(i mod kXcds) + i / kXcds, where XCD x
+// owns blocks [start(x), start(x) + q + (x < r)) of nblk = 8q + r.  A bijection on the grid;
+// (bx, by) become the logical block's coordinates.
+constexpr int kXcds = 8;
+__device__ inline void xcd_block(int* bx, int* by) {
+  const int X = (int)gridDim.x;
+  const int nblk = X * (int)gridDim.y;
+  const int lin = (int)blockIdx.y * X + (int)blockIdx.x;
+  const int q = nblk / kXcds, r = nblk % kXcds;
+  const int x = lin % kXcds;
+  const int logical = x * q + min(x, r) + lin / kXcds;
+  *bx = logical % X;
+  *by = logical / X;
+}
+
 __device__ inline float wave_sum_canonical(float partial) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) partial = partial + __shfl_xor(partial, off, 64);

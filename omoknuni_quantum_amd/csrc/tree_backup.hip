@@ -20,8 +20,10 @@ constexpr int kBigChunk = 8;  // member values per lane held per chunk of a big 
 // signed value per simulation: v(leaf), negated when the leaf depth is odd in leaf-positive
 // mode, so that the contribution at depth d is (d odd ? -sv : sv)
 __global__ void sim_value_kernel(omq_forest f, omq_wave w, int W, int sign_mode) {
-  const int t = blockIdx.y;
-  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  int bx = blockIdx.x, by = blockIdx.y;
+  xcd_block(&bx, &by);  // one contiguous run of blocks (leaves of few trees) per XCD
+  const int t = by;
+  const int s = bx * blockDim.x + threadIdx.x;
   if (s >= W) return;
   const int64_t wb = (int64_t)t * w.max_wave;
   const float v = w.values[wb + w.sim_uid[wb + s]];
@@ -46,7 +48,9 @@ constexpr int kFuseMaxWave = 512;
 template <bool FUSED>
 __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_forest f, omq_wave w,
                                                                        int vli, int sign_mode) {
-  const int t = blockIdx.y;
+  int bx = blockIdx.x, by = blockIdx.y;
+  xcd_block(&bx, &by);  // one contiguous run of blocks (leaves of few trees) per XCD
+  const int t = by;
   const int lane = lane_id();
   const int wib = threadIdx.x / kWave;
   const int64_t tb = (int64_t)t * f.capacity;
@@ -55,7 +59,7 @@ __global__ __launch_bounds__(kBackupThreads) void backup_groups_kernel(omq_fores
   const int64_t gmax = (int64_t)MW * MD;
   const int G = w.gcount[t];
   const int waves_total = gridDim.x * (kBackupThreads / kWave);
-  const int wave_global = blockIdx.x * (kBackupThreads / kWave) + wib;
+  const int wave_global = bx * (kBackupThreads / kWave) + wib;
   const int32_t* uid = w.sim_uid + wb;
   const int32_t* plen = w.path_len + wb;
   const float* uval = w.values + wb;

@@ -73,8 +73,10 @@ constexpr int kLeafInfoThreads = 256;
 
 __global__ __launch_bounds__(kLeafInfoThreads) void leaf_info_kernel(omq_forest f, omq_wave w) {
   __shared__ int s_part[kLeafInfoThreads / kWave];
-  const int t = blockIdx.y;
-  const int u = blockIdx.x * kLeafInfoThreads + threadIdx.x;
+  int bx = blockIdx.x, by = blockIdx.y;
+  xcd_block(&bx, &by);  // one contiguous run of blocks (leaves of few trees) per XCD
+  const int t = by;
+  const int u = bx * kLeafInfoThreads + threadIdx.x;
   const int64_t wb = (int64_t)t * w.max_wave;
   const int64_t tb = (int64_t)t * f.capacity;
   const int nu = w.ucount[t];
@@ -346,9 +348,11 @@ __global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f,
 // ---------------------------------------------------------------------------------------
 __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int t = blockIdx.y;
+  int bx = blockIdx.x, by = blockIdx.y;
+  xcd_block(&bx, &by);  // one contiguous run of blocks (leaves of few trees) per XCD
+  const int t = by;
   const int wave = threadIdx.x / kWave;
-  const int u = blockIdx.x * (blockDim.x / kWave) + wave;
+  const int u = bx * (blockDim.x / kWave) + wave;
   const int lane = lane_id();
   const int64_t tb = (int64_t)t * f.capacity;
   const int64_t wb = (int64_t)t * w.max_wave;
