@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define OMQ_ABI_VERSION 3
+#define OMQ_ABI_VERSION 4
 
 /* error codes */
 #define OMQ_OK 0
@@ -529,6 +529,109 @@ int omq_batched_add_children(const int32_t* parent_indices, int32_t batch,
                              float* value_sums_out, int32_t* col_indices, int32_t* edge_actions,
                              float* edge_priors, int32_t max_nodes, int32_t max_children,
                              int32_t max_edges, int32_t* child_indices, void* stream);
+
+/* ---- more of the reference pybind module's operators (mcts_kernels.cu:2342-2410) ---------- */
+
+/* Per-simulation selection over a parent's row of the dense children table with virtual-loss
+ * counts (parallel_select_with_virtual_loss_enhanced_cuda, python/mcts/gpu/mcts_kernels.cu:
+ * 1936-2000, kernel :962-1053; bound at :2371-2384, probed by
+ * python/mcts/gpu/wave_search.py:1193).  Simulation s scores the children of
+ * p = parent_nodes[s] at table positions [0, max_children) of row p (stride children_stride),
+ * skipping entries < 0 or >= num_nodes: n = N[c] + VL[c], value = W[c] + VL[c] * vl (float),
+ * Q = value / n for n > 0 else 0, ucb = Q + c_puct * P * sqrt(N[p] + 1) / (1 + n), with
+ * P = priors[c], or priors[s * priors_stride + c] when priors_stride > 0 (per-simulation
+ * priors; children >= priors_stride skipped).  With legal_masks ([num_sims,
+ * action_space_size] bytes; NULL: none), a child of a parent other than node 0 whose action
+ * child_actions[c] is in [0, action_space_size) and illegal for s is skipped.  The child of
+ * the first maximum above -inf (strict '>') is written to selected_children[s], else -1 (also
+ * for p < 0 or p outside the rows or arrays).  Then virtual_loss_counts[c] += 1 for every
+ * selection (after all of them).  The reference's dirichlet_noise / dirichlet_epsilon
+ * arguments are ignored by it (priors come pre-mixed) and are not taken here. */
+int omq_parallel_select_with_virtual_loss(
+    const int32_t* parent_nodes, int32_t num_sims, const int32_t* children, int32_t num_rows,
+    int32_t max_children, int32_t children_stride, const int32_t* visit_counts,
+    int32_t* virtual_loss_counts, const float* value_sums, int32_t num_nodes,
+    const float* priors, int32_t priors_stride, const uint8_t* legal_masks,
+    int32_t action_space_size, const int32_t* child_actions, float c_puct,
+    float virtual_loss_value, int32_t* selected_children, void* stream);
+
+/* Root selection with per-simulation Dirichlet-mixed priors (fused_ucb_with_noise_cuda,
+ * python/mcts/gpu/mcts_kernels.cu:1791-1823, kernel :760-797; MCTSGPUAccelerator.
+ * fused_ucb_with_noise, python/mcts/gpu/mcts_gpu_accelerator.py:326-327): for simulation s,
+ * P' = (1 - eps) P[c] + eps * noise[s, c] and ucb = q[c] + c_puct * P' * parent_visits_sqrt /
+ * (1 + N[c]); selected[s] = the position of the first maximum above -1e10, or 0. */
+int omq_fused_ucb_with_noise(const float* q_values, const int32_t* visit_counts,
+                             const float* priors, int32_t num_children,
+                             const float* dirichlet_noise, int32_t num_sims,
+                             float parent_visits_sqrt, float c_puct, float epsilon,
+                             int32_t* selected, void* stream);
+
+/* UCB selection over dense per-item slots (batched_ucb_selection_dense_cuda,
+ * python/mcts/gpu/mcts_kernels.cu:1563-1598, kernel :1364-1409): item b's slots with
+ * valid_mask set and child c in [0, num_valid_children) score
+ * (N[c] > 0 ? V[c] : 0) + c_puct * P[b, slot] * sqrt(pv[b] + 1) / (1 + N[c]); selected[b] = the
+ * child of the first maximum above -1e10, or -1. */
+int omq_batched_ucb_selection_dense(const int32_t* batch_children, const float* batch_priors,
+                                    const int32_t* parent_visits, const uint8_t* valid_mask,
+                                    int32_t batch, int32_t max_children,
+                                    const int32_t* child_visits, const float* child_values,
+                                    int32_t num_valid_children, float c_puct,
+                                    int32_t* selected, void* stream);
+
+/* Rows of Dirichlet(alpha) noise (batched_dirichlet_noise_cuda, python/mcts/gpu/
+ * mcts_kernels.cu:1735-1790, kernels :649-754; MCTSGPUAccelerator.batched_dirichlet_noise,
+ * mcts_gpu_accelerator.py:323-324): noise[s, a] = g[s, a] / sum_a g[s, a] with
+ * g ~ Gamma(alpha, 1), 0 for a row whose sum is 0.  The draws come from the counter-based
+ * stream of omq_root_dirichlet keyed by (seed, counter, row, entry) in place of the
+ * reference's time-seeded cuRAND states; the gammas and the row sum are float64, each quotient
+ * is rounded to float32 once. */
+int omq_batched_dirichlet_noise(int32_t num_sims, int32_t num_actions, double alpha,
+                                uint64_t seed, uint64_t counter, float* noise, void* stream);
+
+/* optimized_backup_scatter_cuda (python/mcts/gpu/mcts_kernels.cu:1825-1870;
+ * MCTSGPUAccelerator.optimized_backup_scatter, mcts_gpu_accelerator.py:329-330): the reference
+ * prepares per-entry updates it never reads and then runs vectorized_backup_kernel, so this is
+ * omq_paths_backup with the leaf-positive sign over plain arrays of num_nodes counts. */
+int omq_optimized_backup_scatter(const int32_t* paths, const int32_t* path_lengths,
+                                 const float* values, int32_t batch, int32_t max_depth,
+                                 int32_t* visit_counts, float* value_sums, int32_t num_nodes,
+                                 void* stream);
+
+/* int32 workspace entries of omq_parallel_bfs_subtree and omq_extract_subtree_edges */
+#define OMQ_BFS_WORKSPACE_INTS(max_nodes) (3 * (int64_t)(max_nodes) + 1)
+#define OMQ_EDGES_WORKSPACE_INTS(num_nodes) \
+  ((int64_t)(num_nodes) + ((int64_t)(num_nodes) + 1023) / 1024 + 1)
+
+/* Breadth-first subtree of root_idx in a CSR graph (parallel_bfs_subtree_cuda,
+ * python/mcts/gpu/mcts_kernels.cu:2246-2287, kernel :2095-2194; bound at :2396-2401; called
+ * from python/mcts/gpu/gpu_bfs.py:49).  row_ptr holds max_nodes + 1 offsets into
+ * col_indices [num_edges] (rows clamped to it).  Writes in_subtree [max_nodes] (0/1),
+ * node_remap [max_nodes] (the new index, -1 outside) and *subtree_count.  New indices follow
+ * a FIFO breadth-first walk: levels in order, each node's children in row order, a child at
+ * its first occurrence (the order of the reference's fallback, gpu_bfs.py:70-127); children
+ * outside [0, max_nodes) are skipped.  *subtree_count = -1 when a level's rows add up past
+ * 2^31 - 1 (overlapping rows).  One workgroup; workspace: OMQ_BFS_WORKSPACE_INTS(max_nodes)
+ * int32 owned by the caller. */
+int omq_parallel_bfs_subtree(const int32_t* row_ptr, const int32_t* col_indices,
+                             int32_t num_edges, int32_t root_idx, int32_t max_nodes,
+                             uint8_t* in_subtree, int32_t* node_remap, int32_t* subtree_count,
+                             int32_t* workspace, int64_t workspace_ints, void* stream);
+
+/* The edges of a subtree found by omq_parallel_bfs_subtree (extract_subtree_edges_cuda,
+ * python/mcts/gpu/mcts_kernels.cu:2289-2337, kernel :2201-2244; bound at :2402-2408; called
+ * from python/mcts/gpu/gpu_bfs.py:149).  For every node i < num_nodes with in_subtree[i], in
+ * ascending i, the edges e of its row (in row order) whose child c is in [0, num_nodes) and in
+ * the subtree give (node_remap[i], node_remap[c], edge_actions[e] or 0 when edge_actions is
+ * NULL), written in that order up to max_edges entries; *edge_count = the number of such edges
+ * (it can exceed max_edges: the caller checks).  Workspace:
+ * OMQ_EDGES_WORKSPACE_INTS(num_nodes) int32 owned by the caller. */
+int omq_extract_subtree_edges(const int32_t* row_ptr, const int32_t* col_indices,
+                              const int16_t* edge_actions, int32_t num_edges,
+                              const uint8_t* in_subtree, const int32_t* node_remap,
+                              int32_t num_nodes, int32_t max_edges, int32_t* edge_parents,
+                              int32_t* edge_children, int16_t* edge_actions_out,
+                              int32_t* edge_count, int32_t* workspace, int64_t workspace_ints,
+                              void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libomq_tree_ops.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # constants of include/omq_tree_ops.h
 OMQ_OK, OMQ_E_ARG, OMQ_E_LAUNCH, OMQ_E_LIMIT = 0, -1, -2, -3
@@ -106,7 +106,32 @@ SIGNATURES = {
                                           ctypes.c_uint64, _p, _p]),
     "omq_root_dirichlet": (ctypes.c_int, [_FP, ctypes.c_double, ctypes.c_uint64,
                                           ctypes.c_uint64, _p, _p]),
+    "omq_parallel_select_with_virtual_loss": (ctypes.c_int, [_p, _i32, _p, _i32, _i32, _i32, _p,
+                                                             _p, _p, _i32, _p, _i32, _p, _i32, _p,
+                                                             ctypes.c_float, ctypes.c_float, _p,
+                                                             _p]),
+    "omq_fused_ucb_with_noise": (ctypes.c_int, [_p, _p, _p, _i32, _p, _i32, ctypes.c_float,
+                                                ctypes.c_float, ctypes.c_float, _p, _p]),
+    "omq_batched_ucb_selection_dense": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p, _i32,
+                                                       ctypes.c_float, _p, _p]),
+    "omq_batched_dirichlet_noise": (ctypes.c_int, [_i32, _i32, ctypes.c_double, ctypes.c_uint64,
+                                                   ctypes.c_uint64, _p, _p]),
+    "omq_optimized_backup_scatter": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _p, _p, _i32, _p]),
+    "omq_parallel_bfs_subtree": (ctypes.c_int, [_p, _p, _i32, _i32, _i32, _p, _p, _p, _p,
+                                                ctypes.c_int64, _p]),
+    "omq_extract_subtree_edges": (ctypes.c_int, [_p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p,
+                                                 _p, _p, _p, ctypes.c_int64, _p]),
 }
+
+
+def bfs_workspace_ints(max_nodes: int) -> int:
+    """OMQ_BFS_WORKSPACE_INTS of include/omq_tree_ops.h."""
+    return 3 * max_nodes + 1
+
+
+def edges_workspace_ints(num_nodes: int) -> int:
+    """OMQ_EDGES_WORKSPACE_INTS of include/omq_tree_ops.h."""
+    return num_nodes + (num_nodes + 1023) // 1024 + 1
 
 
 class LibraryNotBuilt(RuntimeError):

@@ -73,6 +73,33 @@ hipError_t launch_fused_select_expand_opt(const int32_t* roots, int num_paths,
                                           int max_depth, float c_puct, float* ucb_scores,
                                           int32_t* paths, int32_t* path_lengths,
                                           hipStream_t st);
+hipError_t launch_parallel_select_vl(const int32_t* parent_nodes, int num_sims,
+                                     const int32_t* children, int num_rows, int max_children,
+                                     int children_stride, const int32_t* visit_counts,
+                                     const int32_t* vl_counts, const float* value_sums,
+                                     int num_nodes, const float* priors, int priors_stride,
+                                     const uint8_t* legal_masks, int action_space,
+                                     const int32_t* child_actions, float c_puct, float vl_value,
+                                     int32_t* selected, hipStream_t st);
+hipError_t launch_fused_ucb_noise(const float* q_values, const int32_t* visit_counts,
+                                  const float* priors, int num_children, const float* noise,
+                                  int num_sims, float parent_visits_sqrt, float c_puct,
+                                  float epsilon, int32_t* selected, hipStream_t st);
+hipError_t launch_batched_ucb_dense(const int32_t* batch_children, const float* batch_priors,
+                                    const int32_t* parent_visits, const uint8_t* valid_mask,
+                                    int batch, int max_children, const int32_t* child_visits,
+                                    const float* child_values, int num_valid, float c_puct,
+                                    int32_t* selected, hipStream_t st);
+hipError_t launch_batched_dirichlet(int num_sims, int num_actions, double alpha, uint64_t seed,
+                                    uint64_t counter, float* noise, hipStream_t st);
+hipError_t launch_bfs_subtree(const int32_t* row_ptr, const int32_t* col, int num_edges,
+                              int root, int max_nodes, uint8_t* in_subtree, int32_t* remap,
+                              int32_t* count, int32_t* ws, hipStream_t st);
+hipError_t launch_extract_edges(const int32_t* row_ptr, const int32_t* col, const int16_t* actions,
+                                int num_edges, const uint8_t* in_subtree, const int32_t* remap,
+                                int num_nodes, int max_edges, int32_t* out_parent,
+                                int32_t* out_child, int16_t* out_action, int32_t* edge_count,
+                                int32_t* ws, hipStream_t st);
 hipError_t launch_batched_add_children(
     const int32_t* parent_indices, int batch, const int32_t* actions, const float* priors,
     const int32_t* num_children, int32_t* node_counter, int32_t* edge_counter,
@@ -549,3 +576,167 @@ int omq_batched_add_children(const int32_t* parent_indices, int32_t batch,
 }
 
 }  // extern "C"
+
+int omq_parallel_select_with_virtual_loss(
+    const int32_t* parent_nodes, int32_t num_sims, const int32_t* children, int32_t num_rows,
+    int32_t max_children, int32_t children_stride, const int32_t* visit_counts,
+    int32_t* virtual_loss_counts, const float* value_sums, int32_t num_nodes,
+    const float* priors, int32_t priors_stride, const uint8_t* legal_masks,
+    int32_t action_space_size, const int32_t* child_actions, float c_puct,
+    float virtual_loss_value, int32_t* selected_children, void* stream) {
+  const char* who = "omq_parallel_select_with_virtual_loss";
+  if (num_sims < 0 || num_rows < 0 || max_children < 0 || num_nodes < 0 || priors_stride < 0 ||
+      action_space_size < 0 || children_stride < max_children)
+    return fail(OMQ_E_ARG, "%s: num_sims %d, num_rows %d, max_children %d, num_nodes %d, "
+                "priors_stride %d, action_space_size %d must not be negative and "
+                "children_stride %d >= max_children", who, num_sims, num_rows, max_children,
+                num_nodes, priors_stride, action_space_size, children_stride);
+  if (num_sims == 0) return OMQ_OK;
+  if (!parent_nodes || !selected_children ||
+      (num_nodes > 0 && (!visit_counts || !virtual_loss_counts || !value_sums || !priors)) ||
+      (num_rows > 0 && max_children > 0 && !children) ||
+      (legal_masks && (!child_actions || action_space_size == 0)))
+    return fail(OMQ_E_ARG, "%s: a null array", who);
+  hipStream_t st = (hipStream_t)stream;
+  int rc = hip_status(omq::launch_parallel_select_vl(parent_nodes, num_sims, children, num_rows,
+                                                     max_children, children_stride,
+                                                     visit_counts, virtual_loss_counts,
+                                                     value_sums, num_nodes, priors,
+                                                     priors_stride, legal_masks,
+                                                     action_space_size, child_actions, c_puct,
+                                                     virtual_loss_value, selected_children, st),
+                      who);
+  if (rc || num_nodes == 0) return rc;
+  // the virtual loss of every selection, after all of them (selected ids outside the counts,
+  // -1 included, are skipped)
+  omq_forest vf{};
+  vf.num_trees = 1;
+  vf.capacity = num_nodes;
+  vf.visit_counts = virtual_loss_counts;
+  return hip_status(omq::launch_virtual_loss(vf, selected_children, nullptr, num_sims, 1, st),
+                    who);
+}
+
+int omq_fused_ucb_with_noise(const float* q_values, const int32_t* visit_counts,
+                             const float* priors, int32_t num_children,
+                             const float* dirichlet_noise, int32_t num_sims,
+                             float parent_visits_sqrt, float c_puct, float epsilon,
+                             int32_t* selected, void* stream) {
+  if (num_sims < 0 || num_children < 0)
+    return fail(OMQ_E_ARG, "omq_fused_ucb_with_noise: num_sims %d, num_children %d < 0",
+                num_sims, num_children);
+  if (num_sims == 0) return OMQ_OK;
+  if (!selected || (num_children > 0 && (!q_values || !visit_counts || !priors ||
+                                         !dirichlet_noise)))
+    return fail(OMQ_E_ARG, "omq_fused_ucb_with_noise: a null array");
+  return hip_status(omq::launch_fused_ucb_noise(q_values, visit_counts, priors, num_children,
+                                                dirichlet_noise, num_sims, parent_visits_sqrt,
+                                                c_puct, epsilon, selected, (hipStream_t)stream),
+                    "omq_fused_ucb_with_noise");
+}
+
+int omq_batched_ucb_selection_dense(const int32_t* batch_children, const float* batch_priors,
+                                    const int32_t* parent_visits, const uint8_t* valid_mask,
+                                    int32_t batch, int32_t max_children,
+                                    const int32_t* child_visits, const float* child_values,
+                                    int32_t num_valid_children, float c_puct,
+                                    int32_t* selected, void* stream) {
+  if (batch < 0 || max_children < 0 || num_valid_children < 0)
+    return fail(OMQ_E_ARG, "omq_batched_ucb_selection_dense: batch %d, max_children %d, "
+                "num_valid_children %d < 0", batch, max_children, num_valid_children);
+  if (batch == 0) return OMQ_OK;
+  if (!parent_visits || !selected ||
+      (max_children > 0 && (!batch_children || !batch_priors || !valid_mask)) ||
+      (num_valid_children > 0 && (!child_visits || !child_values)))
+    return fail(OMQ_E_ARG, "omq_batched_ucb_selection_dense: a null array");
+  return hip_status(omq::launch_batched_ucb_dense(batch_children, batch_priors, parent_visits,
+                                                  valid_mask, batch, max_children, child_visits,
+                                                  child_values, num_valid_children, c_puct,
+                                                  selected, (hipStream_t)stream),
+                    "omq_batched_ucb_selection_dense");
+}
+
+int omq_batched_dirichlet_noise(int32_t num_sims, int32_t num_actions, double alpha,
+                                uint64_t seed, uint64_t counter, float* noise, void* stream) {
+  if (num_sims < 0 || num_actions < 0)
+    return fail(OMQ_E_ARG, "omq_batched_dirichlet_noise: num_sims %d, num_actions %d < 0",
+                num_sims, num_actions);
+  if (!(alpha > 0.0) || !(alpha < 1e300))
+    return fail(OMQ_E_ARG, "omq_batched_dirichlet_noise: alpha %g must be positive and finite",
+                alpha);
+  if ((int64_t)num_sims * num_actions == 0) return OMQ_OK;
+  if (!noise) return fail(OMQ_E_ARG, "omq_batched_dirichlet_noise: null output");
+  return hip_status(omq::launch_batched_dirichlet(num_sims, num_actions, alpha, seed, counter,
+                                                  noise, (hipStream_t)stream),
+                    "omq_batched_dirichlet_noise");
+}
+
+int omq_optimized_backup_scatter(const int32_t* paths, const int32_t* path_lengths,
+                                 const float* values, int32_t batch, int32_t max_depth,
+                                 int32_t* visit_counts, float* value_sums, int32_t num_nodes,
+                                 void* stream) {
+  if (batch < 0 || max_depth <= 0 || num_nodes < 0)
+    return fail(OMQ_E_ARG, "omq_optimized_backup_scatter: batch %d, num_nodes %d >= 0 and "
+                "max_depth %d >= 1", batch, num_nodes, max_depth);
+  if (batch == 0 || num_nodes == 0) return OMQ_OK;
+  if (!paths || !path_lengths || !values || !visit_counts || !value_sums)
+    return fail(OMQ_E_ARG, "omq_optimized_backup_scatter: a null array");
+  omq_forest vf{};
+  vf.num_trees = 1;
+  vf.capacity = num_nodes;
+  vf.visit_counts = visit_counts;
+  vf.value_sums = value_sums;
+  return hip_status(omq::launch_paths_backup(vf, paths, path_lengths, nullptr, values, batch,
+                                             max_depth, OMQ_SIGN_LEAF_POSITIVE,
+                                             (hipStream_t)stream),
+                    "omq_optimized_backup_scatter");
+}
+
+int omq_parallel_bfs_subtree(const int32_t* row_ptr, const int32_t* col_indices,
+                             int32_t num_edges, int32_t root_idx, int32_t max_nodes,
+                             uint8_t* in_subtree, int32_t* node_remap, int32_t* subtree_count,
+                             int32_t* workspace, int64_t workspace_ints, void* stream) {
+  const char* who = "omq_parallel_bfs_subtree";
+  if (max_nodes <= 0 || num_edges < 0)
+    return fail(OMQ_E_ARG, "%s: max_nodes %d must be positive and num_edges %d >= 0", who,
+                max_nodes, num_edges);
+  if (root_idx < 0 || root_idx >= max_nodes)
+    return fail(OMQ_E_ARG, "%s: root_idx %d outside [0, %d)", who, root_idx, max_nodes);
+  if (!row_ptr || !in_subtree || !node_remap || !subtree_count || !workspace ||
+      (num_edges > 0 && !col_indices))
+    return fail(OMQ_E_ARG, "%s: a null array", who);
+  const int64_t need = OMQ_BFS_WORKSPACE_INTS((int64_t)max_nodes);
+  if (workspace_ints < need)
+    return fail(OMQ_E_ARG, "%s: workspace holds %lld int32, it needs %lld", who,
+                (long long)workspace_ints, (long long)need);
+  return hip_status(omq::launch_bfs_subtree(row_ptr, col_indices, num_edges, root_idx, max_nodes,
+                                            in_subtree, node_remap, subtree_count, workspace,
+                                            (hipStream_t)stream),
+                    who);
+}
+
+int omq_extract_subtree_edges(const int32_t* row_ptr, const int32_t* col_indices,
+                              const int16_t* edge_actions, int32_t num_edges,
+                              const uint8_t* in_subtree, const int32_t* node_remap,
+                              int32_t num_nodes, int32_t max_edges, int32_t* edge_parents,
+                              int32_t* edge_children, int16_t* edge_actions_out,
+                              int32_t* edge_count, int32_t* workspace, int64_t workspace_ints,
+                              void* stream) {
+  const char* who = "omq_extract_subtree_edges";
+  if (num_nodes < 0 || num_edges < 0 || max_edges < 0)
+    return fail(OMQ_E_ARG, "%s: num_nodes %d, num_edges %d, max_edges %d < 0", who, num_nodes,
+                num_edges, max_edges);
+  if (!edge_count || !workspace || (num_nodes > 0 && (!row_ptr || !in_subtree || !node_remap)) ||
+      (num_edges > 0 && !col_indices) ||
+      (max_edges > 0 && (!edge_parents || !edge_children || !edge_actions_out)))
+    return fail(OMQ_E_ARG, "%s: a null array", who);
+  const int64_t need = OMQ_EDGES_WORKSPACE_INTS((int64_t)num_nodes);
+  if (workspace_ints < need)
+    return fail(OMQ_E_ARG, "%s: workspace holds %lld int32, it needs %lld", who,
+                (long long)workspace_ints, (long long)need);
+  return hip_status(omq::launch_extract_edges(row_ptr, col_indices, edge_actions, num_edges,
+                                              in_subtree, node_remap, num_nodes, max_edges,
+                                              edge_parents, edge_children, edge_actions_out,
+                                              edge_count, workspace, (hipStream_t)stream),
+                    who);
+}

@@ -439,6 +439,133 @@ __global__ void add_children_write_kernel(
 
 inline int row_blocks(int items) { return (items + kRowWaves - 1) / kRowWaves; }
 
+// ---- parallel_select_with_virtual_loss -------------------------------------------------------
+// One wave per simulation over its parent's row of the dense table (every position up to
+// max_children; negative entries and entries past the node arrays are skipped, the row does
+// not end at them).  Effective visits n = N + VLc and value W + VLc * vl (float), Q = W / n
+// for n > 0, else 0; the parent's sqrt(N + 1) takes no virtual loss; with the legal filter,
+// a non-root parent's child whose action is illegal for the simulation is skipped.  The first
+// maximum above -inf (strict '>', lowest position on ties) gives the child, else -1.
+__global__ void parallel_select_vl_kernel(const int32_t* parent_nodes, int num_sims,
+                                          const int32_t* children, int num_rows,
+                                          int max_children, int children_stride,
+                                          const int32_t* visit_counts, const int32_t* vl_counts,
+                                          const float* value_sums, int num_nodes,
+                                          const float* priors, int priors_stride,
+                                          const uint8_t* legal_masks, int action_space,
+                                          const int32_t* child_actions, float c_puct,
+                                          float vl_value, int32_t* selected) {
+  const int s = blockIdx.x * kRowWaves + (int)threadIdx.x / kWave;
+  if (s >= num_sims) return;
+  const int lane = lane_id();
+  const int p = parent_nodes[s];
+  if (p < 0 || p >= num_rows || p >= num_nodes) {
+    if (lane == 0) selected[s] = -1;
+    return;
+  }
+  const float sqrt_parent = sqrtf((float)(visit_counts[p] + 1));
+  const bool filter = legal_masks != nullptr && p != 0;
+  const uint8_t* legal = filter ? legal_masks + (int64_t)s * action_space : nullptr;
+  const int32_t* row = children + (int64_t)p * children_stride;
+  float best = -INFINITY;
+  int best_pos = 0x7FFFFFFF, best_child = -1;
+  for (int i = lane; i < max_children; i += kWave) {
+    const int c = row[i];
+    if (c < 0 || c >= num_nodes) continue;
+    if (filter) {
+      const int a = child_actions[c];
+      if (a >= 0 && a < action_space && !legal[a]) continue;
+    }
+    float prior;
+    if (priors_stride > 0) {  // per-simulation priors [num_sims, priors_stride]
+      if (c >= priors_stride) continue;
+      prior = priors[(int64_t)s * priors_stride + c];
+    } else {
+      prior = priors[c];
+    }
+    const int vc = vl_counts[c];
+    const int n = visit_counts[c] + vc;
+    const float w = value_sums[c] + (float)vc * vl_value;
+    const float q = n > 0 ? w / (float)n : 0.0f;
+    const float ucb = q + c_puct * prior * sqrt_parent / (1.0f + (float)n);
+    if (ucb > best) {
+      best = ucb;
+      best_pos = i;
+      best_child = c;
+    }
+  }
+  const uint32_t key = best_pos != 0x7FFFFFFF ? fkey(best + 0.0f) : 0u;
+  const int pos = wave_first_max_pos(key, best_pos);
+  const int child = pos >= 0 ? readlane_i(best_child, pos & (kWave - 1)) : -1;
+  if (lane == 0) selected[s] = child;
+}
+
+// ---- fused_ucb_with_noise ------------------------------------------------------------------
+// One wave per simulation over the shared row of num_children: prior (1 - eps) P + eps * noise
+// of the simulation, ucb = q + c * prior' * sqrt_parent / (1 + N), the first maximum above
+// -1e10 (strict '>'), or position 0 when none is above it.
+__global__ void fused_ucb_noise_kernel(const float* q_values, const int32_t* visit_counts,
+                                       const float* priors, int num_children,
+                                       const float* noise, int num_sims,
+                                       float parent_visits_sqrt, float c_puct, float epsilon,
+                                       int32_t* selected) {
+  const int s = blockIdx.x * kRowWaves + (int)threadIdx.x / kWave;
+  if (s >= num_sims) return;
+  const int lane = lane_id();
+  const float* nz = noise + (int64_t)s * num_children;
+  const float keep = 1.0f - epsilon;
+  float best = -1e10f;
+  int best_pos = 0x7FFFFFFF;
+  for (int c = lane; c < num_children; c += kWave) {
+    const float mixed = keep * priors[c] + epsilon * nz[c];
+    const float ucb = q_values[c] + c_puct * mixed * parent_visits_sqrt /
+                                        (1.0f + (float)visit_counts[c]);
+    if (ucb > best) {
+      best = ucb;
+      best_pos = c;
+    }
+  }
+  const uint32_t key = best_pos != 0x7FFFFFFF ? fkey(best + 0.0f) : 0u;
+  const int pos = wave_first_max_pos(key, best_pos);
+  if (lane == 0) selected[s] = pos >= 0 ? pos : 0;
+}
+
+// ---- batched_ucb_selection_dense ---------------------------------------------------------
+// One wave per batch item over its slots: a slot counts when valid_mask is set and its child
+// lies in [0, num_valid_children); value = child_values when the child is visited, else 0;
+// ucb = value + c * P_slot * sqrt(pv + 1) / (1 + N).  The child of the first maximum above
+// -1e10 (strict '>'), or -1.
+__global__ void batched_ucb_dense_kernel(const int32_t* batch_children, const float* batch_priors,
+                                         const int32_t* parent_visits, const uint8_t* valid_mask,
+                                         int batch, int max_children, const int32_t* child_visits,
+                                         const float* child_values, int num_valid,
+                                         float c_puct, int32_t* selected) {
+  const int b = blockIdx.x * kRowWaves + (int)threadIdx.x / kWave;
+  if (b >= batch) return;
+  const int lane = lane_id();
+  const int64_t rb = (int64_t)b * max_children;
+  const float sqrt_parent = sqrtf((float)parent_visits[b] + 1.0f);
+  float best = -1e10f;
+  int best_pos = 0x7FFFFFFF, best_child = -1;
+  for (int i = lane; i < max_children; i += kWave) {
+    if (!valid_mask[rb + i]) continue;
+    const int c = batch_children[rb + i];
+    if (c < 0 || c >= num_valid) continue;
+    const int n = child_visits[c];
+    const float v = n > 0 ? child_values[c] : 0.0f;
+    const float ucb = v + c_puct * batch_priors[rb + i] * sqrt_parent / (1.0f + (float)n);
+    if (ucb > best) {
+      best = ucb;
+      best_pos = i;
+      best_child = c;
+    }
+  }
+  const uint32_t key = best_pos != 0x7FFFFFFF ? fkey(best + 0.0f) : 0u;
+  const int pos = wave_first_max_pos(key, best_pos);
+  const int child = pos >= 0 ? readlane_i(best_child, pos & (kWave - 1)) : -1;
+  if (lane == 0) selected[b] = child;
+}
+
 }  // namespace
 
 hipError_t launch_find_expansion_nodes(const int32_t* current_nodes, const uint8_t* valid_mask,
@@ -512,6 +639,46 @@ hipError_t launch_batched_add_children(
                      num_children, node_counter, edge_counter, children, parent_indices_out,
                      parent_actions_out, node_priors_out, visit_counts_out, value_sums_out,
                      col_indices, edge_actions, edge_priors, max_children, child_indices);
+  return hipGetLastError();
+}
+
+hipError_t launch_parallel_select_vl(const int32_t* parent_nodes, int num_sims,
+                                     const int32_t* children, int num_rows, int max_children,
+                                     int children_stride, const int32_t* visit_counts,
+                                     const int32_t* vl_counts, const float* value_sums,
+                                     int num_nodes, const float* priors, int priors_stride,
+                                     const uint8_t* legal_masks, int action_space,
+                                     const int32_t* child_actions, float c_puct, float vl_value,
+                                     int32_t* selected, hipStream_t st) {
+  if (num_sims <= 0) return hipSuccess;
+  hipLaunchKernelGGL(parallel_select_vl_kernel, dim3(row_blocks(num_sims)),
+                     dim3(kRowWaves * kWave), 0, st, parent_nodes, num_sims, children, num_rows,
+                     max_children, children_stride, visit_counts, vl_counts, value_sums,
+                     num_nodes, priors, priors_stride, legal_masks, action_space, child_actions,
+                     c_puct, vl_value, selected);
+  return hipGetLastError();
+}
+
+hipError_t launch_fused_ucb_noise(const float* q_values, const int32_t* visit_counts,
+                                  const float* priors, int num_children, const float* noise,
+                                  int num_sims, float parent_visits_sqrt, float c_puct,
+                                  float epsilon, int32_t* selected, hipStream_t st) {
+  if (num_sims <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fused_ucb_noise_kernel, dim3(row_blocks(num_sims)), dim3(kRowWaves * kWave),
+                     0, st, q_values, visit_counts, priors, num_children, noise, num_sims,
+                     parent_visits_sqrt, c_puct, epsilon, selected);
+  return hipGetLastError();
+}
+
+hipError_t launch_batched_ucb_dense(const int32_t* batch_children, const float* batch_priors,
+                                    const int32_t* parent_visits, const uint8_t* valid_mask,
+                                    int batch, int max_children, const int32_t* child_visits,
+                                    const float* child_values, int num_valid, float c_puct,
+                                    int32_t* selected, hipStream_t st) {
+  if (batch <= 0) return hipSuccess;
+  hipLaunchKernelGGL(batched_ucb_dense_kernel, dim3(row_blocks(batch)), dim3(kRowWaves * kWave), 0,
+                     st, batch_children, batch_priors, parent_visits, valid_mask, batch,
+                     max_children, child_visits, child_values, num_valid, c_puct, selected);
   return hipGetLastError();
 }
 

@@ -290,6 +290,40 @@ __global__ __launch_bounds__(kWave) void root_dirichlet_kernel(omq_forest f, dou
   }
 }
 
+// ---- batched Dirichlet noise rows ------------------------------------------------------------
+// The reference's batched_dirichlet_noise (mcts_kernels.cu:649-754, host :1735-1790): rows of
+// num_actions gamma(alpha, 1) variates divided by their sum (a Dirichlet(alpha, ..., alpha)
+// row), left at 0 when the sum is 0.  Entry i of row r is drawn from the stream keyed by
+// (seed, counter, r, i); the sum is the canonical wave sum in float64 and each quotient is
+// rounded to float32 once.  One wavefront per row.
+__global__ __launch_bounds__(kWave) void batched_dirichlet_kernel(int num_actions, double alpha,
+                                                                  uint64_t seed,
+                                                                  uint64_t counter,
+                                                                  float* noise) {
+  const int r = blockIdx.x;
+  const int lane = lane_id();
+  float* row = noise + (int64_t)r * num_actions;
+  double part = 0.0;
+  for (int i = lane; i < num_actions; i += kWave) {
+    Stream st = make_stream(seed, counter, r, i);
+    part = part + gamma_mt(alpha, st);
+  }
+  const double S = wave_sum_canonical_d(part);
+  for (int i = lane; i < num_actions; i += kWave) {
+    Stream st = make_stream(seed, counter, r, i);  // the same draws again (cheaper than LDS)
+    const double g = gamma_mt(alpha, st);
+    row[i] = S > 0.0 ? (float)(g / S) : 0.0f;
+  }
+}
+
+hipError_t launch_batched_dirichlet(int num_sims, int num_actions, double alpha, uint64_t seed,
+                                    uint64_t counter, float* noise, hipStream_t st) {
+  if (num_sims <= 0 || num_actions <= 0) return hipSuccess;
+  hipLaunchKernelGGL(batched_dirichlet_kernel, dim3(num_sims), dim3(kWave), 0, st, num_actions,
+                     alpha, seed, counter, noise);
+  return hipGetLastError();
+}
+
 hipError_t launch_root_policy(const omq_forest& f, double* pol, hipStream_t st) {
   hipLaunchKernelGGL(root_policy_kernel, dim3(f.num_trees), dim3(kRootThreads), 0, st, f, pol);
   return hipGetLastError();

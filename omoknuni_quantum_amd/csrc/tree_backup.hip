@@ -177,12 +177,16 @@ __global__ void paths_backup_kernel(omq_forest f, const int32_t* paths, const in
   const int t = tree_of ? tree_of[b] : 0;
   if (t < 0 || t >= f.num_trees) return;  // entries naming no tree are skipped
   const int64_t tb = (int64_t)t * f.capacity;
-  const int L = min(plen[b], max_depth);
+  // entries d < min(length, max_depth); the leaf-positive sign counts the distance from the
+  // leaf by the length as given (vectorized_backup_kernel, mcts_kernels.cu:142-146), also for a
+  // length past the row
+  const int Lp = plen[b];
+  const int L = min(Lp, max_depth);
   const float v = values[b];
   for (int d = 0; d < L; ++d) {
     const int x = paths[(int64_t)b * max_depth + d];
     if (x < 0 || x >= f.capacity) continue;  // -1 padding and out-of-range entries are skipped
-    const int e = sign_mode == OMQ_SIGN_LEAF_POSITIVE ? (L - 1 - d) : d;
+    const int e = sign_mode == OMQ_SIGN_LEAF_POSITIVE ? (Lp - 1 - d) : d;
     atomicAdd(&f.visit_counts[tb + x], 1);
     unsafeAtomicAdd(&f.value_sums[tb + x], (e & 1) ? -v : v);
   }

@@ -300,3 +300,256 @@ hipError_t launch_shift_root(const omq_forest& f, const int32_t* new_roots, int3
 }
 
 }  // namespace omq
+
+// ===========================================================================================
+// The reference's two-step subtree API: parallel_bfs_subtree and extract_subtree_edges
+// (python/mcts/gpu/mcts_kernels.cu:2095-2337, bound at :2396-2408), over a CSR graph
+// (row_ptr [max_nodes + 1], col_indices [num_edges]).  Their callers are
+// python/mcts/gpu/gpu_bfs.py:49,149 and python/mcts/gpu/compact_subtree.py:220.
+//   - BFS: breadth-first from root_idx, each level's nodes in order and each row's children in
+//     row order; a child not yet in the subtree gets the next new index at its first
+//     occurrence (the order of the reference's fallback, gpu_bfs.py:70-127, and of a FIFO
+//     queue).  Children outside [0, max_nodes) are skipped.  The reference kernel numbers
+//     children in the order its atomics land and marks a bool array through 32-bit CAS at the
+//     child's index (touching the three bytes after it and reading past the array): its order
+//     is one of the orders that can arise, and no other.
+//   - Edges: for every node of the subtree in ascending old index, the edges of its row (in
+//     row order) whose child lies in the subtree, as (new parent, new child, action); the
+//     reference appends them in atomic order, of which this is one.
+// ===========================================================================================
+namespace omq {
+
+constexpr int kBfsThreads = 1024;
+constexpr int kBfsWaves = kBfsThreads / kWave;
+
+// exclusive scan of one int64 per thread over the workgroup; total through *tot
+__device__ inline int64_t bfs_block_scan(int64_t v, int64_t* s_wtot, int64_t* tot) {
+  const int wave = (int)threadIdx.x / kWave, lane = lane_id();
+  int64_t x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int64_t y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  if (lane == kWave - 1) s_wtot[wave] = x;
+  __syncthreads();
+  int64_t before = 0, all = 0;
+  for (int i = 0; i < kBfsWaves; ++i) {
+    const int64_t t = s_wtot[i];
+    before += i < wave ? t : 0;
+    all += t;
+  }
+  __syncthreads();  // s_wtot is reused by the next scan
+  *tot = all;
+  return before + x - v;
+}
+
+// row [a, b) of node, clamped to the edge array
+__device__ inline void bfs_row(const int32_t* row_ptr, int num_edges, int node, int* a, int* b) {
+  int lo = row_ptr[node], hi = row_ptr[node + 1];
+  lo = lo < 0 ? 0 : (lo > num_edges ? num_edges : lo);
+  hi = hi < lo ? lo : (hi > num_edges ? num_edges : hi);
+  *a = lo;
+  *b = hi;
+}
+
+// candidate k of the level: the level position q with off[q] <= k < off[q + 1] (binary search
+// over off[0..L]), and its child
+__device__ inline int bfs_candidate(const int32_t* row_ptr, const int32_t* col, int num_edges,
+                                    const int32_t* level, const int32_t* off, int L, int k) {
+  int lo = 0, hi = L - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (off[mid] <= k) lo = mid; else hi = mid - 1;
+  }
+  int a, b;
+  bfs_row(row_ptr, num_edges, level[lo], &a, &b);
+  return col[a + (k - off[lo])];
+}
+
+// One workgroup.  Workspace: queue [max_nodes], claim [max_nodes], off [max_nodes + 1].
+__global__ __launch_bounds__(kBfsThreads) void bfs_subtree_kernel(
+    const int32_t* row_ptr, const int32_t* col, int num_edges, int root, int max_nodes,
+    uint8_t* in_subtree, int32_t* remap, int32_t* count_out, int32_t* queue, int32_t* claim,
+    int32_t* off) {
+  __shared__ int64_t s_wtot[kBfsWaves];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < max_nodes; i += kBfsThreads) {
+    in_subtree[i] = 0;
+    remap[i] = -1;
+    claim[i] = 0x7FFFFFFF;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    in_subtree[root] = 1;
+    remap[root] = 0;
+    queue[0] = root;
+  }
+  __syncthreads();
+  int start = 0, end = 1;  // the current level: queue[start, end)
+  bool overflow = false;
+  while (start < end) {
+    const int L = end - start;
+    const int32_t* level = queue + start;
+    // offsets of the level's rows in its list of candidates (level order, then row order)
+    int64_t run = 0;
+    for (int c0 = 0; c0 < L; c0 += kBfsThreads) {
+      const int q = c0 + tid;
+      int64_t len = 0;
+      if (q < L) {
+        int a, b;
+        bfs_row(row_ptr, num_edges, level[q], &a, &b);
+        len = b - a;
+      }
+      int64_t tot;
+      const int64_t ex = bfs_block_scan(len, s_wtot, &tot);
+      if (q < L) off[q] = (int32_t)min(run + ex, (int64_t)0x7FFFFFFF);
+      run += tot;
+    }
+    if (run > 0x7FFFFFFF) {  // more candidates than int32 keys (rows that overlap)
+      overflow = true;
+      break;
+    }
+    const int total = (int)run;
+    if (tid == 0) off[L] = total;
+    __syncthreads();
+    // every candidate outside the subtree claims its child with its key (the earliest wins)
+    for (int k = tid; k < total; k += kBfsThreads) {
+      const int c = bfs_candidate(row_ptr, col, num_edges, level, off, L, k);
+      if (c >= 0 && c < max_nodes && !in_subtree[c]) atomicMin(&claim[c], k);
+    }
+    __syncthreads();
+    // the winners, numbered in key order
+    int added = 0;
+    for (int k0 = 0; k0 < total; k0 += kBfsThreads) {
+      const int k = k0 + tid;
+      int c = -1;
+      bool win = false;
+      if (k < total) {
+        c = bfs_candidate(row_ptr, col, num_edges, level, off, L, k);
+        win = c >= 0 && c < max_nodes && !in_subtree[c] && claim[c] == k;
+      }
+      int64_t tot;
+      const int ex = (int)bfs_block_scan(win ? 1 : 0, s_wtot, &tot);
+      if (win) {
+        remap[c] = end + added + ex;
+        queue[end + added + ex] = c;
+      }
+      added += (int)tot;
+    }
+    __syncthreads();
+    for (int i = tid; i < added; i += kBfsThreads) in_subtree[queue[end + i]] = 1;
+    __syncthreads();
+    start = end;
+    end += added;
+  }
+  if (tid == 0) count_out[0] = overflow ? -1 : end;
+}
+
+// Edge extraction: count per node and block scan (pass 1), scan of the block totals (pass 2),
+// writes (pass 3).  Workspace: local [num_nodes], block totals [blocks + 1].
+constexpr int kEdgeThreads = 1024;
+
+__device__ inline int edges_kept(const int32_t* row_ptr, const int32_t* col, int num_edges,
+                                 const uint8_t* in_subtree, int num_nodes, int node) {
+  if (!in_subtree[node]) return 0;
+  int a, b;
+  bfs_row(row_ptr, num_edges, node, &a, &b);
+  int n = 0;
+  for (int e = a; e < b; ++e) {
+    const int c = col[e];
+    n += (c >= 0 && c < num_nodes && in_subtree[c]) ? 1 : 0;
+  }
+  return n;
+}
+
+__global__ __launch_bounds__(kEdgeThreads) void edges_count_kernel(
+    const int32_t* row_ptr, const int32_t* col, int num_edges, const uint8_t* in_subtree,
+    int num_nodes, int32_t* local, int32_t* block_tot) {
+  __shared__ int64_t s_wtot[kEdgeThreads / kWave];
+  const int i = blockIdx.x * kEdgeThreads + threadIdx.x;
+  const int n = i < num_nodes ? edges_kept(row_ptr, col, num_edges, in_subtree, num_nodes, i) : 0;
+  int64_t tot;
+  const int64_t ex = bfs_block_scan(n, s_wtot, &tot);
+  if (i < num_nodes) local[i] = (int32_t)ex;
+  if (threadIdx.x == 0) block_tot[blockIdx.x] = (int32_t)tot;
+}
+
+__global__ __launch_bounds__(kEdgeThreads) void edges_scan_kernel(int32_t* block_tot, int blocks,
+                                                                  int32_t* edge_count) {
+  __shared__ int64_t s_wtot[kEdgeThreads / kWave];
+  int64_t run = 0;
+  for (int b0 = 0; b0 < blocks; b0 += kEdgeThreads) {
+    const int b = b0 + (int)threadIdx.x;
+    const int64_t v = b < blocks ? block_tot[b] : 0;
+    int64_t tot;
+    const int64_t ex = bfs_block_scan(v, s_wtot, &tot);
+    __syncthreads();  // every block total of the chunk is read before any is overwritten
+    if (b < blocks) block_tot[b] = (int32_t)(run + ex);
+    run += tot;
+  }
+  if (threadIdx.x == 0) edge_count[0] = (int32_t)min(run, (int64_t)0x7FFFFFFF);
+}
+
+__global__ __launch_bounds__(kEdgeThreads) void edges_write_kernel(
+    const int32_t* row_ptr, const int32_t* col, const int16_t* actions, int num_edges,
+    const uint8_t* in_subtree, const int32_t* remap, int num_nodes, int max_edges,
+    const int32_t* local, const int32_t* block_off, int32_t* out_parent, int32_t* out_child,
+    int16_t* out_action) {
+  const int i = blockIdx.x * kEdgeThreads + threadIdx.x;
+  if (i >= num_nodes || !in_subtree[i]) return;
+  int a, b;
+  bfs_row(row_ptr, num_edges, i, &a, &b);
+  int64_t pos = (int64_t)block_off[blockIdx.x] + local[i];
+  const int np = remap[i];
+  for (int e = a; e < b && pos < max_edges; ++e) {
+    const int c = col[e];
+    if (c < 0 || c >= num_nodes || !in_subtree[c]) continue;
+    out_parent[pos] = np;
+    out_child[pos] = remap[c];
+    out_action[pos] = actions != nullptr ? actions[e] : (int16_t)0;
+    ++pos;
+  }
+}
+
+hipError_t launch_bfs_subtree(const int32_t* row_ptr, const int32_t* col, int num_edges,
+                              int root, int max_nodes, uint8_t* in_subtree, int32_t* remap,
+                              int32_t* count, int32_t* ws, hipStream_t st) {
+  int32_t* queue = ws;
+  int32_t* claim = ws + max_nodes;
+  int32_t* off = ws + 2 * (int64_t)max_nodes;
+  hipLaunchKernelGGL(bfs_subtree_kernel, dim3(1), dim3(kBfsThreads), 0, st, row_ptr, col,
+                     num_edges, root, max_nodes, in_subtree, remap, count, queue, claim, off);
+  return hipGetLastError();
+}
+
+int edges_blocks(int num_nodes) { return (num_nodes + kEdgeThreads - 1) / kEdgeThreads; }
+
+hipError_t launch_extract_edges(const int32_t* row_ptr, const int32_t* col, const int16_t* actions,
+                                int num_edges, const uint8_t* in_subtree, const int32_t* remap,
+                                int num_nodes, int max_edges, int32_t* out_parent,
+                                int32_t* out_child, int16_t* out_action, int32_t* edge_count,
+                                int32_t* ws, hipStream_t st) {
+  const int blocks = edges_blocks(num_nodes);
+  int32_t* local = ws;
+  int32_t* block_tot = ws + num_nodes;
+  if (blocks == 0) {
+    hipLaunchKernelGGL(edges_scan_kernel, dim3(1), dim3(kEdgeThreads), 0, st, block_tot, 0,
+                       edge_count);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(edges_count_kernel, dim3(blocks), dim3(kEdgeThreads), 0, st, row_ptr, col,
+                     num_edges, in_subtree, num_nodes, local, block_tot);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(edges_scan_kernel, dim3(1), dim3(kEdgeThreads), 0, st, block_tot, blocks,
+                     edge_count);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(edges_write_kernel, dim3(blocks), dim3(kEdgeThreads), 0, st, row_ptr, col,
+                     actions, num_edges, in_subtree, remap, num_nodes, max_edges, local,
+                     block_tot, out_parent, out_child, out_action);
+  return hipGetLastError();
+}
+
+}  // namespace omq

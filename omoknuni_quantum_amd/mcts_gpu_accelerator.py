@@ -89,6 +89,26 @@ class MCTSGPUAccelerator:
     def batch_remove_virtual_loss(self, node_indices, virtual_loss_counts):
         torch_ops.batch_remove_virtual_loss(node_indices, virtual_loss_counts)
 
+    # mcts_gpu_accelerator.py:289-297: the module's operator with no noise, no legal masks and
+    # epsilon 0
+    def parallel_select_with_virtual_loss(self, parent_nodes, children, visit_counts,
+                                          virtual_loss_counts, value_sums, priors,
+                                          child_actions, c_puct, virtual_loss_value):
+        return torch_ops.parallel_select_with_virtual_loss(
+            parent_nodes, children, visit_counts, virtual_loss_counts, value_sums, priors,
+            None, None, child_actions, c_puct, virtual_loss_value, 0.0)
+
+    # mcts_gpu_accelerator.py:323-330: pass-through to the module's operators
+    def batched_dirichlet_noise(self, *args, **kwargs):
+        return torch_ops.batched_dirichlet_noise(*args, **kwargs)
+
+    def fused_ucb_with_noise(self, *args, **kwargs):
+        return torch_ops.fused_ucb_with_noise(*args, **kwargs)
+
+    def optimized_backup_scatter(self, *args, **kwargs):
+        self.stats["backup_calls"] += 1
+        return torch_ops.optimized_backup_scatter(*args, **kwargs)
+
     def get_stats(self) -> dict:
         return {"device": str(self.device), "interface_type": "HIPKernelInterface",
                 "library": _lib.load()._name, **self.stats}

@@ -833,3 +833,226 @@ def batched_add_children(parent_indices, actions, priors, num_children, tree, ma
             tree["edge_priors"][e] = pr
             out[b * max_children + i] = ch
     return out
+
+
+# ---- more operators of the reference's pybind module (mcts_kernels.cu:2342-2410) -----------
+# Sequential loops in the order the reference's kernels visit their elements.  Each takes a
+# `variant` naming a planted misreading, used only by the tests that show the known answers
+# fail on it; None is the operator.
+
+PSVL_VARIANTS = (
+    "sqrt_no_plus1",      # sqrt(N_parent) instead of sqrt(N_parent + 1)
+    "parent_with_vl",     # the parent's virtual-loss count added to its visits
+    "value_without_vl",   # W without VL * virtual_loss_value
+    "row_ends_at_neg",    # the row ends at its first negative entry instead of skipping it
+    "mask_at_root",       # the legal filter applied at node 0 too
+    "vl_between_sims",    # each selection's virtual loss seen by the later simulations
+)
+
+
+def parallel_select_with_virtual_loss(parent_nodes, children, visit_counts, vl_counts,
+                                      value_sums, priors, child_actions, c_puct, vl_value,
+                                      legal_masks=None, variant=None):
+    """parallel_select_with_virtual_loss_kernel (mcts_kernels.cu:962-1053) for every simulation
+    from the same counts, then +1 virtual loss per selection (:1990-1996).  priors: [nodes] or
+    per simulation [sims, stride].  Returns (selected, virtual-loss counts after)."""
+    if variant is not None and variant not in PSVL_VARIANTS:
+        raise ValueError(f"unknown variant {variant!r}")
+    children = np.asarray(children)
+    vl = np.array(vl_counts, np.int32)
+    nn = len(visit_counts)
+    per_sim = np.ndim(priors) == 2
+    out = []
+    c_puct, vlv = F(c_puct), F(vl_value)
+    for s, p in enumerate(parent_nodes):
+        p = int(p)
+        if p < 0 or p >= children.shape[0] or p >= nn:
+            out.append(-1)
+            continue
+        pv = int(visit_counts[p]) + (int(vl[p]) if variant == "parent_with_vl" else 0)
+        sq = F(math.sqrt(float(F(pv if variant == "sqrt_no_plus1" else pv + 1))))
+        best, arg = F(-np.inf), -1
+        for c in children[p]:
+            c = int(c)
+            if c < 0 and variant == "row_ends_at_neg":
+                break
+            if c < 0 or c >= nn:
+                continue
+            if legal_masks is not None and (p != 0 or variant == "mask_at_root"):
+                a = int(child_actions[c])
+                if 0 <= a < legal_masks.shape[1] and not legal_masks[s, a]:
+                    continue
+            if per_sim:
+                if c >= priors.shape[1]:
+                    continue
+                prior = F(priors[s, c])
+            else:
+                prior = F(priors[c])
+            n = int(visit_counts[c]) + int(vl[c])
+            w = F(value_sums[c]) if variant == "value_without_vl" else \
+                F(F(value_sums[c]) + F(F(int(vl[c])) * vlv))
+            q = F(w / F(n)) if n > 0 else F(0.0)
+            ucb = F(q + F(F(F(c_puct * prior) * sq) / F(F(1.0) + F(n))))
+            if ucb > best:
+                best, arg = ucb, c
+        out.append(arg)
+        if variant == "vl_between_sims" and arg >= 0:
+            vl[arg] += 1
+    if variant != "vl_between_sims":
+        for c in out:
+            if 0 <= c < len(vl):
+                vl[c] += 1
+    return np.array(out, np.int32), vl
+
+
+UCBN_VARIANTS = (
+    "prior_unmixed",     # the noise left out of the prior
+    "none_is_minus1",    # -1 instead of 0 when no score is above -1e10
+    "q_zero_unvisited",  # q = 0 for an unvisited child
+)
+
+
+def fused_ucb_with_noise(q_values, visit_counts, priors, noise, parent_visits_sqrt, c_puct,
+                         epsilon, variant=None):
+    """fused_ucb_with_noise_kernel (mcts_kernels.cu:760-797): per simulation, the position of
+    the first maximum above -1e10 of q + c (1-eps) P + eps noise) sqrt / (1 + N), else 0."""
+    if variant is not None and variant not in UCBN_VARIANTS:
+        raise ValueError(f"unknown variant {variant!r}")
+    keep, eps = F(F(1.0) - F(epsilon)), F(epsilon)
+    c, sq = F(c_puct), F(parent_visits_sqrt)
+    out = []
+    for s in range(noise.shape[0]):
+        best, arg = F(-1e10), (-1 if variant == "none_is_minus1" else 0)
+        for i in range(len(q_values)):
+            mixed = F(priors[i]) if variant == "prior_unmixed" else \
+                F(F(keep * F(priors[i])) + F(eps * F(noise[s, i])))
+            n = int(visit_counts[i])
+            q = F(0.0) if (variant == "q_zero_unvisited" and n == 0) else F(q_values[i])
+            ucb = F(q + F(F(F(c * mixed) * sq) / F(F(1.0) + F(n))))
+            if ucb > best:
+                best, arg = ucb, i
+        out.append(arg)
+    return np.array(out, np.int32)
+
+
+UCBD_VARIANTS = (
+    "returns_slot",      # the slot position instead of the child id
+    "sqrt_no_plus1",     # sqrt(pv) instead of sqrt(pv + 1)
+    "value_unvisited",   # the child's value used when it has no visits
+)
+
+
+def batched_ucb_selection_dense(batch_children, batch_priors, parent_visits, child_visits,
+                                child_values, valid_mask, c_puct, variant=None):
+    """batched_ucb_selection_dense_kernel (mcts_kernels.cu:1364-1409): per item, the child of
+    the first maximum above -1e10 over valid slots whose child is in [0, len(child_visits)),
+    else -1."""
+    if variant is not None and variant not in UCBD_VARIANTS:
+        raise ValueError(f"unknown variant {variant!r}")
+    c = F(c_puct)
+    nv = len(child_visits)
+    out = []
+    for b in range(batch_children.shape[0]):
+        pv = int(parent_visits[b])
+        sq = F(math.sqrt(float(F(F(pv) + (F(0.0) if variant == "sqrt_no_plus1" else F(1.0))))))
+        best, arg = F(-1e10), -1
+        for j in range(batch_children.shape[1]):
+            if not valid_mask[b, j]:
+                continue
+            ch = int(batch_children[b, j])
+            if ch < 0 or ch >= nv:
+                continue
+            n = int(child_visits[ch])
+            v = F(child_values[ch]) if (n > 0 or variant == "value_unvisited") else F(0.0)
+            ucb = F(v + F(F(F(c * F(batch_priors[b, j])) * sq) / F(F(1.0) + F(n))))
+            if ucb > best:
+                best, arg = ucb, (j if variant == "returns_slot" else ch)
+        out.append(arg)
+    return np.array(out, np.int32)
+
+
+BFS_VARIANTS = (
+    "dfs",              # depth-first numbering
+    "level_by_id",      # a level's new nodes numbered by old id instead of discovery order
+    "last_occurrence",  # a child met twice in a level numbered at its last occurrence
+)
+
+
+def parallel_bfs_subtree(row_ptr, col_indices, root, max_nodes, variant=None):
+    """The subtree of root in a CSR graph, numbered breadth-first (gpu_bfs.py:70-127, the
+    order of a FIFO queue: levels in order, children in row order, first occurrence), children
+    outside [0, max_nodes) skipped.  Returns (in_subtree, node_remap, count)."""
+    if variant is not None and variant not in BFS_VARIANTS:
+        raise ValueError(f"unknown variant {variant!r}")
+    E = len(col_indices)
+
+    def row(v):
+        a = min(max(int(row_ptr[v]), 0), E)
+        b = min(max(int(row_ptr[v + 1]), a), E)
+        return [int(c) for c in col_indices[a:b]]
+
+    ins = np.zeros(max_nodes, bool)
+    remap = np.full(max_nodes, -1, np.int32)
+    ins[root], remap[root] = True, 0
+    order = [root]
+    if variant == "dfs":
+        stack = [root]
+        while stack:
+            v = stack.pop()
+            for c in reversed(row(v)):
+                if 0 <= c < max_nodes and not ins[c]:
+                    ins[c] = True
+                    remap[c] = len(order)
+                    order.append(c)
+                    stack.append(c)
+        return ins, remap, len(order)
+    level = [root]
+    while level:
+        found = []
+        for v in level:
+            for c in row(v):
+                if 0 <= c < max_nodes and not ins[c]:
+                    if variant == "last_occurrence" and c in found:
+                        found.remove(c)
+                    if c not in found:
+                        found.append(c)
+        if variant == "level_by_id":
+            found = sorted(found)
+        for c in found:
+            ins[c] = True
+            remap[c] = len(order)
+            order.append(c)
+        level = found
+    return ins, remap, len(order)
+
+
+EDGE_VARIANTS = (
+    "by_new_index",     # nodes taken in new-index order instead of old-index order
+    "child_outside",    # edges to children outside the subtree kept (child -1)
+)
+
+
+def extract_subtree_edges(row_ptr, col_indices, edge_actions, in_subtree, node_remap,
+                          variant=None):
+    """The subtree's edges (extract_subtree_edges_kernel, mcts_kernels.cu:2201-2244, in the
+    order of one thread): nodes of the subtree in ascending old index, each row in order, edges
+    whose child lies in the subtree, as (new parent, new child, action or 0)."""
+    if variant is not None and variant not in EDGE_VARIANTS:
+        raise ValueError(f"unknown variant {variant!r}")
+    n, E = len(in_subtree), len(col_indices)
+    nodes = [i for i in range(n) if in_subtree[i]]
+    if variant == "by_new_index":
+        nodes.sort(key=lambda i: int(node_remap[i]))
+    par, chl, act = [], [], []
+    for i in nodes:
+        a = min(max(int(row_ptr[i]), 0), E)
+        b = min(max(int(row_ptr[i + 1]), a), E)
+        for e in range(a, b):
+            c = int(col_indices[e])
+            inside = 0 <= c < n and in_subtree[c]
+            if not inside and not (variant == "child_outside" and 0 <= c < n):
+                continue
+            par.append(int(node_remap[i]))
+            chl.append(int(node_remap[c]))
+            act.append(int(edge_actions[e]) if edge_actions is not None else 0)
+    return np.array(par, np.int32), np.array(chl, np.int32), np.array(act, np.int16)

@@ -145,8 +145,8 @@ def test_torch_ops_match_reference_kernel_semantics(device):
     rng = np.random.default_rng(3)
     n, B, D = 300, 200, 9
     paths = rng.integers(-1, n + 5, (B, D)).astype(np.int32)  # includes -1 and out-of-range
-    plen = rng.integers(0, D + 1, B).astype(np.int32)
-    vals = (rng.integers(-16, 17, B) / 16.0).astype(np.float32)
+    plen = rng.integers(0, D + 4, B).astype(np.int32)  # lengths past the row: the sign still
+    vals = (rng.integers(-16, 17, B) / 16.0).astype(np.float32)  # counts from the length given
     N = np.zeros(n, np.int64)
     Wx = np.zeros(n, np.float64)
     for b in range(B):
