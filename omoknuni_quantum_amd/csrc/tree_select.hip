@@ -24,6 +24,7 @@
 // Virtual loss is materialised once per group (N[p] += VL*m, p is owned by one group per
 // wave), or with one atomic per path entry when vl_atomic is set.
 
+#include <algorithm>
 #include <atomic>
 
 #include "omq_common.h"
@@ -975,12 +976,10 @@ __device__ __noinline__ int unvisited_prefix(const int32_t* N, int64_t tb, int f
 // its register demand within the 128 VGPRs of a 1024-thread workgroup.  WIDE: the kernel's
 // chains keep up to 256 registers (workgroups of at most 512 threads, one per CU).
 template <int RMAX, bool WIDE>
-__device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0,
-                                     int m, int npre, const SelCfg& c, uint32_t* ch, uint16_t* cnt_s,
+__device__ inline int dispatch_chain(ChainRows rows, int64_t tb, int first, int k, int Np0,
+                                     int m, int npre, ChainCfg cc, uint32_t* ch, uint16_t* cnt_s,
                                      float4* cscr, int* progress) {
   const int r = (k + kWave - 1) / kWave;  // 1 <= r <= RMAX (checked by the caller)
-  const ChainRows rows{f.N, f.W, f.P};
-  const ChainCfg cc{c.c_puct, c.vlf, c.vli};
   // contender windows kept open across blocks in the kernels of up to 4 slots per lane and in
   // the WIDE ones (the other wider kernels' chains have no registers left for it)
   constexpr bool kPersist = RMAX <= 4 || WIDE;
@@ -1005,11 +1004,12 @@ __device__ inline int dispatch_chain(const SelArgs& f, int64_t tb, int first, in
 // *all_prefix: every rank was taken by the prefix (distinct children in index order, each
 // picked once).
 template <int RMAX, bool WIDE>
-__device__ inline int group_chain(const SelArgs& f, int64_t tb, int first, int k, int Np0, int m,
-                                  const SelCfg& c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
-                                  int* progress, bool* all_prefix) {
-  const int npre = unvisited_prefix<RMAX>(f.N, tb, first, k, m, c.vli > 0, ch, cnt_s);
+__device__ inline int group_chain(ChainRows rows, int64_t tb, int first, int k, int Np0, int m,
+                                  ChainCfg cc, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
+                                  int* progress, bool* all_prefix, int* npre_out = nullptr) {
+  const int npre = unvisited_prefix<RMAX>(rows.N, tb, first, k, m, cc.vli > 0, ch, cnt_s);
   *all_prefix = npre >= m;
+  if (npre_out != nullptr) *npre_out = npre;
   if (npre >= m) {
     if (progress != nullptr) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -1024,7 +1024,7 @@ __device__ inline int group_chain(const SelArgs& f, int64_t tb, int first, int k
     if (lane_id() == 0)
       __hip_atomic_store(progress, npre, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  return dispatch_chain<RMAX, WIDE>(f, tb, first, k, Np0, m, WIDE ? npre : 0, c, ch, cnt_s,
+  return dispatch_chain<RMAX, WIDE>(rows, tb, first, k, Np0, m, WIDE ? npre : 0, cc, ch, cnt_s,
                                     cscr, progress);
 }
 
@@ -1080,6 +1080,7 @@ struct LevelLds {
   uint16_t* cnt_all;
   uint32_t* pipe_ch;
   uint16_t* pick2;
+  uint32_t* spec;  // [kSpecSlots][W] level-1 chains run ahead by the followers (wide kernels)
 };
 
 template <int NT>
@@ -1093,9 +1094,13 @@ __host__ __device__ inline size_t level_pipe_offset(int W) {
   return (level_base_bytes<NT>(W) + 15) & ~(size_t)15;
 }
 constexpr int kPipeMaxW = 2048;  // waves with LDS for the overlap buffers
+// Level-1 chains run ahead during the root chain, one per wave other than the root chain's
+// (the wide kernels: 8 waves), for waves of at most kPipeMaxW simulations.
+constexpr int kSpecSlots = 7;
 template <int NT>
 __host__ __device__ inline size_t level_lds_bytes(int W, bool with_pipe) {
-  if (!with_pipe || W > kPipeMaxW) return level_base_bytes<NT>(W);
+  if (W > kPipeMaxW) return level_base_bytes<NT>(W);
+  if (!with_pipe) return level_pipe_offset<NT>(W) + (size_t)kSpecSlots * W * 4;
   return level_pipe_offset<NT>(W) + (size_t)(NT / kWave) * kWave * 4 + (size_t)W * 2;
 }
 
@@ -1111,10 +1116,13 @@ __device__ inline LevelLds carve_level_lds(unsigned char* smem, int W, bool with
   L.cnt_all = L.buf + 2 * W;
   L.pipe_ch = nullptr;
   L.pick2 = nullptr;
+  L.spec = nullptr;
   if (with_pipe && W <= kPipeMaxW) {
     L.pipe_ch = reinterpret_cast<uint32_t*>(smem + level_pipe_offset<NT>(W));
     L.pick2 = reinterpret_cast<uint16_t*>(L.pipe_ch + NW * kWave);
   }
+  if (!with_pipe && W <= kPipeMaxW && NW == kSpecSlots + 1)
+    L.spec = reinterpret_cast<uint32_t*>(smem + level_pipe_offset<NT>(W));
   return L;
 }
 
@@ -1131,6 +1139,9 @@ struct LevelShared {
   int gnext;      // next group-log entry of the level, from gbase
   int hist[16];
   int wtot[NT / kWave];
+  int spec_node[8];  // the root child of each run-ahead chain (-1: none)
+  int spec_m[8];     // its ranks
+  int spec_npre[8];  // its first-unvisited prefix
   unsigned long long st[OMQ_NSTATS];
 };
 
@@ -1747,7 +1758,9 @@ __device__ inline void level1_followers(const SelArgs& f, const SelCfg& c, int64
       const bool leaf = (k <= 0) || (first < 0) || (c.max_depth <= 2) || (k > RMAX * kWave);
       if (!leaf) {
         bool allp;
-        group_chain<RMAX, false>(f, tb, first, k, Np0, m, c, chs, cnt_s, cscr, nullptr, &allp);
+        group_chain<RMAX, false>(ChainRows{f.N, f.W, f.P}, tb, first, k, Np0, m,
+                                 ChainCfg{c.c_puct, c.vlf, c.vli}, chs, cnt_s, cscr, nullptr,
+                                 &allp);
         if ((mm >> lane) & 1ull) {
           const int r = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32),
                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
@@ -1802,18 +1815,115 @@ __device__ inline int replay_picks(const uint16_t* mem, int m, int k, const uint
 }
 
 
+// Run-ahead of level-1 chains (the wide kernels).  A group's chain depends on its node's row
+// and count and on nothing of its members: rank r's pick follows from ranks [0, r) alone (the
+// parent count at rank r is N + VL*(r+1)), and no level before 1 writes the counts of a root
+// child or of its children.  So while one wave runs the root chain, follower j runs the chain
+// of the (j+1)-th most visited root child for M ranks, an estimate of the picks the child
+// gets (1.5 times its share of the root's visits, plus 16, in blocks of 64), and records its
+// picks in spec[0, M).  At level 1 that child's group replays ranks [0, m) when m <= M and
+// runs its chain otherwise.  Nothing of the forest is written.  Records (node, M, prefix
+// length) in *node_out / *m_out / *npre_out (node -1: none run).
+template <int RMAX>
+__device__ __noinline__ void run_ahead_chain(ChainRows rows, ChainCfg cc, const int32_t* nchild,
+                                             const int32_t* firsts, int64_t tb, int W,
+                                             int root_first, int root_k, int j, uint32_t* spec,
+                                             uint16_t* cnt_s, float4* cscr, int* node_out,
+                                             int* m_out, int* npre_out) {
+  const int lane = lane_id();
+  // keys (visits, clamped to 22 bits, + 1) << 9 | (511 - child): the largest is the most
+  // visited child, the lower index first among equals; 0 marks no child
+  uint32_t key[RMAX];
+#pragma unroll
+  for (int q = 0; q < RMAX; ++q) {
+    const int i = q * kWave + lane;
+    key[q] = 0u;
+    if (i < root_k) {
+      const int n = rows.N[tb + root_first + 1 + i];
+      key[q] = ((uint32_t)min(max(n, 0), (1 << 22) - 2) + 1u) << 9 | (uint32_t)(511 - i);
+    }
+  }
+  uint32_t top = 0u;
+  for (int it = 0; it <= j; ++it) {
+    uint32_t mx = 0u;
+#pragma unroll
+    for (int q = 0; q < RMAX; ++q) mx = max(mx, key[q]);
+    top = wave_max_u32(mx);
+    if (top == 0u) break;
+#pragma unroll
+    for (int q = 0; q < RMAX; ++q)
+      if (key[q] == top) key[q] = 0u;  // (keys are distinct: one lane, one slot)
+  }
+  int node = -1, m = 0, npre = 0;
+  if (top != 0u) {
+    const int ci = 511 - (int)(top & 511u);
+    const int p = root_first + 1 + ci;
+    const int k = nchild[tb + p];
+    const int first = firsts[tb + p];
+    const int Np0 = rows.N[tb + p];
+    const int Nr = rows.N[tb];
+    if (k > 0 && first >= 0 && k <= RMAX * kWave && Nr > 0) {
+      const float share = (float)Np0 / (float)Nr;
+      const int est = (int)(1.5f * share * (float)W) + 16;
+      m = min(W, (est + kWave - 1) / kWave * kWave);
+      bool allp;
+      group_chain<RMAX, true>(rows, tb, first, k, Np0, m, cc, spec, cnt_s, cscr, nullptr, &allp,
+                              &npre);
+      node = p;
+    }
+  }
+  if (lane == 0) {
+    *node_out = node;
+    *m_out = m;
+    *npre_out = npre;
+  }
+}
+
+// Replays ranks [0, m) of a chain run ahead for at least m ranks (spec, as the chain wrote
+// them) into ch, and the child counts of those ranks into cnt_s[0, k) (packed two to a 32-bit
+// word: counts stay below 2^16).  Returns the first rank without a child, or -1;
+// *all_prefix: every rank was taken by the first-unvisited prefix (npre of the run ahead).
+__device__ inline int replay_spec(const uint32_t* spec, int m, int k, int npre, uint32_t* ch,
+                                  uint16_t* cnt_s, bool* all_prefix) {
+  const int lane = lane_id();
+  for (int i = lane; i < k; i += kWave) cnt_s[i] = 0;
+  wave_sync();
+  uint32_t* cnt2 = reinterpret_cast<uint32_t*>(cnt_s);
+  int fe = -1;
+  for (int r0 = 0; r0 < m; r0 += kWave) {
+    const int r = r0 + lane;
+    const bool v = r < m;
+    const uint32_t cv = v ? spec[r] : kNoChild;
+    if (v) ch[r] = cv;
+    const uint64_t none = __ballot(v && cv == kNoChild);
+    if (fe < 0 && none != 0) fe = r0 + lowest_lane(none);
+    if (cv != kNoChild) {
+      const uint32_t i = cv >> 16;
+      atomicAdd(&cnt2[i >> 1], 1u << ((i & 1u) * 16u));
+    }
+  }
+  wave_sync();
+  *all_prefix = npre >= m;
+  return fe;
+}
+
+
 // The level-by-level selection of a set of groups, from level d0 until no group is left or
 // level dend is reached (its groups then stay in L at parity dend & 1, for the caller).  The
 // groups of level d0 are in L and sh at parity d0 & 1.  Returns the level at which it stopped.
 //   pipe:       the root chain is overlapped with the level-1 chains (root kernel, d0 = 0);
 //               level 1 then replays the followers' picks
 //   vl_done_to: levels 1..vl_done_to have their virtual loss in N already (the overlap)
+//   run_ahead:  (wide kernels, d0 = 0) the followers run level-1 chains ahead during the root
+//               chain (run_ahead_chain); level 1 replays them where they cover a group
+//   root_first, root_k: the root's row (the overlap and the run-ahead)
 //   glog_ctr:   counter of the tree's group-log entries (LDS or global)
 //   lfs, lflag: the tree's per-simulation leaf records (global)
 template <int RMAX, int NT, bool WIDE>
 __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int dend, int W,
                           const LevelLds& L, LevelShared<NT>& sh, int* glog_ctr, int32_t* lfs,
-                          int32_t* lflag, bool pipe, int root_first, int vl_done_to) {
+                          int32_t* lflag, bool pipe, int root_first, int vl_done_to,
+                          bool run_ahead, int root_k) {
   constexpr int NW = NT / kWave;
   using Tr = SelTraits<RMAX>;
   const SelArgs& w = f;
@@ -1876,8 +1986,17 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
                              L.pipe_ch + wave * kWave, cnt_s, cscr, &sh.progress, wave - 1,
                              NW - 1);
     }
-    // (at level 0 of the overlap only wave 0 takes the root)
-    const bool deal = !(pipe && d == 0 && wave != 0);
+    // (wide kernels) the followers run level-1 chains ahead while wave 0 runs the root chain
+    if constexpr (WIDE) {
+      if (d == 0 && run_ahead && wave != 0 && wave <= kSpecSlots) {
+        const int j = wave - 1;
+        run_ahead_chain<RMAX>(ChainRows{f.N, f.W, f.P}, ChainCfg{c.c_puct, c.vlf, c.vli},
+                              f.nchild, f.first, tb, W, root_first, root_k, j, L.spec + j * W,
+                              cnt_s, cscr, &sh.spec_node[j], &sh.spec_m[j], &sh.spec_npre[j]);
+      }
+    }
+    // (at level 0 of the overlap and of the run-ahead only wave 0 takes the root)
+    const bool deal = !((pipe || run_ahead) && d == 0 && wave != 0);
     int gnext = 0;
     if (deal && lane == 0) gnext = atomicAdd(&sh.next[cur], 1);
     for (int it = 0; it <= nb && deal; ++it) {
@@ -1938,9 +2057,22 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
 
       uint32_t* ch = L.choice + seg;
       bool allp = false;
-      const int fe = replay ? replay_picks(mem, m, k, L.pick2, ch, cnt_s)
-                            : group_chain<RMAX, WIDE>(f, tb, first, k, Np0, m, c, ch, cnt_s, cscr,
-                                                pipe && d == 0 ? &sh.progress : nullptr, &allp);
+      // a level-1 group whose chain a follower ran ahead for at least m ranks replays it
+      int spec_j = -1;
+      if constexpr (WIDE) {
+        if (d == 1 && run_ahead) {
+#pragma unroll
+          for (int j = 0; j < kSpecSlots; ++j)
+            if (sh.spec_node[j] == p && sh.spec_m[j] >= m) spec_j = j;
+        }
+      }
+      const int fe =
+          replay ? replay_picks(mem, m, k, L.pick2, ch, cnt_s)
+          : spec_j >= 0
+              ? replay_spec(L.spec + spec_j * W, m, k, sh.spec_npre[spec_j], ch, cnt_s, &allp)
+              : group_chain<RMAX, WIDE>(ChainRows{f.N, f.W, f.P}, tb, first, k, Np0, m,
+                                        ChainCfg{c.c_puct, c.vlf, c.vli}, ch, cnt_s, cscr,
+                                        pipe && d == 0 ? &sh.progress : nullptr, &allp);
       if (lane == 0) {
         atomicAdd(&sh.st[OMQ_ST_INTERNAL], 1ull);
         // (a row whose picks are all first-unvisited children is scanned up to its last pick)
@@ -2073,6 +2205,7 @@ __device__ inline void start_group(const LevelLds& L, LevelShared<NT>& sh, int W
   for (int r = tid; r < m; r += NT)
     L.buf[cur * W + seg + r] = mem_src ? mem_src[r] : (uint16_t)(seg + r);
   if (tid < OMQ_NSTATS) sh.st[tid] = 0;
+  if (tid < 8) sh.spec_node[tid] = -1;
   if (tid == 0) {
     // a single member goes to the single-member groups of the kernels that keep them apart
     const bool big = !SelTraits<RMAX>::kSingles || m > SelTraits<RMAX>::kSmall;
@@ -2164,8 +2297,12 @@ __global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c)
       atomicOr(&f.status[0], OMQ_STATUS_COUNTLIMIT);
   }
   start_group<RMAX, NT>(L, sh, W, 0, 0, 0, W, nullptr);
+  // the run-ahead needs an internal root of a row the kernel takes, an integer virtual loss
+  // and levels below 1 (a level-1 group at the last level is a leaf)
+  const bool run_ahead = NT <= 512 && L.spec != nullptr && c.vli > 0 && c.max_depth >= 3 &&
+                         root_k > 0 && root_first >= 0 && root_k <= RMAX * kWave;
   level_loop<RMAX, NT, NT <= 512>(f, c, t, 0, c.max_depth, W, L, sh, &s_glog, lfs, lflag, pipe,
-                                  root_first, pipe ? 2 : -1);
+                                  root_first, pipe ? 2 : -1, run_ahead, root_k);
   __syncthreads();
   finish_tree<NT>(f, t, W, lfs, lflag, sh.wtot);
   __syncthreads();
@@ -2251,8 +2388,11 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   // the LDS limit is raised once per device and kernel (the attribute is idempotent, so two
   // threads racing here both set it)
   if (!cache || !g_attr_set[dev][rmax].load(std::memory_order_acquire)) {
-    e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)level_lds_bytes<1024>(OMQ_MAX_WAVE, true));
+    const size_t lds_max =
+        k.threads == 1024
+            ? std::max(level_lds_bytes<1024>(OMQ_MAX_WAVE, true), level_lds_bytes<1024>(kPipeMaxW, true))
+            : std::max(level_lds_bytes<512>(OMQ_MAX_WAVE, false), level_lds_bytes<512>(kPipeMaxW, false));
+    e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
     if (e != hipSuccess) return e;
     if (cache) g_attr_set[dev][rmax].store(true, std::memory_order_release);
   }
