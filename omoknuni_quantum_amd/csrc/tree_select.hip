@@ -664,10 +664,12 @@ __device__ __noinline__ uint32_t top64_threshold_near(RowKeys<R> keys, int k, ui
 }
 
 // With `progress` set, the chain publishes its progress after every block of 64 ranks: the
-// block's picks are in ch first (workgroup-scope release), then *progress = ranks done.
-// PARTIAL: ranks [0, npre) were taken by the first-unvisited prefix (unvisited_prefix), whose
-// counts (0 or 1) are in cnt_s; the chain starts at rank npre.  Else npre is 0 and cnt_s is
-// cleared here.
+// block's picks are in ch first (workgroup-scope release), then *progress = ranks done.  With
+// `stop` set, the chain ends after the first block that finds *stop non-zero (its picks up to
+// the last published rank are in ch; its counts in cnt_s are then not kept).
+// PARTIAL: ranks [0, npre) were taken before the chain (by the first-unvisited prefix,
+// unvisited_prefix, or by a chain run ahead), with their picks in ch and their counts per
+// child in cnt_s; the chain starts at rank npre.  Else npre is 0 and cnt_s is cleared here.
 // What a chain reads of the forest and the configuration, passed by value: a chain the
 // compiler keeps out of line then takes them in registers (a reference to the kernel's SelArgs
 // would make every lane store a copy of the whole argument block in its private memory).
@@ -685,7 +687,7 @@ struct ChainCfg {
 template <int R, bool PERSIST, bool PARTIAL>
 __device__ int run_chain(ChainRows f, int64_t tb, int first, int k, int Np0, int m, int npre,
                          ChainCfg c, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
-                         int* progress) {
+                         int* progress, const int* stop) {
   const int lane = lane_id();
   const float vlf = c.vlf;
   const float fvl = (float)c.vli;
@@ -707,8 +709,8 @@ __device__ int run_chain(ChainRows f, int64_t tb, int first, int k, int Np0, int
       cpv = c.c_puct * f.P[node];
       d = (float)(1 + n);
       if (PARTIAL) {
-        const int pre = cnt_s[i];  // a pick of the prefix: one virtual loss more
-        if (pre != 0) d = d + fvl;
+        const int pre = cnt_s[i];  // picks before the chain: a virtual loss each
+        d = d + fvl * (float)pre;  // (exact: integers below 2^24)
         if (j == 0) pre0 = pre;
       }
       negcp = negcp || !(cpv >= 0.0f);
@@ -927,6 +929,10 @@ __device__ int run_chain(ChainRows f, int64_t tb, int first, int k, int Np0, int
       if (lane == 0)
         __hip_atomic_store(progress, r0 + rend, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
+    if (stop != nullptr &&
+        __builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) != 0)
+      break;
   }
   if (R > 1 && PERSIST && wopen) close_window();
   // the chain's pick counts per child (R == 1 keeps them in the lanes until here)
@@ -978,35 +984,43 @@ __device__ __noinline__ int unvisited_prefix(const int32_t* N, int64_t tb, int f
 template <int RMAX, bool WIDE>
 __device__ inline int dispatch_chain(ChainRows rows, int64_t tb, int first, int k, int Np0,
                                      int m, int npre, ChainCfg cc, uint32_t* ch, uint16_t* cnt_s,
-                                     float4* cscr, int* progress) {
+                                     float4* cscr, int* progress, const int* stop = nullptr) {
   const int r = (k + kWave - 1) / kWave;  // 1 <= r <= RMAX (checked by the caller)
   // contender windows kept open across blocks in the kernels of up to 4 slots per lane and in
   // the WIDE ones (the other wider kernels' chains have no registers left for it)
   constexpr bool kPersist = RMAX <= 4 || WIDE;
   if (RMAX <= 1 || r <= 1)
-    return run_chain<1, kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
+    return run_chain<1, kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress, stop);
   if (RMAX >= 2 && r == 2)
-    return run_chain<(RMAX >= 2 ? 2 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 2 ? 2 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress, stop);
   if (RMAX >= 3 && r == 3)
-    return run_chain<(RMAX >= 3 ? 3 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 3 ? 3 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress, stop);
   if (RMAX >= 4 && r == 4)
-    return run_chain<(RMAX >= 4 ? 4 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 4 ? 4 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress, stop);
   if (RMAX >= 5 && r == 5)
-    return run_chain<(RMAX >= 5 ? 5 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 5 ? 5 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress, stop);
   if (RMAX >= 6 && r == 6)
-    return run_chain<(RMAX >= 6 ? 6 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
-  return run_chain<(RMAX >= 8 ? 8 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress);
+    return run_chain<(RMAX >= 6 ? 6 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress, stop);
+  return run_chain<(RMAX >= 8 ? 8 : 1), kPersist, WIDE>(rows, tb, first, k, Np0, m, npre, cc, ch, cnt_s, cscr, progress, stop);
 }
 
 // A group's chain: the first-unvisited prefix, and the chain when the prefix does not take
 // every rank.  The WIDE kernels' chains start after the prefix; the others derive its ranks
 // again (starting after them cost the 1024-thread chains up to 60 spilled registers).
 // *all_prefix: every rank was taken by the prefix (distinct children in index order, each
-// picked once).
+// picked once).  taken > 0 (WIDE): ranks [0, taken) are already in ch and their counts in
+// cnt_s (replayed from a chain run ahead, which went past the prefix); the chain goes on from
+// there.
 template <int RMAX, bool WIDE>
 __device__ inline int group_chain(ChainRows rows, int64_t tb, int first, int k, int Np0, int m,
                                   ChainCfg cc, uint32_t* ch, uint16_t* cnt_s, float4* cscr,
-                                  int* progress, bool* all_prefix, int* npre_out = nullptr) {
+                                  int* progress, bool* all_prefix, int* npre_out = nullptr,
+                                  const int* stop = nullptr, int taken = 0) {
+  if (WIDE && taken > 0) {
+    *all_prefix = false;
+    return dispatch_chain<RMAX, WIDE>(rows, tb, first, k, Np0, m, taken, cc, ch, cnt_s, cscr,
+                                      progress, stop);
+  }
   const int npre = unvisited_prefix<RMAX>(rows.N, tb, first, k, m, cc.vli > 0, ch, cnt_s);
   *all_prefix = npre >= m;
   if (npre_out != nullptr) *npre_out = npre;
@@ -1025,7 +1039,7 @@ __device__ inline int group_chain(ChainRows rows, int64_t tb, int first, int k, 
       __hip_atomic_store(progress, npre, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   return dispatch_chain<RMAX, WIDE>(rows, tb, first, k, Np0, m, WIDE ? npre : 0, cc, ch, cnt_s,
-                                    cscr, progress);
+                                    cscr, progress, stop);
 }
 
 // Block-wide exclusive scan of a[0..n) in place (n <= 4 * NT); returns the total.  a may be
@@ -1140,8 +1154,9 @@ struct LevelShared {
   int hist[16];
   int wtot[NT / kWave];
   int spec_node[8];  // the root child of each run-ahead chain (-1: none)
-  int spec_m[8];     // its ranks
+  int spec_m[8];     // its ranks done
   int spec_npre[8];  // its first-unvisited prefix
+  int root_done;     // the root chain is done (the run-ahead chains end)
   unsigned long long st[OMQ_NSTATS];
 };
 
@@ -1819,18 +1834,22 @@ __device__ inline int replay_picks(const uint16_t* mem, int m, int k, const uint
 // and count and on nothing of its members: rank r's pick follows from ranks [0, r) alone (the
 // parent count at rank r is N + VL*(r+1)), and no level before 1 writes the counts of a root
 // child or of its children.  So while one wave runs the root chain, follower j runs the chain
-// of the (j+1)-th most visited root child for M ranks, an estimate of the picks the child
-// gets (1.5 times its share of the root's visits, plus 16, in blocks of 64), and records its
-// picks in spec[0, M).  At level 1 that child's group replays ranks [0, m) when m <= M and
-// runs its chain otherwise.  Nothing of the forest is written.  Records (node, M, prefix
-// length) in *node_out / *m_out / *npre_out (node -1: none run).
+// of the (j+1)-th most visited root child for up to M ranks, M an estimate of the picks the
+// child gets (3 times its share of the root's visits plus 64, in blocks of 64, at most the
+// wave), recording its picks in spec[0, M).  The chain publishes its ranks done in *m_out
+// after each block and ends early once the root chain is done (*stop), so that level 1 does
+// not wait for it.  At level 1 that child's group replays ranks [0, m) when m <= *m_out, and
+// otherwise replays the ranks done and runs its chain on from there.  Nothing of the forest
+// is written.  Records the node (-1: none run) and the first-unvisited prefix length in
+// *node_out / *npre_out.
 template <int RMAX>
 __device__ __noinline__ void run_ahead_chain(ChainRows rows, ChainCfg cc, const int32_t* nchild,
                                              const int32_t* firsts, int64_t tb, int W,
                                              int root_first, int root_k, int j, uint32_t* spec,
-                                             uint16_t* cnt_s, float4* cscr, int* node_out,
-                                             int* m_out, int* npre_out) {
+                                             uint16_t* cnt_s, float4* cscr, const int* stop,
+                                             int* node_out, int* m_out, int* npre_out) {
   const int lane = lane_id();
+  if (lane == 0) *m_out = 0;
   // keys (visits, clamped to 22 bits, + 1) << 9 | (511 - child): the largest is the most
   // visited child, the lower index first among equals; 0 marks no child
   uint32_t key[RMAX];
@@ -1854,7 +1873,7 @@ __device__ __noinline__ void run_ahead_chain(ChainRows rows, ChainCfg cc, const 
     for (int q = 0; q < RMAX; ++q)
       if (key[q] == top) key[q] = 0u;  // (keys are distinct: one lane, one slot)
   }
-  int node = -1, m = 0, npre = 0;
+  int node = -1, npre = 0;
   if (top != 0u) {
     const int ci = 511 - (int)(top & 511u);
     const int p = root_first + 1 + ci;
@@ -1864,35 +1883,33 @@ __device__ __noinline__ void run_ahead_chain(ChainRows rows, ChainCfg cc, const 
     const int Nr = rows.N[tb];
     if (k > 0 && first >= 0 && k <= RMAX * kWave && Nr > 0) {
       const float share = (float)Np0 / (float)Nr;
-      const int est = (int)(1.5f * share * (float)W) + 16;
-      m = min(W, (est + kWave - 1) / kWave * kWave);
+      const int est = (int)(3.0f * share * (float)W) + 64;
+      const int m = min(W, (est + kWave - 1) / kWave * kWave);
       bool allp;
-      group_chain<RMAX, true>(rows, tb, first, k, Np0, m, cc, spec, cnt_s, cscr, nullptr, &allp,
-                              &npre);
+      group_chain<RMAX, true>(rows, tb, first, k, Np0, m, cc, spec, cnt_s, cscr, m_out, &allp,
+                              &npre, stop);
       node = p;
     }
   }
   if (lane == 0) {
     *node_out = node;
-    *m_out = m;
     *npre_out = npre;
   }
 }
 
-// Replays ranks [0, m) of a chain run ahead for at least m ranks (spec, as the chain wrote
-// them) into ch, and the child counts of those ranks into cnt_s[0, k) (packed two to a 32-bit
-// word: counts stay below 2^16).  Returns the first rank without a child, or -1;
-// *all_prefix: every rank was taken by the first-unvisited prefix (npre of the run ahead).
-__device__ inline int replay_spec(const uint32_t* spec, int m, int k, int npre, uint32_t* ch,
-                                  uint16_t* cnt_s, bool* all_prefix) {
+// Replays ranks [0, n) of a chain run ahead (spec, as the chain wrote them) into ch, and the
+// child counts of those ranks into cnt_s[0, k) (packed two to a 32-bit word: counts stay below
+// 2^16).  Returns the first rank without a child, or -1.
+__device__ inline int replay_spec(const uint32_t* spec, int n, int k, uint32_t* ch,
+                                  uint16_t* cnt_s) {
   const int lane = lane_id();
   for (int i = lane; i < k; i += kWave) cnt_s[i] = 0;
   wave_sync();
   uint32_t* cnt2 = reinterpret_cast<uint32_t*>(cnt_s);
   int fe = -1;
-  for (int r0 = 0; r0 < m; r0 += kWave) {
+  for (int r0 = 0; r0 < n; r0 += kWave) {
     const int r = r0 + lane;
-    const bool v = r < m;
+    const bool v = r < n;
     const uint32_t cv = v ? spec[r] : kNoChild;
     if (v) ch[r] = cv;
     const uint64_t none = __ballot(v && cv == kNoChild);
@@ -1903,7 +1920,6 @@ __device__ inline int replay_spec(const uint32_t* spec, int m, int k, int npre, 
     }
   }
   wave_sync();
-  *all_prefix = npre >= m;
   return fe;
 }
 
@@ -1992,7 +2008,8 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
         const int j = wave - 1;
         run_ahead_chain<RMAX>(ChainRows{f.N, f.W, f.P}, ChainCfg{c.c_puct, c.vlf, c.vli},
                               f.nchild, f.first, tb, W, root_first, root_k, j, L.spec + j * W,
-                              cnt_s, cscr, &sh.spec_node[j], &sh.spec_m[j], &sh.spec_npre[j]);
+                              cnt_s, cscr, &sh.root_done, &sh.spec_node[j], &sh.spec_m[j],
+                              &sh.spec_npre[j]);
       }
     }
     // (at level 0 of the overlap and of the run-ahead only wave 0 takes the root)
@@ -2008,6 +2025,11 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
       const int seg = (int)(sl & 0xFFFFu);
       const int m = (int)(sl >> 16);
       const uint16_t* mem = buf + cur * W + seg;
+      // the node's count and row are read before the group's stores below: a wait for a load
+      // issued after them would wait for the stores as well (one counter, in issue order)
+      int Np0 = N[tb + p];
+      const int k = f.nchild[tb + p];
+      const int first = f.first[tb + p];
 
       // log the group and record the path entries
       int gid = 0;
@@ -2023,9 +2045,6 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
         w.gmembers[((int64_t)t * MD + d) * MW + seg + r] = (uint16_t)s;
       }
 
-      int Np0 = N[tb + p];
-      const int k = f.nchild[tb + p];
-      const int first = f.first[tb + p];
       if (vl_done) {
         Np0 -= c.vli * m;  // the members' virtual loss is in N already
       } else if (c.vl_atomic) {
@@ -2057,22 +2076,46 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
 
       uint32_t* ch = L.choice + seg;
       bool allp = false;
-      // a level-1 group whose chain a follower ran ahead for at least m ranks replays it
-      int spec_j = -1;
+      // a level-1 group whose chain a follower ran ahead replays its ranks: all of them when
+      // the follower reached m ranks; else those done, and its chain goes on from there
+      // (when the first-unvisited prefix ended inside them, which makes the prefix length
+      // known, and none of them is without a child)
+      int fe = -1;
+      int taken = 0;
+      bool ahead_done = false;
       if constexpr (WIDE) {
         if (d == 1 && run_ahead) {
+          int sj = -1;
 #pragma unroll
           for (int j = 0; j < kSpecSlots; ++j)
-            if (sh.spec_node[j] == p && sh.spec_m[j] >= m) spec_j = j;
+            if (sh.spec_node[j] == p) sj = j;
+          sj = __builtin_amdgcn_readfirstlane(sj);
+          if (sj >= 0) {
+            const int Ms = __builtin_amdgcn_readfirstlane(sh.spec_m[sj]);
+            const int sp = __builtin_amdgcn_readfirstlane(sh.spec_npre[sj]);
+            const uint32_t* spec = L.spec + sj * W;
+            if (Ms >= m) {
+              fe = replay_spec(spec, m, k, ch, cnt_s);
+              allp = sp >= m;
+              ahead_done = true;
+            } else if (sp < Ms && replay_spec(spec, Ms, k, ch, cnt_s) < 0) {
+              taken = Ms;
+            }
+          }
         }
       }
-      const int fe =
-          replay ? replay_picks(mem, m, k, L.pick2, ch, cnt_s)
-          : spec_j >= 0
-              ? replay_spec(L.spec + spec_j * W, m, k, sh.spec_npre[spec_j], ch, cnt_s, &allp)
-              : group_chain<RMAX, WIDE>(ChainRows{f.N, f.W, f.P}, tb, first, k, Np0, m,
-                                        ChainCfg{c.c_puct, c.vlf, c.vli}, ch, cnt_s, cscr,
-                                        pipe && d == 0 ? &sh.progress : nullptr, &allp);
+      if (replay)
+        fe = replay_picks(mem, m, k, L.pick2, ch, cnt_s);
+      else if (!ahead_done)
+        fe = group_chain<RMAX, WIDE>(ChainRows{f.N, f.W, f.P}, tb, first, k, Np0, m,
+                                     ChainCfg{c.c_puct, c.vlf, c.vli}, ch, cnt_s, cscr,
+                                     pipe && d == 0 ? &sh.progress : nullptr, &allp, nullptr,
+                                     nullptr, taken);
+      if constexpr (WIDE) {
+        // the followers' chains end at their next block
+        if (d == 0 && run_ahead && lane == 0)
+          __hip_atomic_store(&sh.root_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
       if (lane == 0) {
         atomicAdd(&sh.st[OMQ_ST_INTERNAL], 1ull);
         // (a row whose picks are all first-unvisited children is scanned up to its last pick)
@@ -2220,6 +2263,7 @@ __device__ inline void start_group(const LevelLds& L, LevelShared<NT>& sh, int W
     sh.next[1] = 0;
     sh.snext = 0;
     sh.progress = 0;
+    sh.root_done = 0;
   }
   __syncthreads();
 }
