@@ -15,6 +15,7 @@ roofline, CPU baseline and full-size parity check.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -174,6 +175,8 @@ def measure(name: str, args, steps: int, warmup: int, extras: bool) -> dict:
                 "us_per_launch": round(d_s * 1e6, 3)}
     if traffic_src:
         roofline["traffic_source"] = traffic_src
+    if dominant == "select":
+        roofline["serial_floor"] = serial_floor(st, wl.num_trees, dn, d_s * 1e6)
     whole_bytes = sum(ab.values())
     out = {
         "value": round(value, 1),
@@ -216,6 +219,27 @@ def measure(name: str, args, steps: int, warmup: int, extras: bool) -> dict:
     del eng, ev
     torch.cuda.empty_cache()
     return out
+
+
+def serial_floor(st, trees, launches, select_us) -> dict:
+    """The selection's serial part: each tree's root chain (one dependent argmax step per
+    simulation of the wave) runs before any deeper level can finish, so a launch takes at least
+    its longest root chain.  The kernel times the chain with the device's constant wall clock
+    (counter rootchain, ticks summed over trees and launches); the floor is its mean per tree
+    and launch, beside the steps per launch, the time per step and select's time over it."""
+    from omoknuni_quantum_amd import _lib
+
+    khz = ctypes.c_int32(0)
+    _lib.check(_lib.load().omq_wall_clock_khz(ctypes.byref(khz)), "omq_wall_clock_khz")
+    chain_us = st["rootchain"] / (khz.value * 1e-3) / (trees * launches)
+    steps = st["sims"] / (trees * launches)
+    return {"root_chain_us_per_launch": round(chain_us, 3),
+            "root_chain_steps_per_launch": round(steps, 1),
+            "ns_per_step": round(1e3 * chain_us / steps, 2) if steps else None,
+            "select_over_floor": round(select_us / chain_us, 3) if chain_us else None,
+            "clock_khz": khz.value,
+            "source": "counter rootchain (s_memrealtime around the root group's chain in "
+                      "select_root_kernel), mean over the timed launches and trees"}
 
 
 def run(args) -> dict:

@@ -174,6 +174,9 @@ typedef struct omq_wave {
 #define OMQ_ST_STEPS 8        /* argmax steps (simulation x level decisions) */
 #define OMQ_ST_CAPFAIL 9      /* expansions refused for lack of capacity */
 #define OMQ_ST_ULEAFPATH 10   /* sum over unique leaves of path length (omq_leaf_info) */
+#define OMQ_ST_ROOTCHAIN 11   /* omq_select: duration of the root's chain (the serial part of a
+                                 wave's selection), in ticks of the device's constant wall clock
+                                 (omq_wall_clock_khz) */
 #define OMQ_NSTATS 16
 
 /* device status bits */
@@ -218,6 +221,10 @@ int omq_select_options(int32_t spin_limit);
 /* The spin limit omq_select launches with (for callers that record graphs and key them by
  * the launch arguments); no counterpart in the reference. */
 int32_t omq_select_spin_limit(void);
+
+/* Frequency (kHz) of the constant wall clock of the current device, the unit of
+ * OMQ_ST_ROOTCHAIN; no counterpart in the reference (measurement of selection's serial part). */
+int omq_wall_clock_khz(int32_t* khz);
 
 /* Compute the hash key and the number of legal actions of every unique leaf of the wave.
  * (Game-model step between selection and evaluation; no reference counterpart in the

@@ -25,7 +25,7 @@ OMQ_MAX_WAVE, OMQ_MAX_ROW, OMQ_MAX_DEPTH, OMQ_MAX_ACTIONS = 4096, 512, 128, 8192
 OMQ_NSTATS = 16
 STAT_NAMES = [
     "internal", "rowsum", "pathnodes", "pathentries", "uleaves", "expanded", "newchild",
-    "sims", "steps", "capfail", "uleafpath",
+    "sims", "steps", "capfail", "uleafpath", "rootchain",
 ]
 OMQ_STATUS_NOCHILD, OMQ_STATUS_ROWLIMIT, OMQ_STATUS_STALL, OMQ_STATUS_COUNTLIMIT = 1, 2, 4, 8
 OMQ_RULE_FREESTYLE, OMQ_RULE_RENJU = 0, 1
@@ -80,6 +80,7 @@ SIGNATURES = {
     "omq_leaf_info": (ctypes.c_int, [_FP, _WP, _p]),
     "omq_select_options": (ctypes.c_int, [_i32]),
     "omq_select_spin_limit": (ctypes.c_int32, []),
+    "omq_wall_clock_khz": (ctypes.c_int, [_p]),
     "omq_synthetic_evaluate": (ctypes.c_int, [_FP, _WP, ctypes.c_float, _p]),
     "omq_expand": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _p, ctypes.c_double, _p]),
     "omq_backup": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _i32, _p]),

@@ -9,7 +9,6 @@
 #include "omq_tree_ops.h"
 
 namespace omq {
-size_t select_lds_bytes(int W);
 hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_puct,
                          float virtual_loss, int max_depth, int vl_atomic, hipStream_t stream);
 void select_set_options(int spin_limit);
@@ -232,6 +231,16 @@ int omq_select_options(int32_t spin_limit) {
 }
 
 int32_t omq_select_spin_limit(void) { return omq::select_spin_limit(); }
+
+int omq_wall_clock_khz(int32_t* khz) {
+  if (khz == nullptr) return fail(OMQ_E_ARG, "khz is null");
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&v, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    return fail(OMQ_E_LAUNCH, "hipDeviceGetAttribute(WallClockRate) failed");
+  *khz = v;
+  return OMQ_OK;
+}
 
 int omq_leaf_info(const omq_forest* f, const omq_wave* w, void* stream) {
   int rc = check_forest(f);

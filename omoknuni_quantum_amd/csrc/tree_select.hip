@@ -2104,6 +2104,8 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
           }
         }
       }
+      // (the root's chain is timed: the serial part of the selection)
+      const uint64_t tc0 = d == 0 ? __builtin_amdgcn_s_memrealtime() : 0ull;
       if (replay)
         fe = replay_picks(mem, m, k, L.pick2, ch, cnt_s);
       else if (!ahead_done)
@@ -2116,6 +2118,9 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
         if (d == 0 && run_ahead && lane == 0)
           __hip_atomic_store(&sh.root_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
+      if (d == 0 && lane == 0)
+        atomicAdd(&sh.st[OMQ_ST_ROOTCHAIN],
+                  (unsigned long long)(__builtin_amdgcn_s_memrealtime() - tc0 + (uint64_t)(fe & 0)));
       if (lane == 0) {
         atomicAdd(&sh.st[OMQ_ST_INTERNAL], 1ull);
         // (a row whose picks are all first-unvisited children is scanned up to its last pick)

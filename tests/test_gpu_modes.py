@@ -196,3 +196,33 @@ def test_count_limit_is_reported(device):
         eng.check_status()
     eng.reset()
     eng.check_status()
+
+
+def test_root_chain_counter_within_select_time(device):
+    """The root-chain counter (OMQ_ST_ROOTCHAIN, wall-clock ticks) is positive after a search,
+    and its mean per launch stays below select's own time per launch (the chain is part of the
+    launch), which bench.py's serial floor relies on."""
+    import ctypes
+    from omoknuni_quantum_amd.core.timing import PhaseTimer
+
+    wl = get("C3").scaled(name="C3-floor", num_trees=4, num_simulations=2048, capacity=800_000)
+    params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth,
+                          dirichlet_epsilon=wl.dirichlet_epsilon)
+    eng = WaveEngine(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth, device,
+                     params)
+    eng.set_roots(*wl.root_inputs())
+    ev = SyntheticEvaluator(wl.logit_scale)
+    khz = ctypes.c_int32(0)
+    _lib.check(_lib.load().omq_wall_clock_khz(ctypes.byref(khz)), "omq_wall_clock_khz")
+    assert khz.value > 0
+    eng.search(wl.num_simulations, wl.wave_size, ev)
+    torch.cuda.synchronize()
+    eng.stats.zero_()
+    timer = PhaseTimer(torch.device(device))
+    eng.search(wl.num_simulations, wl.wave_size, ev, timer)
+    tot = timer.totals_ms()
+    st = eng.host_stats()
+    launches = timer.counts["select"]
+    chain_ms = st["rootchain"] / khz.value / (wl.num_trees * launches)
+    assert st["rootchain"] > 0
+    assert 0.0 < chain_ms < tot["select"] / launches
