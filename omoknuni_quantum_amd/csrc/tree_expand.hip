@@ -486,9 +486,13 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
     if (lane == 0) atomicOr(&w.status[0], OMQ_STATUS_ROWLIMIT);
     return;
   }
-  // children: the first k chosen actions, ascending
-  for (int j = lane; j < k; j += kWave) {
-    const int64_t node = tb + cbase + j;
+  // children: the first k chosen actions, ascending.  Rows of at least 4 * 64 children are
+  // written 16 bytes per lane (four children) from the first node index that is a multiple of
+  // 4, the children before it and after the last whole quad one per lane; shorter rows one per
+  // lane (C3 expand_write 48.8 -> 47.6 us; quads on rows of 20-45 children, C4, cost 7 %).
+  const int64_t node0 = tb + cbase;
+  auto put1 = [&](int j) {
+    const int64_t node = node0 + j;
     f.visit_counts[node] = 0;
     f.value_sums[node] = 0.0f;
     f.priors[node] = (float)l.val[j];
@@ -496,7 +500,30 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
     f.actions[node] = l.list[j];
     f.first_child[node] = -1;
     f.num_children[node] = 0;
+  };
+  if (k < 4 * kWave) {
+    for (int j = lane; j < k; j += kWave) put1(j);
+    return;
   }
+  const int hd = (int)((4 - (node0 & 3)) & 3);  // (< 4 <= k)
+  if (lane < hd) put1(lane);
+  const int nq = (k - hd) >> 2;
+  for (int q = lane; q < nq; q += kWave) {
+    const int j = hd + 4 * q;
+    const int64_t node = node0 + j;
+    const float4 pr = make_float4((float)l.val[j], (float)l.val[j + 1], (float)l.val[j + 2],
+                                  (float)l.val[j + 3]);
+    const int4 ac = make_int4(l.list[j], l.list[j + 1], l.list[j + 2], l.list[j + 3]);
+    *reinterpret_cast<int4*>(f.visit_counts + node) = make_int4(0, 0, 0, 0);
+    *reinterpret_cast<float4*>(f.value_sums + node) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    *reinterpret_cast<float4*>(f.priors + node) = pr;
+    *reinterpret_cast<int4*>(f.parents + node) = make_int4(leaf, leaf, leaf, leaf);
+    *reinterpret_cast<int4*>(f.actions + node) = ac;
+    *reinterpret_cast<int4*>(f.first_child + node) = make_int4(-1, -1, -1, -1);
+    *reinterpret_cast<int4*>(f.num_children + node) = make_int4(0, 0, 0, 0);
+  }
+  const int tl = hd + 4 * nq;
+  if (lane < k - tl) put1(tl + lane);
 }
 
 // ---------------------------------------------------------------------------------------
