@@ -47,6 +47,12 @@ CASES = {
     "C4-fullcount": ("C4", {"num_trees": 2}),
     # C2 at its full simulation count and capacity on two trees (1600 simulations, waves of 256)
     "C2-fullcount": ("C2", {"num_trees": 2}),
+    # peaked priors on Go rows: one root child takes most of a wave, so that level-1 groups
+    # outgrow the chains run ahead for them (replayed in part and continued, or run anew)
+    "runahead-peaked": ("C3", {"num_trees": 4, "num_simulations": 3072, "wave_size": 1024,
+                               "capacity": 500_000, "logit_scale": 10.0}),
+    "runahead-depth3": ("C3", {"num_trees": 2, "num_simulations": 2048, "wave_size": 512,
+                               "capacity": 500_000, "max_depth": 3}),
     # tiny capacities: the capacity-full rule at every fill level (first fit in first-occurrence
     # order, refused leaves backed up), with 1-10 children per leaf or counts falling by depth
     "capacity-sparse-60": ("C4", {"model": games.chess_sparse(64, 1, 10), "num_trees": 16,
