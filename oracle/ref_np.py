@@ -614,6 +614,98 @@ def overlap_select(tree: NpTree, W: int, max_depth: int, block: int = 64):
     return paths
 
 
+RUNAHEAD_VARIANTS = ("resume_without_counts", "resume_parent_count_restarted")
+
+
+def runahead_select(tree: NpTree, W: int, max_depth: int, budgets: dict, done: dict,
+                    variant=None):
+    """The run-ahead of level-1 chains (512-thread select kernels), restated.  Before the root
+    chain, root child c (a key of budgets) runs its own chain for budgets[c] ranks from the
+    wave's start state (N of c and of c's children as they are), recording its picks; done[c]
+    <= budgets[c] is how many of those ranks it finished (a chain stopped early).  After the
+    root chain, c's level-1 group of m members takes the record's first m picks when done[c] >=
+    m; otherwise it takes the done[c] recorded picks and continues the chain from rank done[c]
+    with those picks' virtual loss on the children; groups without a record run their chain.
+    Deeper levels as grouped_select.  Returns the paths; must equal W sequential select_paths.
+    variant: "resume_without_counts" continues without the recorded picks' virtual loss;
+    "resume_parent_count_restarted" continues with the parent count of rank 0 at rank done[c]."""
+    vli = tree.vli
+    if (not tree.expanded[0]) or tree.nchild[0] == 0 or max_depth <= 2:
+        return grouped_select(tree, W, max_depth)
+
+    def chain(p, np0, m, start=()):
+        """picks of ranks len(start)..m-1 of p's chain, the picks `start` already made"""
+        f, k = int(tree.first[p]), int(tree.nchild[p])
+        saved = {int(tree.children[f + i]): int(tree.N[int(tree.children[f + i])])
+                 for i in range(k)}
+        extra, picks = {}, list(start)
+        if variant != "resume_without_counts":
+            for c in start:
+                if c >= 0:
+                    extra[c] = extra.get(c, 0) + 1
+        for r in range(len(start) + 1, m + 1):
+            for c, n in saved.items():
+                tree.N[c] = n + vli * extra.get(c, 0)
+            rr = r - len(start) if variant == "resume_parent_count_restarted" else r
+            c = tree.best_child(p, np0 + vli * rr)
+            picks.append(c)
+            if c >= 0:
+                extra[c] = extra.get(c, 0) + 1
+        for c, n in saved.items():
+            tree.N[c] = n
+        return picks
+
+    records = {}
+    for c, M in budgets.items():
+        if tree.expanded[c] and tree.nchild[c] > 0:
+            records[c] = chain(c, int(tree.N[c]), M)[:done[c]]
+    n_root = int(tree.N[0])
+    root_pick = chain(0, n_root, W)
+    tree.N[0] = n_root + vli * W
+    members = {}
+    for s in range(W):
+        if root_pick[s] >= 0:
+            members.setdefault(root_pick[s], []).append(s)
+    for c in members:  # the level-1 nodes' virtual loss
+        tree.N[c] += vli * len(members[c])
+    paths = [[0] for _ in range(W)]
+    groups = {}
+    for c, mem in members.items():
+        for s in mem:
+            paths[s].append(c)
+        if (not tree.expanded[c]) or tree.nchild[c] == 0:
+            continue
+        np0 = int(tree.N[c]) - vli * len(mem)
+        m = len(mem)
+        rec = records.get(c)
+        if rec is not None and len(rec) >= m:
+            picks = rec[:m]
+        elif rec is not None:
+            picks = chain(c, np0, m, start=rec)
+        else:
+            picks = chain(c, np0, m)
+        for s, x in zip(mem, picks):
+            if x >= 0:
+                paths[s].append(x)
+                groups.setdefault(x, []).append(s)
+    depth = 2
+    while groups:
+        nxt = {}
+        for p, mem in groups.items():
+            if (not tree.expanded[p]) or tree.nchild[p] == 0 or depth == max_depth - 1:
+                continue
+            for s, x in zip(mem, chain(p, int(tree.N[p]), len(mem))):
+                if x >= 0:
+                    paths[s].append(x)
+                    nxt.setdefault(x, []).append(s)
+        groups = nxt
+        depth += 1
+    for path in paths:
+        for x in path[2:]:
+            tree.N[x] += vli
+    return paths
+
+
 def fused_ucb_selection(node_indices, children_start, children_end, children, q_values,
                         visit_counts, priors, c_puct):
     """mcts::fused_ucb_selection as its CUDA kernel computes it

@@ -210,6 +210,65 @@ def test_overlap_selection_equals_sequential(seed):
         ref_np.np_wave(t, w, 100, legal_of, pol, val)
 
 
+def _runahead_check(seed):
+    """Run-ahead schedules against sequential select_path on one seeded search; returns how
+    often each planted misreading differed."""
+    import copy
+    rng = np.random.default_rng(500 + seed)
+    bs = 3  # (9 actions: rows fill up, so that picks depend on the parent count)
+    A = bs * bs
+    root_empty = list(range(A))
+    legal_of = lambda pacts: ref_np.board_legal(root_empty, pacts)
+    vl = [3.0, 1.0, 2.0][seed % 3]
+    t = ref_np.NpTree(4000, 1.4, vl)
+    caught = {v: 0 for v in ref_np.RUNAHEAD_VARIANTS}
+    compared = 0
+    for it in range(30):
+        w = 1 if it == 0 else int(rng.integers(2, 9))
+        pol = rng.random((w, A)).astype(np.float32)
+        if seed % 2:
+            pol[:] = 1.0  # equal priors: many exact ties
+        val = np.round(rng.random(w) * 4 - 2).astype(np.float32) / 4
+        W = int(rng.integers(2, 16))
+        if t.expanded[0] and t.nchild[0] > 0:
+            f, k = int(t.first[0]), int(t.nchild[0])
+            kids = [int(t.children[f + i]) for i in range(k)]
+            for max_depth in (100, 3):
+                for trial in range(4):
+                    chosen = rng.choice(kids, size=min(len(kids), int(rng.integers(1, 5))),
+                                        replace=False)
+                    budgets = {int(c): int(rng.integers(1, W + 3)) for c in chosen}
+                    done = {c: int(rng.integers(0, M + 1)) for c, M in budgets.items()}
+                    a, b = copy.deepcopy(t), copy.deepcopy(t)
+                    seq = [a.select_path(max_depth) for _ in range(W)]
+                    ra = ref_np.runahead_select(b, W, max_depth, budgets, done)
+                    assert seq == ra, (it, max_depth, budgets, done)
+                    assert np.array_equal(a.N, b.N), (it, max_depth)
+                    compared += 1
+                    for v in ref_np.RUNAHEAD_VARIANTS:
+                        c = copy.deepcopy(t)
+                        bad = ref_np.runahead_select(c, W, max_depth, budgets, done, variant=v)
+                        caught[v] += int(bad != seq)
+        ref_np.np_wave(t, w, 100, legal_of, pol, val)
+    assert compared >= 40
+    return caught
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_runahead_selection_equals_sequential(seed):
+    """Level-1 chains run ahead of the root chain from the wave's start state, replayed whole
+    or in part and continued (run-ahead budgets and ranks done drawn at random, from none of a
+    group's ranks to more than all), reproduce sequential select_path exactly; continuing
+    without the recorded picks' virtual loss does not."""
+    assert _runahead_check(seed)["resume_without_counts"] > 0
+
+
+def test_runahead_planted_parent_count():
+    """Continuing a recorded chain with the parent count of rank 0 instead of the rank reached
+    differs from sequential select_path (over the seeded searches of the test above)."""
+    assert sum(_runahead_check(seed)["resume_parent_count_restarted"] for seed in (0, 2, 4)) > 0
+
+
 def test_search_invariants_all_workload_models():
     from omoknuni_quantum_amd.synthetic.workloads import get
     for name, kw in [("C1", {"num_simulations": 256}), ("C3", {"num_trees": 1, "num_simulations": 2048}),
