@@ -53,6 +53,14 @@ CASES = {
                                "capacity": 500_000, "logit_scale": 10.0}),
     "runahead-depth3": ("C3", {"num_trees": 2, "num_simulations": 2048, "wave_size": 512,
                                "capacity": 500_000, "max_depth": 3}),
+    # the largest wave (OMQ_MAX_WAVE): no run-ahead chains and no level overlap (their LDS
+    # records hold waves of at most 2048 simulations), in the 6-, 4- and 1-slot kernels
+    "maxwave-C3": ("C3", {"num_trees": 1, "num_simulations": 8192, "wave_size": 4096,
+                          "capacity": 1_000_000}),
+    "maxwave-C2": ("C2", {"num_trees": 2, "num_simulations": 8192, "wave_size": 4096,
+                          "capacity": 400_000}),
+    "maxwave-C4": ("C4", {"num_trees": 1, "num_simulations": 8192, "wave_size": 4096,
+                          "capacity": 400_000}),
     # tiny capacities: the capacity-full rule at every fill level (first fit in first-occurrence
     # order, refused leaves backed up), with 1-10 children per leaf or counts falling by depth
     "capacity-sparse-60": ("C4", {"model": games.chess_sparse(64, 1, 10), "num_trees": 16,
