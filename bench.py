@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0
 TREE_PHASES = ("select", "leaf_info", "expand", "backup")
 
 
-def algorithmic_bytes(st: dict, sims: int) -> dict:
+def algorithmic_bytes(st: dict, sims: int, wave: int) -> dict:
     """Compulsory HBM bytes of each tree-operation kernel family over the timed region,
     from the device counters (the stats slots OMQ_ST_* of omq_tree_ops.h):
       select    16 B per visited node (row header N, first, nchild + N write of the virtual
@@ -39,19 +39,26 @@ def algorithmic_bytes(st: dict, sims: int) -> dict:
                 first-unvisited children is scanned up to its last pick, where the reference's
                 scan stops) + 4 B per path entry (path output) + 8 B per simulation (leaf and
                 path length)
-      leaf_info 8 B per path entry below the root of each unique leaf's path (the entry and its
-                node's action) + 20 B per unique leaf (first simulation, path length, key,
-                legal count)
+      records   the unique leaves' keys and legal counts: 8 B per path entry below the root of
+                each unique leaf's path (the entry and its node's action) + 20 B per unique
+                leaf (first simulation, path length, key, legal count).  Formed at the end of
+                select for waves of at most OMQ_SELECT_RECORDS_MAX_WAVE simulations (counted
+                with select), else by leaf_info_kernel (the leaf_info phase, which also holds
+                the rule kernels when a rule is on; those are not modelled)
       expand    8 B per expanded leaf (row header) + 28 B per child written (N, W, P, parent,
                 action, row offset, row length) + 4 B per prior gathered (= per child in the
                 full policy)
       backup    16 B per visited node (N and W read and written) + 4 B per path entry
                 (signed leaf value read) + 12 B per simulation (value, uid, length)
     """
+    from omoknuni_quantum_amd import _lib
+
     G, K, PE = st["pathnodes"], st["rowsum"], st["pathentries"]
+    records = 8 * (st["uleafpath"] - st["uleaves"]) + 20 * st["uleaves"]
+    in_select = wave <= _lib.OMQ_SELECT_RECORDS_MAX_WAVE
     return {
-        "select": 16 * G + 12 * K + 4 * PE + 8 * sims,
-        "leaf_info": 8 * (st["uleafpath"] - st["uleaves"]) + 20 * st["uleaves"],
+        "select": 16 * G + 12 * K + 4 * PE + 8 * sims + (records if in_select else 0),
+        "leaf_info": 0 if in_select else records,
         "expand": 8 * st["expanded"] + 32 * st["newchild"],
         "backup": 16 * G + 4 * PE + 12 * sims,
     }
@@ -155,7 +162,7 @@ def measure(name: str, args, steps: int, warmup: int, extras: bool) -> dict:
     tree_ms = sum(tot.get(p, 0.0) for p in TREE_PHASES)
     eval_ms = tot.get("eval", 0.0)
     value = sims / (tree_ms / 1e3)
-    ab = algorithmic_bytes(st, st["sims"])
+    ab = algorithmic_bytes(st, st["sims"], wl.wave_size)
     phases = {}
     for p in TREE_PHASES:
         n = timer.counts.get(p, 0)
@@ -314,7 +321,7 @@ def next_rows(wl, eng, ev) -> dict:
             boards = np.zeros((wl.num_trees, wl.model.board_size, wl.model.board_size), np.int8)
         eng.set_gomoku_rules(boards, _lib.OMQ_RULE_FREESTYLE)
         eng.select(wl.wave_size)
-        eng.leaf_info()
+        eng.leaf_info(wl.wave_size)
         reps = 20
         torch.cuda.synchronize()
         start.record()

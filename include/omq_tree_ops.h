@@ -98,6 +98,11 @@ extern "C" {
 #define OMQ_MAX_WAVE 4096   /* simulations per tree per wave */
 #define OMQ_MAX_ROW 512     /* children per node (a selection row is held in registers) */
 #define OMQ_MAX_DEPTH 128   /* nodes on a path */
+/* omq_select forms the unique leaves' records (ukey, ulegal) for waves of at most this many
+ * simulations; after a larger wave the caller runs omq_leaf_info, whose launch over all the
+ * wave's leaves, spread over the device, is the faster of the two there (one workgroup per
+ * tree forms them inside select) */
+#define OMQ_SELECT_RECORDS_MAX_WAVE 512
 #define OMQ_MAX_ACTIONS 8192
 
 typedef struct omq_forest {
@@ -151,8 +156,8 @@ typedef struct omq_wave {
                                leaves, written by omq_go_rules.  When it is not NULL,
                                omq_synthetic_evaluate and omq_expand take a board leaf's legal
                                actions from it (the caller then runs omq_go_rules after
-                               omq_leaf_info in every wave) instead of the root mask minus the
-                               path's cells. */
+                               the leaf records are formed in every wave) instead of the root
+                               mask minus the path's cells. */
 } omq_wave;
 
 /* default bound of the polls of a wait inside omq_select (omq_select_options) */
@@ -173,7 +178,7 @@ typedef struct omq_wave {
 #define OMQ_ST_SIMS 7         /* simulations selected */
 #define OMQ_ST_STEPS 8        /* argmax steps (simulation x level decisions) */
 #define OMQ_ST_CAPFAIL 9      /* expansions refused for lack of capacity */
-#define OMQ_ST_ULEAFPATH 10   /* sum over unique leaves of path length (omq_leaf_info) */
+#define OMQ_ST_ULEAFPATH 10   /* sum over unique leaves of path length (leaf records) */
 #define OMQ_ST_ROOTCHAIN 11   /* omq_select: duration of the root's chain (the serial part of a
                                  wave's selection), in ticks of the device's constant wall clock
                                  (omq_wall_clock_khz) */
@@ -203,9 +208,11 @@ int omq_forest_reset(const omq_forest* f, void* stream);
  * Result equals running CythonLockFreeTree.select_path (cython_tree_optimized.pyx:177-202,
  * best child :421-464) for simulations 0..wave_size-1 one after another: every node on a
  * path receives +(int)virtual_loss visits as the simulation arrives, and later simulations
- * see it.  Writes paths, path_len, leaves, the unique-leaf list and the group log, and adds
- * the virtual loss to visit_counts.  vl_atomic=1 applies the virtual loss with one atomic
- * per path entry instead of one add per visited node.
+ * see it.  Writes paths, path_len, leaves, the unique-leaf list and the group log, and, for
+ * waves of at most OMQ_SELECT_RECORDS_MAX_WAVE simulations, each unique leaf's key and legal
+ * count (ukey, ulegal, as omq_leaf_info forms them; OMQ_ST_ULEAFPATH), and adds the virtual
+ * loss to visit_counts.  vl_atomic=1 applies the virtual loss with
+ * one atomic per path entry instead of one add per visited node.
  * Replaces fused_select_expand(_optimized) / parallel_select_with_virtual_loss /
  * batch_apply_virtual_loss (python/mcts/gpu/mcts_kernels.cu:451-643,845-860,962-1053). */
 int omq_select(const omq_forest* f, const omq_wave* w, int32_t wave_size, float c_puct,
@@ -228,7 +235,10 @@ int omq_wall_clock_khz(int32_t* khz);
 
 /* Compute the hash key and the number of legal actions of every unique leaf of the wave.
  * (Game-model step between selection and evaluation; no reference counterpart in the
- * kernel module: the reference reads GPUGameStates, python/mcts/gpu/gpu_game_states.py.) */
+ * kernel module: the reference reads GPUGameStates, python/mcts/gpu/gpu_game_states.py.)
+ * Needed after a wave of more than OMQ_SELECT_RECORDS_MAX_WAVE simulations; after a smaller
+ * one omq_select has formed them, and this forms them again (adding to OMQ_ST_ULEAFPATH
+ * again). */
 int omq_leaf_info(const omq_forest* f, const omq_wave* w, void* stream);
 
 /* Synthetic evaluator: for every unique leaf, priors = softmax of seeded approximately
@@ -261,8 +271,9 @@ int omq_expand(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
 int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float virtual_loss,
                int32_t sign_mode, int32_t w_mode, void* stream);
 
-/* Gomoku terminal check of every unique leaf of the wave; call it after omq_leaf_info and
- * before omq_expand.  Needs an OMQ_GAME_BOARD forest with num_actions = bs*bs.
+/* Gomoku terminal check of every unique leaf of the wave; call it after the leaf records are
+ * formed (by omq_select, or by omq_leaf_info after a wave of more than
+ * OMQ_SELECT_RECORDS_MAX_WAVE simulations) and before omq_expand.  Needs an OMQ_GAME_BOARD forest with num_actions = bs*bs.
  * - Position.  A leaf's position is the root board root_boards[t*num_actions + cell] (int8:
  *   0 empty, 1 and 2 stones) with the moves of the leaf's path played in alternating colours.
  *   The first move is played by root_player[t]. When root_player is NULL, it is player 1 if the
@@ -283,8 +294,8 @@ int omq_gomoku_terminal(const omq_forest* f, const omq_wave* w, const int8_t* ro
                         const int32_t* root_player, int32_t rule, int32_t* uterminal,
                         void* stream);
 
-/* Go rules of every unique leaf of the wave; call it after omq_leaf_info and before the
- * evaluator and omq_expand.  Needs an OMQ_GAME_GO forest with num_actions = bs*bs + 1 (the pass
+/* Go rules of every unique leaf of the wave; call it after the leaf records are formed (as for
+ * omq_gomoku_terminal) and before the evaluator and omq_expand.  Needs an OMQ_GAME_GO forest with num_actions = bs*bs + 1 (the pass
  * is action bs*bs), w->umask set, and the root positions root_boards [T*bs*bs] (int8: 0 empty,
  * 1 and 2 stones).
  * - Position.  A leaf's position is its root board with the path's moves played in alternating
@@ -313,8 +324,8 @@ int omq_go_rules(const omq_forest* f, const omq_wave* w, const int8_t* root_boar
                  const int32_t* root_player, const int32_t* root_passes, const int32_t* root_ko,
                  int32_t flags, int32_t* uterminal, void* stream);
 
-/* Neural-network feature planes of every wave slot of a Gomoku forest; call it after
- * omq_leaf_info.  Needs an OMQ_GAME_BOARD forest with num_actions = bs*bs.
+/* Neural-network feature planes of every wave slot of a Gomoku forest; call it after the leaf
+ * records are formed (as for omq_gomoku_terminal).  Needs an OMQ_GAME_BOARD forest with num_actions = bs*bs.
  * - Slots.  out holds num_trees*max_wave slots of planes*bs*bs values (slot t*max_wave+u).
  *   Slot u < ucount[t] receives the position of unique leaf u; the other slots receive zeros.
  * - Position.  As in omq_gomoku_terminal: the root board with the path's moves in alternating

@@ -22,6 +22,7 @@ OMQ_EXPAND_FULL, OMQ_EXPAND_REFERENCE_PW = 0, 1
 OMQ_SIGN_LEAF_POSITIVE, OMQ_SIGN_ROOT_POSITIVE = 0, 1
 OMQ_WACC_ORDERED, OMQ_WACC_ATOMIC = 0, 1
 OMQ_MAX_WAVE, OMQ_MAX_ROW, OMQ_MAX_DEPTH, OMQ_MAX_ACTIONS = 4096, 512, 128, 8192
+OMQ_SELECT_RECORDS_MAX_WAVE = 512
 OMQ_NSTATS = 16
 STAT_NAMES = [
     "internal", "rowsum", "pathnodes", "pathentries", "uleaves", "expanded", "newchild",

@@ -236,11 +236,20 @@ class WaveEngine:
                                         p.virtual_loss, p.max_depth, int(p.vl_atomic),
                                         self.stream_handle()), "omq_select")
 
-    def leaf_info(self) -> None:
-        """Keys and legal counts of the unique leaves; with the Gomoku rule on, also the
-        terminal check (terminal leaves get no legal action, so they are not expanded)."""
-        self._check(self.lib.omq_leaf_info(self.forest_ref, self.wave_ref, self.stream_handle()),
-                    "omq_leaf_info")
+    def needs_leaf_info(self, wave_size: int) -> bool:
+        """Whether a wave of wave_size simulations needs leaf_info before its evaluation: its
+        leaves' keys and legal counts are not formed by select, or a rule is on."""
+        return (wave_size > _lib.OMQ_SELECT_RECORDS_MAX_WAVE or self.rule is not None
+                or self.go_flags is not None)
+
+    def leaf_info(self, wave_size: int) -> None:
+        """The unique leaves' keys and legal counts, where select did not form them (waves of
+        more than OMQ_SELECT_RECORDS_MAX_WAVE simulations), then the rule checks (the Gomoku
+        terminal check: terminal leaves get no legal action, so they are not expanded; the Go
+        rules' legal masks)."""
+        if wave_size > _lib.OMQ_SELECT_RECORDS_MAX_WAVE:
+            self._check(self.lib.omq_leaf_info(self.forest_ref, self.wave_ref,
+                                               self.stream_handle()), "omq_leaf_info")
         if self.rule is not None:
             self.leaf_info_terminal_only()
         if self.go_flags is not None:
@@ -363,8 +372,9 @@ class WaveEngine:
         mark = timer.mark if timer is not None else (lambda _p: None)
         mark("select")
         self.select(wave_size)
-        mark("leaf_info")
-        self.leaf_info()
+        if self.needs_leaf_info(wave_size):
+            mark("leaf_info")
+            self.leaf_info(wave_size)
         mark("eval")
         evaluator.evaluate_wave(self)
         mark("expand")

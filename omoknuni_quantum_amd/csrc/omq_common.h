@@ -315,6 +315,51 @@ __device__ inline int sparse_legal_list(const omq_forest& f, uint64_t k, int* li
   return n;
 }
 
+// Leaf record of a unique leaf whose first simulation is s0: the key (the root key folded with
+// the actions of the path's nodes, depths 1..L-1) and the legal count (board games: the root's
+// count, root_count, less the path's moves, a pass excepted: every legal list excludes the
+// moves on its path, so they are distinct and legal at the root; sparse model: from the key).
+// One thread per leaf; returns the path length L.
+__device__ inline int leaf_key_count(const omq_forest& f, const omq_wave& w, int t, int s0,
+                                     int root_count, uint64_t* key_out, int* count_out) {
+  const int64_t wb = (int64_t)t * w.max_wave;
+  const int64_t tb = (int64_t)t * f.capacity;
+  const int L = w.path_len[wb + s0];
+  const int32_t* path = w.paths + (wb + s0) * w.max_depth;
+  const bool board = f.game != OMQ_GAME_SPARSE;
+  const int pass = f.game == OMQ_GAME_GO ? f.num_actions - 1 : -1;
+  const uint32_t* root = f.root_legal + (int64_t)t * f.legal_words;
+  uint64_t key = f.root_keys[t];
+  int taken = 0;
+  // eight depths at a time: their path entries, then their actions, in flight together
+  constexpr int kB = 8;
+  for (int d0 = 1; d0 < L; d0 += kB) {
+    int pv[kB], av[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) pv[j] = d0 + j < L ? path[d0 + j] : 0;
+#pragma unroll
+    for (int j = 0; j < kB; ++j) av[j] = d0 + j < L ? f.actions[tb + pv[j]] : 0;
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      if (d0 + j >= L) break;
+      const int a = av[j];
+      key = child_key(key, a);
+      if (board && a != pass && a >= 0 && a < f.num_actions) taken += (root[a >> 5] >> (a & 31)) & 1u;
+    }
+  }
+  *key_out = key;
+  *count_out = board ? root_count - taken : sparse_legal_count(f, key);
+  return L;
+}
+
+// The root's legal count of tree t (board games).
+__device__ inline int root_legal_count(const omq_forest& f, int t) {
+  const uint32_t* root = f.root_legal + (int64_t)t * f.legal_words;
+  int c = 0;
+  for (int i = 0; i < f.legal_words; ++i) c += __popc(root[i]);
+  return c;
+}
+
 // Load the actions on the path of simulation s (depths 1..L-1) into lanes: lane j holds
 // the action at depth j+1 (and depth j+65 in *a_hi).  Returns L.
 __device__ inline int load_path_actions(const omq_forest& f, const omq_wave& w, int t, int s,

@@ -78,42 +78,13 @@ __global__ __launch_bounds__(kLeafInfoThreads) void leaf_info_kernel(omq_forest 
   const int t = by;
   const int u = bx * kLeafInfoThreads + threadIdx.x;
   const int64_t wb = (int64_t)t * w.max_wave;
-  const int64_t tb = (int64_t)t * f.capacity;
   const int nu = w.ucount[t];
   int L = 0;
   if (u < nu) {
-    const int s0 = w.ufirst[wb + u];
-    L = w.path_len[wb + s0];
-    const int32_t* path = w.paths + (wb + s0) * w.max_depth;
-    const bool board = f.game != OMQ_GAME_SPARSE;
-    const int pass = f.game == OMQ_GAME_GO ? f.num_actions - 1 : -1;
-    const uint32_t* root = f.root_legal + (int64_t)t * f.legal_words;
-    uint64_t key = f.root_keys[t];
-    int taken = 0;
-    // eight depths at a time: their path entries, then their actions, in flight together
-    constexpr int kB = 8;
-    for (int d0 = 1; d0 < L; d0 += kB) {
-      int pv[kB], av[kB];
-#pragma unroll
-      for (int j = 0; j < kB; ++j) pv[j] = d0 + j < L ? path[d0 + j] : 0;
-#pragma unroll
-      for (int j = 0; j < kB; ++j) av[j] = d0 + j < L ? f.actions[tb + pv[j]] : 0;
-#pragma unroll
-      for (int j = 0; j < kB; ++j) {
-        if (d0 + j >= L) break;
-        const int a = av[j];
-        key = child_key(key, a);
-        if (board && a != pass && a >= 0 && a < f.num_actions) taken += (root[a >> 5] >> (a & 31)) & 1u;
-      }
-    }
+    uint64_t key;
     int count;
-    if (board) {
-      int c = 0;
-      for (int i = 0; i < f.legal_words; ++i) c += __popc(root[i]);
-      count = c - taken;
-    } else {
-      count = sparse_legal_count(f, key);
-    }
+    const int rc = f.game != OMQ_GAME_SPARSE ? root_legal_count(f, t) : 0;
+    L = leaf_key_count(f, w, t, w.ufirst[wb + u], rc, &key, &count);
     w.ukey[wb + u] = key;
     w.ulegal[wb + u] = count;
   }

@@ -72,6 +72,22 @@ struct SelArgs {
   int32_t* lfs;    // [T*max_wave] first simulation of a simulation's leaf group
 };
 
+// What the select kernel reads and writes for the unique leaves' records (waves of at most
+// OMQ_SELECT_RECORDS_MAX_WAVE simulations): a kernel argument of its own, after SelArgs and
+// SelCfg, whose places in the argument block it leaves as they were.
+struct RecordArgs {
+  const int32_t* actions;
+  const uint64_t* root_keys;
+  const uint32_t* root_legal;
+  uint64_t* ukey;
+  int32_t* ulegal;
+  int game;
+  int num_actions;
+  int legal_words;
+  int min_legal;
+  int max_legal;
+};
+
 // Max of a uint32 over the 64 lanes, made uniform: DPP row shifts 1,2,4,8 (each a single
 // v_max_u32_dpp; a lane whose DPP source lies outside its row reads 0, the identity) leave
 // each row's maximum in its last lane; the four row maxima are read into scalar registers
@@ -1183,7 +1199,7 @@ struct LevelShared {
 // order.
 constexpr int kLaneGroup = 2;
 
-// Kernels of at least this many slots per lane run 512-thread workgroups (whole_threads).
+// Kernels of at least this many slots per lane run 512-thread workgroups (select_threads).
 // (The 3-slot kernel at 1024 threads, with the level-1 followers, spilled 62 registers; at 512
 // threads it spills none, and a Go 13 x 13 wave's select went 182 -> 170 us.)
 constexpr int kWideRmax = 3;
@@ -2288,13 +2304,36 @@ __device__ inline void start_group(const LevelLds& L, LevelShared<NT>& sh, int W
 }
 
 // Unique leaves of tree t in order of first occurrence, from the per-simulation leaf records
-// lflag / lfs (global; lflag is scanned in place).  Called by every thread of the workgroup.
-template <int NT>
-__device__ inline void finish_tree(const SelArgs& w, int t, int W, int32_t* lfs, int32_t* lflag,
-                                   int* s_wtot) {
+// lflag / lfs (global; lflag is scanned in place), and, with kRecords, each unique leaf's key
+// and legal count (leaf_key_count, as omq_leaf_info forms them).  Called by every thread of
+// the workgroup.
+template <int NT, bool kRecords>
+__device__ inline void finish_tree(const SelArgs& w, const RecordArgs& ra, int t, int W,
+                                   int32_t* lfs, int32_t* lflag, int* s_wtot,
+                                   unsigned long long* s_uleafpath) {
   const int tid = threadIdx.x;
   const int MW = w.max_wave;
   const int nu = block_excl_scan<NT>(lflag, W, s_wtot);
+  int rc = 0;
+  omq_forest fo{};
+  omq_wave wo{};
+  if constexpr (kRecords) {
+    fo.capacity = w.capacity;
+    fo.num_actions = ra.num_actions;
+    fo.game = ra.game;
+    fo.legal_words = ra.legal_words;
+    fo.min_legal = ra.min_legal;
+    fo.max_legal = ra.max_legal;
+    fo.actions = const_cast<int32_t*>(ra.actions);
+    fo.root_keys = const_cast<uint64_t*>(ra.root_keys);
+    fo.root_legal = const_cast<uint32_t*>(ra.root_legal);
+    wo.max_wave = MW;
+    wo.max_depth = w.max_depth_buf;
+    wo.paths = w.paths;
+    wo.path_len = w.path_len;
+    rc = fo.game != OMQ_GAME_SPARSE ? root_legal_count(fo, t) : 0;
+  }
+  int plen_sum = 0;
   for (int s = tid; s < W; s += NT) {
     const int s0 = lfs[s];
     const int uid = lflag[s0];
@@ -2302,7 +2341,18 @@ __device__ inline void finish_tree(const SelArgs& w, int t, int W, int32_t* lfs,
     if (s0 == s) {
       w.uleaf[(int64_t)t * MW + uid] = w.leaves[(int64_t)t * MW + s];
       w.ufirst[(int64_t)t * MW + uid] = s;
+      if constexpr (kRecords) {
+        uint64_t key;
+        int count;
+        plen_sum += leaf_key_count(fo, wo, t, s, rc, &key, &count);
+        ra.ukey[(int64_t)t * MW + uid] = key;
+        ra.ulegal[(int64_t)t * MW + uid] = count;
+      }
     }
+  }
+  if constexpr (kRecords) {
+    const int ws = wave_sum_i(plen_sum);
+    if (lane_id() == 0 && ws > 0) atomicAdd(s_uleafpath, (unsigned long long)ws);
   }
   if (tid == 0) {
     w.ucount[t] = nu;
@@ -2325,9 +2375,14 @@ __device__ inline void flush_stats(const SelArgs& w, int t, LevelShared<NT>& sh)
 
 // ---- Kernels ---------------------------------------------------------------------------
 // The select kernel: one workgroup per tree runs every level of its tree's wave, then the
-// unique-leaf pass.
-template <int RMAX, int NT>
-__global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c) {
+// unique-leaf pass (with kRecords, the unique leaves' keys and legal counts too).  The kRecords
+// kernels are compiled in a code object of their own (tree_select_records.hip): compiled into
+// this one, the records' code cost C3's 6-slot kernel 2.3 us per launch though it did not run
+// there (behind a run-time test), and as a second instantiation beside it, 2.0 us (the
+// out-of-line chain functions the two kernels share were compiled differently).
+template <int RMAX, int NT, bool kRecords>
+__global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c,
+                                                           RecordArgs ra) {
   // the level overlap in the kernels whose chains keep their registers with a second copy of
   // the chain code (the followers'), with a full workgroup of followers (the 1- and 2-slot
   // kernels: every kernel of more slots runs 512 threads)
@@ -2367,7 +2422,7 @@ __global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c)
   level_loop<RMAX, NT, NT <= 512>(f, c, t, 0, c.max_depth, W, L, sh, &s_glog, lfs, lflag, pipe,
                                   root_first, pipe ? 2 : -1, run_ahead, root_k);
   __syncthreads();
-  finish_tree<NT>(f, t, W, lfs, lflag, sh.wtot);
+  finish_tree<NT, kRecords>(f, ra, t, W, lfs, lflag, sh.wtot, &sh.st[OMQ_ST_ULEAFPATH]);
   __syncthreads();
   if (tid == 0) f.gcount[t] = s_glog;
   flush_stats<NT>(f, t, sh);
@@ -2375,38 +2430,58 @@ __global__ __launch_bounds__(NT, 1) void select_root_kernel(SelArgs f, SelCfg c)
 
 }  // namespace omq
 
+namespace omq {
+// Threads of the whole-wave kernel: 512 for the kernels of more than 4 slots per lane, whose
+// chains then keep up to 256 registers (at 1024 threads, 128: the 6-slot chains spilled 12-100
+// registers, depending on the code around them).  The first-unvisited prefix leaves their
+// levels below the root few chains, so 8 waves suffice there.
+constexpr int select_threads(int rmax) { return rmax >= kWideRmax ? 512 : 1024; }
+
+// The kRecords select kernel of rmax slots per lane (tree_select_records.hip).
+const void* select_records_kernel(int rmax);
+}  // namespace omq
+
+#ifdef OMQ_SELECT_RECORDS_TU
+// ---- the kRecords kernels (this file compiled again by tree_select_records.hip) ----
+namespace omq {
+const void* select_records_kernel(int rmax) {
+  switch (rmax) {
+#define OMQ_PICK(R) \
+  case R:           \
+    return (const void*)select_root_kernel<R, select_threads(R), true>;
+    OMQ_PICK(1)
+    OMQ_PICK(2)
+    OMQ_PICK(3)
+    OMQ_PICK(4)
+    OMQ_PICK(5)
+    OMQ_PICK(6)
+    default:
+    OMQ_PICK(8)
+#undef OMQ_PICK
+  }
+}
+}  // namespace omq
+#else
 // ---- host launcher (C++ linkage; the C ABI wrappers live in capi.hip) ----
 namespace omq {
 
 namespace {
 std::atomic<int> g_spin_limit{OMQ_SPIN_LIMIT_DEFAULT};  // polls of a follower's bounded wait
 constexpr int kMaxDevices = 64;
-std::atomic<bool> g_attr_set[kMaxDevices][9];
-
-// Threads of the whole-wave kernel: 512 for the kernels of more than 4 slots per lane, whose
-// chains then keep up to 256 registers (at 1024 threads, 128: the 6-slot chains spilled 12-100
-// registers, depending on the code around them).  The first-unvisited prefix leaves their
-// levels below the root few chains, so 8 waves suffice there.
-template <int RMAX>
-constexpr int whole_threads() {
-  return RMAX >= kWideRmax ? 512 : 1024;
-}
-
-template <int RMAX>
-const void* root_kernel() {
-  return (const void*)select_root_kernel<RMAX, whole_threads<RMAX>()>;
-}
+std::atomic<bool> g_attr_set[kMaxDevices][9][2];
 
 struct SelKernel {
   const void* fn;
   int threads;
 };
 
-SelKernel pick_kernel(int rmax) {
+SelKernel pick_kernel(int rmax, bool records) {
+  if (records) return SelKernel{select_records_kernel(rmax), select_threads(rmax)};
   switch (rmax) {
 #define OMQ_PICK(R) \
   case R:           \
-    return SelKernel{root_kernel<R>(), whole_threads<R>()};
+    return SelKernel{(const void*)select_root_kernel<R, select_threads(R), false>, \
+                     select_threads(R)};
     OMQ_PICK(1)
     OMQ_PICK(2)
     OMQ_PICK(3)
@@ -2426,8 +2501,6 @@ void select_set_options(int spin_limit) {
 
 int select_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
-size_t select_lds_bytes(int W) { return level_lds_bytes<1024>(W, true); }
-
 hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_puct,
                          float virtual_loss, int max_depth, int vl_atomic, hipStream_t stream) {
   SelCfg c;
@@ -2443,21 +2516,23 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   int rmax = (max_row + kWave - 1) / kWave;
   if (rmax < 1) rmax = 1;
   if (rmax > 6) rmax = 8;
-  const SelKernel k = pick_kernel(rmax);
+  // the unique leaves' records in select for the waves of at most OMQ_SELECT_RECORDS_MAX_WAVE
+  const bool records = W <= OMQ_SELECT_RECORDS_MAX_WAVE;
+  const SelKernel k = pick_kernel(rmax, records);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   const bool cache = dev >= 0 && dev < kMaxDevices;
   // the LDS limit is raised once per device and kernel (the attribute is idempotent, so two
   // threads racing here both set it)
-  if (!cache || !g_attr_set[dev][rmax].load(std::memory_order_acquire)) {
+  if (!cache || !g_attr_set[dev][rmax][records].load(std::memory_order_acquire)) {
     const size_t lds_max =
         k.threads == 1024
             ? std::max(level_lds_bytes<1024>(OMQ_MAX_WAVE, true), level_lds_bytes<1024>(kPipeMaxW, true))
             : std::max(level_lds_bytes<512>(OMQ_MAX_WAVE, false), level_lds_bytes<512>(kPipeMaxW, false));
     e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
     if (e != hipSuccess) return e;
-    if (cache) g_attr_set[dev][rmax].store(true, std::memory_order_release);
+    if (cache) g_attr_set[dev][rmax][records].store(true, std::memory_order_release);
   }
   SelArgs a;
   a.N = f.visit_counts;
@@ -2484,7 +2559,18 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
   const int64_t TM = (int64_t)f.num_trees * w.max_wave;
   a.lflag = w.sel_scratch;
   a.lfs = w.sel_scratch + TM;
-  void* args[] = {&a, &c};
+  RecordArgs ra;
+  ra.actions = f.actions;
+  ra.root_keys = f.root_keys;
+  ra.root_legal = f.root_legal;
+  ra.ukey = w.ukey;
+  ra.ulegal = w.ulegal;
+  ra.game = f.game;
+  ra.num_actions = f.num_actions;
+  ra.legal_words = f.legal_words;
+  ra.min_legal = f.min_legal;
+  ra.max_legal = f.max_legal;
+  void* args[] = {&a, &c, &ra};
   const size_t lds = k.threads == 1024 ? level_lds_bytes<1024>(W, true)
                                        : level_lds_bytes<512>(W, false);
   e = hipLaunchKernel(k.fn, dim3(f.num_trees), dim3(k.threads), args, lds, stream);
@@ -2493,3 +2579,4 @@ hipError_t launch_select(const omq_forest& f, const omq_wave& w, int W, float c_
 }
 
 }  // namespace omq
+#endif  // OMQ_SELECT_RECORDS_TU

@@ -226,3 +226,41 @@ def test_root_chain_counter_within_select_time(device):
     chain_ms = st["rootchain"] / khz.value / (wl.num_trees * launches)
     assert st["rootchain"] > 0
     assert 0.0 < chain_ms < tot["select"] / launches
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["C2", "C4"])
+def test_select_leaf_records_equal_leaf_info(device, name):
+    """For a wave of at most OMQ_SELECT_RECORDS_MAX_WAVE simulations, omq_select forms the
+    unique leaves' keys and legal counts itself; omq_leaf_info, run on the same wave, forms the
+    same words (board and sparse models), so the two paths are interchangeable."""
+    wl = get(name).scaled(name=f"{name}-records", num_trees=3, num_simulations=1024,
+                          wave_size=256, capacity=200_000)
+    assert wl.wave_size <= _lib.OMQ_SELECT_RECORDS_MAX_WAVE
+    params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth,
+                          dirichlet_epsilon=wl.dirichlet_epsilon)
+    eng = WaveEngine(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth, device,
+                     params)
+    eng.set_roots(*wl.root_inputs())
+    ev = SyntheticEvaluator(wl.logit_scale)
+    eng.search(3 * wl.wave_size, wl.wave_size, ev)  # a tree a few levels deep
+    eng.select(wl.wave_size)
+    torch.cuda.synchronize()
+    T, MW = eng.T, eng.MW
+    nu = eng.ucount.cpu().numpy()
+    assert nu.min() > 0
+    key_s = eng.ukey.view(T, MW).cpu().numpy()
+    legal_s = eng.ulegal.view(T, MW).cpu().numpy()
+    eng.ukey.fill_(0)
+    eng.ulegal.fill_(-1)
+    torch.cuda.synchronize()
+    _lib.check(eng.lib.omq_leaf_info(eng.forest_ref, eng.wave_ref, eng.stream_handle()),
+               "omq_leaf_info")
+    torch.cuda.synchronize()
+    key_i = eng.ukey.view(T, MW).cpu().numpy()
+    legal_i = eng.ulegal.view(T, MW).cpu().numpy()
+    for t in range(T):
+        n = int(nu[t])
+        assert (key_s[t, :n] == key_i[t, :n]).all()
+        assert (legal_s[t, :n] == legal_i[t, :n]).all()
+        assert (legal_s[t, :n] >= 0).all()
