@@ -156,7 +156,7 @@ constexpr int kPlanThreads = 1024;
 
 __global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f, omq_wave w,
                                                                    ExpCfg c) {
-  extern __shared__ __align__(16) int want[];  // [ucount]
+  extern __shared__ __align__(16) int want[];  // [max_wave] (ucount <= max_wave)
   __shared__ int s_wtot[kPlanThreads / kWave];
   __shared__ int s_total;
   __shared__ unsigned long long s_exp, s_new, s_fail;
@@ -531,7 +531,7 @@ hipError_t launch_expand(const omq_forest& f, const omq_wave& w, int W, float vi
   c.noise = noise;
   c.eps = eps;
   hipLaunchKernelGGL(expand_plan_kernel, dim3(f.num_trees), dim3(kPlanThreads),
-                     (size_t)W * sizeof(int), st, f, w, c);
+                     (size_t)w.max_wave * sizeof(int), st, f, w, c);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t per = expand_lds_per_wave(f);
