@@ -48,5 +48,33 @@ def build_library(out: str | None = None, verbose: bool = False) -> str:
     return out
 
 
+def build_torch_ops(out: str | None = None, verbose: bool = False) -> str:
+    """libomq_torch_ops.so: the torch operators (csrc/torch_ops.cpp), host C++ over the C ABI,
+    linked against libomq_tree_ops.so beside it (build that first)."""
+    import torch
+    from torch.utils import cpp_extension
+
+    out = out or os.path.join(_HERE, "libomq_torch_ops.so")
+    tmp = out + ".tmp"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
+           "-D__HIP_PLATFORM_AMD__", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *(f"-I{p}" for p in cpp_extension.include_paths()), "-I/opt/rocm/include",
+           "-I", os.path.join(_ROOT, "include"),
+           "-o", tmp, os.path.join(_HERE, "csrc", "torch_ops.cpp"),
+           f"-L{_HERE}", "-lomq_tree_ops", "-Wl,-rpath,$ORIGIN",
+           *(f"-L{p}" for p in cpp_extension.library_paths()),
+           *(f"-Wl,-rpath,{p}" for p in cpp_extension.library_paths()),
+           "-lc10", "-lc10_hip", "-ltorch_cpu"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"c++ failed ({r.returncode}):\n{r.stdout}{r.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     print(build_library(verbose=True))
+    print(build_torch_ops(verbose=True))

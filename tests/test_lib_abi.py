@@ -188,3 +188,49 @@ def test_noalloc_shift_root_limit():
     assert "omq_shift_root_noalloc" in msg and str(_lib.OMQ_NOALLOC_SHIFT_INTS) in msg
     g = _forest(num_trees=2, capacity=cap - 1)
     assert lib.omq_shift_root_noalloc(ctypes.byref(g), None, None) == _lib.OMQ_E_ARG
+
+
+def test_torch_ops_come_from_the_cpp_library():
+    """The omq:: operators (and the reference's mcts:: names) are registered by the C++ library
+    libomq_torch_ops.so with the reference's schemas; their Meta kernels give the shapes."""
+    import torch
+
+    from omoknuni_quantum_amd import torch_ops
+
+    backup = ("(Tensor paths, Tensor path_lengths, Tensor values, Tensor(a!) visit_counts, "
+              "Tensor(b!) value_sums) -> ()")
+    for ns in ("omq", "mcts"):
+        for name in ("vectorized_backup", "warp_vectorized_backup"):
+            assert str(getattr(getattr(torch.ops, ns), name).default._schema) == \
+                f"{ns}::{name}{backup}"
+        assert f"{ns}::fused_ucb_selection" in torch_ops.REGISTERED
+        assert torch.ops.omq._mcts_aliased("fused_ucb_selection")
+    dump = torch._C._dispatch_dump("omq::vectorized_backup")
+    assert "torch_ops.cpp" in dump
+    m = torch.empty(5, dtype=torch.int32, device="meta")
+    f = m.float()
+    assert torch.ops.omq.fused_ucb_selection(m, m, m, m, f, m, f, 1.4).shape == (5,)
+
+
+def test_mcts_name_taken_first_is_left_to_its_owner():
+    """A module that registered mcts::vectorized_backup before this package keeps it."""
+    import os
+    import subprocess
+    import sys
+
+    code = (
+        "import torch\n"
+        "@torch.library.custom_op('mcts::vectorized_backup', mutates_args=('visit_counts', "
+        "'value_sums'))\n"
+        "def vb(paths: torch.Tensor, path_lengths: torch.Tensor, values: torch.Tensor, "
+        "visit_counts: torch.Tensor, value_sums: torch.Tensor) -> None:\n"
+        "    pass\n"
+        "from omoknuni_quantum_amd import torch_ops\n"
+        "assert 'mcts::vectorized_backup' not in torch_ops.REGISTERED\n"
+        "assert not torch.ops.omq._mcts_aliased('vectorized_backup')\n"
+        "assert 'mcts::fused_ucb_selection' in torch_ops.REGISTERED\n"
+        "print('ok')\n")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
