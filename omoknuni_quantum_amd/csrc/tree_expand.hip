@@ -316,6 +316,9 @@ __global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f,
   }
 }
 
+// four int32 as a vector of the compiler's own (what __builtin_nontemporal_store takes)
+typedef int IntX4 __attribute__((ext_vector_type(4)));
+
 // ---------------------------------------------------------------------------------------
 __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -461,6 +464,12 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
   // written 16 bytes per lane (four children) from the first node index that is a multiple of
   // 4, the children before it and after the last whole quad one per lane; shorter rows one per
   // lane (C3 expand_write 48.8 -> 47.6 us; quads on rows of 20-45 children, C4, cost 7 %).
+  // The quads of parents and actions, which no kernel of the next waves reads (only subtree
+  // reuse and the leaves' records, along paths), are stored non-temporally, so that they take
+  // no L2 lines from the rows and counts that selection and backup read (C3 101.1 -> 102.2 M
+  // sims/s).  The other five arrays stored so cost the expansion more than they saved
+  // elsewhere, and so did the one-per-lane stores of the head, the tail and short rows (C2's
+  // expansion 28.4 -> 32.5 us).
   const int64_t node0 = tb + cbase;
   auto put1 = [&](int j) {
     const int64_t node = node0 + j;
@@ -488,8 +497,10 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
     *reinterpret_cast<int4*>(f.visit_counts + node) = make_int4(0, 0, 0, 0);
     *reinterpret_cast<float4*>(f.value_sums + node) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     *reinterpret_cast<float4*>(f.priors + node) = pr;
-    *reinterpret_cast<int4*>(f.parents + node) = make_int4(leaf, leaf, leaf, leaf);
-    *reinterpret_cast<int4*>(f.actions + node) = ac;
+    __builtin_nontemporal_store((IntX4){leaf, leaf, leaf, leaf},
+                                reinterpret_cast<IntX4*>(f.parents + node));
+    __builtin_nontemporal_store((IntX4){ac.x, ac.y, ac.z, ac.w},
+                                reinterpret_cast<IntX4*>(f.actions + node));
     *reinterpret_cast<int4*>(f.first_child + node) = make_int4(-1, -1, -1, -1);
     *reinterpret_cast<int4*>(f.num_children + node) = make_int4(0, 0, 0, 0);
   }
