@@ -24,6 +24,17 @@ def test_dense_boards_parity(device, rule):
     assert stats["terminal"] > 50
 
 
+def test_dense_boards_large_wave_parity(device):
+    """Waves above OMQ_SELECT_RECORDS_MAX_WAVE: the leaf records come from omq_leaf_info, and the
+    terminal check overwrites their legal counts after it."""
+    wl = get("C2").scaled(name="dense15-large-wave", model=games.gomoku(15), max_stones=150,
+                          num_trees=3, num_simulations=2048, wave_size=1024, capacity=200_000)
+    assert wl.wave_size > _lib.OMQ_SELECT_RECORDS_MAX_WAVE
+    stats = {}
+    assert run_parity(wl, rule=_lib.OMQ_RULE_FREESTYLE, device=device, stats=stats) >= 2
+    assert stats["terminal"] > 0
+
+
 def _planted_boards(T, bs, seed):
     """Root positions with black and white fours with a gap (a move in the gap makes five)
     and black 2+3 split lines (a move in the gap makes an overline of six)."""
