@@ -28,7 +28,7 @@ sys.path.insert(0, _ROOT)
 
 METRIC = "tree-op simulations/sec (synthetic evaluator) + achieved HBM GB/s, 1 GPU"
 HBM_PEAK_GBS = 8000.0
-TREE_PHASES = ("select", "leaf_info", "expand", "backup")
+TREE_PHASES = ("select", "leaf_info", "expand_backup")
 
 
 def algorithmic_bytes(st: dict, sims: int, wave: int) -> dict:
@@ -45,10 +45,11 @@ def algorithmic_bytes(st: dict, sims: int, wave: int) -> dict:
                 select for waves of at most OMQ_SELECT_RECORDS_MAX_WAVE simulations (counted
                 with select), else by leaf_info_kernel (the leaf_info phase, which also holds
                 the rule kernels when a rule is on; those are not modelled)
-      expand    8 B per expanded leaf (row header) + 28 B per child written (N, W, P, parent,
+      expand_backup  (one phase: omq_expand_backup runs the two side by side)
+        expand  8 B per expanded leaf (row header) + 28 B per child written (N, W, P, parent,
                 action, row offset, row length) + 4 B per prior gathered (= per child in the
                 full policy)
-      backup    16 B per visited node (N and W read and written) + 4 B per path entry
+        backup  16 B per visited node (N and W read and written) + 4 B per path entry
                 (signed leaf value read) + 12 B per simulation (value, uid, length)
     """
     from omoknuni_quantum_amd import _lib
@@ -59,14 +60,13 @@ def algorithmic_bytes(st: dict, sims: int, wave: int) -> dict:
     return {
         "select": 16 * G + 12 * K + 4 * PE + 8 * sims + (records if in_select else 0),
         "leaf_info": 0 if in_select else records,
-        "expand": 8 * st["expanded"] + 32 * st["newchild"],
-        "backup": 16 * G + 4 * PE + 12 * sims,
+        "expand_backup": 8 * st["expanded"] + 32 * st["newchild"] + 16 * G + 4 * PE + 12 * sims,
     }
 
 
 
 KERNEL_OF_PHASE = {"select": "select_root_kernel", "leaf_info": "leaf_info_kernel",
-                   "expand": "expand_write_kernel", "backup": "backup_groups_kernel"}
+                   "expand_backup": "write_backup_kernel"}
 ALL_CONFIGS = ("C1", "C2", "C3", "C4", "C5")
 
 

@@ -271,6 +271,19 @@ int omq_expand(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
 int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float virtual_loss,
                int32_t sign_mode, int32_t w_mode, void* stream);
 
+/* omq_expand followed by omq_backup, with the same arguments, and the same results: the two
+ * write no common address and neither reads what the other writes, so their kernels run side
+ * by side, in two launches instead of four (the expansion plan beside the signed leaf values,
+ * then the child records beside the group backup).  Under OMQ_EXPAND_REFERENCE_PW (whose rule
+ * reads the root's count, which the backup changes), with OMQ_WACC_ATOMIC, or where the
+ * expansion's LDS per leaf exceeds 16 KiB, it runs the two one after the other.
+ * Replaces the expansion and the backup of OptimizedCPUWaveSearch._batch_expand_and_backup
+ * (python/mcts/cpu/optimized_wave_search.py:367-483), run back to back. */
+int omq_expand_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size,
+                      float virtual_loss, int32_t expand_policy, const double* root_noise,
+                      double dirichlet_epsilon, int32_t sign_mode, int32_t w_mode,
+                      void* stream);
+
 /* Gomoku terminal check of every unique leaf of the wave; call it after the leaf records are
  * formed (by omq_select, or by omq_leaf_info after a wave of more than
  * OMQ_SELECT_RECORDS_MAX_WAVE simulations) and before omq_expand.  Needs an OMQ_GAME_BOARD forest with num_actions = bs*bs.

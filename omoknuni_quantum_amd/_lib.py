@@ -79,6 +79,8 @@ SIGNATURES = {
     "omq_forest_reset": (ctypes.c_int, [_FP, _p]),
     "omq_select": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, ctypes.c_float, _i32, _i32, _p]),
     "omq_leaf_info": (ctypes.c_int, [_FP, _WP, _p]),
+    "omq_expand_backup": (ctypes.c_int, [_FP, _WP, _i32, ctypes.c_float, _i32, _p,
+                                         ctypes.c_double, _i32, _i32, _p]),
     "omq_select_options": (ctypes.c_int, [_i32]),
     "omq_select_spin_limit": (ctypes.c_int32, []),
     "omq_wall_clock_khz": (ctypes.c_int, [_p]),

@@ -307,6 +307,16 @@ class WaveEngine:
                                         p.sign_mode, p.w_mode, self.stream_handle()),
                     "omq_backup")
 
+    def expand_backup(self, wave_size: int) -> None:
+        """expand then backup (omq_expand_backup: their kernels side by side where the two
+        cannot interfere, else one after the other)."""
+        p = self.params
+        noise = self.noise.data_ptr() if (self.has_noise and p.dirichlet_epsilon > 0) else None
+        self._check(self.lib.omq_expand_backup(self.forest_ref, self.wave_ref, wave_size,
+                                               p.virtual_loss, p.expand_policy, noise,
+                                               p.dirichlet_epsilon, p.sign_mode, p.w_mode,
+                                               self.stream_handle()), "omq_expand_backup")
+
     def shift_roots(self, new_roots) -> None:
         """Subtree reuse (CSRTree.shift_root): node new_roots[t] of tree t becomes its root
         and keeps its subtree, renumbered breadth-first; -1 (or 0) leaves a tree unchanged.
@@ -367,8 +377,9 @@ class WaveEngine:
                     "omq_paths_backup")
 
     def run_wave(self, wave_size: int, evaluator, timer=None) -> None:
-        """One wave in every tree: select, leaf info, evaluate, expand, backup.  With a
-        PhaseTimer, every phase is bracketed by events on the launch stream."""
+        """One wave in every tree: select, leaf info, evaluate, then expand and backup in one
+        call (omq_expand_backup).  With a PhaseTimer, every phase is bracketed by events on the
+        launch stream (expand and backup are one phase, "expand_backup")."""
         mark = timer.mark if timer is not None else (lambda _p: None)
         mark("select")
         self.select(wave_size)
@@ -377,10 +388,8 @@ class WaveEngine:
             self.leaf_info(wave_size)
         mark("eval")
         evaluator.evaluate_wave(self)
-        mark("expand")
-        self.expand(wave_size)
-        mark("backup")
-        self.backup(wave_size)
+        mark("expand_backup")
+        self.expand_backup(wave_size)
         mark(None)
 
     def launch_signature(self) -> tuple:

@@ -20,6 +20,10 @@ hipError_t launch_expand(const omq_forest& f, const omq_wave& w, int W, float vi
                          int policy, const double* noise, double eps, hipStream_t st);
 hipError_t launch_backup(const omq_forest& f, const omq_wave& w, int W, float virtual_loss,
                          int sign_mode, int w_mode, hipStream_t st);
+bool expand_backup_fusable(const omq_forest& f, int policy, int w_mode);
+hipError_t launch_expand_backup(const omq_forest& f, const omq_wave& w, int W,
+                                float virtual_loss, const double* noise, double eps,
+                                int sign_mode, hipStream_t st);
 hipError_t launch_paths_backup(const omq_forest& f, const int32_t* paths, const int32_t* plen,
                                const int32_t* tree_of, const float* values, int batch,
                                int max_depth, int sign_mode, hipStream_t st);
@@ -427,6 +431,38 @@ int omq_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size, float 
   return hip_status(omq::launch_backup(*f, *w, wave_size, virtual_loss, sign_mode, w_mode,
                                        (hipStream_t)stream),
                     "omq_backup");
+}
+
+int omq_expand_backup(const omq_forest* f, const omq_wave* w, int32_t wave_size,
+                      float virtual_loss, int32_t expand_policy, const double* root_noise,
+                      double dirichlet_epsilon, int32_t sign_mode, int32_t w_mode,
+                      void* stream) {
+  int rc = check_forest(f);
+  if (rc) return rc;
+  rc = check_wave(f, w, wave_size);
+  if (rc) return rc;
+  rc = check_leaf_lds(f);
+  if (rc) return rc;
+  if (expand_policy != OMQ_EXPAND_FULL && expand_policy != OMQ_EXPAND_REFERENCE_PW)
+    return fail(OMQ_E_ARG, "unknown expansion policy %d", expand_policy);
+  if (!(dirichlet_epsilon >= 0.0 && dirichlet_epsilon <= 1.0))
+    return fail(OMQ_E_ARG, "dirichlet_epsilon %g outside [0, 1]", dirichlet_epsilon);
+  if (sign_mode != OMQ_SIGN_LEAF_POSITIVE && sign_mode != OMQ_SIGN_ROOT_POSITIVE)
+    return fail(OMQ_E_ARG, "unknown sign mode %d", sign_mode);
+  if (w_mode != OMQ_WACC_ORDERED && w_mode != OMQ_WACC_ATOMIC)
+    return fail(OMQ_E_ARG, "unknown W accumulation mode %d", w_mode);
+  if (omq::expand_backup_fusable(*f, expand_policy, w_mode))
+    return hip_status(omq::launch_expand_backup(*f, *w, wave_size, virtual_loss, root_noise,
+                                                dirichlet_epsilon, sign_mode,
+                                                (hipStream_t)stream),
+                      "omq_expand_backup");
+  rc = hip_status(omq::launch_expand(*f, *w, wave_size, virtual_loss, expand_policy, root_noise,
+                                     dirichlet_epsilon, (hipStream_t)stream),
+                  "omq_expand_backup");
+  if (rc) return rc;
+  return hip_status(omq::launch_backup(*f, *w, wave_size, virtual_loss, sign_mode, w_mode,
+                                       (hipStream_t)stream),
+                    "omq_expand_backup");
 }
 
 int omq_paths_backup(const omq_forest* f, const int32_t* paths, const int32_t* path_len,

@@ -12,6 +12,7 @@
 //   synth_eval_kernel   wave per unique leaf: synthetic priors/value (evaluator stand-in)
 //   expand_plan_kernel  workgroup per tree: children counts, scan, capacity rule, row headers
 //   expand_write_kernel wave per expanded leaf: priors, children N/W/P/parent/action/row
+#include "backup_groups.h"
 #include "omq_common.h"
 
 namespace omq {
@@ -154,13 +155,13 @@ struct ExpCfg {
 
 constexpr int kPlanThreads = 1024;
 
-__global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f, omq_wave w,
-                                                                   ExpCfg c) {
-  extern __shared__ __align__(16) int want[];  // [max_wave] (ucount <= max_wave)
+// The plan of tree t, by a workgroup of kPlanThreads threads; want is its LDS array of
+// max_wave ints.
+__device__ inline void expand_plan_block(const omq_forest& f, const omq_wave& w, const ExpCfg& c,
+                                         int t, int* want) {
   __shared__ int s_wtot[kPlanThreads / kWave];
   __shared__ int s_total;
   __shared__ unsigned long long s_exp, s_new, s_fail;
-  const int t = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t tb = (int64_t)t * f.capacity;
   const int64_t wb = (int64_t)t * w.max_wave;
@@ -319,12 +320,17 @@ __global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f,
 // four int32 as a vector of the compiler's own (what __builtin_nontemporal_store takes)
 typedef int IntX4 __attribute__((ext_vector_type(4)));
 
+__global__ __launch_bounds__(kPlanThreads) void expand_plan_kernel(omq_forest f, omq_wave w,
+                                                                   ExpCfg c) {
+  extern __shared__ __align__(16) int want[];  // [max_wave] (ucount <= max_wave)
+  expand_plan_block(f, w, c, (int)blockIdx.x, want);
+}
+
 // ---------------------------------------------------------------------------------------
-__global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  int bx = blockIdx.x, by = blockIdx.y;
-  xcd_block(&bx, &by);  // one contiguous run of blocks (leaves of few trees) per XCD
-  const int t = by;
+// Block bx of tree t's expansion writes (one wave per expanded leaf), with the block's
+// dynamic LDS smem.
+__device__ inline void expand_write_block(const omq_forest& f, const omq_wave& w,
+                                          const ExpCfg& c, int bx, int t, unsigned char* smem) {
   const int wave = threadIdx.x / kWave;
   const int u = bx * (blockDim.x / kWave) + wave;
   const int lane = lane_id();
@@ -508,6 +514,51 @@ __global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
   if (lane < k - tl) put1(tl + lane);
 }
 
+__global__ void expand_write_kernel(omq_forest f, omq_wave w, ExpCfg c) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  int bx = blockIdx.x, by = blockIdx.y;
+  xcd_block(&bx, &by);  // one contiguous run of blocks (leaves of few trees) per XCD
+  expand_write_block(f, w, c, bx, by, smem);
+}
+
+// ---------------------------------------------------------------------------------------
+// A wave's expansion and group backup in two launches instead of four.  The expansion writes
+// the expanded leaves' row headers and their new children, the backup N and W of the path
+// nodes: no address is written by both, and neither reads what the other writes (the new
+// children lie past every path node, and the backup reads no row header).  Under the
+// reference_pw rule the expansion reads the root's count, which the backup changes; there the
+// two run one after the other (omq_expand_backup).  So the plan runs beside the signed leaf
+// values, and the child writes beside the group backup.
+
+// Plan of tree blockIdx.y (block 0 of each tree), beside the signed leaf values of its
+// simulations (blocks 1 on, kPlanThreads simulations each).
+__global__ __launch_bounds__(kPlanThreads) void plan_values_kernel(omq_forest f, omq_wave w,
+                                                                   ExpCfg c, int sign_mode) {
+  extern __shared__ __align__(16) int want[];  // [max_wave] (ucount <= max_wave)
+  const int t = blockIdx.y;
+  if (blockIdx.x == 0) {
+    expand_plan_block(f, w, c, t, want);
+    return;
+  }
+  const int s = ((int)blockIdx.x - 1) * kPlanThreads + (int)threadIdx.x;
+  if (s < c.W) sim_value_at(f, w, t, s, sign_mode);
+}
+
+// Blocks [0, nbe) of a tree: expand_write_block (kBackupThreads / 64 leaves each); the rest:
+// backup_groups_block, nbb of them.
+template <bool FUSED>
+__global__ __launch_bounds__(kBackupThreads) void write_backup_kernel(omq_forest f, omq_wave w,
+                                                                      ExpCfg c, int sign_mode,
+                                                                      int nbe, int nbb) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  int bx = blockIdx.x, by = blockIdx.y;
+  xcd_block(&bx, &by);  // one contiguous run of blocks (leaves of few trees) per XCD
+  if (bx < nbe)
+    expand_write_block(f, w, c, bx, by, smem);
+  else
+    backup_groups_block<FUSED>(f, w, c.vli, sign_mode, bx - nbe, by, nbb);
+}
+
 // ---------------------------------------------------------------------------------------
 size_t leaf_lds_per_wave_host(const omq_forest& f) { return leaf_lds_per_wave(f); }
 
@@ -550,6 +601,41 @@ hipError_t launch_expand(const omq_forest& f, const omq_wave& w, int W, float vi
   while (wpb > 1 && per * wpb > 64 * 1024) wpb >>= 1;
   dim3 grid((W + wpb - 1) / wpb, f.num_trees);
   hipLaunchKernelGGL(expand_write_kernel, grid, dim3(wpb * kWave), per * wpb, st, f, w, c);
+  return hipGetLastError();
+}
+
+bool expand_backup_fusable(const omq_forest& f, int policy, int w_mode) {
+  return policy == OMQ_EXPAND_FULL && w_mode == OMQ_WACC_ORDERED &&
+         expand_lds_per_wave(f) * (kBackupThreads / kWave) <= 64 * 1024;
+}
+
+hipError_t launch_expand_backup(const omq_forest& f, const omq_wave& w, int W,
+                                float virtual_loss, const double* noise, double eps,
+                                int sign_mode, hipStream_t st) {
+  ExpCfg c;
+  c.W = W;
+  c.vli = (int)virtual_loss;
+  c.policy = OMQ_EXPAND_FULL;
+  c.noise = noise;
+  c.eps = eps;
+  // the signed leaf values: formed by the group backup itself for the waves it fuses them in
+  const bool fused_values = W <= kFuseMaxWave;
+  const int nvb = fused_values ? 0 : (W + kPlanThreads - 1) / kPlanThreads;
+  hipLaunchKernelGGL(plan_values_kernel, dim3(1 + nvb, f.num_trees), dim3(kPlanThreads),
+                     (size_t)w.max_wave * sizeof(int), st, f, w, c, sign_mode);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  constexpr int wpb = kBackupThreads / kWave;
+  const size_t lds = expand_lds_per_wave(f) * wpb;
+  const int nbe = (W + wpb - 1) / wpb;
+  const int nbb = backup_group_blocks(W);
+  const dim3 grid(nbe + nbb, f.num_trees);
+  if (fused_values)
+    hipLaunchKernelGGL(write_backup_kernel<true>, grid, dim3(kBackupThreads), lds, st, f, w, c,
+                       sign_mode, nbe, nbb);
+  else
+    hipLaunchKernelGGL(write_backup_kernel<false>, grid, dim3(kBackupThreads), lds, st, f, w, c,
+                       sign_mode, nbe, nbb);
   return hipGetLastError();
 }
 

@@ -264,3 +264,44 @@ def test_select_leaf_records_equal_leaf_info(device, name):
         assert (key_s[t, :n] == key_i[t, :n]).all()
         assert (legal_s[t, :n] == legal_i[t, :n]).all()
         assert (legal_s[t, :n] >= 0).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw", [
+    ("C2", {"num_trees": 3, "num_simulations": 1024, "wave_size": 256, "capacity": 200_000}),
+    ("C3", {"num_trees": 2, "num_simulations": 3072, "wave_size": 1024, "capacity": 500_000}),
+    ("C4", {"num_trees": 2, "num_simulations": 4096, "wave_size": 2048, "capacity": 200_000}),
+])
+def test_expand_backup_equals_expand_then_backup(device, name, kw):
+    """omq_expand_backup (the expansion's and the backup's kernels side by side) leaves every
+    node's N, W, P, parent, action and row exactly as omq_expand followed by omq_backup."""
+    wl = get(name).scaled(name=f"{name}-expand-backup", **kw)
+    params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth,
+                          dirichlet_epsilon=wl.dirichlet_epsilon)
+    engs = []
+    for _ in range(2):
+        e = WaveEngine(wl.model, wl.num_trees, wl.capacity, wl.wave_size, wl.max_depth, device,
+                       params)
+        e.set_roots(*wl.root_inputs())
+        e.reset()
+        engs.append(e)
+    ev = SyntheticEvaluator(wl.logit_scale)
+    sizes = [1] + [wl.wave_size] * ((wl.num_simulations - 1) // wl.wave_size)
+    for W in sizes:
+        engs[0].run_wave(W, ev)  # omq_expand_backup
+        e = engs[1]
+        e.select(W)
+        if e.needs_leaf_info(W):
+            e.leaf_info(W)
+        ev.evaluate_wave(e)
+        e.expand(W)
+        e.backup(W)
+    torch.cuda.synchronize()
+    for e in engs:
+        e.check_status()
+    a, b = engs
+    assert torch.equal(a.num_nodes, b.num_nodes)
+    for name_ in ("N", "W", "P", "parent", "first", "nchild", "action"):
+        x, y = getattr(a, name_), getattr(b, name_)
+        assert torch.equal(x.view(torch.int32) if x.dtype == torch.float32 else x,
+                           y.view(torch.int32) if y.dtype == torch.float32 else y), name_
