@@ -544,8 +544,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_values_kernel(omq_forest f,
   if (s < c.W) sim_value_at(f, w, t, s, sign_mode);
 }
 
-// Blocks [0, nbe) of a tree: expand_write_block (kBackupThreads / 64 leaves each); the rest:
-// backup_groups_block, nbb of them.
+// Blocks [0, nbb) of a tree: backup_groups_block; the rest: expand_write_block (kBackupThreads
+// / 64 leaves each), nbe of them.  The backup's blocks come first, so that their dependent
+// loads start with the first writes instead of after the last (C3's expansion-and-backup phase
+// 68.2 -> 63.1 us, C4's 68.0 -> 61.5 us, C2's 33.6 -> 31.6 us against the writes first).
 template <bool FUSED>
 __global__ __launch_bounds__(kBackupThreads) void write_backup_kernel(omq_forest f, omq_wave w,
                                                                       ExpCfg c, int sign_mode,
@@ -553,10 +555,10 @@ __global__ __launch_bounds__(kBackupThreads) void write_backup_kernel(omq_forest
   extern __shared__ __align__(16) unsigned char smem[];
   int bx = blockIdx.x, by = blockIdx.y;
   xcd_block(&bx, &by);  // one contiguous run of blocks (leaves of few trees) per XCD
-  if (bx < nbe)
-    expand_write_block(f, w, c, bx, by, smem);
+  if (bx < nbb)
+    backup_groups_block<FUSED>(f, w, c.vli, sign_mode, bx, by, nbb);
   else
-    backup_groups_block<FUSED>(f, w, c.vli, sign_mode, bx - nbe, by, nbb);
+    expand_write_block(f, w, c, bx - nbb, by, smem);
 }
 
 // ---------------------------------------------------------------------------------------
