@@ -9,9 +9,13 @@
 //
 // Kernels per wave:
 //   leaf_info_kernel    thread per unique leaf: hash key (fold over path actions), legal count
+//                       (waves of more than OMQ_SELECT_RECORDS_MAX_WAVE; select forms them for
+//                       smaller waves)
 //   synth_eval_kernel   wave per unique leaf: synthetic priors/value (evaluator stand-in)
 //   expand_plan_kernel  workgroup per tree: children counts, scan, capacity rule, row headers
 //   expand_write_kernel wave per expanded leaf: priors, children N/W/P/parent/action/row
+//   plan_values_kernel, write_backup_kernel: the plan and the writes side by side with the
+//                       signed leaf values and the group backup (omq_expand_backup)
 #include "backup_groups.h"
 #include "omq_common.h"
 
