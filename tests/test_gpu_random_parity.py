@@ -55,3 +55,38 @@ def test_random_workload_parity(device, i):
           f"vl={wl.virtual_loss} c={wl.c_puct} depth={wl.max_depth} {wl.expand_policy} "
           f"eps={wl.dirichlet_epsilon}", flush=True)
     assert run_parity(wl, device=device) >= 2
+
+
+N_RULE_CASES = 24
+
+
+def _rule_case(i: int):
+    """Board workloads with a rule on: the Gomoku terminal check (freestyle or renju) on dense
+    boards, or the Go rules (ko, ko + suicide)."""
+    rng = np.random.default_rng(9700 + i)
+    W = int(rng.choice([1, 16, 64, 256, 513, 1024]))
+    waves = int(rng.integers(2, 5))
+    T = int(rng.integers(1, 4))
+    if i % 2 == 0:
+        bs = int(rng.integers(5, 16))
+        wl = get("C2").scaled(name=f"random-rule-{i}-gomoku{bs}", model=games.gomoku(bs),
+                              max_stones=int(rng.integers(bs * bs // 4, bs * bs // 2)),
+                              num_trees=T, num_simulations=1 + W * waves, wave_size=W,
+                              capacity=1 + W * waves * bs * bs,
+                              seed=int(rng.integers(1, 1 << 30)))
+        return wl, {"rule": int(rng.integers(0, 2))}
+    bs = int(rng.choice([5, 7, 9, 13]))
+    wl = get("C3").scaled(name=f"random-rule-{i}-go{bs}", model=games.go(bs),
+                          max_stones=int(rng.integers(0, bs * bs // 2)), num_trees=T,
+                          num_simulations=1 + W * waves, wave_size=W,
+                          capacity=1 + W * waves * (bs * bs + 1),
+                          seed=int(rng.integers(1, 1 << 30)))
+    return wl, {"go_flags": int(rng.choice([1, 3]))}
+
+
+@pytest.mark.parametrize("i", range(N_RULE_CASES))
+def test_random_rules_parity(device, i):
+    wl, kw = _rule_case(i)
+    print(f"[random rules parity] {wl.name}: T={wl.num_trees} W={wl.wave_size} "
+          f"sims={wl.num_simulations} {kw}", flush=True)
+    assert run_parity(wl, device=device, **kw) >= 2
