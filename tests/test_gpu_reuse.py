@@ -148,3 +148,70 @@ def test_shift_large_subtree_matches_oracle(device):
     torch.cuda.synchronize()
     assert kept > 3 * 4096
     _assert_trees(eng, orc, "after a large shift")
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_random_shift_and_continue_matches_oracle(device, i):
+    """Seeded random workloads: after a few waves each tree keeps the subtree of a random root
+    child (or stays whole: -1), on the GPU and in the oracle; the compacted trees and two more
+    waves on them are compared."""
+    rng = np.random.default_rng(5200 + i)
+    kind = ["gomoku", "go", "sparse"][i % 3]
+    if kind == "gomoku":
+        model, base = games.gomoku(int(rng.integers(5, 16))), "C2"
+    elif kind == "go":
+        model, base = games.go(int(rng.choice([5, 9, 13, 19]))), "C3"
+    else:
+        lo = int(rng.integers(1, 30))
+        model, base = games.chess_sparse(int(rng.choice([64, 4672])), lo,
+                                         lo + int(rng.integers(0, 30))), "C4"
+    W = int(rng.choice([16, 64, 256, 600]))
+    T = int(rng.integers(1, 5))
+    waves = int(rng.integers(1, 4))
+    stones = int(rng.integers(0, model.num_actions // 3)) if model.kind != "sparse" else 0
+    wl = get(base).scaled(name=f"reuse-random-{i}", model=model, num_trees=T, max_stones=stones,
+                          num_simulations=1 + W * (waves + 2), wave_size=W,
+                          capacity=1 + W * (waves + 2) * (model.max_legal if model.kind ==
+                                                          "sparse" else model.num_actions),
+                          dirichlet_epsilon=0.0, seed=int(rng.integers(1, 1 << 30)))
+    eng, orc, ev = make_pair(wl, device=device)
+    eng.reset()
+    for t in range(T):
+        orc.reset_tree(t)
+    for w in [1] + [W] * waves:
+        eng.run_wave(w, ev)
+        for t in range(T):
+            orc.wave(t, w)
+    torch.cuda.synchronize()
+    keys, legal, _ = wl.root_inputs()
+    new_roots, acts = [], []
+    for t in range(T):
+        tr = orc.tree(t)
+        f, k = tr["first"][0], tr["nchild"][0]
+        if k <= 0 or rng.random() < 0.2:
+            new_roots.append(-1)
+            acts.append(-1)
+            continue
+        pick = int(f + 1 + rng.integers(0, k))
+        new_roots.append(pick)
+        acts.append(int(tr["action"][pick]))
+    eng.shift_roots(new_roots)
+    for t in range(T):
+        if new_roots[t] >= 0:
+            assert orc.shift_root(t, new_roots[t]) >= 1
+    torch.cuda.synchronize()
+    _assert_trees(eng, orc, f"random {i} after shift")
+    keys = np.array([games.child_key(int(kk), a) if a >= 0 else int(kk)
+                     for kk, a in zip(keys, acts)], np.uint64)
+    if wl.model.is_board:
+        for t, a in enumerate(acts):
+            if a >= 0 and not (model.kind == "go" and a == model.num_actions - 1):
+                legal[t, a // 32] &= np.uint32(~(1 << (a % 32)) & 0xFFFFFFFF)
+    eng.set_roots(keys, legal)
+    orc.set_roots(keys, legal)
+    for j in range(2):
+        eng.run_wave(W, ev)
+        for t in range(T):
+            orc.wave(t, W)
+        torch.cuda.synchronize()
+        compare_wave(eng, orc, W, f"random {i} continued wave {j}")
