@@ -1705,7 +1705,7 @@ __device__ inline int size_class(int m) { return 15 - min(15, 31 - __clz(m)); }
 // Chain groups [0, nb) of a level reordered by size class, largest first, so that the dynamic
 // deal hands out the longest chains first and a level does not end on a long chain taken late.
 // The order within a class is arbitrary (groups of one level are independent).  tn/ts is
-// scratch of nb entries (the group arrays of the next level, empty at this point).  Called by
+// scratch of nb entries (a free range of the next level's group arrays).  Called by
 // every thread of the workgroup.  Kept out of line: inlined, it changes the register
 // allocation of the 6-slot kernel's chains.
 template <int NT>
@@ -2017,10 +2017,16 @@ __device__ int level_loop(const SelArgs& f, const SelCfg& c, int t, int d0, int 
       prefix_pass<RMAX, NT>(f, c, t, d, W, tb, gmax, L, sh, lfs, lflag, sh.nbig[cur], vl_done,
                             sg);
     const int nb = sh.nbig[cur];
-    // more chain groups than waves: the longest first
-    if (nb > NW)
-      order_groups<NT>(gnode + cur * W, gsl + cur * W, gnode + nxt * W, gsl + nxt * W, nb,
-                       sh.hist);
+    // more chain groups than waves: the longest first.  The scratch is the next level's group
+    // arrays past the groups already there: the kernels without the single-member passes
+    // keep the prefix pass's groups at the bottom (the others put them at the top).  Those
+    // groups hold members of finished groups and the chain groups at least one member each,
+    // so the free range [nbig[nxt], W - nsmall[nxt]) has room for nb entries.
+    if (nb > NW) {
+      const int toff = Tr::kSingles ? 0 : sh.nbig[nxt];
+      order_groups<NT>(gnode + cur * W, gsl + cur * W, gnode + nxt * W + toff,
+                       gsl + nxt * W + toff, nb, sh.hist);
+    }
     // The chain groups are dealt dynamically: each wave takes the next index from an LDS
     // counter, so a wave that finishes a short chain takes the next group at once.  The next
     // index is requested when a group starts, so that the answer is back by its end.  Every

@@ -14,15 +14,16 @@ pytestmark = pytest.mark.gpu
 N_CASES = 48
 
 
-def _case(i: int):
-    rng = np.random.default_rng(9100 + i)
-    kind = ["gomoku", "go", "sparse"][i % 3]
+def _case(i: int, seed: int = 9100, gomoku_sizes=range(5, 16), go_sizes=(5, 9, 13, 19),
+          kinds=("gomoku", "go", "sparse")):
+    rng = np.random.default_rng(seed + i)
+    kind = kinds[i % len(kinds)]
     if kind == "gomoku":
-        bs = int(rng.integers(5, 16))
+        bs = int(rng.choice(list(gomoku_sizes)))
         model, base = games.gomoku(bs), "C2"
         extra = {"max_stones": int(rng.integers(0, bs * bs // 3))}
     elif kind == "go":
-        bs = int(rng.choice([5, 9, 13, 19]))
+        bs = int(rng.choice(list(go_sizes)))
         model, base = games.go(bs), "C3"
         extra = {"max_stones": int(rng.integers(0, bs * bs // 3))}
     else:
@@ -90,3 +91,46 @@ def test_random_rules_parity(device, i):
     print(f"[random rules parity] {wl.name}: T={wl.num_trees} W={wl.wave_size} "
           f"sims={wl.num_simulations} {kw}", flush=True)
     assert run_parity(wl, device=device, **kw) >= 2
+
+
+# Boards of 257-320 and 385-512 actions: the select kernels of five and eight slots per lane,
+# which keep single-member groups with the chain groups (a level's group ordering once
+# overwrote the next level's groups that its first-unvisited pass had formed there), and, above
+# 384 actions, the expansion that reads the policy row from memory instead of staging it.
+WIDE_BOARDS = [
+    ("gomoku", 17, 256, {}), ("go", 17, 600, {"go_flags": 1}),
+    ("gomoku", 20, 256, {}), ("gomoku", 21, 600, {}), ("gomoku", 22, 256, {"rule": 1}),
+    ("go", 20, 600, {}), ("go", 21, 256, {"go_flags": 3}), ("go", 22, 1024, {"go_flags": 1}),
+]
+
+
+@pytest.mark.parametrize("i", range(len(WIDE_BOARDS)))
+def test_wide_board_parity(device, i):
+    kind, bs, W, kw = WIDE_BOARDS[i]
+    rng = np.random.default_rng(9900 + i)
+    model = games.gomoku(bs) if kind == "gomoku" else games.go(bs)
+    waves = 3
+    lo = bs * bs // 4 if "rule" in kw else 0
+    wl = get("C2" if kind == "gomoku" else "C3").scaled(
+        name=f"wide-{kind}{bs}", model=model, num_trees=2,
+        max_stones=int(rng.integers(lo, bs * bs // 3)), num_simulations=1 + W * waves,
+        wave_size=W, capacity=1 + W * waves * model.num_actions,
+        seed=int(rng.integers(1, 1 << 30)))
+    print(f"[wide board parity] {wl.name}: A={model.num_actions} W={W} {kw}", flush=True)
+    assert run_parity(wl, device=device, **kw) >= 2
+
+
+N_WIDE_CASES = 16
+
+
+@pytest.mark.parametrize("i", range(N_WIDE_CASES))
+def test_random_wide_board_parity(device, i):
+    """The random knobs of test_random_workload_parity on boards of 257-512 actions (select
+    kernels of five, six and eight slots per lane)."""
+    wl = _case(i, seed=9300, gomoku_sizes=(17, 18, 20, 21, 22), go_sizes=(17, 18, 20, 21, 22),
+               kinds=("gomoku", "go"))
+    print(f"[random wide parity] {wl.name}: A={wl.model.num_actions} T={wl.num_trees} "
+          f"W={wl.wave_size} sims={wl.num_simulations} cap={wl.capacity} "
+          f"vl={wl.virtual_loss} c={wl.c_puct} depth={wl.max_depth} {wl.expand_policy} "
+          f"eps={wl.dirichlet_epsilon}", flush=True)
+    assert run_parity(wl, device=device) >= 2
