@@ -134,3 +134,48 @@ def test_random_wide_board_parity(device, i):
           f"vl={wl.virtual_loss} c={wl.c_puct} depth={wl.max_depth} {wl.expand_policy} "
           f"eps={wl.dirichlet_epsilon}", flush=True)
     assert run_parity(wl, device=device) >= 2
+
+
+N_EDGE_CASES = 24
+
+
+def _edge_case(i: int):
+    """Knobs at the edges of what the library accepts: virtual loss 0 (every rank of a chain
+    takes the first rank's child), fractional (the count grows by its integer part, Q's
+    denominator by the whole), or large; c_puct 0 (pure Q); depth limits of 1 (every path ends
+    at the root) and 2; every select kernel width."""
+    rng = np.random.default_rng(9500 + i)
+    kind = ["gomoku", "go", "sparse"][i % 3]
+    if kind == "gomoku":
+        bs = int(rng.choice([5, 9, 15, 17, 19, 22]))
+        model, base = games.gomoku(bs), "C2"
+        extra = {"max_stones": int(rng.integers(0, bs * bs // 3))}
+    elif kind == "go":
+        bs = int(rng.choice([5, 13, 17, 19, 21]))
+        model, base = games.go(bs), "C3"
+        extra = {"max_stones": int(rng.integers(0, bs * bs // 3))}
+    else:
+        lo = int(rng.integers(1, 40))
+        model, base = games.chess_sparse(int(rng.choice([64, 4672])), lo,
+                                         lo + int(rng.integers(0, 25))), "C4"
+        extra = {}
+    W = int(rng.choice([1, 16, 64, 256, 600, 1024]))
+    waves = int(rng.integers(2, 5))
+    width = model.num_actions if kind != "sparse" else lo + 25
+    return get(base).scaled(
+        name=f"edge-{i}-{kind}", model=model, num_trees=int(rng.integers(1, 4)),
+        num_simulations=1 + W * waves, wave_size=W, capacity=1 + W * waves * width,
+        virtual_loss=float(rng.choice([0.0, 0.5, 1.5, 2.5, 7.0])),
+        c_puct=float(rng.choice([0.0, 0.25, 1.0, 3.0])),
+        max_depth=int(rng.choice([1, 2, 5, 100])),
+        expand_policy="reference_pw" if rng.random() < 0.25 else "full",
+        seed=int(rng.integers(1, 1 << 30)), **extra)
+
+
+@pytest.mark.parametrize("i", range(N_EDGE_CASES))
+def test_edge_knob_parity(device, i):
+    wl = _edge_case(i)
+    print(f"[edge parity] {wl.name}: A={wl.model.num_actions} T={wl.num_trees} "
+          f"W={wl.wave_size} sims={wl.num_simulations} vl={wl.virtual_loss} c={wl.c_puct} "
+          f"depth={wl.max_depth} {wl.expand_policy}", flush=True)
+    assert run_parity(wl, device=device) >= 2
