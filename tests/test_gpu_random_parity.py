@@ -179,3 +179,21 @@ def test_edge_knob_parity(device, i):
           f"W={wl.wave_size} sims={wl.num_simulations} vl={wl.virtual_loss} c={wl.c_puct} "
           f"depth={wl.max_depth} {wl.expand_policy}", flush=True)
     assert run_parity(wl, device=device) >= 2
+
+
+N_MODE_CASES = 18
+
+
+@pytest.mark.parametrize("i", range(N_MODE_CASES))
+def test_random_modes_parity(device, i):
+    """The random workloads with the other accumulation modes, over every select kernel width:
+    atomic virtual loss (one atomic per arrival), atomic W (float atomics, compared within
+    1e-5) and the root-positive sign, one or two of them at a time."""
+    wl = _case(i, seed=9600, gomoku_sizes=(5, 9, 15, 17, 20, 22), go_sizes=(5, 13, 17, 19, 21))
+    rng = np.random.default_rng(9650 + i)
+    kw = [dict(vl_atomic=True), dict(w_mode=1), dict(sign_mode=1),
+          dict(vl_atomic=True, w_mode=1), dict(vl_atomic=True, sign_mode=1),
+          dict(w_mode=1, sign_mode=1)][int(rng.integers(0, 6))]
+    print(f"[random modes parity] {wl.name}: A={wl.model.num_actions} T={wl.num_trees} "
+          f"W={wl.wave_size} sims={wl.num_simulations} {kw}", flush=True)
+    assert run_parity(wl, device=device, **kw) >= 2
