@@ -107,3 +107,20 @@ def test_features_small_board_deep_paths(device):
     eng.search(160, W, ev)
     torch.cuda.synchronize()
     assert ev.waves == 11
+
+
+@pytest.mark.parametrize("bs", [5, 11, 19, 22])
+def test_features_board_sizes(device, bs):
+    # boards from 5x5 to 22x22 (484 cells, the widest board the library takes), a third full
+    model = games.gomoku(bs)
+    T, W = 2, 64
+    boards = games.random_boards(T, bs, bs * bs // 3, 11 + bs)
+    keys = games.root_keys(11 + bs, T)
+    legal = games.legal_masks(model, boards, T)
+    eng = WaveEngine(model, T, 1 + 4 * W * bs * bs, W, 100, device,
+                     SearchParams(c_puct=1.4, virtual_loss=3.0))
+    eng.set_roots(keys, legal)
+    ev = _CheckingEvaluator(eng, boards)
+    eng.search(3 * W, W, ev)
+    torch.cuda.synchronize()
+    assert ev.waves == 4
