@@ -155,12 +155,23 @@ def test_random_shift_and_continue_matches_oracle(device, i):
     """Seeded random workloads: after a few waves each tree keeps the subtree of a random root
     child (or stays whole: -1), on the GPU and in the oracle; the compacted trees and two more
     waves on them are compared."""
-    rng = np.random.default_rng(5200 + i)
-    kind = ["gomoku", "go", "sparse"][i % 3]
+    _shift_and_continue(device, i, np.random.default_rng(5200 + i), wide=False)
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_random_shift_and_continue_wide_boards(device, i):
+    """The same on boards of 289-485 actions (select kernels of five, six and eight slots)."""
+    _shift_and_continue(device, i, np.random.default_rng(5400 + i), wide=True)
+
+
+def _shift_and_continue(device, i, rng, wide):
+    kind = ["gomoku", "go"][i % 2] if wide else ["gomoku", "go", "sparse"][i % 3]
     if kind == "gomoku":
-        model, base = games.gomoku(int(rng.integers(5, 16))), "C2"
+        model, base = games.gomoku(int(rng.choice([17, 18, 20, 21, 22]) if wide
+                                       else rng.integers(5, 16))), "C2"
     elif kind == "go":
-        model, base = games.go(int(rng.choice([5, 9, 13, 19]))), "C3"
+        model, base = games.go(int(rng.choice([17, 20, 21, 22] if wide
+                                              else [5, 9, 13, 19]))), "C3"
     else:
         lo = int(rng.integers(1, 30))
         model, base = games.chess_sparse(int(rng.choice([64, 4672])), lo,
