@@ -78,3 +78,30 @@ def test_search_with_device_noise_matches_oracle(device):
             orc.wave(t, w)
         torch.cuda.synchronize()
         compare_wave(eng, orc, w, f"device noise wave {i}")
+
+
+@pytest.mark.parametrize("kind,bs", [("gomoku", 22), ("go", 21)])
+def test_root_ops_wide_boards(device, kind, bs):
+    """Policies, move sampling and root noise on boards of 442-484 actions."""
+    model = games.gomoku(bs) if kind == "gomoku" else games.go(bs)
+    wl = get("C2" if kind == "gomoku" else "C3").scaled(
+        model=model, num_trees=4, num_simulations=768, wave_size=256, max_stones=bs * bs // 4,
+        capacity=1 + 4 * 256 * model.num_actions)
+    eng, orc, ev = make_pair(wl, device=device)
+    eng.search(wl.num_simulations, wl.wave_size, ev)
+    orc.search(wl.num_simulations, wl.wave_size)
+    pol = eng.root_policies()
+    lib = load()
+    for t in range(wl.num_trees):
+        assert np.array_equal(pol[t], orc.root_policy(t))
+    for temperature in (0.0, 1.0):
+        for counter in range(3):
+            acts = eng.sample_actions(temperature, 99, counter)
+            for t in range(wl.num_trees):
+                row = np.ascontiguousarray(pol[t])
+                want = lib.orc_sample_action(row.ctypes.data, eng.A, temperature, 99, counter, t)
+                assert acts[t] == want, (temperature, counter, t)
+    eng.device_root_noise(0.03, 31, 4)
+    got = eng.noise.view(eng.T, eng.A).cpu().numpy()
+    for t in range(eng.T):
+        assert np.array_equal(got[t], orc.root_dirichlet(t, 0.03, 31, 4)), t
