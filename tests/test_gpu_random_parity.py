@@ -197,3 +197,16 @@ def test_random_modes_parity(device, i):
     print(f"[random modes parity] {wl.name}: A={wl.model.num_actions} T={wl.num_trees} "
           f"W={wl.wave_size} sims={wl.num_simulations} {kw}", flush=True)
     assert run_parity(wl, device=device, **kw) >= 2
+
+
+@pytest.mark.parametrize("lo,hi,W,depth", [(1, 1, 4, 128), (1, 2, 16, 128), (1, 2, 64, 60),
+                                           (1, 3, 1, 128)])
+def test_deep_paths_parity(device, lo, hi, W, depth):
+    """Narrow sparse rows (one to three children), so that paths grow by about a node a wave
+    and reach the depth limit: up to OMQ_MAX_DEPTH (128) nodes on a path."""
+    waves = 150 if W <= 4 else 40
+    wl = get("C4").scaled(name=f"deep-{lo}-{hi}-W{W}", model=games.chess_sparse(64, lo, hi),
+                          num_trees=2, num_simulations=1 + W * waves, wave_size=W,
+                          capacity=1 + W * waves * hi, max_depth=depth, seed=4242 + W)
+    print(f"[deep parity] {wl.name}: depth limit {depth}, {waves} waves", flush=True)
+    assert run_parity(wl, device=device, check_every=10) >= 2
