@@ -210,3 +210,17 @@ def test_deep_paths_parity(device, lo, hi, W, depth):
                           capacity=1 + W * waves * hi, max_depth=depth, seed=4242 + W)
     print(f"[deep parity] {wl.name}: depth limit {depth}, {waves} waves", flush=True)
     assert run_parity(wl, device=device, check_every=10) >= 2
+
+
+@pytest.mark.parametrize("base,model,T,W", [("C2", games.gomoku(9), 300, 16),
+                                            ("C3", games.go(19), 130, 64),
+                                            ("C4", games.chess_sparse(4672, 20, 45), 257, 33)])
+def test_many_trees_parity(device, base, model, T, W):
+    """Forests of more trees than the device has CUs (select: one workgroup per tree; the
+    expansion's and backup's grids remapped over the XCDs)."""
+    width = model.max_legal if model.kind == "sparse" else model.num_actions
+    wl = get(base).scaled(name=f"many-{base}-T{T}", model=model, num_trees=T,
+                          num_simulations=1 + 3 * W, wave_size=W,
+                          capacity=1 + 3 * W * width, max_stones=5)
+    print(f"[many trees parity] {wl.name}: A={model.num_actions} W={W}", flush=True)
+    assert run_parity(wl, device=device) >= 2
