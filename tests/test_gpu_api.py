@@ -365,3 +365,20 @@ def test_search_graph_replay_matches_eager(device):
             assert a[0] == b[0], i
             for x, y in zip(a[1:], b[1:]):
                 assert np.array_equal(x, y), i
+
+
+@pytest.mark.parametrize("game,bs,wave", [("gomoku", 20, 64), ("go", 21, 256), ("gomoku", 9, 16)])
+def test_search_board_sizes_match_oracle(device, game, bs, wave):
+    """MCTS.search on boards of other sizes (81-484 actions) and wave sizes."""
+    gt = GameType.GOMOKU if game == "gomoku" else GameType.GO
+    cfg = _config(board_size=bs, game_type=gt, max_wave_size=wave, num_simulations=4 * wave,
+                  max_tree_nodes=1 + 5 * wave * (bs * bs + 1))
+    board = games.random_boards(1, bs, bs * bs // 5, 3 + bs)[0]
+    m = MCTS(cfg, SyntheticEvaluator())
+    pol = m.search(board)
+    orc = _oracle_for(cfg, board[None])
+    orc.search(4 * wave, wave)
+    A = bs * bs + (1 if game == "go" else 0)
+    assert pol.shape == (A,)
+    assert np.array_equal(pol, orc.root_policy(0))
+    _assert_tree_equal(m, orc)
