@@ -50,7 +50,7 @@ def _same_f32(a, b):
     return np.array_equal(np.asarray(a, F).view(np.int32), np.asarray(b, F).view(np.int32))
 
 
-@pytest.mark.parametrize("mc", [3, 64, 65, 300])
+@pytest.mark.parametrize("mc", [3, 64, 65, 300, 1000])
 def test_find_expansion_nodes(device, mc):
     rng = np.random.default_rng(mc)
     nn = 2000
@@ -103,7 +103,7 @@ def test_batched_ucb_selection(device, seed):
     assert (bad.cpu() == -1).all()
 
 
-@pytest.mark.parametrize("mc", [4, 64, 150])
+@pytest.mark.parametrize("mc", [4, 64, 150, 700])
 def test_fused_select_expand(device, mc):
     rng = np.random.default_rng(7 + mc)
     nn = 3000
@@ -123,7 +123,7 @@ def test_fused_select_expand(device, mc):
     assert want[1].max() >= 4
 
 
-@pytest.mark.parametrize("mc", [4, 64, 150])
+@pytest.mark.parametrize("mc", [4, 64, 150, 700])
 def test_fused_select_expand_optimized(device, mc):
     rng = np.random.default_rng(11 + mc)
     nn = 3000

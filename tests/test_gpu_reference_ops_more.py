@@ -42,7 +42,8 @@ def test_psvl_known_answer_on_gpu(device):
 
 
 @pytest.mark.parametrize("seed,mc,per_sim,masked", [(0, 8, False, False), (1, 64, False, True),
-                                                    (2, 65, True, False), (3, 300, True, True)])
+                                                    (2, 65, True, False), (3, 300, True, True),
+                                                    (4, 1000, True, True)])
 def test_psvl_random(device, seed, mc, per_sim, masked):
     rng = np.random.default_rng(40 + seed)
     nn, S, A = 1500, 2100, 50
@@ -82,7 +83,7 @@ def test_psvl_accelerator_method(device):
 
 
 # ---- fused_ucb_with_noise ----------------------------------------------------------------------
-@pytest.mark.parametrize("C", [1, 64, 65, 362])
+@pytest.mark.parametrize("C", [1, 64, 65, 362, 4672])
 def test_fused_ucb_with_noise_random(device, C):
     rng = np.random.default_rng(C)
     S = 700
@@ -111,7 +112,7 @@ def test_ucb_dense_known_answer_on_gpu(device):
     assert _np(torch_ops.batched_ucb_selection_dense(*args, 1.0)).tolist() == UCBD_EXPECT
 
 
-@pytest.mark.parametrize("M", [3, 64, 65, 200])
+@pytest.mark.parametrize("M", [3, 64, 65, 200, 1000])
 def test_ucb_dense_random(device, M):
     rng = np.random.default_rng(100 + M)
     B, NV = 1300, 400
@@ -130,7 +131,7 @@ def test_ucb_dense_random(device, M):
 
 # ---- batched_dirichlet_noise -------------------------------------------------------------------
 @pytest.mark.parametrize("S,A,alpha", [(5, 362, 0.03), (40, 225, 0.3), (3, 1, 1.5),
-                                       (7, 70, 2.5)])
+                                       (7, 70, 2.5), (2, 4672, 0.3)])
 def test_dirichlet_rows_match_oracle(device, S, A, alpha):
     torch_ops.set_noise_seed(1234)
     got = torch_ops.batched_dirichlet_noise(S, A, alpha, 0.25, device)
