@@ -224,3 +224,33 @@ def test_many_trees_parity(device, base, model, T, W):
                           capacity=1 + 3 * W * width, max_stones=5)
     print(f"[many trees parity] {wl.name}: A={model.num_actions} W={W}", flush=True)
     assert run_parity(wl, device=device) >= 2
+
+
+N_RULE_KNOB_CASES = 16
+
+
+@pytest.mark.parametrize("i", range(N_RULE_KNOB_CASES))
+def test_random_rules_with_knobs_parity(device, i):
+    """The rules with the other knobs drawn too: the widening rule, root noise, virtual loss,
+    c_puct, cramped capacities and depth limits, on boards of 5x5 to 22x22."""
+    rng = np.random.default_rng(9800 + i)
+    W = int(rng.choice([1, 16, 64, 256, 600, 1024]))
+    waves = int(rng.integers(2, 5))
+    gomoku = i % 2 == 0
+    bs = int(rng.choice([5, 9, 15, 17, 20, 22] if gomoku else [5, 7, 13, 17, 19, 21]))
+    model = games.gomoku(bs) if gomoku else games.go(bs)
+    cap_full = 1 + W * waves * model.num_actions
+    wl = get("C2" if gomoku else "C3").scaled(
+        name=f"rule-knobs-{i}-{model.kind}{bs}", model=model, num_trees=int(rng.integers(1, 4)),
+        max_stones=int(rng.integers(bs * bs // 5, bs * bs // 2)),
+        num_simulations=1 + W * waves, wave_size=W,
+        capacity=int(cap_full if rng.random() < 0.6 else max(64, cap_full // 8)),
+        virtual_loss=float(rng.choice([0.5, 1.0, 3.0])), c_puct=float(rng.choice([0.5, 1.4, 3.0])),
+        max_depth=int(rng.choice([3, 100])),
+        expand_policy="reference_pw" if rng.random() < 0.5 else "full",
+        dirichlet_alpha=0.3, dirichlet_epsilon=0.25 if rng.random() < 0.5 else 0.0,
+        seed=int(rng.integers(1, 1 << 30)))
+    kw = {"rule": int(rng.integers(0, 2))} if gomoku else {"go_flags": int(rng.choice([1, 3]))}
+    print(f"[rules+knobs parity] {wl.name}: T={wl.num_trees} W={W} cap={wl.capacity} "
+          f"vl={wl.virtual_loss} {wl.expand_policy} eps={wl.dirichlet_epsilon} {kw}", flush=True)
+    assert run_parity(wl, device=device, **kw) >= 2
