@@ -254,3 +254,15 @@ def test_random_rules_with_knobs_parity(device, i):
     print(f"[rules+knobs parity] {wl.name}: T={wl.num_trees} W={W} cap={wl.capacity} "
           f"vl={wl.virtual_loss} {wl.expand_policy} eps={wl.dirichlet_epsilon} {kw}", flush=True)
     assert run_parity(wl, device=device, **kw) >= 2
+
+
+def test_parity_on_a_side_stream(device):
+    """Every launch and copy of a search goes to the caller's current stream: a search run
+    under another stream (default priority) follows the oracle too."""
+    import torch
+
+    wl = get("C3").scaled(name="side-stream", num_trees=3, num_simulations=1 + 3 * 600,
+                          wave_size=600, capacity=1 + 3 * 600 * 362)
+    s = torch.cuda.Stream(device=device)
+    with torch.cuda.stream(s):
+        assert run_parity(wl, device=device) >= 2
