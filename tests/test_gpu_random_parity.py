@@ -266,3 +266,33 @@ def test_parity_on_a_side_stream(device):
     s = torch.cuda.Stream(device=device)
     with torch.cuda.stream(s):
         assert run_parity(wl, device=device) >= 2
+
+
+def test_interleaved_engines_parity(device):
+    """Three engines of different models (select kernels of eight, six and one slot; board and
+    sparse expansion) in one process, their waves interleaved, each against its own oracle."""
+    import torch
+
+    from oracle.parity import compare_wave, make_pair
+
+    wls = [get("C2").scaled(name="mix-gomoku20", model=games.gomoku(20), num_trees=2,
+                            num_simulations=1 + 3 * 256, wave_size=256,
+                            capacity=1 + 3 * 256 * 400, max_stones=40),
+           get("C3").scaled(name="mix-go19", num_trees=2, num_simulations=1 + 3 * 600,
+                            wave_size=600, capacity=1 + 3 * 600 * 362),
+           get("C4").scaled(name="mix-sparse", num_trees=2, num_simulations=1 + 3 * 1024,
+                            wave_size=1024, capacity=1 + 3 * 1024 * 45)]
+    pairs = [make_pair(wl, device=device) for wl in wls]
+    for eng, orc, _ in pairs:
+        eng.reset()
+        for t in range(eng.T):
+            orc.reset_tree(t)
+    for i in range(4):
+        for wl, (eng, orc, ev) in zip(wls, pairs):
+            W = 1 if i == 0 else wl.wave_size
+            eng.run_wave(W, ev)
+            for t in range(eng.T):
+                orc.wave(t, W)
+        torch.cuda.synchronize()
+        for wl, (eng, orc, _) in zip(wls, pairs):
+            compare_wave(eng, orc, 1 if i == 0 else wl.wave_size, f"{wl.name} wave {i}")
