@@ -61,6 +61,12 @@ CASES = {
                           "capacity": 400_000}),
     "maxwave-C4": ("C4", {"num_trees": 1, "num_simulations": 8192, "wave_size": 4096,
                           "capacity": 400_000}),
+    # the widest and the five-slot select kernels at the largest wave
+    "maxwave-gomoku22": ("C2", {"num_trees": 1, "num_simulations": 8192, "wave_size": 4096,
+                                "capacity": 1_000_000, "model": games.gomoku(22),
+                                "max_stones": 60}),
+    "maxwave-go17": ("C3", {"num_trees": 1, "num_simulations": 8192, "wave_size": 4096,
+                            "capacity": 1_000_000, "model": games.go(17)}),
     # tiny capacities: the capacity-full rule at every fill level (first fit in first-occurrence
     # order, refused leaves backed up), with 1-10 children per leaf or counts falling by depth
     "capacity-sparse-60": ("C4", {"model": games.chess_sparse(64, 1, 10), "num_trees": 16,
