@@ -229,13 +229,18 @@ def test_root_chain_counter_within_select_time(device):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["C2", "C4"])
-def test_select_leaf_records_equal_leaf_info(device, name):
+@pytest.mark.parametrize("name,bs", [("C2", None), ("C4", None), ("C3", None), ("C3", 17),
+                                     ("C2", 22)])
+def test_select_leaf_records_equal_leaf_info(device, name, bs):
     """For a wave of at most OMQ_SELECT_RECORDS_MAX_WAVE simulations, omq_select forms the
     unique leaves' keys and legal counts itself; omq_leaf_info, run on the same wave, forms the
-    same words (board and sparse models), so the two paths are interchangeable."""
+    same words (board and sparse models, select kernels of one, four, five, six and eight
+    slots), so the two paths are interchangeable."""
+    kw = {}
+    if bs is not None:
+        kw = {"model": games.go(bs) if name == "C3" else games.gomoku(bs), "max_stones": 40}
     wl = get(name).scaled(name=f"{name}-records", num_trees=3, num_simulations=1024,
-                          wave_size=256, capacity=200_000)
+                          wave_size=256, capacity=400_000, **kw)
     assert wl.wave_size <= _lib.OMQ_SELECT_RECORDS_MAX_WAVE
     params = SearchParams(c_puct=wl.c_puct, virtual_loss=wl.virtual_loss, max_depth=wl.max_depth,
                           dirichlet_epsilon=wl.dirichlet_epsilon)
